@@ -1,0 +1,76 @@
+"""ctypes binding of the C-ABI library libshmaxx.so (declared in include/shmaxx.h).
+
+Mirrors the reference's loader (moondream/gpu/hgemm.py:21-33, hattn.py:5-15): one CDLL, explicit argtypes, int
+status returns, raw device pointers and the caller's HIP stream. There is no fallback: if the library is missing the
+first call raises, so a GPU run can never silently use another implementation.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libshmaxx.so")
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+L = ctypes.c_long
+F = ctypes.c_float
+
+# name -> argtypes (every entry point returns int status)
+SIGNATURES = {
+    "mx_gemm_bf16": [P, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I],
+    "mx_gemm_check": [I, P, L, P, L, P, P, L, P, L, I, I, I, I],
+    "mx_gemm_pick": [I, I, I],
+    "mx_gemm_ncfg": [],
+    "mx_gemm_cfg_tile": [I, ctypes.POINTER(I), ctypes.POINTER(I)],
+    "mx_sdpa": [P, P, L, L, L, P, L, L, L, P, L, L, L, P, L, L, L, I, I, I, I, I, F, I, I],
+    "mx_sdpa_check": [P, L, P, L, P, L, P, L, I, I, I, I, I],
+    "mx_layernorm": [P, P, L, P, P, P, L, I, I, F],
+    "mx_rmsnorm": [P, P, L, P, P, L, I, I, F],
+    "mx_patchify_u8": [P, P, P, L, I, I, I, I],
+}
+
+STATUS = {0: "ok", -1: "bad config", -2: "unsupported shape/stride", -3: "split-K workspace too small",
+          -4: "operand layout/alignment", -5: "HIP launch failed", -6: "null pointer"}
+
+_lib = None
+
+
+class MxError(RuntimeError):
+    pass
+
+
+def load():
+    """Load libshmaxx.so (built by build.py) and declare every entry point."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MxError(f"{LIB_PATH} is missing: build it first (python __graft_entry__.py build)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = I
+        _lib = lib
+    return _lib
+
+
+def check(rc, what):
+    if rc != 0:
+        raise MxError(f"{what} returned {rc} ({STATUS.get(rc, 'unknown')})")
+
+
+def call(name, *args):
+    """Call entry point `name`; raise MxError on a non-zero status."""
+    rc = getattr(load(), name)(*args)
+    check(rc, name)
+    return rc
+
+
+def stream():
+    """The HIP stream handle of torch's current stream (launches are asynchronous on it)."""
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()

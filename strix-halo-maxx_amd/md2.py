@@ -1,0 +1,97 @@
+"""moondream2 per-model forwards on the MI355X kernels: the SigLIP vision tower (this file) and the text decoder
+(md2text.py).
+
+Structure follows the reference's FastMD2 (moondream/gpu/md2fast.py:70-287): the same block loop, the same
+`lin_cls` plug-in point for the Linear class, `_vision` as the tower body, `capture()` for HIP-graph replay. The
+differences are MI355X-side only:
+  * any batch of crops (the reference runs batch 1), stacked as (B * 729) token rows so every GEMM sees M = B * 729;
+  * the input normalisation + patchify is one kernel writing the patch-embedding GEMM's operand directly (K padded
+    588 -> 592), and the position embedding is added in that GEMM's epilogue (broadcast over the batch);
+  * q, k, v are read by the attention kernel straight out of the fused qkv GEMM output (strided views, no copies),
+    and the attention output is written in (token, head * 72) order, i.e. already "transposed back";
+  * residual adds and GELU run in the GEMM epilogues (the reference's fused_gelu / fused_res flags).
+"""
+import torch
+
+from . import ops
+from .synth import VIS
+
+BF = torch.bfloat16
+
+
+class VisionTower:
+    """SigLIP so400m tower: patch-embed + pos -> `layers` pre-LN blocks -> post-LN [-> projection MLP]."""
+
+    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", attn=None):
+        c = VIS
+        self.dev = torch.device(device)
+        self.D, self.H, self.hd, self.P, self.G = c["dim"], c["heads"], c["hd"], c["patch"], c["grid"]
+        self.T = self.G * self.G
+        self.eps = c["ln_eps"]
+        g = lambda n: weights[n].to(self.dev, BF).contiguous()
+        lin = lambda n: lin_cls(weights[n + ".weight"], weights[n + ".bias"], BF)
+        self.patch_emb = lin("patch_emb")
+        self.pos_emb = g("pos_emb").view(self.T, self.D)
+        n = 0
+        while f"blocks.{n}.ln1.weight" in weights:
+            n += 1
+        self.blocks = [dict(ln1=(g(f"blocks.{i}.ln1.weight"), g(f"blocks.{i}.ln1.bias")), qkv=lin(f"blocks.{i}.attn.qkv"),
+                            proj=lin(f"blocks.{i}.attn.proj"), ln2=(g(f"blocks.{i}.ln2.weight"), g(f"blocks.{i}.ln2.bias")),
+                            fc1=lin(f"blocks.{i}.mlp.fc1"), fc2=lin(f"blocks.{i}.mlp.fc2")) for i in range(n)]
+        self.post_ln = (g("post_ln.weight"), g("post_ln.bias"))
+        self.has_proj = "proj_mlp.fc1.weight" in weights
+        if self.has_proj:
+            self.proj_fc1, self.proj_fc2 = lin("proj_mlp.fc1"), lin("proj_mlp.fc2")
+        self.attn = attn or ops.Attn(self.H, self.T, self.hd)
+        self.graphs = {}
+
+    # ---- one pre-LN block (md2fast.py:152-157)
+    def block(self, b, x, B):
+        T, H, hd, D = self.T, self.H, self.hd, self.D
+        h = ops.layernorm(x, *b["ln1"], eps=self.eps)
+        qkv = b["qkv"](h)                                   # (B*T, 3D)
+        q5 = qkv.view(B, T, 3, H, hd)
+        q, k, v = (q5[:, :, i].transpose(1, 2) for i in range(3))   # (B, H, T, hd) strided views
+        a = self.attn(q, k, v)                              # (B, T, D)
+        x = b["proj"](a.view(B * T, D), res=x)
+        return b["fc2"](b["fc1"](ops.layernorm(x, *b["ln2"], eps=self.eps), gelu=True), res=x)
+
+    def embed(self, img_u8):
+        B = img_u8.shape[0]
+        a = ops.patchify(img_u8, self.P, mode=0, ldo=self.patch_emb.Kp)        # (B*T, 592)
+        return self.patch_emb(a, res=self.pos_emb)                            # (B*T, D), + pos_emb per image
+
+    def _vision(self, img_u8, project=None):
+        """img_u8 (B, 378, 378, 3) uint8 on the device -> (B, 729, 1152) post-LN features
+        (or (B, 729, 2048) after the projection MLP when project=True)."""
+        B = img_u8.shape[0]
+        x = self.embed(img_u8)
+        for b in self.blocks:
+            x = self.block(b, x, B)
+        x = ops.layernorm(x, *self.post_ln, eps=self.eps)
+        if project:
+            x = self.project(x)
+        return x.view(B, self.T, -1)
+
+    def project(self, x):
+        """Projection MLP on cat([x, x]) (md2fast.py:159-160): the global crop doubles as the local crop at 378x378."""
+        feats = torch.cat([x, x], dim=-1)
+        return self.proj_fc2(self.proj_fc1(feats, gelu=True))
+
+    __call__ = _vision
+
+    # ---- HIP-graph capture of the whole tower for a fixed input buffer (md2fast.py:238-256)
+    def capture(self, img_buf):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self._vision(img_buf)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = self._vision(img_buf)
+        torch.cuda.synchronize()
+        self.graphs[img_buf.data_ptr()] = (g, out)
+        return g, out

@@ -1,0 +1,167 @@
+"""Kernel-level parity of the HIP path (through the C ABI) against plain fp32 references of the same op, at the
+vision / decoder / TRecViT shapes (the reference's kernel regression test, moondream/gpu/test_hgemm.py:15-50, with
+asserting tolerances). References are computed in fp32 on the CPU."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+import strix_halo_maxx_amd.ops as ops
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def within_ulps(a, b, n=1, frac=1e-3):
+    """|a - b| <= n bf16 ulps everywhere, and a != b on at most `frac` of the elements."""
+    a, b = a.float().cpu(), b.float().cpu()
+    tol = n * 2.0 ** -7 * torch.maximum(a.abs(), b.abs()) + 1e-30
+    return bool(((a - b).abs() <= tol).all()) and (a != b).float().mean().item() <= frac
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+GEMM_SHAPES = [(729, 1152, 3456), (729, 1152, 1152), (729, 1152, 4304), (729, 4304, 1152), (729, 592, 1152),
+               (1, 2048, 6144), (37, 2048, 2048), (1280, 768, 1536), (1458, 1152, 1152)]
+
+
+@pytest.mark.parametrize("M,K,N", GEMM_SHAPES)
+def test_gemm_bias_vs_fp32(dev, M, K, N):
+    g = gen(M * 7 + N)
+    x = torch.randn(M, K, generator=g).to(BF)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    ref = x.float() @ w.float().t() + b.float()
+    lin = ops.MxLin(w, b)
+    print(f"gemm M={M} K={K} N={N}", flush=True)
+    y = lin(x.to(dev))
+    torch.cuda.synchronize()
+    assert y.shape == (M, N) and y.dtype == BF
+    assert rel(y, ref) < 5e-3
+    # the output is the bf16 rounding of an fp32 accumulation: within 1 bf16 ulp-ish of the fp32 result
+    assert (y.float().cpu() - ref).abs().max().item() < 0.02 * ref.abs().max().item() + 1e-2
+
+
+@pytest.mark.parametrize("cfg", range(6))
+def test_gemm_every_tile_config(dev, cfg):
+    M, K, N = 300, 1152, 1152 + 64  # ragged M and N tails for every tile shape
+    g = gen(cfg)
+    x = torch.randn(M, K, generator=g).to(BF)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    ref = x.float() @ w.float().t()
+    lin = ops.MxLin(w, None)
+    lin.cfgs[M] = cfg
+    print(f"gemm cfg={cfg}", flush=True)
+    y = lin(x.to(dev))
+    assert rel(y, ref) < 5e-3
+
+
+def test_gemm_epilogues_match_unfused(dev):
+    """GELU applied to the bf16-rounded linear output, then + residual (md2fast.py:55-67; i8gemm.hip:378)."""
+    M, K, N = 729, 1152, 4304
+    g = gen(3)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    r = torch.randn(M, N, generator=g).to(BF).to(dev)
+    lin = ops.MxLin(w, b)
+    y0 = lin(x).cpu()
+    y_t = lin(x, gelu=True).cpu()
+    y_e = lin(x, act="erf").cpu()
+    y_r = lin(x, res=r).cpu()
+    y_tr = lin(x, gelu=True, res=r).cpu()
+    # the same op sequence on the CPU from the kernel's own bf16 linear output; GELU's fp32 tanh/erf may differ
+    # from the CPU's by an fp32 ulp, which can move a result by one bf16 ulp
+    assert within_ulps(y_t, F.gelu(y0.float(), approximate="tanh").to(BF))
+    assert within_ulps(y_e, F.gelu(y0.float()).to(BF))
+    assert torch.equal(y_r, (y0.float() + r.cpu().float()).to(BF))
+    exp_tr = (F.gelu(y0.float(), approximate="tanh").to(BF).float() + r.cpu().float()).to(BF)
+    assert within_ulps(y_tr, exp_tr, n=2)
+
+
+def test_gemm_residual_row_broadcast(dev):
+    """r_rows: a (T, N) table added to every T-row slab of the output (the position embedding)."""
+    T, B, K, N = 729, 3, 592, 1152
+    g = gen(5)
+    x = torch.randn(B * T, K, generator=g).to(BF).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    pos = torch.randn(T, N, generator=g).to(BF).to(dev)
+    lin = ops.MxLin(w, None)
+    y = lin(x, res=pos).cpu()
+    y0 = lin(x).cpu()
+    assert torch.equal(y, (y0.float() + pos.cpu().float().repeat(B, 1)).to(BF))
+
+
+def _sdpa_ref(q, k, v, scale, mask=None):
+    q, k, v = q.float().cpu(), k.float().cpu(), v.float().cpu()
+    s = (q @ k.transpose(-1, -2)) * scale
+    if mask is not None:
+        s = s.masked_fill(~mask, float("-inf"))
+    return torch.softmax(s, dim=-1) @ v
+
+
+@pytest.mark.parametrize("B,H,T,D", [(1, 16, 729, 72), (2, 16, 729, 72), (1, 12, 1280, 64), (1, 32, 730, 64), (1, 4, 33, 72)])
+def test_sdpa_strided_views(dev, B, H, T, D):
+    """q, k, v as strided views of a fused qkv output (the vision layout, md2fast.py:154)."""
+    g = gen(B * 100 + T)
+    qkv = torch.randn(B, T, 3 * H * D, generator=g).to(BF)
+    q, k, v = [t.view(B, T, H, D).transpose(1, 2) for t in qkv.chunk(3, dim=-1)]
+    ref = _sdpa_ref(q, k, v, D ** -0.5).transpose(1, 2).reshape(B, T, H * D)
+    qd = qkv.to(dev)
+    q2, k2, v2 = [t.view(B, T, H, D).transpose(1, 2) for t in qd.chunk(3, dim=-1)]
+    print(f"sdpa B={B} H={H} T={T} D={D}", flush=True)
+    out = ops.sdpa(q2, k2, v2)
+    assert out.shape == (B, T, H * D)
+    assert rel(out, ref) < 1e-2
+    assert (out.float().cpu() - ref).abs().max().item() < 5e-2
+
+
+def test_sdpa_prefix_causal_mask(dev):
+    """Prompt prefill mask (md2fast.py:132-136): prompt row i sees all prefix keys and prompt keys <= i."""
+    H, P, L, D = 32, 730, 64, 64
+    g = gen(11)
+    kc = torch.randn(1, H, P + L, D, generator=g).to(BF)
+    vc = torch.randn(1, H, P + L, D, generator=g).to(BF)
+    q = torch.randn(1, H, L, D, generator=g).to(BF)
+    m = torch.zeros(L, P + L, dtype=torch.bool)
+    m[:, :P] = True
+    m[:, P:] = torch.tril(torch.ones(L, L, dtype=torch.bool))
+    ref = _sdpa_ref(q, kc, vc, 0.125, m[None, None]).transpose(1, 2).reshape(1, L, H * D)
+    out = ops.sdpa(q.to(dev), kc.to(dev), vc.to(dev), qpos0=P, causal_from=P)
+    assert rel(out, ref) < 1e-2
+    # a plain causal self-attention, too
+    T = 200
+    q3 = torch.randn(1, 8, T, 64, generator=g).to(BF)
+    cm = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    ref3 = _sdpa_ref(q3, q3, q3, 0.125, cm[None, None]).transpose(1, 2).reshape(1, T, 512)
+    qd = q3.to(dev)
+    out3 = ops.sdpa(qd, qd, qd, causal_from=0)
+    assert rel(out3, ref3) < 1e-2
+
+
+@pytest.mark.parametrize("rows,D", [(729, 1152), (1458, 1152), (730, 2048), (1, 2048), (1280, 768)])
+def test_layernorm(dev, rows, D):
+    g = gen(rows + D)
+    x = (torch.randn(rows, D, generator=g) * 3 + 1).to(BF)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(BF)
+    b = (0.1 * torch.randn(D, generator=g)).to(BF)
+    ref = F.layer_norm(x.float(), (D,), w.float(), b.float(), 1e-5)
+    y = ops.layernorm(x.to(dev), w.to(dev), b.to(dev), eps=1e-5)
+    assert rel(y, ref) < 4e-3
+    # one rounding of the fp32 result: at most 1 ulp away
+    assert ((y.float().cpu() - ref).abs() <= ref.abs() * 2 ** -8 + 1e-6).float().mean().item() > 0.999
+
+
+def test_patchify_matches_oracle(dev):
+    import oracle.md2_vision as ov
+    img = torch.randint(0, 256, (2, 378, 378, 3), generator=gen(1), dtype=torch.uint8)
+    ref = ov.normalize_patchify(img).reshape(2 * 729, 588)
+    y = ops.patchify(img.to(dev), 14, mode=0, ldo=592).cpu()
+    assert torch.equal(y[:, :588], ref)
+    assert torch.count_nonzero(y[:, 588:]) == 0
