@@ -17,9 +17,11 @@ F = ctypes.c_float
 
 # name -> argtypes (every entry point returns int status)
 SIGNATURES = {
-    "mx_gemm_bf16": [P, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I],
-    "mx_gemm_check": [I, P, L, P, L, P, P, L, P, L, I, I, I, I],
+    "mx_gemm_bf16": [P, I, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I, I, P, L, P, L],
+    "mx_gemm_check": [I, I, P, L, P, L, P, P, L, P, L, I, I, I, I, I, P, L, P, L],
     "mx_gemm_pick": [I, I, I],
+    "mx_gemm_ws_elems": [I, I, I, I],
+    "mx_gemm_ws_counters": [I, I, I, I],
     "mx_gemm_ncfg": [],
     "mx_gemm_cfg_tile": [I, ctypes.POINTER(I), ctypes.POINTER(I)],
     "mx_sdpa": [P, P, L, L, L, P, L, L, L, P, L, L, L, P, L, L, L, I, I, I, I, I, F, I, I],
@@ -31,6 +33,8 @@ SIGNATURES = {
 
 STATUS = {0: "ok", -1: "bad config", -2: "unsupported shape/stride", -3: "split-K workspace too small",
           -4: "operand layout/alignment", -5: "HIP launch failed", -6: "null pointer"}
+
+RESTYPE = {"mx_gemm_ws_elems": L, "mx_gemm_ws_counters": L}
 
 _lib = None
 
@@ -49,7 +53,7 @@ def load():
         for name, args in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = args
-            fn.restype = I
+            fn.restype = RESTYPE.get(name, I)
         _lib = lib
     return _lib
 

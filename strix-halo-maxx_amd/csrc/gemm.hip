@@ -1,80 +1,105 @@
 // bf16 GEMM with fused epilogues on gfx950 MFMA:
 //   C[M,N] = epi( A[M,K] . W[N,K]^T + bias[N] )      epi = round-bf16 -> optional GELU (tanh | erf) -> optional + R
-// A and W are both K-contiguous (torch Linear layout). fp32 accumulation in MFMA 32x32x16 tiles.
+// A and W are K-contiguous (torch Linear layout); fp32 accumulation in MFMA 32x32x16 tiles.
 //
-// Design (gfx950, 64-wide waves, 160 KB LDS per CU):
+// Design (gfx950: 64-wide waves, 160 KB LDS per CU, 256 CUs in 8 XCDs):
 //  * 256-thread workgroups (4 waves) own a BM x BN tile of C; each wave owns a (BM/WGM) x (BN/WGN) sub-tile.
-//  * K is walked in BK = 64 steps. Global -> register prefetch of step k+1 overlaps the MFMAs of step k; the
-//    prefetched tile is stored to the other LDS buffer (double buffering, one barrier per step).
-//  * LDS rows are 64 bf16 (128 B) with the 16-byte chunk index XOR-swizzled by (row & 7), so the 32 rows read by
-//    one MFMA operand fetch (ds_read_b128) spread over all banks without padding.
-//  * The MFMA is issued "swapped" (W as the row operand, A as the column operand), so every lane ends up with 4
-//    consecutive output columns of one output row: 8-byte stores, and bias / residual read as vectors.
-//  * Workgroup ids are remapped so that consecutive tiles (which share W panels) land on the same XCD and its L2.
+//  * Operands go global -> LDS with the asynchronous LDS-DMA load (global_load_lds_dwordx4: 64 lanes x 16 B land
+//    as 1 KB in LDS without passing through VGPRs), into an S-stage LDS ring, S-1 k-steps ahead of the MFMAs.
+//    The compiler cannot see which ring slot an LDS read touches, so these loads are issued from inline asm and the
+//    wait for "stage k has landed" is an explicit `s_waitcnt vmcnt(n)` that leaves the later stages in flight.
+//  * LDS rows are 64 bf16 (128 B) with the 16-byte chunk index XOR-swizzled by (row & 7): the DMA lane -> address
+//    map is fixed (lane l writes bytes 16 l.. of the 1 KB block), so each lane fetches the global chunk that belongs
+//    at its slot, and the 32 rows read by one MFMA operand fetch (ds_read_b128) spread over all banks.
+//  * The MFMA is issued "swapped" (W as the row operand, A as the column operand): every lane ends up with 4
+//    consecutive output columns of one output row -> 8-byte stores; bias / residual are read as vectors.
+//  * Split-K for small grids (batch-1 shapes on 256 CUs): each split writes an fp32 partial tile; the last split to
+//    arrive (atomic counter per tile) adds the partials in split order (deterministic) and runs the epilogue, then
+//    re-arms the counter. No workgroup ever waits on another.
+//  * Workgroup ids are remapped so consecutive tiles (sharing W panels) land on the same XCD and its L2.
 // Rounding follows torch's bf16 Linear path: the linear output is rounded to bf16, GELU is applied to that rounded
 // value and rounded again, then the residual is added in fp32 and rounded once more.
+//
+// Operand contract: A has K valid columns; the k loop runs to Kw (a multiple of 64, >= K) and W must hold zeros in
+// columns [K, Kw). A chunks beyond K are fetched from column 0 of the same row (finite data times W's zeros).
 #include "common.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"
 
 namespace {
 
 constexpr int BK = 64;
 
-template <int BM, int BN, int WGM, int WGN>
-__global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long lda,
-                                                        const uint16_t* __restrict__ W, long ldw,
-                                                        const float* __restrict__ bias,
-                                                        const uint16_t* __restrict__ R, long ldr, int r_rows,
-                                                        uint16_t* __restrict__ C, long ldc,
-                                                        int M, int N, int K, int act, int tiles_m, int tiles_n) {
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) void*)p);
+}
+
+// 64 lanes x 16 bytes from global (per-lane address) into LDS at m0 = lds (wave-uniform) + 16 * lane.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int WGM, int WGN, int S>
+__global__ __launch_bounds__(256) void gemm_bf16_kernel(
+    const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
+    const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
+    uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act,
+    int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt) {
   static_assert(WGM * WGN == 4, "4 waves per workgroup");
+  static_assert(S >= 2, "at least a double buffer");
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int ACH = BM * BK / 8 / 256;  // 16-byte chunks per thread per stage (A)
-  constexpr int WCH = BN * BK / 8 / 256;  // (W)
-  static_assert(ACH >= 1 && WCH >= 1 && FM >= 1 && FN >= 1, "tile too small");
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * BK];
+  constexpr int QA = BM / 32, QW = BN / 32;  // DMA instructions per wave per stage
+  constexpr int LPS = QA + QW;
+  constexpr int STAGE = (BM + BN) * BK;      // elements per ring stage
+  static_assert(FM >= 1 && FN >= 1 && QA >= 1 && QW >= 1, "tile too small");
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[S * STAGE];
+  __shared__ int s_last;
 
-  // ---- XCD-aware tile order: dispatch sends workgroup b to XCD (b % 8); give each XCD a contiguous tile range.
-  const int nt = tiles_m * tiles_n;
+  // ---- XCD-aware order over (split, tile_n, tile_m): dispatch sends workgroup b to XCD (b % 8).
+  const int nt = tiles_m * tiles_n * splits;
   const int b = blockIdx.x;
   const int per = nt / 8, rem = nt % 8, xcd = b % 8, idx = b / 8;
   const int t = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
-  const int tile_m = t % tiles_m, tile_n = t / tiles_m;
+  const int tile = t % (tiles_m * tiles_n), split = t / (tiles_m * tiles_n);
+  const int tile_m = tile % tiles_m, tile_n = tile / tiles_m;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
+  const int nk_all = Kw / BK;
+  const int kt0 = split * kt_per_split;
+  const int nkl = min(nk_all, kt0 + kt_per_split) - kt0;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WGM, wn = wave / WGM;
   const int lr = lane & 31, hk = lane >> 5;
+  const uint32_t sbase = lds_off(smem);
 
-  u32x4 ra[ACH], rw[WCH];
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-
-  auto gload = [&](int k0) {
+  // per-lane DMA source rows / chunk (fixed for the whole k loop)
+  const int drow = lane >> 3, dch = (lane & 7) ^ (lane >> 3);
+  const uint16_t* a_src[QA];
+  const uint16_t* w_src[QW];
 #pragma unroll
-    for (int j = 0; j < ACH; j++) {
-      const int i = tid + 256 * j, r = i >> 3, c = i & 7;
-      const int gm = min(m0 + r, M - 1), kk = k0 + c * 8;
-      ra[j] = (kk < K) ? *reinterpret_cast<const u32x4*>(A + (long)gm * lda + kk) : zero;
-    }
+  for (int q = 0; q < QA; q++) {
+    const int gm = min(m0 + 8 * (q * 4 + wave) + drow, M - 1);
+    a_src[q] = A + (long)gm * lda;
+  }
 #pragma unroll
-    for (int j = 0; j < WCH; j++) {
-      const int i = tid + 256 * j, r = i >> 3, c = i & 7;
-      const int gn = min(n0 + r, N - 1), kk = k0 + c * 8;
-      rw[j] = (kk < K) ? *reinterpret_cast<const u32x4*>(W + (long)gn * ldw + kk) : zero;
-    }
-  };
-  auto sstore = [&](int buf) {
+  for (int q = 0; q < QW; q++) {
+    const int gn = min(n0 + 8 * (q * 4 + wave) + drow, N - 1);
+    w_src[q] = W + (long)gn * ldw;
+  }
+  auto issue = [&](int kt, int s) {
+    const int kk = kt * BK + dch * 8;
+    const int ka = kk < K ? kk : 0;
+    const uint32_t st = sbase + (uint32_t)(s * STAGE * 2);
 #pragma unroll
-    for (int j = 0; j < ACH; j++) {
-      const int i = tid + 256 * j, r = i >> 3, c = i & 7;
-      *reinterpret_cast<u32x4*>(&As[buf][r * BK + ((c ^ (r & 7)) << 3)]) = ra[j];
-    }
+    for (int q = 0; q < QA; q++) dma16(a_src[q] + ka, __builtin_amdgcn_readfirstlane(st + (q * 4 + wave) * 1024));
 #pragma unroll
-    for (int j = 0; j < WCH; j++) {
-      const int i = tid + 256 * j, r = i >> 3, c = i & 7;
-      *reinterpret_cast<u32x4*>(&Ws[buf][r * BK + ((c ^ (r & 7)) << 3)]) = rw[j];
-    }
+    for (int q = 0; q < QW; q++)
+      dma16(w_src[q] + kk, __builtin_amdgcn_readfirstlane(st + BM * 128 + (q * 4 + wave) * 1024));
   };
 
   f32x16 acc[FN][FM];
@@ -85,13 +110,20 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  const int nk = (K + BK - 1) / BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+  for (int s = 0; s < S - 1; s++)
+    if (s < nkl) issue(kt0 + s, s);
+
+  for (int it = 0; it < nkl; it++) {
+    // stage `it` has landed once at most (stages issued after it) x LPS loads are still in flight
+    const int ahead = min(S - 2, nkl - 1 - it);
+    if (S >= 4 && ahead >= 2) wait_vm<(S >= 4 ? 2 : 0) * LPS>();
+    else if (S >= 3 && ahead >= 1) wait_vm<(S >= 3 ? 1 : 0) * LPS>();
+    else wait_vm<0>();
+    __syncthreads();
+    if (it + S - 1 < nkl) issue(kt0 + it + S - 1, (it + S - 1) % S);
+    const uint16_t* As = smem + (it % S) * STAGE;
+    const uint16_t* Ws = As + BM * BK;
 #pragma unroll
     for (int s = 0; s < BK / 16; s++) {
       const int c = 2 * s + hk;
@@ -99,23 +131,54 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
 #pragma unroll
       for (int i = 0; i < FM; i++) {
         const int r = wm * WTM + i * 32 + lr;
-        af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[buf][r * BK + ((c ^ (r & 7)) << 3)]));
+        af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[r * BK + ((c ^ (r & 7)) << 3)]));
       }
 #pragma unroll
       for (int i = 0; i < FN; i++) {
         const int r = wn * WTN + i * 32 + lr;
-        wf[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[buf][r * BK + ((c ^ (r & 7)) << 3)]));
+        wf[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ (r & 7)) << 3)]));
       }
 #pragma unroll
       for (int i = 0; i < FN; i++)
 #pragma unroll
         for (int j = 0; j < FM; j++) acc[i][j] = mfma32(wf[i], af[j], acc[i][j]);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
-    __syncthreads();
   }
 
-  // ---- epilogue: lane holds output row m = .. + lr, columns n .. n+3 for each 8-row group j of the MFMA result
+  // ---- split-K: partial tile to the workspace; the last split to arrive reduces in split order
+  if (splits > 1) {
+    constexpr int TE = BM * BN;
+    float* mine = ws + (long)(tile * splits + split) * TE;
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) mine[(((wave * FN + i) * FM + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = (atomicAdd(&cnt[tile], 1) == splits - 1);
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const long o = (((wave * FN + i) * FM + j) * 16 + e) * 64 + lane;
+          float v = 0.f;
+          for (int s = 0; s < splits; s++) {
+            const float p = (s == split) ? acc[i][j][e] : __builtin_nontemporal_load(ws + (long)(tile * splits + s) * TE + o);
+            v = (s == 0) ? p : v + p;
+          }
+          acc[i][j][e] = v;
+        }
+    if (tid == 0) cnt[tile] = 0;
+  }
+
+  // ---- epilogue: lane holds output row m, columns n .. n+3 for each 8-row group g of the MFMA result
 #pragma unroll
   for (int i = 0; i < FN; i++) {
 #pragma unroll
@@ -152,17 +215,26 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
   }
 }
 
-struct Cfg { int bm, bn; };
-constexpr Cfg kCfgs[] = {{128, 128}, {64, 128}, {128, 64}, {64, 64}, {256, 128}, {128, 256}};
+struct Cfg { int bm, bn, stages, per_cu; };
+// per_cu: workgroups that fit one CU at once (LDS-limited)
+constexpr Cfg kCfgs[] = {{128, 128, 4, 1}, {64, 128, 4, 1}, {128, 64, 4, 1}, {64, 64, 4, 2},
+                         {256, 128, 3, 1}, {128, 256, 3, 1}, {64, 64, 3, 3}, {128, 128, 2, 2}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-template <int BM, int BN, int WGM, int WGN>
-hipError_t launch(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* bias,
-                  const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int K, int act) {
+template <int BM, int BN, int WGM, int WGN, int S>
+hipError_t launch(hipStream_t st, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                  const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N,
+                  int K, int Kw, int act, float* ws, int* cnt) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WGM, WGN>), dim3(tm * tn), dim3(256), 0, st, A, lda, W, ldw, bias, R,
-                     ldr, r_rows, C, ldc, M, N, K, act, tm, tn);
+  const int nk = Kw / BK;
+  const int kps = (nk + splits - 1) / splits;
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn * splits), dim3(256), 0, st, A, lda, W,
+                     ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, tm, tn, splits, kps, ws, cnt);
   return hipGetLastError();
+}
+
+long tiles_of(int cfg, int M, int N) {
+  return (long)((M + kCfgs[cfg].bm - 1) / kCfgs[cfg].bm) * ((N + kCfgs[cfg].bn - 1) / kCfgs[cfg].bn);
 }
 
 }  // namespace
@@ -176,59 +248,93 @@ extern "C" int mx_gemm_cfg_tile(int cfg, int* bm, int* bn) {
   return MX_OK;
 }
 
-// Tile choice when the caller passes cfg < 0: minimise (rounds of workgroups over 256 CUs) x (tile work / tile
-// efficiency). Larger tiles re-read less from L2 per MFMA; smaller ones fill the 256 CUs at batch-1 sizes.
-extern "C" int mx_gemm_pick(int M, int N, int K) {
-  static const float eff[kNCfg] = {1.0f, 0.80f, 0.80f, 0.62f, 1.08f, 1.08f};
-  static const int per_cu[kNCfg] = {2, 2, 2, 2, 1, 1};
-  (void)K;
-  int best = 0;
-  float bt = 1e30f;
-  for (int c = 0; c < kNCfg; c++) {
-    const long tiles = (long)((M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((N + kCfgs[c].bn - 1) / kCfgs[c].bn);
-    const long slots = 256L * per_cu[c];
-    const long rounds = (tiles + slots - 1) / slots;
-    // a partially filled last round still costs a full tile time per CU in flight
-    const float t = (float)rounds * kCfgs[c].bm * kCfgs[c].bn / eff[c] / (float)per_cu[c];
-    if (t < bt) { bt = t; best = c; }
-  }
-  return best;
+// Workspace a (cfg, splits) call needs: fp32 partial tiles and one counter per output tile.
+extern "C" long mx_gemm_ws_elems(int cfg, int splits, int M, int N) {
+  if (cfg < 0 || cfg >= kNCfg || splits <= 1) return 0;
+  return tiles_of(cfg, M, N) * splits * kCfgs[cfg].bm * kCfgs[cfg].bn;
+}
+extern "C" long mx_gemm_ws_counters(int cfg, int splits, int M, int N) {
+  if (cfg < 0 || cfg >= kNCfg || splits <= 1) return 0;
+  return tiles_of(cfg, M, N);
 }
 
-// Validate a GEMM call without launching (0 or a negative status). Shared by mx_gemm_bf16 and host-side tests.
-extern "C" int mx_gemm_check(int cfg, const void* A, long lda, const void* W, long ldw, const void* bias,
-                             const void* R, long ldr, const void* C, long ldc, int M, int N, int K, int act) {
+// Default (cfg, splits) when the caller passes cfg < 0: minimise estimated time = rounds of workgroups over the
+// 256 CUs x per-tile time, with per-tile time ~ BM*BN*(k-steps)/efficiency. Returns cfg * 16 + splits.
+extern "C" int mx_gemm_pick(int M, int N, int Kw) {
+  static const float eff[kNCfg] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f};
+  const int nk = Kw / BK;
+  int best = 0, bsplit = 1;
+  float bt = 1e30f;
+  for (int c = 0; c < kNCfg; c++) {
+    for (int sp = 1; sp <= 8; sp *= 2) {
+      if (sp > 1 && (nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk)) break;
+      const long tiles = tiles_of(c, M, N) * sp;
+      const long slots = 256L * kCfgs[c].per_cu;
+      const long rounds = (tiles + slots - 1) / slots;
+      const float tk = (float)((nk + sp - 1) / sp);
+      float t = (float)rounds * kCfgs[c].bm * kCfgs[c].bn * (tk + 2.0f) / eff[c];
+      if (sp > 1) t *= 4.0f;  // partial-tile traffic and the cross-XCD release fence of the reduction
+      if (t < bt) { bt = t; best = c; bsplit = sp; }
+    }
+  }
+  return best * 16 + bsplit;
+}
+
+// Validate a GEMM call without launching (0 or a negative status).
+extern "C" int mx_gemm_check(int cfg, int splits, const void* A, long lda, const void* W, long ldw, const void* bias,
+                             const void* R, long ldr, const void* C, long ldc, int M, int N, int K, int Kw, int act,
+                             const void* ws, long ws_elems, const void* cnt, long n_cnt) {
   if (!A || !W || !C) return MX_ENULL;
   if (cfg >= kNCfg) return MX_EBADCFG;
   if (act < 0 || act > 2) return MX_EBADCFG;
   if (M < 1 || N < 1 || K < 8) return MX_ESHAPE;
-  if (K % 8 || lda % 8 || ldw % 8 || lda < K || ldw < K) return MX_ESHAPE;
+  if (K % 8 || Kw % BK || Kw < K || lda % 8 || ldw % 8 || lda < K || ldw < Kw) return MX_ESHAPE;
   if (N % 4 || ldc % 4 || ldc < N) return MX_ESHAPE;
   if (((uintptr_t)A | (uintptr_t)W) & 15) return MX_ELAYOUT;
   if ((uintptr_t)C & 7) return MX_ELAYOUT;
   if (bias && ((uintptr_t)bias & 15)) return MX_ELAYOUT;
   if (R && (((uintptr_t)R & 7) || ldr % 4 || ldr < N)) return MX_ELAYOUT;
+  if (cfg >= 0 && splits > 1) {
+    const int nk = Kw / BK, kps = (nk + splits - 1) / splits;
+    if (splits > nk || (splits - 1) * kps >= nk) return MX_ESPLIT;  // every split must own >= 1 k-step
+    if (!ws || !cnt) return MX_ENULL;
+    if (ws_elems < mx_gemm_ws_elems(cfg, splits, M, N) || n_cnt < mx_gemm_ws_counters(cfg, splits, M, N))
+      return MX_ESPLIT;
+  }
   return MX_OK;
 }
 
-// R (optional residual) row for output row m is (r_rows > 0 ? m % r_rows : m): r_rows broadcasts one [r_rows, N]
-// table (e.g. a position embedding) over a batch of stacked sequences.
-extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, const uint16_t* A, long lda, const uint16_t* W, long ldw,
-                            const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M,
-                            int N, int K, int act) {
-  const int rc = mx_gemm_check(cfg, A, lda, W, ldw, bias, R, ldr, C, ldc, M, N, K, act);
-  if (rc) return rc;
+// C = epi(A W^T + bias). cfg < 0: the library's pick (only split-free picks unless a workspace is given).
+// ws / cnt: split-K workspace (fp32 elements) and per-tile counters (must be zero before first use; the kernel
+// leaves them zero). R row for output row m is (r_rows > 0 ? m % r_rows : m).
+extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda, const uint16_t* W,
+                            long ldw, const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C,
+                            long ldc, int M, int N, int K, int Kw, int act, float* ws, long ws_elems, int* cnt,
+                            long n_cnt) {
   if (r_rows < 0) return MX_ESHAPE;
-  if (cfg < 0) cfg = mx_gemm_pick(M, N, K);
+  if (cfg < 0) {
+    const int p = mx_gemm_pick(M, N, Kw);
+    cfg = p / 16;
+    splits = p % 16;
+    if (splits > 1 && (ws_elems < mx_gemm_ws_elems(cfg, splits, M, N) || n_cnt < mx_gemm_ws_counters(cfg, splits, M, N)))
+      splits = 1;
+  }
+  if (splits < 1) splits = 1;
+  const int rc = mx_gemm_check(cfg, splits, A, lda, W, ldw, bias, R, ldr, C, ldc, M, N, K, Kw, act, ws, ws_elems, cnt, n_cnt);
+  if (rc) return rc;
   hipError_t e;
+#define L_(BM, BN, S) launch<BM, BN, 2, 2, S>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, ws, cnt)
   switch (cfg) {
-    case 0: e = launch<128, 128, 2, 2>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, act); break;
-    case 1: e = launch<64, 128, 2, 2>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, act); break;
-    case 2: e = launch<128, 64, 2, 2>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, act); break;
-    case 3: e = launch<64, 64, 2, 2>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, act); break;
-    case 4: e = launch<256, 128, 2, 2>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, act); break;
-    case 5: e = launch<128, 256, 2, 2>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, act); break;
+    case 0: e = L_(128, 128, 4); break;
+    case 1: e = L_(64, 128, 4); break;
+    case 2: e = L_(128, 64, 4); break;
+    case 3: e = L_(64, 64, 4); break;
+    case 4: e = L_(256, 128, 3); break;
+    case 5: e = L_(128, 256, 3); break;
+    case 6: e = L_(64, 64, 3); break;
+    case 7: e = L_(128, 128, 2); break;
     default: return MX_EBADCFG;
   }
+#undef L_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

@@ -25,39 +25,105 @@ def _rows(x, K):
     return x2
 
 
+class Workspace:
+    """Split-K scratch shared by every GEMM on one device: fp32 partial tiles + per-tile arrival counters.
+
+    Grown on demand outside graph capture (call reserve() before capturing); counters start at zero and every
+    kernel that uses them leaves them at zero. Kernels on one stream serialise, so one buffer serves all layers (as
+    the reference's single split-K workspace, moondream/gpu/hgemm.py:78-83); concurrent GEMMs on two streams would
+    race on it.
+    """
+    _by_dev = {}
+
+    def __init__(self, device):
+        self.dev = device
+        self.ws = torch.empty(0, device=device, dtype=torch.float32)
+        self.cnt = torch.zeros(0, device=device, dtype=torch.int32)
+
+    @classmethod
+    def get(cls, device):
+        d = torch.device(device)
+        key = d.index if d.index is not None else torch.cuda.current_device()
+        if key not in cls._by_dev:
+            cls._by_dev[key] = cls(d)
+        return cls._by_dev[key]
+
+    def reserve(self, elems, counters):
+        if elems > self.ws.numel():
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("split-K workspace must be reserved before graph capture")
+            self.ws = torch.empty(int(elems * 1.25) + 1024, device=self.dev, dtype=torch.float32)
+        if counters > self.cnt.numel():
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("split-K counters must be reserved before graph capture")
+            torch.cuda.synchronize(self.dev)
+            self.cnt = torch.zeros(int(counters * 1.25) + 64, device=self.dev, dtype=torch.int32)
+
+
+_TUNED = {}  # (M, N, Kw) -> (cfg, splits), shared by every layer of that shape
+
+
+def _ws_need(cfg, splits, M, N):
+    lib = _lib.load()
+    return lib.mx_gemm_ws_elems(cfg, splits, M, N), lib.mx_gemm_ws_counters(cfg, splits, M, N)
+
+
 class MxLin:
     """bf16 Linear on the MFMA GEMM: y = epi(x W^T + b) with epi = [GELU tanh|erf] then [+ res], torch's rounding.
 
-    Weights stay in torch's (N, K) layout (K padded with zeros to a multiple of 8 when needed, e.g. the 588-wide patch
-    embedding, whose input then comes padded from the patchify kernel). Bias is held in fp32, as the reference's
-    HLin does (hgemm.py:153).
+    Weights stay in torch's (N, K) layout, zero-padded along K to a multiple of 64 (the kernel's k-step); inputs need
+    K columns (K rounded up to 8: the 588-wide patch embedding takes its input zero-padded to 592 by the patchify
+    kernel). Bias is held in fp32, as the reference's HLin does (hgemm.py:153). The tile config and split-K factor
+    are chosen per (M, N, K) by timing every candidate once (the reference's pick_cfg autotune, hgemm.py:52-76),
+    or taken from the library's default pick when tuning is off.
     """
     fused_gelu = True
     fused_res = True
+    autotune = True
 
     def __init__(self, weight, bias, dtype=BF, device="cuda"):
         assert dtype == BF, "bf16 only"
         w = weight.detach().to(device=device, dtype=BF)
-        self.N, self.K = w.shape
-        self.Kp = (self.K + 7) // 8 * 8
+        self.N, self.K0 = w.shape
+        self.K = (self.K0 + 7) // 8 * 8          # input columns expected
+        self.Kw = (self.K0 + 63) // 64 * 64      # padded weight row
         if self.N % 4:
             raise ValueError(f"N={self.N} must be a multiple of 4")
-        if self.Kp != self.K:
-            wp = torch.zeros(self.N, self.Kp, device=device, dtype=BF)
-            wp[:, :self.K] = w
-            w = wp
-        self.w = w.contiguous()
+        wp = torch.zeros(self.N, self.Kw, device=device, dtype=BF)
+        wp[:, :self.K0] = w
+        self.w = wp
+        self.Kp = self.K                         # width of the input this layer reads
         self.b = None if bias is None else bias.detach().to(device=device, dtype=torch.float32).contiguous()
-        self.cfgs = {}  # M -> tile config (None: the library's own pick)
+        self.cfgs = {}  # M -> (cfg, splits); absent: tuned (or library pick) on first use
+        self.dev = self.w.device
+
+    def _launch(self, cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws):
+        return _lib.load().mx_gemm_bf16(
+            stream(), cfg, splits, x2.data_ptr(), x2.stride(0), self.w.data_ptr(), self.w.stride(0), ptr(self.b),
+            ptr(r2), ldr, r_rows, y2.data_ptr(), y2.stride(0), M, self.N, self.K, self.Kw, a,
+            ptr(ws.ws), ws.ws.numel(), ptr(ws.cnt), ws.cnt.numel())
+
+    def _pick(self, M, x2, y2, a, r2, ldr, r_rows, ws):
+        key = (M, self.N, self.Kw)
+        if key in _TUNED:
+            return _TUNED[key]
+        lib = _lib.load()
+        if not MxLin.autotune or torch.cuda.is_current_stream_capturing():
+            p = lib.mx_gemm_pick(M, self.N, self.Kw)
+            c = (p // 16, p % 16)
+        else:
+            c = tune_gemm(self, M, x2, y2, a, r2, ldr, r_rows, ws)
+        _TUNED[key] = c
+        return c
 
     def __call__(self, x, gelu=False, res=None, pre=None, act=None, out=None):
         a = ACT[act if act is not None else gelu]
         x2 = _rows(x, self.K)
-        if x2.shape[1] == self.K and self.Kp != self.K:
-            xp = torch.zeros(x2.shape[0], self.Kp, device=x2.device, dtype=BF)
-            xp[:, :self.K] = x2
+        if x2.shape[1] == self.K0 and self.K != self.K0:
+            xp = torch.zeros(x2.shape[0], self.K, device=x2.device, dtype=BF)
+            xp[:, :self.K0] = x2
             x2 = xp
-        if x2.shape[1] != self.Kp:
+        if x2.shape[1] != self.K:
             raise ValueError(f"input width {x2.shape[1]} != {self.K}")
         M = x2.shape[0]
         y = out if out is not None else torch.empty(M, self.N, device=x2.device, dtype=BF)
@@ -74,10 +140,48 @@ class MxLin:
                 if M % r2.shape[0]:
                     raise ValueError("residual rows must equal or divide the output rows")
                 r_rows = r2.shape[0]
-        cfg = self.cfgs.get(M, -1)
-        call("mx_gemm_bf16", stream(), cfg, x2.data_ptr(), x2.stride(0), self.w.data_ptr(), self.w.stride(0),
-             ptr(self.b), ptr(r2), ldr, r_rows, y2.data_ptr(), y2.stride(0), M, self.N, self.Kp, a)
+        ws = Workspace.get(x2.device)
+        cfg, splits = self.cfgs.get(M) or self._pick(M, x2, y2, a, r2, ldr, r_rows, ws)
+        if splits > 1:
+            ws.reserve(*_ws_need(cfg, splits, M, self.N))
+        _lib.check(self._launch(cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws), "mx_gemm_bf16")
         return y2.view(*x.shape[:-1], self.N) if out is None else y
+
+
+def tune_gemm(lin, M, x2, y2, a, r2, ldr, r_rows, ws, reps=10):
+    """Time every (tile config, split-K) candidate on the real operands; return the fastest. Runs eagerly on the
+    current stream (writes y2, which the caller overwrites right after)."""
+    lib = _lib.load()
+    cands = []
+    nk = lin.Kw // 64
+    for cfg in range(lib.mx_gemm_ncfg()):
+        for sp in ((1, 2, 3, 4, 6, 8) if tune_gemm.split_k else (1,)):
+            if sp > 1 and (nk // sp < 3 or (sp - 1) * (-(-nk // sp)) >= nk):
+                continue
+            cands.append((cfg, sp))
+    best, bt = None, float("inf")
+    for cfg, sp in cands:
+        if sp > 1:
+            ws.reserve(*_ws_need(cfg, sp, M, lin.N))
+        run = lambda: lin._launch(cfg, sp, x2, y2, M, a, r2, ldr, r_rows, ws)
+        if run() != 0:
+            continue
+        run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            run()
+        e1.record()
+        e1.synchronize()
+        t = e0.elapsed_time(e1)
+        if t < bt:
+            best, bt = (cfg, sp), t
+    return best
+
+
+# Split-K candidates in the tuner: off by default (the cross-XCD release fence of the last-arriver reduction costs
+# more than the extra parallelism buys at these shapes; the path stays available and tested).
+tune_gemm.split_k = False
 
 
 def sdpa(q, k, v, out=None, scale=None, qpos0=0, causal_from=None):

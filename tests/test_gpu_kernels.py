@@ -48,18 +48,24 @@ def test_gemm_bias_vs_fp32(dev, M, K, N):
     assert (y.float().cpu() - ref).abs().max().item() < 0.02 * ref.abs().max().item() + 1e-2
 
 
-@pytest.mark.parametrize("cfg", range(6))
-def test_gemm_every_tile_config(dev, cfg):
-    M, K, N = 300, 1152, 1152 + 64  # ragged M and N tails for every tile shape
+@pytest.mark.parametrize("cfg", range(8))
+@pytest.mark.parametrize("splits", [1, 3])
+def test_gemm_every_tile_config(dev, cfg, splits):
+    """Every tile config, with and without split-K, on ragged M / N / K tails (K = 1000: the last k-step is partial
+    and reads A's padding columns against W's zero padding)."""
+    M, K, N = 300, 1000, 1152 + 68
     g = gen(cfg)
     x = torch.randn(M, K, generator=g).to(BF)
     w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
-    ref = x.float() @ w.float().t()
-    lin = ops.MxLin(w, None)
-    lin.cfgs[M] = cfg
-    print(f"gemm cfg={cfg}", flush=True)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    ref = x.float() @ w.float().t() + b.float()
+    lin = ops.MxLin(w, b)
+    lin.cfgs[M] = (cfg, splits)
+    print(f"gemm cfg={cfg} splits={splits}", flush=True)
     y = lin(x.to(dev))
     assert rel(y, ref) < 5e-3
+    y2 = lin(x.to(dev))  # counters re-armed: a second call gives the same bits
+    assert torch.equal(y.cpu(), y2.cpu())
 
 
 def test_gemm_epilogues_match_unfused(dev):

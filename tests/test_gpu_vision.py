@@ -1,10 +1,15 @@
 """SigLIP vision tower parity: the HIP path (VisionTower) vs the oracle's restatement of the reference's PyTorch bf16
 path (oracle/md2_vision.py) on identical seeded weights and pixels.
 
-Tolerances (stated for the floating-point hidden states): per block, given the same block input, rel-L2 <= 1e-2 and
-max-abs <= 5e-2 beyond one bf16 ulp of the reference value (a value >= 8 has a bf16 ulp of 0.0625 > 5e-2, so two
-correct bf16 results that round an fp32 value to neighbouring bf16 numbers would otherwise fail; the raw max-abs is
-printed); end to end (27 blocks + post-LN, errors compound), rel-L2 <= 2e-2."""
+Tolerances (stated for the floating-point hidden states): per block, given the same block input,
+  * rel-L2 <= 1e-2;
+  * elementwise |diff| <= 5e-2 + 2 bf16 ulps of the oracle value, and |diff| > 5e-2 on under 1e-3 of the elements;
+  * no less accurate than the oracle itself: max |hip - fp32| <= 1.5 max |oracle - fp32| + 1e-2, where fp32 is the
+    same block computed in fp32 from the same bf16 input and weights.
+The ulp allowance exists because the residual stream grows past 4 and 8 in the later blocks (1.4 % of block 27's
+elements exceed 8 at this seed), where the bf16 spacing is 0.03 / 0.06: the oracle's own bf16 result is up to 0.066
+away from fp32 there, so two correct bf16 computations accumulating in different orders can differ by more than
+5e-2. End to end (27 blocks + post-LN, errors compound), rel-L2 <= 2e-2."""
 import pytest
 import torch
 
@@ -21,11 +26,19 @@ def rel(a, b):
     return ((a - b).norm() / b.norm()).item()
 
 
-def maxabs(a, b):
-    """max |a - b| in excess of one bf16 ulp of b."""
+def check(a, b):
+    """(rel-L2, excess, frac_over, raw): excess = max(|a - b| - (5e-2 + 2 bf16 ulps of b)) (<= 0 when within
+    tolerance), frac_over = fraction of elements with |a - b| > 5e-2, raw = max |a - b|."""
     a, b = a.float().cpu(), b.float().cpu()
     ulp = torch.where(b == 0, torch.zeros_like(b), torch.ldexp(torch.ones_like(b), torch.frexp(b)[1] - 8))
-    return ((a - b).abs() - ulp).clamp_min(0).max().item()
+    d = (a - b).abs()
+    excess = (d - (MAXABS + 2 * ulp)).max().item()
+    return rel(a, b), excess, (d > MAXABS).float().mean().item(), d.max().item()
+
+
+def ok(a, b):
+    r, ex, fr, raw = check(a, b)
+    return r <= REL and ex <= 0 and fr < 1e-3, (r, ex, fr, raw)
 
 
 def rawmax(a, b):
@@ -47,8 +60,9 @@ def test_one_block_config0(dev):
     ref = ov.block(w, 0, x)
     vt = md2.VisionTower(w)
     y = vt.block(vt.blocks[0], x.view(729, 1152).to(dev), 1).view(1, 729, 1152)
-    print("block0 rel", rel(y, ref), "maxabs beyond 1 ulp", maxabs(y, ref), "raw", rawmax(y, ref), flush=True)
-    assert rel(y, ref) <= REL and maxabs(y, ref) <= MAXABS
+    good, st = ok(y, ref)
+    print("block0 (rel, excess, frac>5e-2, raw max-abs)", st, flush=True)
+    assert good, st
 
 
 def test_batch2_block_matches_batch1(dev):
@@ -67,14 +81,20 @@ def test_tower_per_block_and_end_to_end(dev, full):
     w, img, ref, hs = full
     vt = md2.VisionTower(w)
     emb = vt.embed(img.to(dev))
-    print("embed rel", rel(emb, hs[0][0]), flush=True)
-    assert rel(emb, hs[0][0]) <= REL and maxabs(emb, hs[0][0]) <= MAXABS
+    good, st = ok(emb, hs[0][0])
+    print("embed", st, flush=True)
+    assert good, st
     worst = 0.0
+    w32 = {k: v.float() for k, v in w.items()}
     for i, b in enumerate(vt.blocks):
         y = vt.block(b, hs[i][0].to(dev), 1)
-        r, m = rel(y, hs[i + 1][0]), maxabs(y, hs[i + 1][0])
-        worst = max(worst, r)
-        assert r <= REL and m <= MAXABS, (i, r, m)
+        good, st = ok(y, hs[i + 1][0])
+        worst = max(worst, st[0])
+        assert good, (i, st)
+        if i % 4 == 3 or i == len(vt.blocks) - 1:
+            y32 = ov.block(w32, i, hs[i].float())[0]
+            e_hip, e_ora = rawmax(y, y32), rawmax(hs[i + 1][0], y32)
+            assert e_hip <= 1.5 * e_ora + 1e-2, (i, e_hip, e_ora)
     out = vt(img.to(dev))
     print("last block raw max-abs", rawmax(y, hs[-1][0]), flush=True)
     print("worst block rel", worst, "end-to-end rel", rel(out, ref), flush=True)
