@@ -118,6 +118,48 @@ def cpu_baseline(budget_s=20.0):
                       f"median of {n} frames after 1 warm-up, torch.set_num_threads({threads})"}
 
 
+def decode_bench(steps_tokens=128):
+    """Config 2: prefill (1 + 729 image tokens mask-free, then 64 prompt ids) + greedy decode on one HIP graph per
+    step. Returns prefill ms, decode tok/s and the decode step's HBM roofline (algorithmic bytes = every weight once
+    + the KV cache read per token)."""
+    import torch
+    import strix_halo_maxx_amd.md2text as mt
+    import strix_halo_maxx_amd.synth as S
+    dev = torch.device("cuda:0")
+    w = S.text_weights(0)
+    dec = mt.TextDecoder(w, device=dev, ctx=1024)
+    del w
+    img = S.activations(3, (729, 2048), "img").to(dev)
+    prompt = S.prompt_ids(4, 64)
+    for _ in range(2):
+        dec.generate(img, prompt, 8)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.prefill(img, prompt)
+    torch.cuda.synchronize()
+    t_pre = time.perf_counter() - t0
+    dec.start_decode()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps_tokens - 1):
+        dec.graph.replay()
+    torch.cuda.synchronize()
+    t_dec = (time.perf_counter() - t0) / (steps_tokens - 1)
+    c = S.TXT
+    D, F, L, V = c["dim"], c["ff"], c["layers"], c["vocab"]
+    wbytes = 2 * (L * (3 * D * D + D * D + 2 * D * F) + V * D)
+    ctx_mid = dec.pos_base + steps_tokens // 2
+    kvbytes = 2 * 2 * L * ctx_mid * D
+    bpt = wbytes + kvbytes
+    return {"prefill_ms": round(t_pre * 1e3, 3), "decode_tok_s": round(1.0 / t_dec, 1),
+            "decode_ms_per_token": round(t_dec * 1e3, 4),
+            "decode_roofline": {"bound": "hbm", "achieved": round(bpt / t_dec / 1e9, 1), "peak": PEAK_HBM / 1e9,
+                                "unit": "GB/s", "frac": round(bpt / t_dec / PEAK_HBM, 4),
+                                "bytes_per_token": bpt},
+            "workload": "moondream2 text decoder, 24 layers, prefill 730 + 64 tokens, greedy "
+                        f"{steps_tokens} tokens, batch 1, one HIP graph per decode step"}
+
+
 def tower_time(vt, img, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -168,7 +210,7 @@ def main():
             "per_kernel_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in agg.items()},
             "flops_per_launch": fl // n}
     tower_flops = vision_flops_per_frame()
-    out = {"metric": "ms/frame moondream2 vision tower bs=1", "value": round(ms, 4), "unit": "ms/frame", "n_gpus": 1,
+    out = {"metric": "ms/frame moondream2 vision tower bs=1; decode tok/s; % MFMA / HBM roofline", "value": round(ms, 4), "unit": "ms/frame", "n_gpus": 1,
            "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded u8 pixels, N(0,0.02) weights)",
            "config": {"workload": "moondream2 SigLIP vision tower, 27 blocks + post-LN, 729 tokens, batch 1, HIP graph",
@@ -186,6 +228,11 @@ def main():
                 del imgs
                 vt.graphs.clear()
                 torch.cuda.empty_cache()
+    del vt
+    torch.cuda.empty_cache()
+    print("[bench] decoder", file=sys.stderr, flush=True)
+    with torch.inference_mode():
+        out.setdefault("extra", {})["decoder"] = decode_bench()
     if not a.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline()

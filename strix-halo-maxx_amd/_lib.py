@@ -29,6 +29,13 @@ SIGNATURES = {
     "mx_layernorm": [P, P, L, P, P, P, L, I, I, F],
     "mx_rmsnorm": [P, P, L, P, P, L, I, I, F],
     "mx_patchify_u8": [P, P, P, L, I, I, I, I],
+    "mx_rope_kv": [P, P, L, P, P, P, P, I, I, I, I, I, I, I],
+    "mx_ln_gemv2": [P, P, P, P, F, P, L, P, I, I, I, P, P, I],
+    "mx_gemv_dual_res": [P, P, P, P, I, P, P, P, I, P, P, I],
+    "mx_lm_argmax_nparts": [I],
+    "mx_ln_gemv_argmax": [P, P, P, P, F, P, L, P, I, I, P, P, I],
+    "mx_embed_step": [P, P, I, P, I, P, I, P, P],
+    "mx_decode_attn": [P, P, P, P, P, I, I, P, I, F, P, P, P],
 }
 
 STATUS = {0: "ok", -1: "bad config", -2: "unsupported shape/stride", -3: "split-K workspace too small",

@@ -1,0 +1,436 @@
+// Batch-1 greedy decode kernels for the moondream2 text model (hidden 2048, 32 heads x 64, MLP 8192, vocab 51200).
+//
+// A decode step is HBM-bound: every weight (2.6 GB) is read once per token. The step is 3 kernels per layer plus
+// 2 per token, all replayed from one HIP graph, with the step's position and the token living in device memory:
+//   ln_gemv2      h = LN(x) (recomputed per wave from the 4 KB row), [qkv | fc1] = h [Wqkv | Wfc1]^T + b, GELU on
+//                 the fc1 part (the reference's qkv and fc1 both read the same LN output, md2fast.py:173-198)
+//   decode_attn   rope on q / k of the new token, K/V append at `pos`, split-KV attention over keys 0..pos with a
+//                 last-arriver merge of the splits (no workgroup ever waits on another)
+//   gemv_dual_res x' = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)): the parallel residual of
+//                 md2fast.py:198 with the reference's rounding order, both GEMVs in one pass over [Wfc2 | Wproj]
+//   ln_gemv_argmax  logits = LN(x) Wlm^T + b (bf16, as the reference's bf16 lm_head) and a per-workgroup argmax
+//   embed_step    reduce the per-workgroup argmaxes (first index wins ties, like torch.argmax), append the token to
+//                 the output, x = wte[token], advance the position counter
+// GEMV layout: a 64-wide wave owns R weight rows; lane l reads 16-byte chunks l, l + 64, ... of each row (1 KB per
+// wave per load instruction, all rows' loads issued before any arithmetic), fp32 FMAs, a wave reduction per row.
+#include "common.h"
+
+namespace {
+
+__device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc) {
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    acc = __builtin_fmaf(lo_bf(w[e]), lo_bf(x[e]), acc);
+    acc = __builtin_fmaf(hi_bf(w[e]), hi_bf(x[e]), acc);
+  }
+  return acc;
+}
+
+// LayerNorm of a row held as KC chunks per lane (chunk c = lane + 64 i): bf16 result in place (torch F.layer_norm
+// numerics: fp32 statistics, biased variance, one rounding).
+template <int KC>
+__device__ __forceinline__ void ln_chunks(u32x4 (&xc)[KC], const uint16_t* gamma, const uint16_t* beta, float eps,
+                                          int K, int lane) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < KC; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) s += lo_bf(xc[i][e]) + hi_bf(xc[i][e]);
+  const float mean = wave_sum(s) / (float)K;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < KC; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float d0 = lo_bf(xc[i][e]) - mean, d1 = hi_bf(xc[i][e]) - mean;
+      ss += d0 * d0 + d1 * d1;
+    }
+  const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)K + eps);
+#pragma unroll
+  for (int i = 0; i < KC; i++) {
+    const int c = lane + 64 * i;
+    const u32x4 g = *reinterpret_cast<const u32x4*>(gamma + c * 8);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(beta + c * 8);
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      xc[i][e] = pack2((lo_bf(xc[i][e]) - mean) * rstd * lo_bf(g[e]) + lo_bf(b[e]),
+                       (hi_bf(xc[i][e]) - mean) * rstd * hi_bf(g[e]) + hi_bf(b[e]));
+  }
+}
+
+template <int KC>
+__device__ __forceinline__ void load_vec(u32x4 (&xc)[KC], const uint16_t* x, int lane) {
+#pragma unroll
+  for (int i = 0; i < KC; i++) xc[i] = *reinterpret_cast<const u32x4*>(x + (lane + 64 * i) * 8);
+}
+
+// ---------------------------------------------------------------------------------------------- ln_gemv2
+template <int KC, int R>
+__global__ __launch_bounds__(256) void ln_gemv2_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
+                                                       const uint16_t* __restrict__ beta, float eps,
+                                                       const uint16_t* __restrict__ W, long ldw,
+                                                       const float* __restrict__ bias, int N, int n1,
+                                                       uint16_t* __restrict__ out1, uint16_t* __restrict__ out2,
+                                                       int act2) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  if (row0 >= N) return;
+  u32x4 wv[R][KC];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const uint16_t* wr = W + (long)min(row0 + r, N - 1) * ldw;
+#pragma unroll
+    for (int i = 0; i < KC; i++) wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (lane + 64 * i) * 8));
+  }
+  u32x4 xc[KC];
+  load_vec<KC>(xc, x, lane);
+  if (gamma) ln_chunks<KC>(xc, gamma, beta, eps, KC * 512, lane);
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < KC; i++) acc = dot8(wv[r][i], xc[i], acc);
+    acc = wave_sum(acc);
+    const int n = row0 + r;
+    if (lane == 0 && n < N) {
+      float v = rbf(acc + (bias ? bias[n] : 0.f));
+      if (n < n1) {
+        out1[n] = f2bf(v);
+      } else {
+        if (act2 == 1) v = gelu_tanh(v);
+        else if (act2 == 2) v = gelu_erf(v);
+        out2[n - n1] = f2bf(v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- gemv_dual_res
+template <int KC1, int KC2, int R>
+__global__ __launch_bounds__(256) void gemv_dual_res_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ W2,
+                                                            const float* __restrict__ b2,
+                                                            const uint16_t* __restrict__ a, const uint16_t* __restrict__ Wp,
+                                                            const float* __restrict__ bp,
+                                                            const uint16_t* __restrict__ xres, uint16_t* __restrict__ out,
+                                                            int N) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  if (row0 >= N) return;
+  u32x4 w2[R][KC1], wp[R][KC2];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int n = min(row0 + r, N - 1);
+#pragma unroll
+    for (int i = 0; i < KC1; i++)
+      w2[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W2 + (long)n * KC1 * 512 + (lane + 64 * i) * 8));
+#pragma unroll
+    for (int i = 0; i < KC2; i++)
+      wp[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Wp + (long)n * KC2 * 512 + (lane + 64 * i) * 8));
+  }
+  u32x4 gc[KC1], ac[KC2];
+  load_vec<KC1>(gc, g, lane);
+  load_vec<KC2>(ac, a, lane);
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    float s2 = 0.f, sp = 0.f;
+#pragma unroll
+    for (int i = 0; i < KC1; i++) s2 = dot8(w2[r][i], gc[i], s2);
+#pragma unroll
+    for (int i = 0; i < KC2; i++) sp = dot8(wp[r][i], ac[i], sp);
+    s2 = wave_sum(s2);
+    sp = wave_sum(sp);
+    const int n = row0 + r;
+    if (lane == 0 && n < N) {
+      const float pr = rbf(rbf(sp + bp[n]) + bf2f(xres[n]));
+      out[n] = f2bf(rbf(s2 + b2[n]) + pr);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- lm head + argmax
+// Argmax key: orderable bits of the bf16 logit in the high word, (0xffffffff - index) in the low word, so the
+// largest key is the largest logit and, among equal logits, the smallest index.
+__device__ __forceinline__ unsigned long long amax_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+
+template <int KC, int R>
+__global__ __launch_bounds__(256) void ln_gemv_argmax_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ gamma,
+                                                             const uint16_t* __restrict__ beta, float eps,
+                                                             const uint16_t* __restrict__ W, long ldw,
+                                                             const float* __restrict__ bias, int N,
+                                                             uint16_t* __restrict__ logits,
+                                                             unsigned long long* __restrict__ part) {
+  __shared__ unsigned long long sbest[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  unsigned long long best = 0ull;
+  if (row0 < N) {
+    u32x4 wv[R][KC];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint16_t* wr = W + (long)min(row0 + r, N - 1) * ldw;
+#pragma unroll
+      for (int i = 0; i < KC; i++) wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (lane + 64 * i) * 8));
+    }
+    u32x4 xc[KC];
+    load_vec<KC>(xc, x, lane);
+    ln_chunks<KC>(xc, gamma, beta, eps, KC * 512, lane);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < KC; i++) acc = dot8(wv[r][i], xc[i], acc);
+      acc = wave_sum(acc);
+      const int n = row0 + r;
+      if (n < N) {
+        const float v = rbf(acc + bias[n]);
+        if (logits && lane == 0) logits[n] = f2bf(v);
+        const unsigned long long k = amax_key(v, n);
+        best = k > best ? k : best;
+      }
+    }
+  }
+  if (lane == 0) sbest[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = sbest[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) b = sbest[w] > b ? sbest[w] : b;
+    part[blockIdx.x] = b;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- embed_step
+// state[0] = step s (tokens emitted so far), state[1] = position of the token fed this step (= pos_base + s).
+__global__ __launch_bounds__(1024) void embed_step_kernel(const unsigned long long* __restrict__ part, int nparts,
+                                                          const uint16_t* __restrict__ wte, int D,
+                                                          int* __restrict__ state, int pos_base,
+                                                          int* __restrict__ tokens, uint16_t* __restrict__ x) {
+  __shared__ unsigned long long sb[16];
+  __shared__ int stok;
+  unsigned long long b = 0ull;
+  for (int i = threadIdx.x; i < nparts; i += 1024) b = part[i] > b ? part[i] : b;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const unsigned long long t = __shfl_xor(b, o, 64);
+    b = t > b ? t : b;
+  }
+  if ((threadIdx.x & 63) == 0) sb[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long m = sb[0];
+    for (int w = 1; w < 16; w++) m = sb[w] > m ? sb[w] : m;
+    const int tok = (int)(0xffffffffu - (uint32_t)(m & 0xffffffffull));
+    stok = tok;
+    const int s = state[0];
+    tokens[s] = tok;
+    state[1] = pos_base + s;
+    state[0] = s + 1;
+  }
+  __syncthreads();
+  const int tok = stok;
+  for (int i = threadIdx.x; i < D / 8; i += 1024)
+    *reinterpret_cast<u32x4*>(x + i * 8) = *reinterpret_cast<const u32x4*>(wte + (long)tok * D + i * 8);
+}
+
+// ---------------------------------------------------------------------------------------------- decode attention
+constexpr int DA_MAXK = 1024;  // keys per split held in LDS
+
+__global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
+                                                          uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                          int H, int ctx, const int* __restrict__ state, int S,
+                                                          float scale_log2, float* __restrict__ ws,
+                                                          int* __restrict__ cnt, uint16_t* __restrict__ out) {
+  __shared__ float sc[DA_MAXK];
+  __shared__ float qs[64];
+  __shared__ uint16_t knew[64], vnew[64];
+  __shared__ float red[8];
+  __shared__ float osum[4][64];
+  __shared__ int s_last;
+  const int h = blockIdx.x, split = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pos = state[1];
+  const int L = pos + 1;
+  const int chunk = (L + S - 1) / S;
+  const int k0 = split * chunk, k1 = min(L, k0 + chunk);
+  const float* cp = cs + (long)pos * 32;
+  const uint16_t* src = qkv + h * 64;
+  const uint16_t* ksrc = qkv + H * 64 + h * 64;
+  const uint16_t* vsrc = qkv + 2 * H * 64 + h * 64;
+  // rope of q and k for the new token (fp32, as the prefill rope kernel)
+  if (tid < 64) {
+    const int d = tid;
+    float qv, kv;
+    if (d < 32) {
+      const int j = d >> 1;
+      const float c = cp[2 * j], s = cp[2 * j + 1];
+      const float qa = bf2f(src[j]), qb = bf2f(src[16 + j]), ka = bf2f(ksrc[j]), kb = bf2f(ksrc[16 + j]);
+      qv = (d & 1) ? __fadd_rn(__fmul_rn(qa, s), __fmul_rn(qb, c)) : __fsub_rn(__fmul_rn(qa, c), __fmul_rn(qb, s));
+      kv = (d & 1) ? __fadd_rn(__fmul_rn(ka, s), __fmul_rn(kb, c)) : __fsub_rn(__fmul_rn(ka, c), __fmul_rn(kb, s));
+    } else {
+      qv = bf2f(src[d]);
+      kv = bf2f(ksrc[d]);
+    }
+    qs[d] = rbf(qv);
+    knew[d] = f2bf(kv);
+    vnew[d] = vsrc[d];
+  }
+  __syncthreads();
+  const bool has_new = (k0 <= pos && pos < k1);
+  if (has_new && tid < 64) {  // the split that owns key `pos` appends it to the cache (and uses it from LDS)
+    kc[((long)h * ctx + pos) * 64 + tid] = knew[tid];
+    vc[((long)h * ctx + pos) * 64 + tid] = vnew[tid];
+  }
+  // ---- scores: 8 lanes per key (lane % 8 -> dims 8 (lane % 8) ..), 8 keys per wave per step
+  const int sub = lane & 7, kg = lane >> 3;
+  float qv[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) qv[e] = qs[sub * 8 + e];
+  float mloc = -1e30f;
+  for (int key = k0 + wave * 8 + kg; key < k1; key += 32) {
+    u32x4 kk;
+    if (key == pos) kk = *reinterpret_cast<const u32x4*>(&knew[sub * 8]);
+    else kk = *reinterpret_cast<const u32x4*>(kc + ((long)h * ctx + key) * 64 + sub * 8);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      s = __builtin_fmaf(lo_bf(kk[e]), qv[2 * e], s);
+      s = __builtin_fmaf(hi_bf(kk[e]), qv[2 * e + 1], s);
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    s *= scale_log2;
+    if (sub == 0) sc[key - k0] = s;
+    mloc = fmaxf(mloc, s);
+  }
+  mloc = wave_max(mloc);
+  if (lane == 0) red[wave] = mloc;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // ---- P (rounded to bf16) and PV with the same key mapping
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+  for (int key = k0 + wave * 8 + kg; key < k1; key += 32) {
+    const float p = rbf(__builtin_amdgcn_exp2f(sc[key - k0] - m));
+    if (sub == 0) lsum += p;
+    u32x4 vv;
+    if (key == pos) vv = *reinterpret_cast<const u32x4*>(&vnew[sub * 8]);
+    else vv = *reinterpret_cast<const u32x4*>(vc + ((long)h * ctx + key) * 64 + sub * 8);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      o[2 * e] = __builtin_fmaf(p, lo_bf(vv[e]), o[2 * e]);
+      o[2 * e + 1] = __builtin_fmaf(p, hi_bf(vv[e]), o[2 * e + 1]);
+    }
+  }
+  // reduce over the 8 key groups of the wave, then over the 4 waves
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    o[e] += __shfl_xor(o[e], 8, 64);
+    o[e] += __shfl_xor(o[e], 16, 64);
+    o[e] += __shfl_xor(o[e], 32, 64);
+  }
+  lsum = wave_sum(lsum);
+  __syncthreads();
+  if (kg == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) osum[wave][sub * 8 + e] = o[e];
+  }
+  if (lane == 0) red[4 + wave] = lsum;
+  __syncthreads();
+  float* rec = ws + ((long)h * S + split) * 66;  // (m, l, o[64])
+  if (tid < 64) rec[2 + tid] = osum[0][tid] + osum[1][tid] + osum[2][tid] + osum[3][tid];
+  if (tid == 0) { rec[0] = (k1 > k0) ? m : -1e30f; rec[1] = red[4] + red[5] + red[6] + red[7]; }
+  // ---- last split to finish merges all splits of this head
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = (atomicAdd(&cnt[h], 1) == S - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  if (tid < 64) {
+    float M = -1e30f;
+    for (int sp = 0; sp < S; sp++) M = fmaxf(M, __builtin_nontemporal_load(ws + ((long)h * S + sp) * 66));
+    float Lt = 0.f, acc = 0.f;
+    for (int sp = 0; sp < S; sp++) {
+      const float* r = ws + ((long)h * S + sp) * 66;
+      const float f = __builtin_amdgcn_exp2f(__builtin_nontemporal_load(r) - M);
+      Lt += __builtin_nontemporal_load(r + 1) * f;
+      acc += __builtin_nontemporal_load(r + 2 + tid) * f;
+    }
+    out[h * 64 + tid] = f2bf(acc / Lt);
+  }
+  if (tid == 0) cnt[h] = 0;
+}
+
+}  // namespace
+
+extern "C" int mx_ln_gemv2(hipStream_t st, const uint16_t* x, const uint16_t* gamma, const uint16_t* beta, float eps,
+                           const uint16_t* W, long ldw, const float* bias, int N, int K, int n1, uint16_t* out1,
+                           uint16_t* out2, int act2) {
+  if (!x || !W || !out1 || (n1 < N && !out2)) return MX_ENULL;
+  if ((gamma == nullptr) != (beta == nullptr)) return MX_ENULL;
+  if (N < 1 || n1 < 0 || n1 > N || ldw < K || ldw % 8 || act2 < 0 || act2 > 2) return MX_ESHAPE;
+  if (((uintptr_t)x | (uintptr_t)W) & 15) return MX_ELAYOUT;
+  constexpr int R = 4;
+  const dim3 g((N + 4 * R - 1) / (4 * R));
+  if (K == 2048) hipLaunchKernelGGL((ln_gemv2_kernel<4, R>), g, dim3(256), 0, st, x, gamma, beta, eps, W, ldw, bias, N, n1, out1, out2, act2);
+  else if (K == 1024) hipLaunchKernelGGL((ln_gemv2_kernel<2, R>), g, dim3(256), 0, st, x, gamma, beta, eps, W, ldw, bias, N, n1, out1, out2, act2);
+  else return MX_ESHAPE;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+extern "C" int mx_gemv_dual_res(hipStream_t st, const uint16_t* g, const uint16_t* W2, const float* b2, int K2,
+                                const uint16_t* a, const uint16_t* Wp, const float* bp, int Kp, const uint16_t* xres,
+                                uint16_t* out, int N) {
+  if (!g || !W2 || !b2 || !a || !Wp || !bp || !xres || !out) return MX_ENULL;
+  if (N < 1) return MX_ESHAPE;
+  if (((uintptr_t)g | (uintptr_t)W2 | (uintptr_t)a | (uintptr_t)Wp) & 15) return MX_ELAYOUT;
+  constexpr int R = 2;
+  const dim3 gr((N + 4 * R - 1) / (4 * R));
+  if (K2 == 8192 && Kp == 2048)
+    hipLaunchKernelGGL((gemv_dual_res_kernel<16, 4, R>), gr, dim3(256), 0, st, g, W2, b2, a, Wp, bp, xres, out, N);
+  else if (K2 == 4096 && Kp == 1024)
+    hipLaunchKernelGGL((gemv_dual_res_kernel<8, 2, R>), gr, dim3(256), 0, st, g, W2, b2, a, Wp, bp, xres, out, N);
+  else return MX_ESHAPE;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+extern "C" int mx_lm_argmax_nparts(int N) { return (N + 4 * 8 - 1) / (4 * 8); }
+
+extern "C" int mx_ln_gemv_argmax(hipStream_t st, const uint16_t* x, const uint16_t* gamma, const uint16_t* beta,
+                                 float eps, const uint16_t* W, long ldw, const float* bias, int N, int K,
+                                 uint16_t* logits, unsigned long long* part, int nparts) {
+  if (!x || !gamma || !beta || !W || !bias || !part) return MX_ENULL;
+  if (N < 1 || ldw < K || ldw % 8) return MX_ESHAPE;
+  if (nparts < mx_lm_argmax_nparts(N)) return MX_ESPLIT;
+  if (((uintptr_t)x | (uintptr_t)W) & 15) return MX_ELAYOUT;
+  constexpr int R = 8;
+  const dim3 g(mx_lm_argmax_nparts(N));
+  if (K == 2048) hipLaunchKernelGGL((ln_gemv_argmax_kernel<4, R>), g, dim3(256), 0, st, x, gamma, beta, eps, W, ldw, bias, N, logits, part);
+  else if (K == 1024) hipLaunchKernelGGL((ln_gemv_argmax_kernel<2, R>), g, dim3(256), 0, st, x, gamma, beta, eps, W, ldw, bias, N, logits, part);
+  else return MX_ESHAPE;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+extern "C" int mx_embed_step(hipStream_t st, const unsigned long long* part, int nparts, const uint16_t* wte, int D,
+                             int* state, int pos_base, int* tokens, uint16_t* x) {
+  if (!part || !wte || !state || !tokens || !x) return MX_ENULL;
+  if (nparts < 1 || D % 8) return MX_ESHAPE;
+  hipLaunchKernelGGL(embed_step_kernel, dim3(1), dim3(1024), 0, st, part, nparts, wte, D, state, pos_base, tokens, x);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// ws: >= H * S * 66 floats; cnt: >= H ints, zero before first use (left zero).
+extern "C" int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H,
+                              int ctx, const int* state, int S, float scale, float* ws, int* cnt, uint16_t* out) {
+  if (!qkv || !cs || !kc || !vc || !state || !ws || !cnt || !out) return MX_ENULL;
+  if (H < 1 || S < 1 || ctx < 1 || (ctx + S - 1) / S > DA_MAXK) return MX_ESHAPE;
+  hipLaunchKernelGGL(decode_attn_kernel, dim3(H, S), dim3(256), 0, st, qkv, cs, kc, vc, H, ctx, state, S,
+                     scale * 1.4426950408889634f, ws, cnt, out);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}

@@ -89,9 +89,12 @@ class MxLin:
         self.Kw = (self.K0 + 63) // 64 * 64      # padded weight row
         if self.N % 4:
             raise ValueError(f"N={self.N} must be a multiple of 4")
-        wp = torch.zeros(self.N, self.Kw, device=device, dtype=BF)
-        wp[:, :self.K0] = w
-        self.w = wp
+        if self.Kw == self.K0 and w.stride(1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0:
+            self.w = w  # already in the kernel's layout: share the storage (e.g. a row slice of a fused weight)
+        else:
+            wp = torch.zeros(self.N, self.Kw, device=device, dtype=BF)
+            wp[:, :self.K0] = w
+            self.w = wp
         self.Kp = self.K                         # width of the input this layer reads
         self.b = None if bias is None else bias.detach().to(device=device, dtype=torch.float32).contiguous()
         self.cfgs = {}  # M -> (cfg, splits); absent: tuned (or library pick) on first use

@@ -1,0 +1,208 @@
+"""moondream2 text decoder parity: the HIP path (TextDecoder) vs the oracle's restatement (oracle/md2_text.py).
+
+Kernel level (fp32 references of the same op): rope + KV write, the LN-fused [qkv | fc1] GEMV, the fused
+fc2 / proj / residual GEMV, the LM-head argmax, split-KV decode attention.
+Model level (seeded weights N(0, 0.02), image tokens N(0, 1), prompt ids uniform):
+  * prefill hidden states: rel-L2 <= 1e-2 (2 layers), <= 2e-2 end to end through all 24 layers (errors compound,
+    as the vision tower's end-to-end bound);
+  * greedy decode, teacher-forced on the HIP path's tokens: every step's logits within rel-L2 1e-2 (2e-2 at 24
+    layers) of the oracle's,
+    and the HIP token is the oracle's argmax unless the oracle's top-2 gap is below TIE (then it must be within TIE
+    of the oracle's max);
+  * free-running: the token sequences are identical up to the first oracle near-tie (gap < TIE), and identical
+    outright when no such tie occurs (the seeded full config).
+TIE = 0.05 (logit std ~0.9; bf16 logit spacing at |logit| in [2, 4) is 0.0156)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle.md2_text as ot
+import strix_halo_maxx_amd.md2text as mt
+import strix_halo_maxx_amd.ops as ops
+import strix_halo_maxx_amd.synth as S
+from strix_halo_maxx_amd import _lib
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+TIE = 0.05
+
+
+def rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def gen(s):
+    return torch.Generator().manual_seed(s)
+
+
+def test_rope_kv_matches_oracle(dev):
+    H, n, ctx, pos0 = 32, 37, 1024, 730
+    qkv = torch.randn(n, 3 * H * 64, generator=gen(1)).to(BF)
+    fr = S.freqs_cis(32, 2048)
+    q_ref = ot.rope(qkv[:, :H * 64].view(1, n, H, 64).transpose(1, 2), fr[pos0:pos0 + n, :, 0], fr[pos0:pos0 + n, :, 1])
+    k_ref = ot.rope(qkv[:, H * 64:2 * H * 64].view(1, n, H, 64).transpose(1, 2), fr[pos0:pos0 + n, :, 0], fr[pos0:pos0 + n, :, 1])
+    v_ref = qkv[:, 2 * H * 64:].view(1, n, H, 64).transpose(1, 2)
+    qd, frd = qkv.to(dev), fr.to(dev)
+    q = torch.empty(1, H, n, 64, device=dev, dtype=BF)
+    kc = torch.zeros(1, H, ctx, 64, device=dev, dtype=BF)
+    vc = torch.zeros(1, H, ctx, 64, device=dev, dtype=BF)
+    _lib.call("mx_rope_kv", _lib.stream(), qd.data_ptr(), qd.stride(0), frd.data_ptr(), q.data_ptr(),
+              kc.data_ptr(), vc.data_ptr(), 1, n, H, ctx, pos0, 1, 0)
+    assert torch.equal(q.cpu(), q_ref)
+    assert torch.equal(kc[:, :, pos0:pos0 + n].cpu(), k_ref)
+    assert torch.equal(vc[:, :, pos0:pos0 + n].cpu(), v_ref)
+    assert torch.count_nonzero(kc[:, :, :pos0]) == 0
+
+
+def test_ln_gemv2_and_dual_res(dev):
+    D, N1, F_ = 2048, 6144, 8192
+    g = gen(2)
+    x = torch.randn(D, generator=g).to(BF)
+    lw, lb = (1 + 0.1 * torch.randn(D, generator=g)).to(BF), (0.1 * torch.randn(D, generator=g)).to(BF)
+    W = (torch.randn(N1 + F_, D, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N1 + F_, generator=g) * 0.02).to(BF)
+    h = F.layer_norm(x.float(), (D,), lw.float(), lb.float(), 1e-5).to(BF)
+    ref = h.float() @ W.float().t() + b.float()
+    # device copies are bound to names: a temporary inside the call's argument list could be freed (and its memory
+    # reused by the next temporary) before the kernel reads it
+    Wd, bd, xd, lwd, lbd = W.to(dev), b.float().to(dev), x.to(dev), lw.to(dev), lb.to(dev)
+    o1 = torch.empty(N1, device=dev, dtype=BF)
+    o2 = torch.empty(F_, device=dev, dtype=BF)
+    _lib.call("mx_ln_gemv2", _lib.stream(), xd.data_ptr(), lwd.data_ptr(), lbd.data_ptr(), 1e-5,
+              Wd.data_ptr(), D, bd.data_ptr(), N1 + F_, D, N1, o1.data_ptr(), o2.data_ptr(), 1)
+    assert rel(o1, ref[:N1]) < 5e-3
+    assert rel(o2, F.gelu(ref[N1:], approximate="tanh")) < 5e-3
+    # dual: x' = bf(bf(fc2(g) + b2) + bf(bf(proj(a) + bp) + x))
+    gi = torch.randn(F_, generator=g).to(BF)
+    a = torch.randn(D, generator=g).to(BF)
+    W2 = (torch.randn(D, F_, generator=g) * 0.02).to(BF)
+    Wp = (torch.randn(D, D, generator=g) * 0.02).to(BF)
+    b2 = torch.randn(D, generator=g) * 0.02
+    bp = torch.randn(D, generator=g) * 0.02
+    ref2 = (W2.float() @ gi.float() + b2) + (Wp.float() @ a.float() + bp) + x.float()
+    out = torch.empty(D, device=dev, dtype=BF)
+    gd, W2d, b2d, ad, Wpd, bpd = gi.to(dev), W2.to(dev), b2.to(dev), a.to(dev), Wp.to(dev), bp.to(dev)
+    _lib.call("mx_gemv_dual_res", _lib.stream(), gd.data_ptr(), W2d.data_ptr(), b2d.data_ptr(), F_,
+              ad.data_ptr(), Wpd.data_ptr(), bpd.data_ptr(), D, xd.data_ptr(), out.data_ptr(), D)
+    assert rel(out, ref2) < 5e-3
+
+
+def test_lm_argmax_first_index_on_ties(dev):
+    D, V = 2048, 51200
+    g = gen(3)
+    x = torch.randn(D, generator=g).to(BF)
+    lw, lb = torch.ones(D, dtype=BF), torch.zeros(D, dtype=BF)
+    W = (torch.randn(V, D, generator=g) * 0.02).to(BF)
+    W[777] = W[40000]  # an exact tie between two rows: the smaller index must win
+    b = torch.zeros(V)
+    b[40000] = b[777] = 5.0
+    h = F.layer_norm(x.float(), (D,), None, None, 1e-5).to(BF)
+    nparts = _lib.load().mx_lm_argmax_nparts(V)
+    part = torch.zeros(nparts, device=dev, dtype=torch.int64)
+    logits = torch.empty(V, device=dev, dtype=BF)
+    xd, lwd, lbd, Wd, bd = x.to(dev), lw.to(dev), lb.to(dev), W.to(dev), b.to(dev)
+    _lib.call("mx_ln_gemv_argmax", _lib.stream(), xd.data_ptr(), lwd.data_ptr(), lbd.data_ptr(),
+              1e-5, Wd.data_ptr(), D, bd.data_ptr(), V, D, logits.data_ptr(), part.data_ptr(), nparts)
+    ref = h.float() @ W.float().t() + b
+    assert rel(logits, ref) < 5e-3
+    state = torch.zeros(2, device=dev, dtype=torch.int32)
+    toks = torch.zeros(4, device=dev, dtype=torch.int32)
+    xe = torch.empty(D, device=dev, dtype=BF)
+    wte = torch.randn(V, D, generator=g).to(BF).to(dev)
+    _lib.call("mx_embed_step", _lib.stream(), part.data_ptr(), nparts, wte.data_ptr(), D, state.data_ptr(), 100,
+              toks.data_ptr(), xe.data_ptr())
+    assert int(toks[0]) == int(torch.argmax(logits.cpu())) == 777
+    assert torch.equal(xe, wte[777]) and state.tolist() == [1, 100]
+
+
+@pytest.mark.parametrize("L", [1, 7, 300, 922])
+def test_decode_attn_vs_fp32(dev, L):
+    H, ctx, pos = 32, 1024, L - 1
+    g = gen(L)
+    kc = torch.randn(1, H, ctx, 64, generator=g).to(BF)
+    vc = torch.randn(1, H, ctx, 64, generator=g).to(BF)
+    qkv = torch.randn(3 * H * 64, generator=g).to(BF)
+    fr = S.freqs_cis(32, 2048)
+    q = ot.rope(qkv[:H * 64].view(1, 1, H, 64).transpose(1, 2), fr[pos:pos + 1, :, 0], fr[pos:pos + 1, :, 1])
+    k = ot.rope(qkv[H * 64:2 * H * 64].view(1, 1, H, 64).transpose(1, 2), fr[pos:pos + 1, :, 0], fr[pos:pos + 1, :, 1])
+    kref, vref = kc.clone(), vc.clone()
+    kref[:, :, pos] = k[:, :, 0]
+    vref[:, :, pos] = qkv[2 * H * 64:].view(H, 64)
+    s = (q.float() @ kref[:, :, :L].float().transpose(-1, -2)) * 0.125
+    ref = (torch.softmax(s, -1) @ vref[:, :, :L].float()).reshape(-1)
+    kd, vd = kc.to(dev), vc.to(dev)
+    state = torch.tensor([0, pos], device=dev, dtype=torch.int32)
+    S_ = 8
+    ws = torch.zeros(H * S_ * 66, device=dev)
+    cnt = torch.zeros(H, device=dev, dtype=torch.int32)
+    out = torch.empty(H * 64, device=dev, dtype=BF)
+    qkvd, frd = qkv.to(dev), fr.to(dev)
+    for _ in range(2):  # counters are re-armed by the kernel
+        _lib.call("mx_decode_attn", _lib.stream(), qkvd.data_ptr(), frd.data_ptr(), kd.data_ptr(),
+                  vd.data_ptr(), H, ctx, state.data_ptr(), S_, 0.125, ws.data_ptr(), cnt.data_ptr(), out.data_ptr())
+        assert rel(out, ref) < 1e-2
+    assert torch.equal(kd[:, :, pos].cpu(), k[:, :, 0]) and torch.equal(vd[:, :, pos].cpu(), vref[:, :, pos])
+    assert torch.count_nonzero(cnt) == 0
+
+
+def _models(layers, seed=0):
+    w = S.text_weights(seed, layers=layers)
+    fr = S.freqs_cis(32, 2048)
+    return w, ot.Text(w, 1024, fr), mt.TextDecoder(w, ctx=1024)
+
+
+def _check_decode(dec, ora, img, prompt, n_tokens, tol=1e-2):
+    """Teacher-forced logits + near-tie-aware token check; returns the HIP path's tokens."""
+    lg0, hp, xp = ora.prefill(img, prompt, return_hidden=True)
+    xg = dec.prefill(img.to(dec.dev), prompt)
+    assert rel(xg, xp[0]) <= tol, rel(xg, xp[0])
+    assert rel(dec.logits, lg0) <= tol
+    dec.start_decode()
+    gl = [dec.logits.cpu().clone()]
+    for _ in range(n_tokens - 1):
+        dec.decode_step(logits=True)
+        gl.append(dec.logits.cpu().clone())
+    toks = dec.tokens[:n_tokens].cpu().tolist()
+    # teacher-forced oracle on the HIP tokens
+    lg = lg0
+    for t in range(n_tokens):
+        assert rel(gl[t], lg) <= tol, (t, rel(gl[t], lg))
+        top2 = lg.float().topk(2).values
+        if (top2[0] - top2[1]).item() >= TIE:
+            assert toks[t] == int(torch.argmax(lg)), t
+        else:
+            assert lg.float()[toks[t]].item() >= top2[0].item() - TIE, t
+        if t + 1 < n_tokens:
+            lg = ora.step(toks[t])
+    return toks
+
+
+def test_decoder_two_layers(dev):
+    w, ora, dec = _models(2)
+    img = S.activations(3, (729, 2048), "img")
+    prompt = S.prompt_ids(4, 64)
+    toks = _check_decode(dec, ora, img, prompt, 24)
+    # the graph-replayed loop gives the same tokens as the eager loop
+    g_toks = dec.generate(img.to(dev), prompt, 24).cpu().tolist()
+    assert g_toks == toks
+
+
+def test_decoder_full_config_greedy_128(dev):
+    """Config 2: 24 layers, prefill 1 + 729 image tokens + 64 prompt ids, greedy 128 tokens (graph replay)."""
+    w, ora, dec = _models(None)
+    img = S.activations(3, (729, 2048), "img")
+    prompt = S.prompt_ids(4, 64)
+    toks = dec.generate(img.to(dev), prompt, 128).cpu().tolist()
+    ref, lgs = ora.generate(img, prompt, 128)
+    # teacher-forced on the graph-replayed tokens: the eager step with logits gives the same tokens
+    w2, ora2, dec2 = w, ot.Text(w, 1024, S.freqs_cis(32, 2048)), dec
+    dec2.graph = None
+    assert _check_decode(dec2, ora2, img, prompt, 128, tol=2e-2) == toks
+    first_tie = next((t for t, lg in enumerate(lgs) if (lambda v: (v[0] - v[1]).item())(lg.float().topk(2).values) < TIE), None)
+    n_same = next((t for t in range(128) if toks[t] != ref[t]), 128)
+    print(f"greedy 128: identical prefix {n_same}, first oracle near-tie at {first_tie}", flush=True)
+    if first_tie is None:
+        assert toks == ref
+    else:
+        assert n_same >= first_tie
