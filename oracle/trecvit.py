@@ -1,0 +1,133 @@
+"""Oracle: the TAPNext TRecViT block, restated on the CPU with torch's bf16 numerics.
+
+The TAPNext model itself (model.py, weights) is external to the reference snapshot; its block is restated from the
+reference's own restatements:
+  * block order                     tapnext/npu/step8.py:470-488 (region-by-region check against the torch block)
+  * RMSNorm  x * rstd * (1 + scale) tapnext/npu/pack8.py:222-229 (rmsnorm_ref), eps 1e-6
+  * LayerNorm (fp32 inside, eps 1e-6) pack8.py:232-238 (layernorm_ref)
+  * GELU tanh (ssm y gate, gated MLP) / erf (ViT MLP)   pack8.py:241-250, r6/capture.py:5-8
+  * conv_1d + gates + RG-LRU + z    pack8.py:253-279 (ssm_ref), r9/cpuemu.py:33-47 (RGLRU.forward); first frame:
+                                    zero conv history and h = gated x (step8.py:232-233, cpuemu.py:41-42)
+  * gated MLP gate/up split         r6/capture.py:66-69 (`gate, up = ffw_up(x).chunk(2)`)
+  * attention: in_proj -> q, k, v heads -> softmax(q k^T / 8) v -> out_proj   r6/capture.py:78-84, pack8.py:10
+  * patch embedding + image_pos_emb, queries appended as rows   step8.py:251-267; preprocess /127.5 - 1 step8.py:379-383
+The query embedding (external embed_queries) is replaced by a linear map of (y, x) / 256: the same stand-in the GPU
+path uses; it is outside the block and not part of the parity claim.
+"""
+import torch
+import torch.nn.functional as F
+
+BF = torch.bfloat16
+
+
+def f(v):
+    """round to bf16 and back to fp32"""
+    return v.to(BF).float()
+
+
+def rmsnorm(x, scale, eps=1e-6):
+    """pack8.py:222-229 in torch: x bf16 [R, D], scale bf16 [D] (sc1 = bf16(scale + 1))."""
+    sc1 = (scale.float() + 1).to(BF).float()
+    xf = x.float()
+    s = f(xf * xf).sum(dim=1, dtype=torch.float32)
+    mean = f(s / x.shape[1])
+    rstd = f(1.0 / torch.sqrt(f(mean + eps)))
+    return f(f(xf * rstd[:, None]) * sc1[None]).to(BF)
+
+
+def layernorm(x, w, b, eps=1e-6):
+    return F.layer_norm(x, (x.shape[-1],), w, b, eps)
+
+
+def ssm(yg, xx, hist, h0, conv_w, conv_b, a_param, wx, bx, wa, ba, first):
+    """pack8.py:253-279 (ssm_ref) for all 12 heads at once. xx / yg bf16 [T, 768]; hist = [x_{t-1}, x_{t-2}, x_{t-3}];
+    h0 fp32 [T, 768]; wx / wa [H, 64 in, 64 out]. Returns (z bf16, h fp32)."""
+    T, C = xx.shape
+    H = wx.shape[0]
+    taps = [hist[2], hist[1], hist[0], xx]  # oldest .. current
+    if first:
+        taps = [torch.zeros_like(xx)] * 3 + [xx]
+    s = sum(f(t.float() * f(conv_w[i].float())[None]) for i, t in enumerate(taps))
+    xc = f(f(s) + f(conv_b.float())[None])
+    xh = xc.double().view(T, H, 64)
+    gx_pre = f(f(torch.einsum("thi,hij->thj", xh, wx.double()).reshape(T, C).float()) + f(bx.float().reshape(-1))[None])
+    ga_pre = f(f(torch.einsum("thi,hij->thj", xh, wa.double()).reshape(T, C).float()) + f(ba.float().reshape(-1))[None])
+    gate_x = f(torch.sigmoid(gx_pre.double()).float())
+    gate_a = f(torch.sigmoid(ga_pre.double()).float())
+    sp = f(torch.log1p(torch.exp(a_param.double())).float())
+    log_a = f(f(-8.0 * gate_a) * sp[None])
+    a = f(torch.exp(log_a.double()).float())
+    gated = f(xc * gate_x)
+    if first:
+        h = gated.clone()
+    else:
+        e2 = f(torch.exp(f(2.0 * log_a).double()).float())
+        mult = f(torch.sqrt(f(1.0 - e2)))
+        nx = f(gated * mult)
+        h = a * h0 + nx
+    z = f(f(h) * yg.float())
+    return z.to(BF), h
+
+
+class Model:
+    def __init__(self, w, H=12):
+        self.w = w
+        self.H = H
+        n = 0
+        while f"blocks.{n}.ssm_block.temporal_pre_norm.scale" in w:
+            n += 1
+        self.n = n
+        self.reset()
+
+    def reset(self):
+        self.hist = [None] * self.n  # [x_{t-1}, x_{t-2}, x_{t-3}] per block
+        self.h = [None] * self.n
+        self.t = 0
+
+    def embed(self, frame_u8, qfeat):
+        w = self.w
+        x = frame_u8.permute(2, 0, 1)[None].float() / 127.5 - 1.0
+        x = F.conv2d(x.to(BF), w["lin_proj.weight"], w["lin_proj.bias"], stride=w["lin_proj.weight"].shape[-1])
+        x = x[0].flatten(1).transpose(0, 1) + w["image_pos_emb"][0]
+        q = F.linear(qfeat.to(BF), w["query_proj.weight"], w["query_proj.bias"])
+        return torch.cat([x, q], dim=0)
+
+    def block(self, i, x):
+        w = self.w
+        rb = f"blocks.{i}.ssm_block.recurrent_block."
+        mb = f"blocks.{i}.ssm_block.mlp_block."
+        vb = f"blocks.{i}.vit_block."
+        sb = f"blocks.{i}.ssm_block."
+        T, C = x.shape
+        first = self.t == 0
+        t0 = rmsnorm(x, w[sb + "temporal_pre_norm.scale"])
+        y, xx = F.linear(t0, w[rb + "linear_yx.weight"], w[rb + "linear_yx.bias"]).chunk(2, dim=-1)
+        yg = F.gelu(y, approximate="tanh")
+        hist = self.hist[i] or [torch.zeros_like(xx)] * 3
+        h0 = self.h[i] if self.h[i] is not None else torch.zeros(T, C)
+        z, h = ssm(yg, xx, hist, h0, w[rb + "conv_1d.w"], w[rb + "conv_1d.b"], w[rb + "rg_lru.a_param"],
+                   w[rb + "rg_lru.input_gate.w"], w[rb + "rg_lru.input_gate.b"], w[rb + "rg_lru.a_gate.w"],
+                   w[rb + "rg_lru.a_gate.b"], first)
+        self.hist[i] = [xx, hist[0], hist[1]]
+        self.h[i] = h
+        res = F.linear(z, w[rb + "linear_out.weight"], w[rb + "linear_out.bias"]) + x
+        l1 = rmsnorm(res, w[sb + "channel_pre_norm.scale"])
+        gate, up = F.linear(l1, w[mb + "ffw_up.weight"], w[mb + "ffw_up.bias"]).chunk(2, dim=-1)
+        x1 = F.linear(F.gelu(gate, approximate="tanh") * up, w[mb + "ffw_down.weight"], w[mb + "ffw_down.bias"]) + res
+        qkv = F.linear(layernorm(x1, w[vb + "ln_1.weight"], w[vb + "ln_1.bias"]), w[vb + "self_attention.in_proj_weight"],
+                       w[vb + "self_attention.in_proj_bias"])
+        q, k, v = qkv.view(T, 3, self.H, C // self.H).permute(1, 2, 0, 3)
+        a = F.scaled_dot_product_attention(q, k, v).transpose(0, 1).reshape(T, C)
+        x2 = x1 + F.linear(a, w[vb + "self_attention.out_proj.weight"], w[vb + "self_attention.out_proj.bias"])
+        m = F.gelu(F.linear(layernorm(x2, w[vb + "ln_2.weight"], w[vb + "ln_2.bias"]), w[vb + "mlp.0.weight"], w[vb + "mlp.0.bias"]))
+        return x2 + F.linear(m, w[vb + "mlp.3.weight"], w[vb + "mlp.3.bias"])
+
+    def step(self, frame_u8, qfeat, return_blocks=False):
+        x = self.embed(frame_u8, qfeat)
+        hs = [x]
+        for i in range(self.n):
+            x = self.block(i, x)
+            hs.append(x)
+        self.t += 1
+        fin = layernorm(x, self.w["encoder_norm.weight"], self.w["encoder_norm.bias"])
+        return (fin, hs) if return_blocks else fin

@@ -17,7 +17,7 @@ F = ctypes.c_float
 
 # name -> argtypes (every entry point returns int status)
 SIGNATURES = {
-    "mx_gemm_bf16": [P, I, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I, I, P, L, P, L],
+    "mx_gemm_bf16": [P, I, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I, I, I, P, L, P, L],
     "mx_gemm_check": [I, I, P, L, P, L, P, P, L, P, L, I, I, I, I, I, P, L, P, L],
     "mx_gemm_pick": [I, I, I],
     "mx_gemm_ws_elems": [I, I, I, I],
@@ -36,6 +36,10 @@ SIGNATURES = {
     "mx_ln_gemv_argmax": [P, P, P, P, F, P, L, P, I, I, P, P, I],
     "mx_embed_step": [P, P, I, P, I, P, I, P, P],
     "mx_decode_attn": [P, P, P, P, P, I, I, P, I, F, P, P, P],
+    "mx_ssm_step": [P, P, P, P, P, L, P, L, P, P, P, P, P, P, P, P, P, P, L, I, I],
+    "mx_ssm_prep": [P, P, L, L, P, P, P, P, P, P, P, P, P, P, I, I, I],
+    "mx_rglru_scan": [P, P, P, P, I, I, I, P, L, L, P, L, L],
+    "mx_counter_add": [P, P, I],
 }
 
 STATUS = {0: "ok", -1: "bad config", -2: "unsupported shape/stride", -3: "split-K workspace too small",

@@ -47,7 +47,7 @@ template <int BM, int BN, int WGM, int WGN, int S>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
     const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
-    uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act,
+    uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols,
     int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt) {
   static_assert(WGM * WGN == 4, "4 waves per workgroup");
   static_assert(S >= 2, "at least a double buffer");
@@ -194,7 +194,15 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
         if (bias) bv = *reinterpret_cast<const f32x4*>(bias + n);
 #pragma unroll
         for (int e = 0; e < 4; e++) v[e] = rbf(acc[i][j][4 * g + e] + bv[e]);
-        if (act == 1) {
+        if (act == 3) {
+          // gated GELU on interleaved (gate, up) column pairs -> output column n / 2 + {0, 1}
+          const uint32_t o = pack2(rbf(gelu_tanh(v[0])) * v[1], rbf(gelu_tanh(v[2])) * v[3]);
+          *reinterpret_cast<uint32_t*>(C + (long)m * ldc + (n >> 1)) = o;
+          continue;
+        }
+        if (act_ncols > 0 && n >= act_ncols) {
+          // no activation on this column range
+        } else if (act == 1) {
 #pragma unroll
           for (int e = 0; e < 4; e++) v[e] = rbf(gelu_tanh(v[e]));
         } else if (act == 2) {
@@ -224,12 +232,12 @@ constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 template <int BM, int BN, int WGM, int WGN, int S>
 hipError_t launch(hipStream_t st, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
                   const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N,
-                  int K, int Kw, int act, float* ws, int* cnt) {
+                  int K, int Kw, int act, int act_ncols, float* ws, int* cnt) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   const int nk = Kw / BK;
   const int kps = (nk + splits - 1) / splits;
   hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn * splits), dim3(256), 0, st, A, lda, W,
-                     ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, tm, tn, splits, kps, ws, cnt);
+                     ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, tm, tn, splits, kps, ws, cnt);
   return hipGetLastError();
 }
 
@@ -286,10 +294,11 @@ extern "C" int mx_gemm_check(int cfg, int splits, const void* A, long lda, const
                              const void* ws, long ws_elems, const void* cnt, long n_cnt) {
   if (!A || !W || !C) return MX_ENULL;
   if (cfg >= kNCfg) return MX_EBADCFG;
-  if (act < 0 || act > 2) return MX_EBADCFG;
+  if (act < 0 || act > 3) return MX_EBADCFG;
   if (M < 1 || N < 1 || K < 8) return MX_ESHAPE;
   if (K % 8 || Kw % BK || Kw < K || lda % 8 || ldw % 8 || lda < K || ldw < Kw) return MX_ESHAPE;
-  if (N % 4 || ldc % 4 || ldc < N) return MX_ESHAPE;
+  if (N % 4 || ldc % 2 || ldc < (act == 3 ? N / 2 : N) || (act != 3 && ldc % 4)) return MX_ESHAPE;
+  if (act == 3 && R) return MX_EBADCFG;
   if (((uintptr_t)A | (uintptr_t)W) & 15) return MX_ELAYOUT;
   if ((uintptr_t)C & 7) return MX_ELAYOUT;
   if (bias && ((uintptr_t)bias & 15)) return MX_ELAYOUT;
@@ -307,10 +316,13 @@ extern "C" int mx_gemm_check(int cfg, int splits, const void* A, long lda, const
 // C = epi(A W^T + bias). cfg < 0: the library's pick (only split-free picks unless a workspace is given).
 // ws / cnt: split-K workspace (fp32 elements) and per-tile counters (must be zero before first use; the kernel
 // leaves them zero). R row for output row m is (r_rows > 0 ? m % r_rows : m).
+// act: 0 none, 1 GELU-tanh, 2 GELU-erf, 3 gated GELU-tanh on interleaved (gate, up) weight-row pairs (output width
+// N / 2: column j = bf16(bf16(gelu(gate_j)) * up_j) with gate_j / up_j = linear rows 2 j / 2 j + 1). act 1-2 apply
+// to output columns < act_ncols only when act_ncols > 0 (e.g. GELU on the y half of a fused [y | x] projection).
 extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda, const uint16_t* W,
                             long ldw, const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C,
-                            long ldc, int M, int N, int K, int Kw, int act, float* ws, long ws_elems, int* cnt,
-                            long n_cnt) {
+                            long ldc, int M, int N, int K, int Kw, int act, int act_ncols, float* ws, long ws_elems,
+                            int* cnt, long n_cnt) {
   if (r_rows < 0) return MX_ESHAPE;
   if (cfg < 0) {
     const int p = mx_gemm_pick(M, N, Kw);
@@ -323,7 +335,7 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
   const int rc = mx_gemm_check(cfg, splits, A, lda, W, ldw, bias, R, ldr, C, ldc, M, N, K, Kw, act, ws, ws_elems, cnt, n_cnt);
   if (rc) return rc;
   hipError_t e;
-#define L_(BM, BN, S) launch<BM, BN, 2, 2, S>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, ws, cnt)
+#define L_(BM, BN, S) launch<BM, BN, 2, 2, S>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt)
   switch (cfg) {
     case 0: e = L_(128, 128, 4); break;
     case 1: e = L_(64, 128, 4); break;

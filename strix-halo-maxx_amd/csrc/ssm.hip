@@ -1,0 +1,263 @@
+// TRecViT recurrent block core on gfx950: temporal depthwise conv (4 taps) + block-diagonal input / decay gates +
+// RG-LRU + the y-gate product, with torch's bf16 op-by-op rounding as restated in tapnext/npu/pack8.py:253-279
+// (ssm_ref) and tapnext/npu/r9/cpuemu.py:33-47 (RGLRU.forward):
+//
+//   xc   = bf(bf(sum_fp32_{i=0..3} bf(x_{t-3+i} * w_i)) + b)           taps oldest .. current, zero before the video
+//   gx   = bf(bf(xc_h Wx_h) + bx), ga = bf(bf(xc_h Wa_h) + ba)          per head h: 64 x 64 blocks (MFMA 32x32x16)
+//   sx   = bf(sigmoid(gx)), sa = bf(sigmoid(ga))
+//   loga = bf(bf(-8 sa) * sp)            sp = bf(softplus(a_param))
+//   a    = bf(exp(loga)), g = bf(xc * sx)
+//   first frame: h = g ;  else: mult = bf(sqrt(bf(1 - bf(exp(bf(2 loga)))))), h = a * h0 + bf(g * mult)   (fp32)
+//   z    = bf(bf(h) * yg)
+//
+// Two forms:
+//   mx_ssm_step  one streamed frame: h (fp32 state) updated in place, z written (the model.step contract)
+//   mx_ssm_prep + mx_rglru_scan  a clip of F frames at once: prep writes the per-frame affine map h -> A h + B
+//                (A = a, B = bf(g * mult); first frame A = 0, B = g) for every (frame, token, channel) in one launch,
+//                then the scan composes the maps along time with a 64-lane wave scan (one lane per frame, shuffle
+//                steps 1, 2, 4, .., 32) and writes z for every frame. Same h as the streamed loop up to fp32
+//                reassociation.
+// Tile: a workgroup owns 64 tokens x one 64-channel head of one frame; the conv output tile is staged in LDS as the
+// MFMA row operand; the gate weights are pre-transposed [head][out][in] so both operands are 16-byte lane reads; the
+// MFMA result layout (lane = output channel, registers = tokens) makes the elementwise tail coalesced along channels.
+#include "common.h"
+
+namespace {
+
+constexpr int XS = 72;  // LDS row stride of the conv tile (64 + 8)
+
+__device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+struct SsmArgs {
+  const uint16_t* tap[4];  // tap i (0 = current frame t, 1 = t-1, 2 = t-2, 3 = t-3) of frame 0 of the launch
+  long ld_x;               // row stride of the tap matrices (elements)
+  long fs_x;               // frame stride of the tap matrices (clip form)
+  const uint16_t* yg; long ld_y; long fs_y;
+  const uint16_t* conv_w;  // [4][C], row 0 = oldest tap (t-3)
+  const uint16_t* conv_b;  // [C]
+  const uint16_t* wxT; const uint16_t* bx;  // [H][64 out][64 in], [C]
+  const uint16_t* waT; const uint16_t* ba;
+  const uint16_t* sp;      // [C] bf16(softplus(a_param))
+  const int* frame;        // global index of frame 0 of this launch (first frame of the video <=> index 0)
+  float* h; long fs_h;     // fp32 state [T][C] (step form) / unused (prep form)
+  uint16_t* z; long ld_z; long fs_z;
+  float* A; float* B; long fs_ab;  // prep form outputs [F][T][C]
+  int T, C, mode;          // mode 0 = step, 1 = prep
+};
+
+__global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[64 * XS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, hk = lane >> 5;
+  const int t0 = blockIdx.x * 64, q = blockIdx.y, f = blockIdx.z;
+  const int c0 = q * 64;
+  const bool first = (*p.frame + f) == 0;
+
+  // ---- temporal conv of this 64 x 64 tile into LDS (8 channels per item, 2 items per thread)
+#pragma unroll
+  for (int it = 0; it < 2; it++) {
+    const int ch = tid + 256 * it;
+    const int tok = ch >> 3, cc = (ch & 7) * 8;
+    const int token = min(t0 + tok, p.T - 1);
+    u32x4 xv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (i == 0 || !first) v = *reinterpret_cast<const u32x4*>(p.tap[i] + f * p.fs_x + (long)token * p.ld_x + c0 + cc);
+      xv[i] = v;
+    }
+    const u32x4 bb = *reinterpret_cast<const u32x4*>(p.conv_b + c0 + cc);
+    u32x4 w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) w[i] = *reinterpret_cast<const u32x4*>(p.conv_w + i * p.C + c0 + cc);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      float r[2];
+#pragma unroll
+      for (int hl = 0; hl < 2; hl++) {
+        auto get = [&](u32x4 v) { return hl ? hi_bf(v[e]) : lo_bf(v[e]); };
+        // w row i = tap (t-3+i): oldest first; xv index 3-i holds frame t-3+i
+        float s = rbf(get(xv[3]) * get(w[0]));
+        s = s + rbf(get(xv[2]) * get(w[1]));
+        s = s + rbf(get(xv[1]) * get(w[2]));
+        s = s + rbf(get(xv[0]) * get(w[3]));
+        r[hl] = rbf(s) + get(bb);
+      }
+      o[e] = pack2(r[0], r[1]);
+    }
+    *reinterpret_cast<u32x4*>(&xs[tok * XS + cc]) = o;
+  }
+  __syncthreads();
+
+  // ---- gates: wave -> 32 tokens (tm) x 32 output channels (tn) of both gates
+  const int tm = wave >> 1, tn = wave & 1;
+  f32x16 gx, ga;
+#pragma unroll
+  for (int e = 0; e < 16; e++) { gx[e] = 0.f; ga[e] = 0.f; }
+  const uint16_t* wxr = p.wxT + ((long)q * 64 + tn * 32 + lr) * 64;
+  const uint16_t* war = p.waT + ((long)q * 64 + tn * 32 + lr) * 64;
+#pragma unroll
+  for (int s = 0; s < 4; s++) {
+    const int k = 16 * s + 8 * hk;
+    const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(&xs[(tm * 32 + lr) * XS + k]));
+    gx = mfma32(a, as_bf16x8(*reinterpret_cast<const u32x4*>(wxr + k)), gx);
+    ga = mfma32(a, as_bf16x8(*reinterpret_cast<const u32x4*>(war + k)), ga);
+  }
+
+  // ---- elementwise RG-LRU: lane = channel, registers = 16 tokens
+  const int cl = tn * 32 + lr, c = c0 + cl;
+  const float spc = bf2f(p.sp[c]), bxc = bf2f(p.bx[c]), bac = bf2f(p.ba[c]);
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int tl = tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
+    const int token = t0 + tl;
+    if (token >= p.T) continue;
+    const float xcv = bf2f(xs[tl * XS + cl]);
+    const float gxp = rbf(rbf(gx[r]) + bxc), gap = rbf(rbf(ga[r]) + bac);
+    const float sx = rbf(sigm(gxp)), sa = rbf(sigm(gap));
+    const float loga = rbf(rbf(-8.0f * sa) * spc);
+    const float av = rbf(expf(loga));
+    const float g = rbf(xcv * sx);
+    float Am, Bm;
+    if (first) {
+      Am = 0.f;
+      Bm = g;
+    } else {
+      const float e2 = rbf(expf(rbf(2.0f * loga)));
+      const float mult = rbf(sqrtf(rbf(1.0f - e2)));
+      Am = av;
+      Bm = rbf(g * mult);
+    }
+    const long idx = (long)token * p.C + c;
+    if (p.mode == 0) {
+      float* hp = p.h + idx;
+      const float h = first ? g : __fadd_rn(__fmul_rn(Am, *hp), Bm);
+      *hp = h;
+      const float yv = bf2f(p.yg[f * p.fs_y + (long)token * p.ld_y + c]);
+      p.z[f * p.fs_z + (long)token * p.ld_z + c] = f2bf(rbf(h) * yv);
+    } else {
+      p.A[f * p.fs_ab + idx] = Am;
+      p.B[f * p.fs_ab + idx] = Bm;
+    }
+  }
+}
+
+// ---- time scan: h_t = A_t h_{t-1} + B_t for every (token, channel), frames on the lanes of a wave
+constexpr int SC = 64;  // channels per workgroup
+
+__global__ __launch_bounds__(256) void rglru_scan_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                         long fs_ab, float* __restrict__ h, int F, int C,
+                                                         const uint16_t* __restrict__ yg, long ld_y, long fs_y,
+                                                         uint16_t* __restrict__ z, long ld_z, long fs_z) {
+  __shared__ float sa[64][SC + 1];
+  __shared__ float sb[64][SC + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c0 = blockIdx.x * SC, token = blockIdx.y;
+  const int T = gridDim.y;
+  (void)T;
+  // carried state for this wave's 16 channels: lane j < 16 of each wave holds channel wave*16 + j
+  float carry = 0.f;
+  if (lane < 16 && c0 + wave * 16 + lane < C) carry = h[(long)token * C + c0 + wave * 16 + lane];
+  for (int f0 = 0; f0 < F; f0 += 64) {
+    const int nf = min(64, F - f0);
+    __syncthreads();
+    // coalesced tile load: rows = frames, 64 channels each
+    for (int i = tid; i < 64 * SC; i += 256) {
+      const int fr = i / SC, cc = i % SC;
+      float av = 1.f, bv = 0.f;  // identity map beyond the clip
+      if (fr < nf && c0 + cc < C) {
+        const long o = (long)(f0 + fr) * fs_ab + (long)token * C + c0 + cc;
+        av = A[o];
+        bv = B[o];
+      }
+      sa[fr][cc] = av;
+      sb[fr][cc] = bv;
+    }
+    __syncthreads();
+    // each wave scans 16 channels, one at a time: lane = frame
+    for (int j = 0; j < 16; j++) {
+      const int cc = wave * 16 + j;
+      float a = sa[lane][cc], b = sb[lane][cc];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float ap = __shfl_up(a, d, 64), bp = __shfl_up(b, d, 64);
+        if (lane >= d) {
+          b = __fadd_rn(__fmul_rn(a, bp), b);
+          a = __fmul_rn(a, ap);
+        }
+      }
+      const float c_in = __shfl(carry, j, 64);
+      const float hv = __fadd_rn(__fmul_rn(a, c_in), b);
+      sb[lane][cc] = hv;
+      const float last = __shfl(hv, nf - 1, 64);
+      if (lane == j) carry = last;
+    }
+    __syncthreads();
+    // z = bf(bf(h) * yg) for the tile, coalesced along channels
+    for (int i = tid; i < 64 * SC; i += 256) {
+      const int fr = i / SC, cc = i % SC;
+      if (fr < nf && c0 + cc < C) {
+        const long f = f0 + fr;
+        const float yv = bf2f(yg[f * fs_y + (long)token * ld_y + c0 + cc]);
+        z[f * fs_z + (long)token * ld_z + c0 + cc] = f2bf(rbf(sb[fr][cc]) * yv);
+      }
+    }
+  }
+  if (lane < 16 && c0 + wave * 16 + lane < C) h[(long)token * C + c0 + wave * 16 + lane] = carry;
+}
+
+int check_common(const SsmArgs& p, int F) {
+  for (int i = 0; i < 4; i++)
+    if (!p.tap[i]) return MX_ENULL;
+  if (!p.conv_w || !p.conv_b || !p.wxT || !p.bx || !p.waT || !p.ba || !p.sp || !p.frame) return MX_ENULL;
+  if (p.T < 1 || F < 1 || p.C % 64 || p.ld_x % 8 || p.C > 65535 * 64) return MX_ESHAPE;
+  for (int i = 0; i < 4; i++)
+    if ((uintptr_t)p.tap[i] & 15) return MX_ELAYOUT;
+  if (((uintptr_t)p.conv_w | (uintptr_t)p.conv_b | (uintptr_t)p.wxT | (uintptr_t)p.waT) & 15) return MX_ELAYOUT;
+  return MX_OK;
+}
+
+}  // namespace
+
+// One streamed frame. taps: current frame x_t and the three previous frames (rows of width >= C, stride ld_x);
+// h [T][C] fp32 updated in place; z [T][ld_z] bf16; yg [T][ld_y] bf16; frame: device int, 0 = first frame.
+extern "C" int mx_ssm_step(hipStream_t st, const uint16_t* x0, const uint16_t* x1, const uint16_t* x2,
+                           const uint16_t* x3, long ld_x, const uint16_t* yg, long ld_y, const uint16_t* conv_w,
+                           const uint16_t* conv_b, const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT,
+                           const uint16_t* ba, const uint16_t* sp, const int* frame, float* h, uint16_t* z, long ld_z,
+                           int T, int C) {
+  SsmArgs p{{x0, x1, x2, x3}, ld_x, 0, yg, ld_y, 0, conv_w, conv_b, wxT, bx, waT, ba, sp, frame, h, 0, z, ld_z, 0,
+            nullptr, nullptr, 0, T, C, 0};
+  int rc = check_common(p, 1);
+  if (rc) return rc;
+  if (!yg || !h || !z) return MX_ENULL;
+  hipLaunchKernelGGL(ssm_kernel, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// Clip form, part 1: F frames at once. x_stack holds F + 3 frames of the conv input (frame stride fs_x; the first 3
+// are the history before the clip, zero at the start of a video); A, B: [F][T][C] fp32 outputs.
+extern "C" int mx_ssm_prep(hipStream_t st, const uint16_t* x_stack, long ld_x, long fs_x, const uint16_t* conv_w,
+                           const uint16_t* conv_b, const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT,
+                           const uint16_t* ba, const uint16_t* sp, const int* frame, float* A, float* B, int F, int T,
+                           int C) {
+  SsmArgs p{{x_stack + 3 * fs_x, x_stack + 2 * fs_x, x_stack + fs_x, x_stack}, ld_x, fs_x, nullptr, 0, 0, conv_w,
+            conv_b, wxT, bx, waT, ba, sp, frame, nullptr, 0, nullptr, 0, 0, A, B, (long)T * C, T, C, 1};
+  int rc = check_common(p, F);
+  if (rc) return rc;
+  if (!A || !B) return MX_ENULL;
+  if (fs_x % 8 || F > 65535) return MX_ESHAPE;
+  hipLaunchKernelGGL(ssm_kernel, dim3((T + 63) / 64, C / 64, F), dim3(256), 0, st, p);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// Clip form, part 2: h (fp32 [T][C], state before the clip, updated to the state after it); z for every frame.
+extern "C" int mx_rglru_scan(hipStream_t st, const float* A, const float* B, float* h, int F, int T, int C,
+                             const uint16_t* yg, long ld_y, long fs_y, uint16_t* z, long ld_z, long fs_z) {
+  if (!A || !B || !h || !yg || !z) return MX_ENULL;
+  if (F < 1 || T < 1 || T > 65535 || C % 64) return MX_ESHAPE;
+  hipLaunchKernelGGL(rglru_scan_kernel, dim3(C / SC, T), dim3(256), 0, st, A, B, (long)T * C, h, F, C, yg, ld_y,
+                     fs_y, z, ld_z, fs_z);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}

@@ -14,7 +14,7 @@ from . import _lib
 from ._lib import call, ptr, stream
 
 BF = torch.bfloat16
-ACT = {None: 0, False: 0, True: 1, "tanh": 1, "erf": 2}
+ACT = {None: 0, False: 0, True: 1, "tanh": 1, "erf": 2, "glu": 3}
 
 
 def _rows(x, K):
@@ -100,10 +100,10 @@ class MxLin:
         self.cfgs = {}  # M -> (cfg, splits); absent: tuned (or library pick) on first use
         self.dev = self.w.device
 
-    def _launch(self, cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws):
+    def _launch(self, cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws, act_cols=0):
         return _lib.load().mx_gemm_bf16(
             stream(), cfg, splits, x2.data_ptr(), x2.stride(0), self.w.data_ptr(), self.w.stride(0), ptr(self.b),
-            ptr(r2), ldr, r_rows, y2.data_ptr(), y2.stride(0), M, self.N, self.K, self.Kw, a,
+            ptr(r2), ldr, r_rows, y2.data_ptr(), y2.stride(0), M, self.N, self.K, self.Kw, a, act_cols,
             ptr(ws.ws), ws.ws.numel(), ptr(ws.cnt), ws.cnt.numel())
 
     def _pick(self, M, x2, y2, a, r2, ldr, r_rows, ws):
@@ -119,8 +119,11 @@ class MxLin:
         _TUNED[key] = c
         return c
 
-    def __call__(self, x, gelu=False, res=None, pre=None, act=None, out=None):
+    def __call__(self, x, gelu=False, res=None, pre=None, act=None, out=None, act_cols=0):
+        """act: None / "tanh" / "erf" / "glu" (gated GELU on interleaved (gate, up) weight rows: output width N / 2);
+        act_cols > 0 limits the activation to output columns < act_cols."""
         a = ACT[act if act is not None else gelu]
+        Nout = self.N // 2 if a == 3 else self.N
         x2 = _rows(x, self.K)
         if x2.shape[1] == self.K0 and self.K != self.K0:
             xp = torch.zeros(x2.shape[0], self.K, device=x2.device, dtype=BF)
@@ -129,10 +132,10 @@ class MxLin:
         if x2.shape[1] != self.K:
             raise ValueError(f"input width {x2.shape[1]} != {self.K}")
         M = x2.shape[0]
-        y = out if out is not None else torch.empty(M, self.N, device=x2.device, dtype=BF)
-        if y.shape[-1] != self.N or y.stride(-1) != 1:
+        y = out if out is not None else torch.empty(M, Nout, device=x2.device, dtype=BF)
+        if y.shape[-1] != Nout or y.stride(-1) != 1:
             raise ValueError("out must be (M, N) with unit column stride")
-        y2 = y.view(-1, self.N) if y.dim() != 2 else y
+        y2 = y.view(-1, Nout) if y.dim() != 2 else y
         r2, r_rows, ldr = None, 0, 0
         if res is not None:
             r2 = res.reshape(-1, self.N)
@@ -147,8 +150,8 @@ class MxLin:
         cfg, splits = self.cfgs.get(M) or self._pick(M, x2, y2, a, r2, ldr, r_rows, ws)
         if splits > 1:
             ws.reserve(*_ws_need(cfg, splits, M, self.N))
-        _lib.check(self._launch(cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws), "mx_gemm_bf16")
-        return y2.view(*x.shape[:-1], self.N) if out is None else y
+        _lib.check(self._launch(cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws, act_cols), "mx_gemm_bf16")
+        return y2.view(*x.shape[:-1], Nout) if out is None else y
 
 
 def tune_gemm(lin, M, x2, y2, a, r2, ldr, r_rows, ws, reps=10):

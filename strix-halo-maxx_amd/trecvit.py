@@ -1,0 +1,210 @@
+"""TAPNext-style TRecViT on the MI355X kernels: per-frame streaming step (the model.step(frame, queries, caches)
+contract, tapnext/npu/davis_cpu.py:78) and a clip-parallel form that runs F frames through each block at once with
+the RG-LRU recurrence as a time scan.
+
+Block (tapnext/npu/step8.py:470-488):
+    t0 = RMSNorm(x); [y | xx] = linear_yx(t0); yg = gelu_tanh(y)
+    xc = conv_1d(xx over frames t-3..t); xl = RG-LRU(xc, h); hh = linear_out(xl * yg); res = hh + x
+    x1 = ffw_down(gelu_tanh(gate) * up) + res, [gate | up] = ffw_up(RMSNorm(res))
+    x2 = x1 + out_proj(MHA(LN(x1)))  (12 heads x 64, scale 1/8, non-causal over all tokens of the frame)
+    x3 = x2 + mlp3(gelu_erf(mlp0(LN(x2))))
+then encoder_norm after the last block.
+
+Kernel mapping (per block, one frame = 1280 tokens):
+    RMSNorm -> GEMM yx (GELU on the y columns only, output straight into this frame's slot of a 4-frame ring: the
+    conv reads its history from the ring, nothing is copied) -> fused conv + gates + RG-LRU + y-gate (mx_ssm_step)
+    -> GEMM out (+x) -> RMSNorm -> GEMM up with the gated-GELU epilogue (weight rows interleaved gate/up at load
+    time) -> GEMM down (+res) -> LN -> GEMM qkv -> fused SDPA -> GEMM out_proj (+x1) -> LN -> GEMM mlp0 (GELU erf)
+    -> GEMM mlp3 (+x2). A frame is one HIP graph per ring phase (4 graphs), with the frame counter in device memory.
+Inputs per frame: patch conv 8x8/8 of the /127.5 - 1 normalised frame (patchify kernel + GEMM, position embedding
+added in the epilogue) and 256 query tokens from a linear embedding of the (y, x) coordinates / 256 (a stand-in:
+the real embed_queries lives in the external model and is not part of the block).
+"""
+import math
+
+import torch
+
+from . import _lib, ops
+from ._lib import call, ptr, stream
+from .synth import TRV
+
+BF = torch.bfloat16
+
+
+def _interleave_rows(w, b):
+    """ffw_up [gate (F) | up (F)] rows -> (gate_0, up_0, gate_1, up_1, ...) for the gated-GELU epilogue."""
+    F = w.shape[0] // 2
+    wi = torch.stack([w[:F], w[F:]], dim=1).reshape(2 * F, -1)
+    bi = torch.stack([b[:F], b[F:]], dim=1).reshape(2 * F)
+    return wi, bi
+
+
+class TRecViT:
+    def __init__(self, weights, n_tokens=None, device="cuda", lin_cls=ops.MxLin):
+        c = TRV
+        self.dev = dev = torch.device(device)
+        self.D, self.H, self.hd = c["dim"], c["heads"], c["hd"]
+        self.P = c["patch"]
+        self.G = c["img"] // self.P
+        self.n_img = self.G * self.G
+        self.n_q = c["n_q"]
+        self.T = self.n_img + self.n_q if n_tokens is None else n_tokens
+        self.rms_eps, self.ln_eps = c["rms_eps"], c["ln_eps"]
+        g = lambda n: weights[n].to(dev, BF).contiguous()
+        lin = lambda n, wn=None, bn=None: lin_cls(weights[wn or n + ".weight"], weights[bn or n + ".bias"], BF)
+        n = 0
+        while f"blocks.{n}.ssm_block.temporal_pre_norm.scale" in weights:
+            n += 1
+        self.blocks = []
+        for i in range(n):
+            rb = f"blocks.{i}.ssm_block.recurrent_block."
+            mb = f"blocks.{i}.ssm_block.mlp_block."
+            vb = f"blocks.{i}.vit_block."
+            sb = f"blocks.{i}.ssm_block."
+            sc1 = lambda k: (weights[k].float() + 1).to(BF).to(dev).contiguous()  # torch: 1 + scale in bf16
+            wu, bu = _interleave_rows(weights[mb + "ffw_up.weight"], weights[mb + "ffw_up.bias"])
+            ap = weights[rb + "rg_lru.a_param"].double()
+            blk = dict(
+                sc0=sc1(sb + "temporal_pre_norm.scale"), sc1=sc1(sb + "channel_pre_norm.scale"),
+                yx=lin(rb + "linear_yx"), out=lin(rb + "linear_out"),
+                up=lin_cls(wu, bu, BF), down=lin(mb + "ffw_down"),
+                ln1=(g(vb + "ln_1.weight"), g(vb + "ln_1.bias")), ln2=(g(vb + "ln_2.weight"), g(vb + "ln_2.bias")),
+                qkv=lin(None, vb + "self_attention.in_proj_weight", vb + "self_attention.in_proj_bias"),
+                oproj=lin(vb + "self_attention.out_proj"), mlp0=lin(vb + "mlp.0"), mlp3=lin(vb + "mlp.3"),
+                conv_w=g(rb + "conv_1d.w"), conv_b=g(rb + "conv_1d.b"),
+                wxT=weights[rb + "rg_lru.input_gate.w"].transpose(-1, -2).to(dev, BF).contiguous(),
+                bx=weights[rb + "rg_lru.input_gate.b"].reshape(-1).to(dev, BF).contiguous(),
+                waT=weights[rb + "rg_lru.a_gate.w"].transpose(-1, -2).to(dev, BF).contiguous(),
+                ba=weights[rb + "rg_lru.a_gate.b"].reshape(-1).to(dev, BF).contiguous(),
+                # pack8.py:141-142 / ssm_ref: sp = bf16(softplus(a_param)), computed in fp64
+                sp=torch.log1p(torch.exp(ap)).to(BF).to(dev).contiguous(),
+            )
+            self.blocks.append(blk)
+        self.enc_norm = (g("encoder_norm.weight"), g("encoder_norm.bias"))
+        self.patch = lin_cls(weights["lin_proj.weight"].reshape(self.D, -1), weights["lin_proj.bias"], BF)
+        self.pos = g("image_pos_emb").view(self.n_img, self.D)
+        self.qproj = lin_cls(weights["query_proj.weight"], weights["query_proj.bias"], BF)
+        # ---- streaming state: per block a 4-frame ring of [yg | xx] rows and the fp32 RG-LRU state
+        T, D = self.T, self.D
+        self.ring = [[torch.zeros(T, 2 * D, device=dev, dtype=BF) for _ in range(4)] for _ in self.blocks]
+        self.h = [torch.zeros(T, D, device=dev, dtype=torch.float32) for _ in self.blocks]
+        self.frame = torch.zeros(1, device=dev, dtype=torch.int32)
+        self.x0 = torch.zeros(T, D, device=dev, dtype=BF)
+        self.img = torch.zeros(c["img"], c["img"], 3, device=dev, dtype=torch.uint8)
+        self.qfeat = torch.zeros(self.n_q, 2, device=dev, dtype=BF)
+        self.t = 0  # host copy of the frame index (selects the ring phase)
+        self.graphs = {}
+        self.out = None
+
+    def reset(self):
+        """A new video: zero every block's conv history and RG-LRU state and mark the next frame first
+        (Step8.reset, tapnext/npu/step8.py:244-249)."""
+        for rs in self.ring:
+            for r in rs:
+                r.zero_()
+        for h in self.h:
+            h.zero_()
+        self.frame.zero_()
+        self.t = 0
+
+    # ------------------------------------------------------------------ per-frame input (X0)
+    def embed(self, img_u8, qfeat, out):
+        a = ops.patchify(img_u8[None], self.P, mode=1, ldo=self.patch.K)
+        self.patch(a, res=self.pos, out=out[:self.n_img])
+        self.qproj(qfeat, out=out[self.n_img:self.n_img + qfeat.shape[0]])
+        return out
+
+    # ------------------------------------------------------------------ one block, one frame
+    def block_step(self, i, x, phase):
+        b = self.blocks[i]
+        T, D = self.T, self.D
+        ring = self.ring[i]
+        cur = ring[phase]
+        t0 = ops.rmsnorm(x, b["sc0"], eps=self.rms_eps)
+        b["yx"](t0, gelu=True, act_cols=D, out=cur)             # [gelu(y) | xx] into this frame's ring slot
+        z = torch.empty(T, D, device=self.dev, dtype=BF)
+        taps = [ring[(phase - k) % 4][:, D:] for k in range(4)]
+        call("mx_ssm_step", stream(), *(t.data_ptr() for t in taps), 2 * D, cur.data_ptr(), 2 * D,
+             b["conv_w"].data_ptr(), b["conv_b"].data_ptr(), b["wxT"].data_ptr(), b["bx"].data_ptr(),
+             b["waT"].data_ptr(), b["ba"].data_ptr(), b["sp"].data_ptr(), self.frame.data_ptr(), self.h[i].data_ptr(),
+             z.data_ptr(), D, T, D)
+        return self._block_tail(b, z, x, 1)
+
+    def _block_tail(self, b, z, x, B):
+        T, D, H = self.T, self.D, self.H
+        res = b["out"](z, res=x)
+        g = b["up"](ops.rmsnorm(res, b["sc1"], eps=self.rms_eps), act="glu")
+        x1 = b["down"](g, res=res)
+        qkv = b["qkv"](ops.layernorm(x1, *b["ln1"], eps=self.ln_eps))
+        q5 = qkv.view(B, T, 3, H, self.hd)
+        q, k, v = (q5[:, :, j].transpose(1, 2) for j in range(3))
+        a = ops.sdpa(q, k, v, scale=1.0 / 8.0)
+        x2 = b["oproj"](a.view(B * T, D), res=x1)
+        return b["mlp3"](b["mlp0"](ops.layernorm(x2, *b["ln2"], eps=self.ln_eps), act="erf"), res=x2)
+
+    def _frame(self, phase):
+        x = self.embed(self.img, self.qfeat, self.x0)
+        for i in range(len(self.blocks)):
+            x = self.block_step(i, x, phase)
+        fin = ops.layernorm(x, *self.enc_norm, eps=self.ln_eps)
+        call("mx_counter_add", stream(), self.frame.data_ptr(), 1)
+        return fin
+
+    def step(self, frame_u8, qfeat, use_graph=False):
+        """One streamed frame: frame_u8 (256, 256, 3) uint8, qfeat (n_q, 2) -> encoder-normed tokens (T, D).
+        The RG-LRU state and conv history advance (model.step)."""
+        self.img.copy_(frame_u8, non_blocking=True)
+        self.qfeat.copy_(qfeat, non_blocking=True)
+        phase = self.t % 4
+        if use_graph:
+            if phase not in self.graphs:
+                self.capture()
+            g, out = self.graphs[phase]
+            g.replay()
+        else:
+            out = self._frame(phase)
+        self.t += 1
+        return out
+
+    def capture(self):
+        """One HIP graph per ring phase (kernel arguments differ only in which ring slots they read/write)."""
+        for phase in range(4):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                out = self._frame(phase)
+            self.graphs[phase] = (g, out)
+
+    # ------------------------------------------------------------------ clip-parallel form
+    def clip_state(self, F):
+        """Buffers for F-frame clips: per block a stack of F + 3 frames of [yg | xx] rows (3 history frames first)."""
+        T, D = self.T, self.D
+        self.F = F
+        self.stack = [torch.zeros(F + 3, T, 2 * D, device=self.dev, dtype=BF) for _ in self.blocks]
+        self.Ab = torch.empty(F, T, D, device=self.dev, dtype=torch.float32)
+        self.Bb = torch.empty(F, T, D, device=self.dev, dtype=torch.float32)
+
+    def forward_clip(self, frames_u8, qfeat):
+        """F frames at once through every block (GEMMs with M = F x T rows, attention batched over frames, the RG-LRU
+        as a time scan). frames_u8 (F, 256, 256, 3); returns (F, T, D). Continues from the stacked history / state."""
+        F, T, D = frames_u8.shape[0], self.T, self.D
+        x = torch.empty(F, T, D, device=self.dev, dtype=BF)
+        for f in range(F):
+            self.embed(frames_u8[f], qfeat, x[f])
+        x = x.view(F * T, D)
+        for i, b in enumerate(self.blocks):
+            st = self.stack[i]
+            t0 = ops.rmsnorm(x, b["sc0"], eps=self.rms_eps)
+            b["yx"](t0, gelu=True, act_cols=D, out=st[3:].view(F * T, 2 * D))
+            xs = st[:, :, D:]
+            call("mx_ssm_prep", stream(), xs.data_ptr(), 2 * D, T * 2 * D, b["conv_w"].data_ptr(), b["conv_b"].data_ptr(),
+                 b["wxT"].data_ptr(), b["bx"].data_ptr(), b["waT"].data_ptr(), b["ba"].data_ptr(), b["sp"].data_ptr(),
+                 self.frame.data_ptr(), self.Ab.data_ptr(), self.Bb.data_ptr(), F, T, D)
+            z = torch.empty(F, T, D, device=self.dev, dtype=BF)
+            call("mx_rglru_scan", stream(), self.Ab.data_ptr(), self.Bb.data_ptr(), self.h[i].data_ptr(), F, T, D,
+                 st[3:].data_ptr(), 2 * D, T * 2 * D, z.data_ptr(), D, T * D)
+            st[:3].copy_(st[F:F + 3])  # the last 3 frames become the next clip's history
+            x = self._block_tail(b, z.view(F * T, D), x, F)
+        fin = ops.layernorm(x, *self.enc_norm, eps=self.ln_eps)
+        call("mx_counter_add", stream(), self.frame.data_ptr(), F)
+        self.t += F
+        return fin.view(F, T, D)
