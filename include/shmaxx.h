@@ -7,7 +7,8 @@
  *    returns 0 or a negative status:
  *      -1 unknown config / head dim / mode   -2 unsupported shape or stride   -3 workspace too small
  *      -4 pointer alignment / layout         -5 HIP launch failed             -6 required pointer is null
- *  - shapes are validated on the host before any launch (the *_check functions run that validation alone).
+ *  - shapes are validated on the host before any launch (the *_check functions run that validation alone);
+ *  - every entry point is HIP-graph capturable (no host reads of device data, no memsets).
  */
 #ifndef SHMAXX_H
 #define SHMAXX_H
@@ -18,50 +19,115 @@
 extern "C" {
 #endif
 
-/* ---------------------------------------------------------------------------------------------- GEMM (MFMA)
- * C[M,N] = epi(A[M,K] . W[N,K]^T + bias[N]); epi: act (0 none, 1 GELU-tanh, 2 GELU-erf) applied to the bf16-rounded
- * linear output, then "+ R" (R row = m % r_rows when r_rows > 0, else m), each step rounded to bf16.
- * Requirements: K % 8 == 0, lda/ldw % 8 == 0, A/W 16-byte aligned, N % 4 == 0, ldc/ldr % 4 == 0, bias 16-byte aligned.
- * cfg < 0 lets the library pick the tile; 0..mx_gemm_ncfg()-1 forces one.
- * Replaces: bf16gemm_launch (moondream/gpu/hip/i8gemm.hip:534-552, bound in hgemm.py:28), whose act flag is the
- * `gelu` argument and whose residual the reference adds outside (md2fast.py:64-67). */
-int mx_gemm_bf16(hipStream_t st, int cfg, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* bias,
-                 const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int K, int act);
-/* Host-only validation of an mx_gemm_bf16 call. Replaces the shape checks at i8gemm.hip:535. */
-int mx_gemm_check(int cfg, const void* A, long lda, const void* W, long ldw, const void* bias, const void* R, long ldr,
-                  const void* C, long ldc, int M, int N, int K, int act);
-/* Tile config the library would pick for (M, N, K). Replaces pick_cfg's FIXED table (hgemm.py:47-51). */
-int mx_gemm_pick(int M, int N, int K);
+/* ============================================================================================ GEMM (MFMA)
+ * C[M,N] = epi(A[M,K] . W[N,K]^T + bias[N]); the k loop runs to Kw (multiple of 64, >= K), W must be zero in
+ * columns [K, Kw). act: 0 none, 1 GELU-tanh, 2 GELU-erf (applied to the bf16-rounded linear output; with
+ * act_ncols > 0 only on output columns < act_ncols), 3 gated GELU-tanh on interleaved (gate, up) weight rows
+ * (output width N / 2). Then "+ R" (R row = m % r_rows when r_rows > 0, else m), each step rounded to bf16.
+ * cfg < 0: the library's tile pick; splits > 1 needs ws (fp32) and cnt (ints, zero before first use, left zero).
+ * Requirements: K % 8 == 0, lda/ldw % 8 == 0, A/W 16-byte aligned, N % 4 == 0, bias 16-byte aligned.
+ * Replaces: bf16gemm_launch (moondream/gpu/hip/i8gemm.hip:534-552, bound in moondream/gpu/hgemm.py:28) with its
+ * `gelu` flag; the residual the reference adds outside the GEMM (md2fast.py:64-67); the gated-MLP epilogue of the
+ * TRecViT ffw_up (tapnext/npu/NOTES.md:36, pack8.py:96-102 interleave_gated). */
+int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                 const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int K,
+                 int Kw, int act, int act_ncols, float* ws, long ws_elems, int* cnt, long n_cnt);
+/* Host-only validation of an mx_gemm_bf16 call. Replaces the shape checks at i8gemm.hip:535, :557-561. */
+int mx_gemm_check(int cfg, int splits, const void* A, long lda, const void* W, long ldw, const void* bias,
+                  const void* R, long ldr, const void* C, long ldc, int M, int N, int K, int Kw, int act,
+                  const void* ws, long ws_elems, const void* cnt, long n_cnt);
+/* Default (cfg * 16 + splits) for (M, N, Kw). Replaces pick_cfg's FIXED table (moondream/gpu/hgemm.py:47-51). */
+int mx_gemm_pick(int M, int N, int Kw);
 /* Number of tile configs / the (BM, BN) tile of one. Replaces bf16gemm_ncfg (i8gemm.hip:553). */
 int mx_gemm_ncfg(void);
 int mx_gemm_cfg_tile(int cfg, int* bm, int* bn);
+/* Split-K workspace a (cfg, splits) call needs: fp32 elements / tile counters. Replaces the fixed-size
+ * workspace() of moondream/gpu/hgemm.py:78-83. */
+long mx_gemm_ws_elems(int cfg, int splits, int M, int N);
+long mx_gemm_ws_counters(int cfg, int splits, int M, int N);
 
-/* ---------------------------------------------------------------------------------------------- attention
+/* ============================================================================================ attention
  * O[b, i, h*D + d] = softmax(scale * Q K^T) V over visible keys; key j visible to query i iff j < Tk and
  * (j < causal_from || j <= qpos0 + i). D in {64, 72}. Q/K/V/O addressed as base + b*s_b + h*s_h + t*s_t + d.
- * Replaces: attn_fwd2 + vtranspose (moondream/gpu/hip/attn.hip:442-451, :275-288; bound in hattn.py:11-14), which
- * are mask-free and batch 1; the masked prompt prefill (md2fast.py:132-136, :185) used torch SDPA there. */
+ * Replaces: attn_fwd2 + vtranspose (moondream/gpu/hip/attn.hip:442-451, :275-288; bound in moondream/gpu/hattn.py:11-14),
+ * which are mask-free and batch 1; the masked prompt prefill (md2fast.py:132-136, :185) and the TRecViT attention
+ * (tapnext/npu/step8.py:484-486) used torch SDPA there. */
 int mx_sdpa(hipStream_t st, const uint16_t* Q, long sq_b, long sq_h, long sq_t, const uint16_t* K, long sk_b,
             long sk_h, long sk_t, const uint16_t* V, long sv_b, long sv_h, long sv_t, uint16_t* O, long so_b, long so_h,
             long so_t, int B, int H, int Tq, int Tk, int D, float scale, int qpos0, int causal_from);
 int mx_sdpa_check(const void* Q, long sq_t, const void* K, long sk_t, const void* V, long sv_t, const void* O,
                   long so_t, int B, int H, int Tq, int Tk, int D);
 
-/* ---------------------------------------------------------------------------------------------- norms
+/* ============================================================================================ norms
  * LayerNorm over rows of D (fp32 statistics, one rounding). Replaces F.layer_norm in _ln (md2fast.py:43-44) and the
- * TRecViT ln_1 / ln_2 / encoder_norm (tapnext/npu/pack8.py:232-238 restates its numerics). */
+ * TRecViT ln_1 / ln_2 / encoder_norm (numerics restated at tapnext/npu/pack8.py:232-238). */
 int mx_layernorm(hipStream_t st, const uint16_t* X, long ldx, const uint16_t* gamma, const uint16_t* beta, uint16_t* Y,
                  long ldy, int rows, int D, float eps);
 /* TRecViT RMSNorm with torch's bf16 rounding; sc1 = bf16(scale + 1). Replaces temporal_pre_norm / channel_pre_norm
- * (tapnext/npu/step8.py:474, :480; numerics pack8.py:222-229). */
+ * (tapnext/npu/step8.py:474, :480; numerics tapnext/npu/pack8.py:222-229). */
 int mx_rmsnorm(hipStream_t st, const uint16_t* X, long ldx, const uint16_t* sc1, uint16_t* Y, long ldy, int rows, int D,
                float eps);
 
-/* ---------------------------------------------------------------------------------------------- input
+/* ============================================================================================ inputs
  * u8 HWC images -> patch rows (c, ky, kx) for the patch-embedding GEMM, zero padded to ldo columns.
- * mode 0: moondream2 normalisation (md2fast.py:148-149); mode 1: TRecViT /127.5 - 1 (step8.py:379-383).
- * Replaces the torch permute/div/sub/reshape sequence at md2fast.py:148-149 and the CPU conv input of step8.py:256. */
+ * mode 0: moondream2 normalisation (md2fast.py:148-149); mode 1: TRecViT /127.5 - 1 (tapnext/npu/step8.py:379-383).
+ * Replaces the torch permute/div/sub/reshape at md2fast.py:148-149 and the CPU conv input of step8.py:256. */
 int mx_patchify_u8(hipStream_t st, const uint8_t* img, uint16_t* out, long ldo, int B, int S, int P, int mode);
+
+/* ============================================================================================ text decoder
+ * Partial rotary (dims 0..31) of q and k from fused qkv rows at positions pos0.., q -> q_out [B][H][n][64], rotated k
+ * and raw v -> caches [slot][H][ctx][64]; cs = (ctx_table, 16, 2) fp32 (cos, sin). bcast: B = 1 rows to every slot.
+ * Replaces rope_cache / _rope_cache (moondream/gpu/fused.py:5-41; reference rotation fused.py:53-58). */
+int mx_rope_kv(hipStream_t st, const uint16_t* qkv, long ldq, const float* cs, uint16_t* q_out, uint16_t* kc,
+               uint16_t* vc, int B, int n, int H, int ctx, int pos0, int nslots, int bcast);
+/* Batch-1 decode: out1[0:n1] = LN(x)W[0:n1]^T + b; out2 = act2(LN(x)W[n1:N]^T + b) (LN skipped when gamma is null).
+ * The M = 1 form of the reference's small-M split-K GEMM (i8gemm_small_launch, i8gemm.hip:555-592) for the fused
+ * [qkv | fc1] projection of one token (md2fast.py:173-198). K in {1024, 2048}. */
+int mx_ln_gemv2(hipStream_t st, const uint16_t* x, const uint16_t* gamma, const uint16_t* beta, float eps,
+                const uint16_t* W, long ldw, const float* bias, int N, int K, int n1, uint16_t* out1, uint16_t* out2,
+                int act2);
+/* out = bf16(bf16(W2 g + b2) + bf16(bf16(Wp a + bp) + xres)): the parallel residual of md2fast.py:198
+ * (mlp(..., res=lin_res(proj, a, x))) for one token, both GEMVs in one pass. */
+int mx_gemv_dual_res(hipStream_t st, const uint16_t* g, const uint16_t* W2, const float* b2, int K2, const uint16_t* a,
+                     const uint16_t* Wp, const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N);
+/* LM head: logits = LN(x) W^T + b (bf16; written when logits != null) and one argmax key per workgroup in part
+ * (first index wins ties). Replaces the lm_head / lm_small call and the argmax of md2fast.py:212, :281. */
+int mx_ln_gemv_argmax(hipStream_t st, const uint16_t* x, const uint16_t* gamma, const uint16_t* beta, float eps,
+                      const uint16_t* W, long ldw, const float* bias, int N, int K, uint16_t* logits,
+                      unsigned long long* part, int nparts);
+int mx_lm_argmax_nparts(int N);
+/* Reduce the argmax keys -> token; tokens[state[0]] = token; state[1] = pos_base + state[0]; state[0]++;
+ * x = wte[token]. Replaces the host-side argmax + F.embedding of a greedy step (md2fast.py:209). */
+int mx_embed_step(hipStream_t st, const unsigned long long* part, int nparts, const uint16_t* wte, int D, int* state,
+                  int pos_base, int* tokens, uint16_t* x);
+/* One decode token: rope of q and k at pos = state[1], K/V append at pos, split-KV (S splits) attention over keys
+ * 0..pos into out (H * 64). ws >= H * S * 66 floats, cnt >= H ints (zero before first use, left zero). Replaces the
+ * SDPA over the KV cache of md2fast.py:185 for one query. */
+int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H, int ctx,
+                   const int* state, int S, float scale, float* ws, int* cnt, uint16_t* out);
+
+/* ============================================================================================ TRecViT recurrence
+ * One streamed frame of conv_1d + block-diagonal gates + RG-LRU + y-gate (numerics of tapnext/npu/pack8.py:253-279
+ * ssm_ref and tapnext/npu/r9/cpuemu.py:33-47 RGLRU.forward): taps x0 (current) .. x3 (t-3), h fp32 updated in place,
+ * z = bf16(bf16(h) * yg). frame: device int, 0 = first frame of the video. Replaces the NPU EW core's ew_ssm
+ * (tapnext/npu/ew8.cc:1351, :1556-1578) and the torch recurrent_block of model.step. */
+int mx_ssm_step(hipStream_t st, const uint16_t* x0, const uint16_t* x1, const uint16_t* x2, const uint16_t* x3,
+                long ld_x, const uint16_t* yg, long ld_y, const uint16_t* conv_w, const uint16_t* conv_b,
+                const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT, const uint16_t* ba, const uint16_t* sp,
+                const int* frame, float* h, uint16_t* z, long ld_z, int T, int C);
+/* Clip form of the same recurrence: per-frame affine maps h -> A h + B for F frames (x_stack = 3 history frames then
+ * the F frames, frame stride fs_x), then the time scan. No reference counterpart (the reference only streams):
+ * a frame-parallel restatement of the same recurrence. */
+int mx_ssm_prep(hipStream_t st, const uint16_t* x_stack, long ld_x, long fs_x, const uint16_t* conv_w,
+                const uint16_t* conv_b, const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT, const uint16_t* ba,
+                const uint16_t* sp, const int* frame, float* A, float* B, int F, int T, int C);
+int mx_rglru_scan(hipStream_t st, const float* A, const float* B, float* h, int F, int T, int C, const uint16_t* yg,
+                  long ld_y, long fs_y, uint16_t* z, long ld_z, long fs_z);
+
+/* ============================================================================================ misc
+ * p[0] += v on the stream: the frame counter a captured frame graph advances (no counterpart in the reference,
+ * whose frame index lives on the host: tapnext/npu/step8.py:232-249 set_first / reset). */
+int mx_counter_add(hipStream_t st, int* p, int v);
 
 #ifdef __cplusplus
 }

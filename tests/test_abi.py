@@ -1,0 +1,117 @@
+"""C ABI checks that run without a GPU: the library loads, exports every entry point include/shmaxx.h declares, and
+its host-side validation rejects the shapes / layouts / configs the kernels do not support (the reference's
+negative status codes, moondream/gpu/hip/i8gemm.hip:481-482, :535, :557-561; attn.hip:435-440). No kernel is
+launched here: every call below is refused before any HIP API call."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from strix_halo_maxx_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "shmaxx.h")
+A16 = 0x10000  # fake 16-byte aligned device addresses: validation never dereferences them
+
+
+def declared():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|long)\s+(mx_\w+)\s*\(", src, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert len(names) >= 20
+    assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for n in declared():
+        assert hasattr(lib, n), n
+    # and the binding declares nothing the header does not
+    assert set(_lib.SIGNATURES) <= set(declared())
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
+    with pytest.raises(_lib.MxError):
+        _lib.load()
+
+
+def gemm_check(**kw):
+    a = dict(cfg=0, splits=1, A=A16, lda=1152, W=A16, ldw=1152, bias=A16, R=None, ldr=0, C=A16, ldc=1152, M=729,
+             N=1152, K=1152, Kw=1152, act=0, ws=None, ws_elems=0, cnt=None, n_cnt=0)
+    a.update(kw)
+    return _lib.load().mx_gemm_check(*a.values())
+
+
+def test_gemm_validation():
+    assert gemm_check() == 0
+    assert gemm_check(K=1150, lda=1150) == -2          # K not a multiple of 8
+    assert gemm_check(Kw=1100) == -2                    # weight row not a multiple of the 64-wide k-step
+    assert gemm_check(N=1150, ldc=1152) == -2           # N not a multiple of 4
+    assert gemm_check(A=A16 + 2) == -4                  # A not 16-byte aligned
+    assert gemm_check(C=A16 + 2) == -4
+    assert gemm_check(act=4) == -1
+    assert gemm_check(cfg=99) == -1
+    assert gemm_check(A=None) == -6
+    assert gemm_check(act=3, R=A16, ldr=1152) == -1     # gated GELU has no residual
+    assert gemm_check(act=3, ldc=576) == 0              # gated GELU writes N / 2 columns
+    assert gemm_check(splits=4) == -6                   # split-K needs a workspace
+    need = _lib.load().mx_gemm_ws_elems(0, 4, 729, 1152)
+    ncnt = _lib.load().mx_gemm_ws_counters(0, 4, 729, 1152)
+    assert need == 6 * 9 * 4 * 128 * 128 and ncnt == 54
+    assert gemm_check(splits=4, ws=A16, ws_elems=need, cnt=A16, n_cnt=ncnt) == 0
+    assert gemm_check(splits=4, ws=A16, ws_elems=need - 1, cnt=A16, n_cnt=ncnt) == -3
+    assert gemm_check(splits=18, ws=A16, ws_elems=10 ** 9, cnt=A16, n_cnt=10 ** 6) == 0
+    assert gemm_check(splits=17, ws=A16, ws_elems=10 ** 9, cnt=A16, n_cnt=10 ** 6) == -3  # an empty split
+
+
+def test_gemm_entry_point_refuses_before_launch():
+    lib = _lib.load()
+    rc = lib.mx_gemm_bf16(None, 0, 1, A16, 1150, A16, 1152, None, None, 0, 0, A16, 1152, 729, 1152, 1150, 1152, 0, 0,
+                          None, 0, None, 0)
+    assert rc == -2
+
+
+def test_gemm_pick_is_a_valid_config():
+    lib = _lib.load()
+    for M, N, K in [(729, 3456, 1152), (729, 1152, 4352), (186624, 4304, 1152), (1, 6144, 2048)]:
+        p = lib.mx_gemm_pick(M, N, K)
+        cfg, sp = p // 16, p % 16
+        assert 0 <= cfg < lib.mx_gemm_ncfg() and sp >= 1
+        bm, bn = ctypes.c_int(), ctypes.c_int()
+        assert lib.mx_gemm_cfg_tile(cfg, ctypes.byref(bm), ctypes.byref(bn)) == 0
+        assert bm.value in (64, 128, 256) and bn.value in (64, 128, 256)
+
+
+def test_sdpa_validation():
+    lib = _lib.load()
+    ok = lambda **kw: lib.mx_sdpa_check(*dict(dict(Q=A16, sq_t=3456, K=A16, sk_t=3456, V=A16, sv_t=3456, O=A16,
+                                                   so_t=1152, B=1, H=16, Tq=729, Tk=729, D=72), **kw).values())
+    assert ok() == 0
+    assert ok(D=80) == -1          # head dims 64 and 72 only (the reference's DP table, hattn.py:21)
+    assert ok(sq_t=3455) == -2
+    assert ok(K=A16 + 8) == -4
+    assert ok(Tk=0) == -2
+    rc = lib.mx_sdpa(None, A16, 0, 72, 3456, A16, 0, 72, 3456, A16, 0, 72, 3456, A16, 0, 72, 1152, 1, 16, 729, 729, 80,
+                     0.1, 0, 729)
+    assert rc == -1
+
+
+def test_other_entry_points_refuse_bad_shapes():
+    lib = _lib.load()
+    assert lib.mx_layernorm(None, A16, 1152, A16, A16, A16, 1152, 729, 1150, 1e-5) == -2
+    assert lib.mx_rmsnorm(None, A16 + 4, 768, A16, A16, 768, 10, 768, 1e-6) == -4
+    assert lib.mx_patchify_u8(None, A16, A16, 500, 1, 378, 14, 0) == -2          # ldo < 588
+    assert lib.mx_rope_kv(None, A16, 6144, A16, A16, A16, A16, 1, 100, 32, 1024, 1000, 1, 0) == -2  # pos past ctx
+    assert lib.mx_ln_gemv2(None, A16, A16, A16, 1e-5, A16, 2048, A16, 100, 3000, 50, A16, A16, 1) == -2  # K
+    assert lib.mx_ln_gemv_argmax(None, A16, A16, A16, 1e-5, A16, 2048, A16, 51200, 2048, None, A16, 10) == -3
+    assert lib.mx_decode_attn(None, A16, A16, A16, A16, 32, 100000, A16, 8, 0.125, A16, A16, A16) == -2
+    assert lib.mx_ssm_step(None, A16, A16, A16, A16, 1536, A16, 1536, A16, A16, A16, A16, A16, A16, A16, A16, A16,
+                           A16, 768, 1280, 700) == -2                                 # C not a multiple of 64
+    assert lib.mx_rglru_scan(None, A16, A16, A16, 4, 1280, 700, A16, 1536, 0, A16, 768, 0) == -2
+    assert lib.mx_counter_add(None, None, 1) == -6

@@ -1,0 +1,408 @@
+"""Pins of the oracle (CPU, no GPU needed). The reference ships no golden vectors for this path (its regression files
+davis_reg.npy / regress_*.npz / ref/baseline.json are referenced but absent), so each oracle function is checked
+against what the mathematics fixes: closed forms, fp64 brute force on small inputs, invariants and special cases.
+Each check is chosen so that a plausible restatement mistake (wrong eps, swapped GELU form, swapped rope halves,
+missing residual, wrong scan operator order, wrong tap order) fails it."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle.md2_text as ot
+import oracle.md2_vision as ov
+import oracle.trecvit as otr
+import strix_halo_maxx_amd.synth as S
+
+BF = torch.bfloat16
+
+
+def bfr(x):
+    return torch.as_tensor(x).to(BF).double()
+
+
+def gen(s):
+    return torch.Generator().manual_seed(s)
+
+
+# ---------------------------------------------------------------------------------------------- shared ops
+def test_layernorm_matches_closed_form_and_eps():
+    """F.layer_norm on bf16 (md2fast.py:43-44, eps 1e-5) == bf16((x - mean) / sqrt(var + eps) * g + b) in fp64;
+    small-variance rows make the eps term visible (eps 1e-6 would fail)."""
+    x = (torch.randn(64, 1152, generator=gen(1)) * 3e-3).to(BF)
+    g = (1 + 0.1 * torch.randn(1152, generator=gen(2))).to(BF)
+    b = (0.1 * torch.randn(1152, generator=gen(3))).to(BF)
+    xd = x.double()
+    y = ((xd - xd.mean(1, keepdim=True)) / torch.sqrt(xd.var(1, unbiased=False, keepdim=True) + 1e-5)) * g.double() + b.double()
+    out = ov.ln(x, g, b).double()
+    assert (out - bfr(y)).abs().max() <= 2 ** -7 * y.abs().max()
+    wrong = ((xd - xd.mean(1, keepdim=True)) / torch.sqrt(xd.var(1, unbiased=False, keepdim=True) + 1e-6)) * g.double() + b.double()
+    assert (out - bfr(wrong)).abs().max() > 0.05
+
+
+def test_gelu_tanh_closed_form():
+    """gelu = 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))) (tgemm.py:21-25, i8gemm.hip:11), not the erf form."""
+    x = torch.linspace(-6, 6, 4001).to(BF)
+    xd = x.double()
+    ref = 0.5 * xd * (1 + torch.tanh(0.7978845608028654 * (xd + 0.044715 * xd ** 3)))
+    assert (ov.gelu(x).double() - bfr(ref)).abs().max() <= 2 ** -8 * 4
+    erf = 0.5 * xd * (1 + torch.erf(xd / math.sqrt(2)))
+    assert (ov.gelu(x).double() - bfr(erf)).abs().max() > 1e-3  # the two forms are distinguishable here
+
+
+def test_sdpa_default_scale_and_softmax_brute_force():
+    """The oracle's SDPA (default scale D^-0.5, md2fast.py:155; hattn.py:24) vs an fp64 loop over keys."""
+    H, T, D = 2, 9, 72
+    q, k, v = (torch.randn(1, H, T, D, generator=gen(i)).to(BF) for i in range(3))
+    out = F.scaled_dot_product_attention(q, k, v).double()
+    ref = torch.zeros(1, H, T, D, dtype=torch.float64)
+    for h in range(H):
+        for i in range(T):
+            s = [sum(q[0, h, i, d].item() * k[0, h, j, d].item() for d in range(D)) / math.sqrt(D) for j in range(T)]
+            m = max(s)
+            p = [math.exp(x - m) for x in s]
+            z = sum(p)
+            for j in range(T):
+                ref[0, h, i] += p[j] / z * v[0, h, j].double()
+    assert (out - ref).abs().max() < 2e-2
+    wrong = F.scaled_dot_product_attention(q, k, v, scale=0.125).double()  # a 1/8 scale (TRecViT's) would show
+    assert (wrong - ref).abs().max() > 2e-2
+
+
+# ---------------------------------------------------------------------------------------------- vision
+def test_patchify_order_and_normalisation():
+    """(u8 / 255 - 0.5) / 0.5 in bf16 steps, patch rows in (c, ky, kx) order (md2fast.py:148-149)."""
+    img = torch.randint(0, 256, (1, 378, 378, 3), generator=gen(4), dtype=torch.uint8)
+    p = ov.normalize_patchify(img)
+    for (gy, gx, c, ky, kx) in [(0, 0, 0, 0, 0), (3, 20, 2, 13, 5), (26, 26, 1, 7, 13), (5, 9, 0, 13, 0)]:
+        u = img[0, gy * 14 + ky, gx * 14 + kx, c].item()
+        a = torch.tensor(float(u)).to(BF).div(255.0).to(BF)
+        expect = ((a.float() - 0.5).to(BF).float() / 0.5).to(BF)
+        assert p[0, gy * 27 + gx, c * 196 + ky * 14 + kx] == expect
+
+
+def _tiny_vision(D=32, Fh=48, H=4):
+    w = {}
+    g = gen(5)
+    for name, shape in (("attn.qkv", (3 * D, D)), ("attn.proj", (D, D)), ("mlp.fc1", (Fh, D)), ("mlp.fc2", (D, Fh))):
+        w["blocks.0." + name + ".weight"] = (torch.randn(*shape, generator=g) * 0.2).to(BF)
+        w["blocks.0." + name + ".bias"] = (torch.randn(shape[0], generator=g) * 0.2).to(BF)
+    for n in ("ln1", "ln2"):
+        w[f"blocks.0.{n}.weight"] = (1 + 0.1 * torch.randn(D, generator=g)).to(BF)
+        w[f"blocks.0.{n}.bias"] = (0.1 * torch.randn(D, generator=g)).to(BF)
+    return w
+
+
+def test_vision_block_structure_vs_fp64():
+    """pre-LN block: x + proj(attn(LN1 x)), then + fc2(gelu(fc1(LN2 .))) (md2fast.py:153-157), fp64 restatement."""
+    D, H = 32, 4
+    w = _tiny_vision(D, 48, H)
+    x = torch.randn(2, 11, D, generator=gen(6)).to(BF)
+    out = ov.block(w, 0, x, H=H).double()
+    wd = {k: v.double() for k, v in w.items()}
+    p = "blocks.0."
+    xd = x.double()
+    lnd = lambda t, n: F.layer_norm(t, (D,), wd[p + n + ".weight"], wd[p + n + ".bias"], 1e-5)
+    qkv = F.linear(lnd(xd, "ln1"), wd[p + "attn.qkv.weight"], wd[p + "attn.qkv.bias"])
+    q, k, v = [t.view(2, 11, H, -1).transpose(1, 2) for t in qkv.chunk(3, -1)]
+    a = torch.softmax(q @ k.transpose(-1, -2) / math.sqrt(D // H), -1) @ v
+    x1 = xd + F.linear(a.transpose(1, 2).reshape(2, 11, D), wd[p + "attn.proj.weight"], wd[p + "attn.proj.bias"])
+    hdn = F.linear(lnd(x1, "ln2"), wd[p + "mlp.fc1.weight"], wd[p + "mlp.fc1.bias"])
+    hdn = 0.5 * hdn * (1 + torch.tanh(0.7978845608028654 * (hdn + 0.044715 * hdn ** 3)))
+    ref = x1 + F.linear(hdn, wd[p + "mlp.fc2.weight"], wd[p + "mlp.fc2.bias"])
+    assert ((out - ref).norm() / ref.norm()) < 1e-2
+    no_res = ref - x1  # a block missing its second residual is far off
+    assert ((out - no_res).norm() / ref.norm()) > 0.3
+
+
+# ---------------------------------------------------------------------------------------------- text
+def test_rope_against_explicit_rotation():
+    """rope (md2fast.py:162-167 / fused.py:53-58): a = x[0:16], b = x[16:32] (halves), output pairs interleaved
+    (a c - b s, a s + b c), dims 32..63 passed through."""
+    x = torch.randn(1, 2, 5, 64, generator=gen(7)).to(BF)
+    fr = S.freqs_cis(32, 64)
+    pos = torch.arange(10, 15)
+    out = ot.rope(x, fr[pos, :, 0], fr[pos, :, 1])
+    for h in range(2):
+        for t in range(5):
+            for j in range(16):
+                c, s = fr[pos[t], j, 0].item(), fr[pos[t], j, 1].item()
+                a, b = x[0, h, t, j].item(), x[0, h, t, 16 + j].item()
+                assert out[0, h, t, 2 * j].item() == pytest.approx(torch.tensor(a * c - b * s).to(BF).item(), abs=2e-2)
+                assert out[0, h, t, 2 * j + 1].item() == pytest.approx(torch.tensor(a * s + b * c).to(BF).item(), abs=2e-2)
+            assert torch.equal(out[0, h, t, 32:], x[0, h, t, 32:])
+
+
+def test_freqs_cis_closed_form():
+    fr = S.freqs_cis(32, 2048, 10000.0)
+    for p, i in [(0, 0), (1, 0), (730, 3), (2047, 15)]:
+        ang = p * 10000.0 ** (-2 * i / 32)
+        assert fr[p, i, 0].item() == pytest.approx(math.cos(ang), abs=2e-4)
+        assert fr[p, i, 1].item() == pytest.approx(math.sin(ang), abs=2e-4)
+
+
+def _tiny_text(D=64, Fh=96, V=97, L=2):
+    g = gen(8)
+    w = {"wte": (torch.randn(V, D, generator=g) * 0.5).to(BF)}
+    for i in range(L):
+        p = f"blocks.{i}."
+        w[p + "ln.weight"] = (1 + 0.1 * torch.randn(D, generator=g)).to(BF)
+        w[p + "ln.bias"] = (0.1 * torch.randn(D, generator=g)).to(BF)
+        for name, shape in (("attn.qkv", (3 * D, D)), ("attn.proj", (D, D)), ("mlp.fc1", (Fh, D)), ("mlp.fc2", (D, Fh))):
+            w[p + name + ".weight"] = (torch.randn(*shape, generator=g) * 0.15).to(BF)
+            w[p + name + ".bias"] = (torch.randn(shape[0], generator=g) * 0.1).to(BF)
+    w["post_ln.weight"], w["post_ln.bias"] = torch.ones(D, dtype=BF), torch.zeros(D, dtype=BF)
+    w["lm_head.weight"] = (torch.randn(V, D, generator=g) * 0.3).to(BF)
+    w["lm_head.bias"] = torch.zeros(V, dtype=BF)
+    return w
+
+
+def _fp64_text_prefill(w, img, prompt, H, fr, bos):
+    """fp64 restatement: prefix non-causal, prompt sees prefix + causal prompt, parallel residual."""
+    wd = {k: v.double() for k, v in w.items()}
+    D = wd["wte"].shape[1]
+    hd = D // H
+    x = torch.cat([wd["wte"][bos:bos + 1], img.double(), wd["wte"][prompt]], 0)
+    n = x.shape[0]
+    P = 1 + img.shape[0]
+    mask = torch.zeros(n, n, dtype=torch.bool)
+    mask[:, :P] = True
+    for i in range(P, n):
+        mask[i, P:i + 1] = True
+    mask[:P, P:] = False
+    cos, sin = fr[:n, :, 0].double(), fr[:n, :, 1].double()
+
+    def rope(t):  # (H, n, hd)
+        a, b = t[..., :16], t[..., 16:32]
+        o = torch.stack((a * cos - b * sin, a * sin + b * cos), -1).flatten(-2)
+        return torch.cat([o, t[..., 32:]], -1)
+    i = 0
+    while f"blocks.{i}.ln.weight" in wd:
+        p = f"blocks.{i}."
+        h = F.layer_norm(x, (D,), wd[p + "ln.weight"], wd[p + "ln.bias"], 1e-5)
+        q, k, v = F.linear(h, wd[p + "attn.qkv.weight"], wd[p + "attn.qkv.bias"]).split(D, -1)
+        q, k, v = (t.view(n, H, hd).transpose(0, 1) for t in (q, k, v))
+        q, k = rope(q), rope(k)
+        s = (q @ k.transpose(-1, -2)) / math.sqrt(hd)
+        a = torch.softmax(s.masked_fill(~mask, float("-inf")), -1) @ v
+        a = a.transpose(0, 1).reshape(n, D)
+        f1 = F.linear(h, wd[p + "mlp.fc1.weight"], wd[p + "mlp.fc1.bias"])
+        f1 = 0.5 * f1 * (1 + torch.tanh(0.7978845608028654 * (f1 + 0.044715 * f1 ** 3)))
+        x = F.linear(f1, wd[p + "mlp.fc2.weight"], wd[p + "mlp.fc2.bias"]) + F.linear(a, wd[p + "attn.proj.weight"], wd[p + "attn.proj.bias"]) + x
+        i += 1
+    h = F.layer_norm(x[-1], (D,), wd["post_ln.weight"], wd["post_ln.bias"], 1e-5)
+    return F.linear(h, wd["lm_head.weight"], wd["lm_head.bias"])
+
+
+def test_text_prefill_vs_fp64():
+    """Prefix prefill (mask-free) + prompt prefill (prefix + causal mask, md2fast.py:132-136) + parallel residual +
+    post-LN + lm head, against an fp64 restatement that builds the whole mask explicitly."""
+    D, H, V = 64, 2, 97
+    w = _tiny_text(D, 96, V)
+    fr = S.freqs_cis(32, 256)
+    img = (torch.randn(13, D, generator=gen(9)) * 0.5).to(BF)
+    prompt = torch.randint(0, V, (6,), generator=gen(10))
+    m = ot.Text(w, 64, fr, bos=3, H=H)
+    lg = m.prefill(img, prompt).double()
+    ref = _fp64_text_prefill(w, img, prompt, H, fr, 3)
+    assert ((lg - ref).norm() / ref.norm()) < 2e-2
+
+
+def test_text_decode_step_equals_longer_prefill():
+    """A greedy step at position p over the KV cache == the fp64 prefill of the prompt extended by that token
+    (decode attends to every cached key; no mask needed for the last query)."""
+    D, H, V = 64, 2, 97
+    w = _tiny_text(D, 96, V)
+    fr = S.freqs_cis(32, 256)
+    img = (torch.randn(13, D, generator=gen(11)) * 0.5).to(BF)
+    prompt = torch.randint(0, V, (6,), generator=gen(12))
+    m = ot.Text(w, 64, fr, bos=3, H=H)
+    toks, lgs = m.generate(img, prompt, 3)
+    ref = _fp64_text_prefill(w, img, torch.cat([prompt, torch.tensor(toks[:2])]), H, fr, 3)
+    assert ((lgs[2].double() - ref).norm() / ref.norm()) < 2e-2
+    assert toks[0] == int(torch.argmax(lgs[0]))
+
+
+def test_argmax_first_index_on_ties():
+    """torch.argmax (the greedy rule) returns the first index among equal maxima; the GPU argmax key does too."""
+    v = torch.tensor([0.5, 2.0, -1.0, 2.0, 2.0]).to(BF)
+    assert int(torch.argmax(v)) == 1
+
+
+# ---------------------------------------------------------------------------------------------- TRecViT
+def test_rmsnorm_rounding_chain():
+    """pack8.py:222-229: s = sum_fp32 bf(x^2), ms = bf(s / D), rstd = bf(1 / sqrt(bf(ms + 1e-6))),
+    y = bf(bf(x rstd) * bf(scale + 1)) -- restated in numpy fp32 step by step."""
+    x = torch.randn(16, 768, generator=gen(13)).to(BF)
+    sc = (0.1 * torch.randn(768, generator=gen(14))).to(BF)
+    out = otr.rmsnorm(x, sc).float().numpy()
+    f = lambda a: torch.from_numpy(np.asarray(a, np.float32)).to(BF).float().numpy()
+    xf = x.float().numpy()
+    s = f(xf * xf).sum(axis=1, dtype=np.float32)
+    ms = f(s / np.float32(768))
+    rstd = f(np.float32(1) / np.sqrt(f(ms + np.float32(1e-6))))
+    sc1 = f(sc.float().numpy() + 1)
+    ref = f(f(xf * rstd[:, None]) * sc1[None])
+    assert np.abs(out - ref).max() <= 2 ** -7 * np.abs(ref).max()
+    # and the plain math (no intermediate roundings) agrees to bf16 precision
+    plain = xf / np.sqrt((xf.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * (sc.double().numpy() + 1)
+    assert np.abs(out - plain).max() < 0.05
+
+
+def _ssm_case(T=64, C=128, H=2, seed=15):
+    g = gen(seed)
+    n = lambda *s, std=1.0: torch.randn(*s, generator=g) * std
+    return dict(yg=n(T, C).to(BF), xx=n(T, C).to(BF), hist=[n(T, C).to(BF) for _ in range(3)], h0=n(T, C),
+                conv_w=n(4, C, std=0.3).to(BF), conv_b=n(C, std=0.1).to(BF),
+                a_param=(torch.rand(C, generator=g) * 3.5 - 3.0).to(BF),
+                wx=n(H, 64, 64, std=0.15).to(BF), bx=n(H, 64, std=0.3).to(BF),
+                wa=n(H, 64, 64, std=0.15).to(BF), ba=n(H, 64, std=0.3).to(BF))
+
+
+def _run_ssm(d, first, **over):
+    a = dict(d, **over)
+    return otr.ssm(a["yg"], a["xx"], a["hist"], a["h0"], a["conv_w"], a["conv_b"], a["a_param"], a["wx"], a["bx"],
+                   a["wa"], a["ba"], first)
+
+
+def test_ssm_first_frame_is_gated_input():
+    """First frame (cpuemu.py:41-42): zero conv history and h = gated_x = bf(xc * sigmoid(gx)), computed here
+    independently (conv = current tap * w_3 + b only)."""
+    d = _ssm_case()
+    z, h = _run_ssm(d, True)
+    xc = bfr(bfr(bfr(d["xx"].double() * bfr(d["conv_w"][3].double()))) + bfr(d["conv_b"].double()))
+    gx = bfr(bfr(torch.einsum("thi,hij->thj", xc.view(64, 2, 64), d["wx"].double()).reshape(64, 128)) + bfr(d["bx"].double().reshape(-1)))
+    gated = bfr(xc * bfr(torch.sigmoid(gx)))
+    assert (h.double() - gated).abs().max() <= 2 ** -8 * gated.abs().max()
+    assert torch.equal(z, (h.to(BF).float() * d["yg"].float()).to(BF))
+
+
+def test_ssm_tap_order():
+    """conv_w row 0 multiplies the OLDEST frame (t-3), row 3 the current one (ew8.cc:1194-1200 / pack8.py:258)."""
+    d = _ssm_case()
+    w = torch.zeros_like(d["conv_w"])
+    w[0] = 1.0  # only the oldest tap
+    _, h_old = _run_ssm(d, False, conv_w=w, conv_b=torch.zeros_like(d["conv_b"]))
+    hist = [torch.zeros_like(t) for t in d["hist"]]
+    hist[2] = d["hist"][2]  # keep only x_{t-3}
+    _, h_same = _run_ssm(d, False, conv_w=w, conv_b=torch.zeros_like(d["conv_b"]), hist=hist)
+    assert torch.equal(h_old, h_same)
+    hist2 = [torch.zeros_like(t) for t in d["hist"]]
+    hist2[0] = d["hist"][2]  # the same data as x_{t-1} must give something else
+    _, h_diff = _run_ssm(d, False, conv_w=w, conv_b=torch.zeros_like(d["conv_b"]), hist=hist2)
+    assert not torch.equal(h_old, h_diff)
+
+
+def test_ssm_decay_to_one_keeps_state():
+    """a_param -> -inf: softplus -> 0, a -> 1, sqrt(1 - a^2) -> 0: the state is carried unchanged."""
+    d = _ssm_case()
+    _, h = _run_ssm(d, False, a_param=torch.full_like(d["a_param"], -60.0))
+    assert torch.equal(h, d["h0"])
+
+
+def test_rglru_fixed_point():
+    """Constant input over many frames: h converges to the fixed point h* = mult g / (1 - a) (a < 1), i.e.
+    B / (1 - A) of the per-frame affine map h -> A h + B."""
+    d = _ssm_case(T=8, C=64, H=1)
+    d["a_param"] = torch.full_like(d["a_param"], 0.0)
+    d["hist"] = [d["xx"]] * 3  # a constant input sequence
+    h = d["h0"]
+    for _ in range(400):
+        _, h = _run_ssm(d, False, h0=h)
+    _, h1 = _run_ssm(d, False, h0=torch.zeros_like(h))            # B = h(0)
+    _, h2 = _run_ssm(d, False, h0=torch.ones_like(h))             # A + B = h(1)
+    A, B = (h2 - h1).double(), h1.double()
+    assert (A < 1).all() and (A > 0).all()
+    assert (h.double() - B / (1 - A)).abs().max() < 1e-4
+
+
+def scan_fp64(A, B, h0):
+    """The time scan the GPU kernel runs: inclusive prefix over frames of (a, b) o (a', b') = (a' a, a' b + b')."""
+    a, b = A.clone(), B.clone()
+    Fr = A.shape[0]
+    d = 1
+    while d < Fr:
+        a_new, b_new = a.clone(), b.clone()
+        a_new[d:] = a[d:] * a[:-d]
+        b_new[d:] = a[d:] * b[:-d] + b[d:]
+        a, b = a_new, b_new
+        d *= 2
+    return a * h0[None] + b
+
+
+def test_associative_scan_equals_sequential_fp64():
+    g = gen(16)
+    Fr, C = 37, 50
+    A = torch.rand(Fr, C, generator=g, dtype=torch.float64)
+    B = torch.randn(Fr, C, generator=g, dtype=torch.float64)
+    h0 = torch.randn(C, generator=g, dtype=torch.float64)
+    seq = []
+    h = h0
+    for t in range(Fr):
+        h = A[t] * h + B[t]
+        seq.append(h)
+    assert torch.allclose(scan_fp64(A, B, h0), torch.stack(seq), rtol=1e-12, atol=1e-12)
+    # the other composition order is a different (wrong) recurrence
+    a, b = A.clone(), B.clone()
+    d = 1
+    while d < Fr:
+        a_new, b_new = a.clone(), b.clone()
+        b_new[d:] = a[:-d] * b[d:] + b[:-d]
+        a_new[d:] = a[d:] * a[:-d]
+        a, b = a_new, b_new
+        d *= 2
+    assert not torch.allclose(a * h0[None] + b, torch.stack(seq), rtol=1e-6)
+
+
+def test_trecvit_block_first_frame_vs_fp64():
+    """One TRecViT block, first frame, tiny width (2 heads): the oracle's bf16 chain vs an fp64 restatement of
+    step8.py:470-488 (RMSNorm (1 + scale), [y | x] split, tanh GELU gate, RG-LRU first frame h = x sigmoid(gx),
+    gated MLP gate/up, LN eps 1e-6, attention scale 1/8, erf GELU ViT MLP, residuals)."""
+    D, H, Fh = 128, 2, 96
+    g = gen(17)
+    n = lambda *s, std=0.1: (torch.randn(*s, generator=g) * std).to(BF)
+    rb, mb, vb, sb = "blocks.0.ssm_block.recurrent_block.", "blocks.0.ssm_block.mlp_block.", "blocks.0.vit_block.", "blocks.0.ssm_block."
+    w = {sb + "temporal_pre_norm.scale": n(D), sb + "channel_pre_norm.scale": n(D)}
+    for name, shape in ((rb + "linear_yx", (2 * D, D)), (rb + "linear_out", (D, D)), (mb + "ffw_up", (2 * Fh, D)),
+                        (mb + "ffw_down", (D, Fh)), (vb + "self_attention.out_proj", (D, D)), (vb + "mlp.0", (Fh, D)),
+                        (vb + "mlp.3", (D, Fh))):
+        w[name + ".weight"], w[name + ".bias"] = n(*shape), n(shape[0])
+    w[vb + "self_attention.in_proj_weight"], w[vb + "self_attention.in_proj_bias"] = n(3 * D, D), n(3 * D)
+    w[rb + "conv_1d.w"], w[rb + "conv_1d.b"] = n(4, D, std=0.3), n(D)
+    w[rb + "rg_lru.a_param"] = n(D, std=1.0)
+    for gname in ("input_gate", "a_gate"):
+        w[rb + f"rg_lru.{gname}.w"], w[rb + f"rg_lru.{gname}.b"] = n(H, 64, 64, std=0.15), n(H, 64, std=0.3)
+    for ln in ("ln_1", "ln_2"):
+        w[vb + ln + ".weight"], w[vb + ln + ".bias"] = (1 + n(D)).to(BF), n(D)
+    x = torch.randn(40, D, generator=g).to(BF)
+    m = otr.Model(w, H=H)
+    out = m.block(0, x).double()
+    wd = {k: v.double() for k, v in w.items()}
+    xd = x.double()
+    rms = lambda t, s: t / torch.sqrt((t ** 2).mean(1, keepdim=True) + 1e-6) * (1 + s)
+    gt = lambda t: 0.5 * t * (1 + torch.tanh(0.7978845608028654 * (t + 0.044715 * t ** 3)))
+    y, xx = F.linear(rms(xd, wd[sb + "temporal_pre_norm.scale"]), wd[rb + "linear_yx.weight"], wd[rb + "linear_yx.bias"]).chunk(2, -1)
+    xc = xx * wd[rb + "conv_1d.w"][3] + wd[rb + "conv_1d.b"]
+    gx = torch.einsum("thi,hij->thj", xc.view(40, H, 64), wd[rb + "rg_lru.input_gate.w"]).reshape(40, D) + wd[rb + "rg_lru.input_gate.b"].reshape(-1)
+    hh = xc * torch.sigmoid(gx)
+    res = F.linear(hh * gt(y), wd[rb + "linear_out.weight"], wd[rb + "linear_out.bias"]) + xd
+    gate, up = F.linear(rms(res, wd[sb + "channel_pre_norm.scale"]), wd[mb + "ffw_up.weight"], wd[mb + "ffw_up.bias"]).chunk(2, -1)
+    x1 = F.linear(gt(gate) * up, wd[mb + "ffw_down.weight"], wd[mb + "ffw_down.bias"]) + res
+    lnd = lambda t, nm: F.layer_norm(t, (D,), wd[vb + nm + ".weight"], wd[vb + nm + ".bias"], 1e-6)
+    q, k, v = F.linear(lnd(x1, "ln_1"), wd[vb + "self_attention.in_proj_weight"], wd[vb + "self_attention.in_proj_bias"]).view(40, 3, H, 64).permute(1, 2, 0, 3)
+    a = (torch.softmax(q @ k.transpose(-1, -2) / 8.0, -1) @ v).transpose(0, 1).reshape(40, D)
+    x2 = x1 + F.linear(a, wd[vb + "self_attention.out_proj.weight"], wd[vb + "self_attention.out_proj.bias"])
+    m0 = F.linear(lnd(x2, "ln_2"), wd[vb + "mlp.0.weight"], wd[vb + "mlp.0.bias"])
+    ref = x2 + F.linear(0.5 * m0 * (1 + torch.erf(m0 / math.sqrt(2))), wd[vb + "mlp.3.weight"], wd[vb + "mlp.3.bias"])
+    assert ((out - ref).norm() / ref.norm()) < 1e-2
+
+
+# ---------------------------------------------------------------------------------------------- synthetic inputs
+def test_synth_is_seeded_per_tensor():
+    """A subset of a model gets exactly the tensors the full model would get (per-name seeds)."""
+    a = S.vision_weights(0, layers=1)
+    b = S.vision_weights(0, layers=2)
+    for k, v in a.items():
+        assert torch.equal(v, b[k]), k
+    assert not torch.equal(S.vision_weights(1, layers=1)["blocks.0.attn.qkv.weight"], a["blocks.0.attn.qkv.weight"])
