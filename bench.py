@@ -38,60 +38,64 @@ def gemm_symbol(cfg):
     return f"gemm_bf16_kernel<{bm}, {bn}, 2, 2, {GEMM_STAGES[cfg]}>"
 
 
-def instrumented_pass(vt, img, reps=3):
-    """Eager tower passes with HIP events around every kernel launch (on torch's current stream, where the kernels
-    run). Returns {kernel symbol: [total_ms, launches, total_flops]}."""
+def op_timing(vt, img, reps=5):
+    """Per-kernel launch time inside the tower: one eager pass keeps every block's real operands, then for each op
+    class a HIP graph of its 27 launches (each on its own block's weights and activations, as in the tower) is
+    replayed `reps` times between two HIP events recorded on the stream the kernels run on. Returns
+    {label: [total_ms, launches, flops_per_launch, kernel symbol]}."""
     import torch
     import strix_halo_maxx_amd.ops as ops
-    from strix_halo_maxx_amd._lib import load
-    lib = load()
     B = img.shape[0]
     T, D, H, hd = vt.T, vt.D, vt.H, vt.hd
     M = B * T
-    recs = []
+    blocks = vt.blocks
+    saved = []
+    x = vt.embed(img)
+    for b in blocks:
+        h = ops.layernorm(x, *b["ln1"], eps=vt.eps)
+        qkv = b["qkv"](h)
+        q5 = qkv.view(B, T, 3, H, hd)
+        q, k, v = (q5[:, :, i].transpose(1, 2) for i in range(3))
+        a = vt.attn(q, k, v)
+        x1 = b["proj"](a.view(M, D), res=x)
+        h2 = ops.layernorm(x1, *b["ln2"], eps=vt.eps)
+        f = b["fc1"](h2, gelu=True)
+        saved.append((x, h, qkv, (q, k, v), a, x1, h2, f))
+        x = b["fc2"](f, res=x1)
+    outs = {n: torch.empty(M, w, device=x.device, dtype=torch.bfloat16)
+            for n, w in (("h", D), ("qkv", 3 * D), ("x", D), ("f", blocks[0]["fc1"].N))}
+    a_out = torch.empty(B, T, D, device=x.device, dtype=torch.bfloat16)
 
-    def timed(sym, flops, fn):
+    def sym(l):
+        cfg = l.cfgs.get(M) or ops._TUNED.get((M, l.N, l.Kw))
+        return gemm_symbol(cfg[0])
+    attn_sym = "attn_fwd_kernel<80, 96, {}>".format("4, 1, 64" if ((T + 127) // 128) * H * B >= 512 else "1, 4, 32")
+    classes = {
+        "ln": ("layernorm_kernel<4>", 0, lambda i, b: ops.layernorm(saved[i][0], *b["ln1"], eps=vt.eps, out=outs["h"])),
+        "qkv": (sym(blocks[0]["qkv"]), 2 * M * D * 3 * D, lambda i, b: b["qkv"](saved[i][1], out=outs["qkv"])),
+        "attn": (attn_sym, 4 * B * H * T * T * hd, lambda i, b: ops.sdpa(*saved[i][3], out=a_out)),
+        "proj": (sym(blocks[0]["proj"]), 2 * M * D * D, lambda i, b: b["proj"](saved[i][4].view(M, D), res=saved[i][0], out=outs["x"])),
+        "fc1": (sym(blocks[0]["fc1"]), 2 * M * D * blocks[0]["fc1"].N, lambda i, b: b["fc1"](saved[i][6], gelu=True, out=outs["f"])),
+        "fc2": (sym(blocks[0]["fc2"]), 2 * M * blocks[0]["fc2"].K * D, lambda i, b: b["fc2"](saved[i][7], res=saved[i][5], out=outs["x"])),
+    }
+    res = {}
+    for name, (ksym, fl, fn) in classes.items():
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i, b in enumerate(blocks):
+                fn(i, b)
+        g.replay()
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        r = fn()
+        for _ in range(reps):
+            g.replay()
         e1.record()
-        recs.append((sym, flops, e0, e1))
-        return r
-
-    def lin_sym(l, m):
-        cfg = l.cfgs.get(m) or ops._TUNED.get((m, l.N, l.Kw))
-        return gemm_symbol(cfg[0]) + f" M={m} N={l.N} K={l.K}"
-
-    attn_sym = "attn_fwd_kernel<80, 96, {}>".format("4, 1, 64" if ((T + 127) // 128) * H * B >= 512 else "1, 4, 32")
-    # Park the GPU in a sleep kernel long enough for the host to enqueue every pass: the kernels then run back to
-    # back, so each event pair brackets only its kernel (no host enqueue gaps inside the intervals).
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    torch.cuda._sleep(1_000_000)
-    e1.record()
-    torch.cuda.synchronize()
-    cycles = int(1_000_000 * 60.0 * reps / max(e0.elapsed_time(e1), 1e-3))
-    torch.cuda._sleep(cycles)
-    for _ in range(reps):
-        x = vt.embed(img)
-        for b in vt.blocks:
-            h = timed("layernorm_kernel<4>", 0, lambda: ops.layernorm(x, *b["ln1"], eps=vt.eps))
-            qkv = timed(lin_sym(b["qkv"], M), 2 * M * D * 3 * D, lambda: b["qkv"](h))
-            q5 = qkv.view(B, T, 3, H, hd)
-            q, k, v = (q5[:, :, i].transpose(1, 2) for i in range(3))
-            a = timed(attn_sym, 4 * B * H * T * T * hd, lambda: vt.attn(q, k, v))
-            x = timed(lin_sym(b["proj"], M), 2 * M * D * D, lambda: b["proj"](a.view(M, D), res=x))
-            h2 = timed("layernorm_kernel<4>", 0, lambda: ops.layernorm(x, *b["ln2"], eps=vt.eps))
-            f = timed(lin_sym(b["fc1"], M), 2 * M * D * b["fc1"].N, lambda: b["fc1"](h2, gelu=True))
-            x = timed(lin_sym(b["fc2"], M), 2 * M * b["fc2"].Kp * D, lambda: b["fc2"](f, res=x))
-    torch.cuda.synchronize()
-    agg = {}
-    for sym, fl, e0, e1 in recs:
-        a = agg.setdefault(sym, [0.0, 0, 0])
-        a[0] += e0.elapsed_time(e1)
-        a[1] += 1
-        a[2] += fl
-    return agg
+        e1.synchronize()
+        n = reps * len(blocks)
+        res[name] = [e0.elapsed_time(e1), n, fl, ksym]
+        del g
+    return res
 
 
 def cpu_baseline(budget_s=20.0):
@@ -160,6 +164,56 @@ def decode_bench(steps_tokens=128):
                         f"{steps_tokens} tokens, batch 1, one HIP graph per decode step"}
 
 
+def trecvit_bench(frames=64, clip=16):
+    """Config 3: TRecViT, 12 blocks, 1024 patch + 256 query tokens, streamed for `frames` frames (one HIP graph per
+    frame), plus the clip-parallel form (`clip` frames per pass through every block)."""
+    import torch
+    import strix_halo_maxx_amd.synth as S
+    import strix_halo_maxx_amd.trecvit as tv
+    dev = torch.device("cuda:0")
+    m = tv.TRecViT(S.trecvit_weights(0), device=dev)
+    fr = S.frames_u8(1, frames).to(dev)
+    q = S.query_points(5, 256)
+    qf = (q[:, 1:] / 256.0).to(torch.bfloat16).to(dev)
+    m.reset()
+    for t in range(4):
+        m.step(fr[t], qf)  # eager warm-up (GEMM tile tuning)
+    m.reset()
+    m.capture()
+    for t in range(4):
+        m.step(fr[t], qf, use_graph=True)
+    m.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(frames):
+        m.step(fr[t], qf, use_graph=True)
+    torch.cuda.synchronize()
+    ms_stream = (time.perf_counter() - t0) / frames * 1e3
+    m.graphs.clear()
+    m.reset()
+    m.clip_state(clip)
+    m.forward_clip(fr[:clip], qf)
+    m.reset()
+    m.clip_state(clip)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for c0 in range(0, frames, clip):
+        m.forward_clip(fr[c0:c0 + clip], qf)
+    torch.cuda.synchronize()
+    ms_clip = (time.perf_counter() - t0) / frames * 1e3
+    c = S.TRV
+    T, D = 1280, c["dim"]
+    gemm = 2 * T * (D * 2 * D + D * D + D * 2 * c["ff_gated"] + c["ff_gated"] * D + D * 3 * D + D * D + 2 * D * c["ff_vit"])
+    attn = 4 * T * T * D
+    gates = 2 * 2 * T * D * 64
+    fl = c["layers"] * (gemm + attn + gates)
+    return {"stream_ms_per_frame": round(ms_stream, 3), "clip_ms_per_frame": round(ms_clip, 3), "clip_frames": clip,
+            "frames": frames, "gflop_per_frame": round(fl / 1e9, 1),
+            "stream_mfma_frac": round(fl / (ms_stream / 1e3) / PEAK_BF16, 4),
+            "clip_mfma_frac": round(fl / (ms_clip / 1e3) / PEAK_BF16, 4),
+            "workload": "TAPNext-style TRecViT, 12 blocks, hidden 768, 1024 patch + 256 query tokens, 64 frames"}
+
+
 def tower_time(vt, img, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -199,16 +253,16 @@ def main():
     print(f"[bench] tower batch 1: warmup {a.warmup}, steps {a.steps}", file=sys.stderr, flush=True)
     with torch.inference_mode():
         s = tower_time(vt, img, a.steps, a.warmup)
-        agg = instrumented_pass(vt, img)
+        agg = op_timing(vt, img)
     ms = s * 1e3
-    sym, (tot_ms, n, fl) = max(agg.items(), key=lambda kv: kv[1][0])
+    label, (tot_ms, n, fl, sym) = max(agg.items(), key=lambda kv: kv[1][0])
     avg_s = tot_ms / n / 1e3
-    achieved = fl / n / avg_s
-    roof = {"bound": "mfma", "kernel": sym, "achieved": round(achieved / 1e12, 1), "peak": PEAK_BF16 / 1e12,
-            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
-            "avg_launch_us": round(avg_s * 1e6, 2), "launches": n,
-            "per_kernel_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in agg.items()},
-            "flops_per_launch": fl // n}
+    achieved = fl / avg_s
+    roof = {"bound": "mfma", "kernel": sym, "op": label, "achieved": round(achieved / 1e12, 1),
+            "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
+            "avg_launch_us": round(avg_s * 1e6, 2), "launches_timed": n, "flops_per_launch": fl,
+            "per_op_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in agg.items()},
+            "per_op_kernel": {k: v[3] for k, v in agg.items()}}
     tower_flops = vision_flops_per_frame()
     out = {"metric": "ms/frame moondream2 vision tower bs=1; decode tok/s; % MFMA / HBM roofline", "value": round(ms, 4), "unit": "ms/frame", "n_gpus": 1,
            "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
@@ -233,6 +287,10 @@ def main():
     print("[bench] decoder", file=sys.stderr, flush=True)
     with torch.inference_mode():
         out.setdefault("extra", {})["decoder"] = decode_bench()
+    torch.cuda.empty_cache()
+    print("[bench] trecvit", file=sys.stderr, flush=True)
+    with torch.inference_mode():
+        out["extra"]["trecvit"] = trecvit_bench()
     if not a.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline()

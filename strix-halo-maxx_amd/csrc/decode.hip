@@ -4,8 +4,8 @@
 // 2 per token, all replayed from one HIP graph, with the step's position and the token living in device memory:
 //   ln_gemv2      h = LN(x) (recomputed per wave from the 4 KB row), [qkv | fc1] = h [Wqkv | Wfc1]^T + b, GELU on
 //                 the fc1 part (the reference's qkv and fc1 both read the same LN output, md2fast.py:173-198)
-//   decode_attn   rope on q / k of the new token, K/V append at `pos`, split-KV attention over keys 0..pos with a
-//                 last-arriver merge of the splits (no workgroup ever waits on another)
+//   decode_attn   rope on q / k of the new token, K/V append at `pos`, split-KV attention over keys 0..pos, then a
+//                 small per-head merge kernel
 //   gemv_dual_res x' = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)): the parallel residual of
 //                 md2fast.py:198 with the reference's rounding order, both GEMVs in one pass over [Wfc2 | Wproj]
 //   ln_gemv_argmax  logits = LN(x) Wlm^T + b (bf16, as the reference's bf16 lm_head) and a per-workgroup argmax
@@ -239,18 +239,17 @@ __global__ __launch_bounds__(1024) void embed_step_kernel(const unsigned long lo
 
 // ---------------------------------------------------------------------------------------------- decode attention
 constexpr int DA_MAXK = 1024;  // keys per split held in LDS
+constexpr int DA_UNROLL = 4;   // key rounds (32 keys each) whose loads are issued together
 
 __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
                                                           uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                                                           int H, int ctx, const int* __restrict__ state, int S,
-                                                          float scale_log2, float* __restrict__ ws,
-                                                          int* __restrict__ cnt, uint16_t* __restrict__ out) {
+                                                          float scale_log2, float* __restrict__ ws) {
   __shared__ float sc[DA_MAXK];
   __shared__ float qs[64];
   __shared__ uint16_t knew[64], vnew[64];
   __shared__ float red[8];
   __shared__ float osum[4][64];
-  __shared__ int s_last;
   const int h = blockIdx.x, split = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = state[1];
@@ -261,6 +260,8 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
   const uint16_t* src = qkv + h * 64;
   const uint16_t* ksrc = qkv + H * 64 + h * 64;
   const uint16_t* vsrc = qkv + 2 * H * 64 + h * 64;
+  const uint16_t* kh = kc + (long)h * ctx * 64;
+  const uint16_t* vh = vc + (long)h * ctx * 64;
   // rope of q and k for the new token (fp32, as the prefill rope kernel)
   if (tid < 64) {
     const int d = tid;
@@ -285,28 +286,39 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
     kc[((long)h * ctx + pos) * 64 + tid] = knew[tid];
     vc[((long)h * ctx + pos) * 64 + tid] = vnew[tid];
   }
-  // ---- scores: 8 lanes per key (lane % 8 -> dims 8 (lane % 8) ..), 8 keys per wave per step
+  // ---- scores: 8 lanes per key (lane % 8 -> dims 8 (lane % 8) ..), 8 keys per wave per round, DA_UNROLL rounds
+  // of loads in flight
   const int sub = lane & 7, kg = lane >> 3;
   float qv[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) qv[e] = qs[sub * 8 + e];
   float mloc = -1e30f;
-  for (int key = k0 + wave * 8 + kg; key < k1; key += 32) {
-    u32x4 kk;
-    if (key == pos) kk = *reinterpret_cast<const u32x4*>(&knew[sub * 8]);
-    else kk = *reinterpret_cast<const u32x4*>(kc + ((long)h * ctx + key) * 64 + sub * 8);
-    float s = 0.f;
+  for (int base = k0 + wave * 8 + kg; base < k1; base += 32 * DA_UNROLL) {
+    u32x4 kk[DA_UNROLL];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      s = __builtin_fmaf(lo_bf(kk[e]), qv[2 * e], s);
-      s = __builtin_fmaf(hi_bf(kk[e]), qv[2 * e + 1], s);
+    for (int u = 0; u < DA_UNROLL; u++) {
+      const int key = base + 32 * u;
+      kk[u] = (key < k1 && key != pos) ? *reinterpret_cast<const u32x4*>(kh + (long)key * 64 + sub * 8)
+                                       : *reinterpret_cast<const u32x4*>(&knew[sub * 8]);
     }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
-    s *= scale_log2;
-    if (sub == 0) sc[key - k0] = s;
-    mloc = fmaxf(mloc, s);
+#pragma unroll
+    for (int u = 0; u < DA_UNROLL; u++) {
+      const int key = base + 32 * u;
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        s = __builtin_fmaf(lo_bf(kk[u][e]), qv[2 * e], s);
+        s = __builtin_fmaf(hi_bf(kk[u][e]), qv[2 * e + 1], s);
+      }
+      s += __shfl_xor(s, 1, 64);
+      s += __shfl_xor(s, 2, 64);
+      s += __shfl_xor(s, 4, 64);
+      s *= scale_log2;
+      if (key < k1) {
+        if (sub == 0) sc[key - k0] = s;
+        mloc = fmaxf(mloc, s);
+      }
+    }
   }
   mloc = wave_max(mloc);
   if (lane == 0) red[wave] = mloc;
@@ -315,16 +327,26 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
   // ---- P (rounded to bf16) and PV with the same key mapping
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
-  for (int key = k0 + wave * 8 + kg; key < k1; key += 32) {
-    const float p = rbf(__builtin_amdgcn_exp2f(sc[key - k0] - m));
-    if (sub == 0) lsum += p;
-    u32x4 vv;
-    if (key == pos) vv = *reinterpret_cast<const u32x4*>(&vnew[sub * 8]);
-    else vv = *reinterpret_cast<const u32x4*>(vc + ((long)h * ctx + key) * 64 + sub * 8);
+  for (int base = k0 + wave * 8 + kg; base < k1; base += 32 * DA_UNROLL) {
+    u32x4 vv[DA_UNROLL];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      o[2 * e] = __builtin_fmaf(p, lo_bf(vv[e]), o[2 * e]);
-      o[2 * e + 1] = __builtin_fmaf(p, hi_bf(vv[e]), o[2 * e + 1]);
+    for (int u = 0; u < DA_UNROLL; u++) {
+      const int key = base + 32 * u;
+      vv[u] = (key < k1 && key != pos) ? *reinterpret_cast<const u32x4*>(vh + (long)key * 64 + sub * 8)
+                                       : *reinterpret_cast<const u32x4*>(&vnew[sub * 8]);
+    }
+#pragma unroll
+    for (int u = 0; u < DA_UNROLL; u++) {
+      const int key = base + 32 * u;
+      if (key < k1) {
+        const float p = rbf(__builtin_amdgcn_exp2f(sc[key - k0] - m));
+        if (sub == 0) lsum += p;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          o[2 * e] = __builtin_fmaf(p, lo_bf(vv[u][e]), o[2 * e]);
+          o[2 * e + 1] = __builtin_fmaf(p, hi_bf(vv[u][e]), o[2 * e + 1]);
+        }
+      }
     }
   }
   // reduce over the 8 key groups of the wave, then over the 4 waves
@@ -335,36 +357,31 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
     o[e] += __shfl_xor(o[e], 32, 64);
   }
   lsum = wave_sum(lsum);
-  __syncthreads();
   if (kg == 0) {
 #pragma unroll
     for (int e = 0; e < 8; e++) osum[wave][sub * 8 + e] = o[e];
   }
   if (lane == 0) red[4 + wave] = lsum;
   __syncthreads();
-  float* rec = ws + ((long)h * S + split) * 66;  // (m, l, o[64])
+  float* rec = ws + ((long)h * S + split) * 66;  // (m, l, o[64]) of this split, merged by decode_combine_kernel
   if (tid < 64) rec[2 + tid] = osum[0][tid] + osum[1][tid] + osum[2][tid] + osum[3][tid];
   if (tid == 0) { rec[0] = (k1 > k0) ? m : -1e30f; rec[1] = red[4] + red[5] + red[6] + red[7]; }
-  // ---- last split to finish merges all splits of this head
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(&cnt[h], 1) == S - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (tid < 64) {
-    float M = -1e30f;
-    for (int sp = 0; sp < S; sp++) M = fmaxf(M, __builtin_nontemporal_load(ws + ((long)h * S + sp) * 66));
-    float Lt = 0.f, acc = 0.f;
-    for (int sp = 0; sp < S; sp++) {
-      const float* r = ws + ((long)h * S + sp) * 66;
-      const float f = __builtin_amdgcn_exp2f(__builtin_nontemporal_load(r) - M);
-      Lt += __builtin_nontemporal_load(r + 1) * f;
-      acc += __builtin_nontemporal_load(r + 2 + tid) * f;
-    }
-    out[h * 64 + tid] = f2bf(acc / Lt);
+}
+
+// merge the S split partials of each head: out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
+__global__ __launch_bounds__(64) void decode_combine_kernel(const float* __restrict__ ws, int S,
+                                                            uint16_t* __restrict__ out) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  const float* base = ws + (long)h * S * 66;
+  float M = -1e30f;
+  for (int sp = 0; sp < S; sp++) M = fmaxf(M, base[sp * 66]);
+  float Lt = 0.f, acc = 0.f;
+  for (int sp = 0; sp < S; sp++) {
+    const float f = __builtin_amdgcn_exp2f(base[sp * 66] - M);
+    Lt += base[sp * 66 + 1] * f;
+    acc += base[sp * 66 + 2 + d] * f;
   }
-  if (tid == 0) cnt[h] = 0;
+  out[h * 64 + d] = f2bf(acc / Lt);
 }
 
 }  // namespace
@@ -376,7 +393,7 @@ extern "C" int mx_ln_gemv2(hipStream_t st, const uint16_t* x, const uint16_t* ga
   if ((gamma == nullptr) != (beta == nullptr)) return MX_ENULL;
   if (N < 1 || n1 < 0 || n1 > N || ldw < K || ldw % 8 || act2 < 0 || act2 > 2) return MX_ESHAPE;
   if (((uintptr_t)x | (uintptr_t)W) & 15) return MX_ELAYOUT;
-  constexpr int R = 4;
+  constexpr int R = 8;
   const dim3 g((N + 4 * R - 1) / (4 * R));
   if (K == 2048) hipLaunchKernelGGL((ln_gemv2_kernel<4, R>), g, dim3(256), 0, st, x, gamma, beta, eps, W, ldw, bias, N, n1, out1, out2, act2);
   else if (K == 1024) hipLaunchKernelGGL((ln_gemv2_kernel<2, R>), g, dim3(256), 0, st, x, gamma, beta, eps, W, ldw, bias, N, n1, out1, out2, act2);
@@ -425,12 +442,16 @@ extern "C" int mx_embed_step(hipStream_t st, const unsigned long long* part, int
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
-// ws: >= H * S * 66 floats; cnt: >= H ints, zero before first use (left zero).
+// ws: >= H * S * 66 floats (split partials); cnt: unused (kept for ABI stability, may be null). Two launches:
+// the split-KV pass and the per-head merge (a kernel boundary instead of a device-scope fence + counter).
 extern "C" int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H,
                               int ctx, const int* state, int S, float scale, float* ws, int* cnt, uint16_t* out) {
-  if (!qkv || !cs || !kc || !vc || !state || !ws || !cnt || !out) return MX_ENULL;
+  (void)cnt;
+  if (!qkv || !cs || !kc || !vc || !state || !ws || !out) return MX_ENULL;
   if (H < 1 || S < 1 || ctx < 1 || (ctx + S - 1) / S > DA_MAXK) return MX_ESHAPE;
   hipLaunchKernelGGL(decode_attn_kernel, dim3(H, S), dim3(256), 0, st, qkv, cs, kc, vc, H, ctx, state, S,
-                     scale * 1.4426950408889634f, ws, cnt, out);
+                     scale * 1.4426950408889634f, ws);
+  if (hipGetLastError() != hipSuccess) return MX_ELAUNCH;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(H), dim3(64), 0, st, ws, S, out);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
