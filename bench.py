@@ -29,12 +29,16 @@ def vision_flops_per_frame(layers=27, T=729, D=1152, F=4304, H=16, hd=72, Kp=588
     return layers * (g + a) + 2 * T * Kp * D
 
 
-GEMM_STAGES = {0: 4, 1: 4, 2: 4, 3: 4, 4: 3, 5: 3, 6: 3, 7: 2}
+# LDS ring depth of each GEMM tile config (the kernel template's last argument)
+GEMM_STAGES = {0: 4, 1: 4, 2: 4, 3: 4, 4: 3, 5: 3, 6: 3, 7: 2, 8: 4, 9: 4, 10: 4, 11: 8, 12: 6, 13: 6, 14: 6}
 
 
 def gemm_symbol(cfg):
     import strix_halo_maxx_amd.ops as ops
+    from strix_halo_maxx_amd import _lib
     bm, bn = ops.gemm_tile(cfg)
+    if _lib.load().mx_gemm_cfg_kind(cfg) == 1:
+        return f"gemm_ks_kernel<{bm}, {bn}, {GEMM_STAGES[cfg]}>"
     return f"gemm_bf16_kernel<{bm}, {bn}, 2, 2, {GEMM_STAGES[cfg]}>"
 
 

@@ -41,6 +41,9 @@ int mx_gemm_pick(int M, int N, int Kw);
 /* Number of tile configs / the (BM, BN) tile of one. Replaces bf16gemm_ncfg (i8gemm.hip:553). */
 int mx_gemm_ncfg(void);
 int mx_gemm_cfg_tile(int cfg, int* bm, int* bn);
+/* Kernel kind of a tile config: 0 = LDS-shared tile (split-K capable), 1 = wave-split K (splits must be 1), or
+ * MX_EBADCFG. No counterpart in the reference (its configs are all one kind). */
+int mx_gemm_cfg_kind(int cfg);
 /* Split-K workspace a (cfg, splits) call needs: fp32 elements / tile counters. Replaces the fixed-size
  * workspace() of moondream/gpu/hgemm.py:78-83. */
 long mx_gemm_ws_elems(int cfg, int splits, int M, int N);

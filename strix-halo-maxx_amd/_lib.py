@@ -24,6 +24,7 @@ SIGNATURES = {
     "mx_gemm_ws_counters": [I, I, I, I],
     "mx_gemm_ncfg": [],
     "mx_gemm_cfg_tile": [I, ctypes.POINTER(I), ctypes.POINTER(I)],
+    "mx_gemm_cfg_kind": [I],
     "mx_sdpa": [P, P, L, L, L, P, L, L, L, P, L, L, L, P, L, L, L, I, I, I, I, I, F, I, I],
     "mx_sdpa_check": [P, L, P, L, P, L, P, L, I, I, I, I, I],
     "mx_layernorm": [P, P, L, P, P, P, L, I, I, F],

@@ -8,15 +8,22 @@
 //    as 1 KB in LDS without passing through VGPRs), into an S-stage LDS ring, S-1 k-steps ahead of the MFMAs.
 //    The compiler cannot see which ring slot an LDS read touches, so these loads are issued from inline asm and the
 //    wait for "stage k has landed" is an explicit `s_waitcnt vmcnt(n)` that leaves the later stages in flight.
-//  * LDS rows are 64 bf16 (128 B) with the 16-byte chunk index XOR-swizzled by (row & 7): the DMA lane -> address
-//    map is fixed (lane l writes bytes 16 l.. of the 1 KB block), so each lane fetches the global chunk that belongs
-//    at its slot, and the 32 rows read by one MFMA operand fetch (ds_read_b128) spread over all banks.
+//  * LDS rows are 64 bf16 (128 B) with the 16-byte chunk index XOR-swizzled by ((row >> 1) & 7): a ds_read_b128
+//    serves 16 lanes (256 B, two rows per bank sweep of the 64 banks) at a time, and the 16 rows those lanes read
+//    then cover every (row parity, chunk) pair once. The DMA lane -> address map is fixed (lane l writes bytes
+//    16 l.. of a 1 KB block of 8 rows), so each lane fetches the global chunk that belongs at its slot; for rows
+//    8 g + (l >> 3) the swizzle is (l >> 4) | ((g & 1) << 2), and g & 1 is the wave's parity.
 //  * The MFMA is issued "swapped" (W as the row operand, A as the column operand): every lane ends up with 4
 //    consecutive output columns of one output row -> 8-byte stores; bias / residual are read as vectors.
 //  * Split-K for small grids (batch-1 shapes on 256 CUs): each split writes an fp32 partial tile; the last split to
 //    arrive (atomic counter per tile) adds the partials in split order (deterministic) and runs the epilogue, then
 //    re-arms the counter. No workgroup ever waits on another.
 //  * Workgroup ids are remapped so consecutive tiles (sharing W panels) land on the same XCD and its L2.
+//  * A second kernel kind for grids that cannot put several workgroups on every CU (batch-1 shapes), where one wave
+//    per SIMD has nothing to hide the ds_read -> MFMA chain of a k-step behind: the same LDS ring, but the waves
+//    split each 64-wide k-step instead of the tile. Wave w multiplies k columns [16 w, 16 w + 16) into its own copy
+//    of the whole BM x BN tile, so its (BM / 32) x (BN / 32) MFMAs per k-step are independent and each LDS byte is
+//    read by one wave only; the four partial tiles are summed through LDS in a fixed order after the k loop.
 // Rounding follows torch's bf16 Linear path: the linear output is rounded to bf16, GELU is applied to that rounded
 // value and rounded again, then the residual is added in fp32 and rounded once more.
 //
@@ -40,7 +47,58 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
 }
 template <int N>
 __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt field");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait until at most min(ahead, A) ring stages of LPS loads each are still in flight.
+template <int LPS, int A>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      wait_vm<A * LPS>();
+      return;
+    }
+    wait_stages<LPS, A - 1>(ahead);
+  } else {
+    wait_vm<0>();
+  }
+}
+
+// Epilogue for output row m, columns n .. n+3 from fp32 sums s[0..3]: + bias, round to bf16, optional activation
+// (rounded again), optional + residual (fp32 add, rounded once more); act 3 writes the gated pair results to
+// columns n / 2, n / 2 + 1.
+__device__ __forceinline__ void epi4(const float* s, int m, int n, const float* __restrict__ bias,
+                                     const uint16_t* __restrict__ R, long ldr, int r_rows, uint16_t* __restrict__ C,
+                                     long ldc, int act, int act_ncols) {
+  float v[4];
+  f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+  if (bias) bv = *reinterpret_cast<const f32x4*>(bias + n);
+#pragma unroll
+  for (int e = 0; e < 4; e++) v[e] = rbf(s[e] + bv[e]);
+  if (act == 3) {
+    // gated GELU on interleaved (gate, up) column pairs -> output column n / 2 + {0, 1}
+    const uint32_t o = pack2(rbf(gelu_tanh(v[0])) * v[1], rbf(gelu_tanh(v[2])) * v[3]);
+    *reinterpret_cast<uint32_t*>(C + (long)m * ldc + (n >> 1)) = o;
+    return;
+  }
+  if (act_ncols > 0 && n >= act_ncols) {
+    // no activation on this column range
+  } else if (act == 1) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = rbf(gelu_tanh(v[e]));
+  } else if (act == 2) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = rbf(gelu_erf(v[e]));
+  }
+  if (R) {
+    const int rm = r_rows > 0 ? m % r_rows : m;
+    const u32x2 rr = *reinterpret_cast<const u32x2*>(R + (long)rm * ldr + n);
+    v[0] += lo_bf(rr.x); v[1] += hi_bf(rr.x); v[2] += lo_bf(rr.y); v[3] += hi_bf(rr.y);
+  }
+  u32x2 o;
+  o.x = pack2(v[0], v[1]);
+  o.y = pack2(v[2], v[3]);
+  *reinterpret_cast<u32x2*>(C + (long)m * ldc + n) = o;
 }
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -78,7 +136,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
   const uint32_t sbase = lds_off(smem);
 
   // per-lane DMA source rows / chunk (fixed for the whole k loop)
-  const int drow = lane >> 3, dch = (lane & 7) ^ (lane >> 3);
+  const int drow = lane >> 3, dch = (lane & 7) ^ ((lane >> 4) | ((wave & 1) << 2));
   const uint16_t* a_src[QA];
   const uint16_t* w_src[QW];
 #pragma unroll
@@ -116,10 +174,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
 
   for (int it = 0; it < nkl; it++) {
     // stage `it` has landed once at most (stages issued after it) x LPS loads are still in flight
-    const int ahead = min(S - 2, nkl - 1 - it);
-    if (S >= 4 && ahead >= 2) wait_vm<(S >= 4 ? 2 : 0) * LPS>();
-    else if (S >= 3 && ahead >= 1) wait_vm<(S >= 3 ? 1 : 0) * LPS>();
-    else wait_vm<0>();
+    wait_stages<LPS, S - 2>(nkl - 1 - it);
     __syncthreads();
     if (it + S - 1 < nkl) issue(kt0 + it + S - 1, (it + S - 1) % S);
     const uint16_t* As = smem + (it % S) * STAGE;
@@ -131,12 +186,12 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
 #pragma unroll
       for (int i = 0; i < FM; i++) {
         const int r = wm * WTM + i * 32 + lr;
-        af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[r * BK + ((c ^ (r & 7)) << 3)]));
+        af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
       }
 #pragma unroll
       for (int i = 0; i < FN; i++) {
         const int r = wn * WTN + i * 32 + lr;
-        wf[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ (r & 7)) << 3)]));
+        wf[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
       }
 #pragma unroll
       for (int i = 0; i < FN; i++)
@@ -189,44 +244,149 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
       for (int g = 0; g < 4; g++) {
         const int n = n0 + wn * WTN + i * 32 + 8 * g + 4 * hk;
         if (n >= N) continue;
-        float v[4];
-        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-        if (bias) bv = *reinterpret_cast<const f32x4*>(bias + n);
-#pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = rbf(acc[i][j][4 * g + e] + bv[e]);
-        if (act == 3) {
-          // gated GELU on interleaved (gate, up) column pairs -> output column n / 2 + {0, 1}
-          const uint32_t o = pack2(rbf(gelu_tanh(v[0])) * v[1], rbf(gelu_tanh(v[2])) * v[3]);
-          *reinterpret_cast<uint32_t*>(C + (long)m * ldc + (n >> 1)) = o;
-          continue;
-        }
-        if (act_ncols > 0 && n >= act_ncols) {
-          // no activation on this column range
-        } else if (act == 1) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) v[e] = rbf(gelu_tanh(v[e]));
-        } else if (act == 2) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) v[e] = rbf(gelu_erf(v[e]));
-        }
-        if (R) {
-          const int rm = r_rows > 0 ? m % r_rows : m;
-          const u32x2 rr = *reinterpret_cast<const u32x2*>(R + (long)rm * ldr + n);
-          v[0] += lo_bf(rr.x); v[1] += hi_bf(rr.x); v[2] += lo_bf(rr.y); v[3] += hi_bf(rr.y);
-        }
-        u32x2 o;
-        o.x = pack2(v[0], v[1]);
-        o.y = pack2(v[2], v[3]);
-        *reinterpret_cast<u32x2*>(C + (long)m * ldc + n) = o;
+        const float a4[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        epi4(a4, m, n, bias, R, ldr, r_rows, C, ldc, act, act_ncols);
       }
     }
   }
 }
 
-struct Cfg { int bm, bn, stages, per_cu; };
-// per_cu: workgroups that fit one CU at once (LDS-limited)
-constexpr Cfg kCfgs[] = {{128, 128, 4, 1}, {64, 128, 4, 1}, {128, 64, 4, 1}, {64, 64, 4, 2},
-                         {256, 128, 3, 1}, {128, 256, 3, 1}, {64, 64, 3, 3}, {128, 128, 2, 2}};
+// Wave-split-K kernel (see the header): 4 waves share the LDS ring of a BM x BN tile; wave w multiplies the k
+// columns [16 w, 16 w + 16) of every 64-wide k-step into its own copy of the whole tile.
+template <int BM, int BN, int S>
+__global__ __launch_bounds__(256) void gemm_ks_kernel(
+    const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
+    const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
+    uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols, int tiles_m, int tiles_n) {
+  static_assert(S >= 2, "at least a double buffer");
+  constexpr int FM = BM / 32, FN = BN / 32;
+  constexpr int QA = BM / 32, QW = BN / 32;  // DMA instructions per wave per stage
+  constexpr int LPS = QA + QW;
+  constexpr int STAGE = (BM + BN) * BK;      // elements per ring stage
+  constexpr int G = FM * FN * 4;             // 4-column output groups per lane
+  constexpr int RING_B = S * STAGE * 2, RED_B = 2 * G * 64 * 16;
+  // the k loop's ring, reused after the loop for the two partial tiles of the cross-wave sum
+  __shared__ __attribute__((aligned(1024))) uint8_t smem_b[RING_B > RED_B ? RING_B : RED_B];
+  uint16_t* smem = reinterpret_cast<uint16_t*>(smem_b);
+  f32x4* red = reinterpret_cast<f32x4*>(smem_b);
+
+  const int nt = tiles_m * tiles_n;
+  const int b = blockIdx.x;
+  const int per = nt / 8, rem = nt % 8, xcd = b % 8, idx = b / 8;
+  const int t = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  const int tile_m = t % tiles_m, tile_n = t / tiles_m;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  const int nk = Kw / BK;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, hk = lane >> 5;
+  const uint32_t sbase = lds_off(smem);
+
+  const int drow = lane >> 3, dch = (lane & 7) ^ ((lane >> 4) | ((wave & 1) << 2));
+  const uint16_t* a_src[QA];
+  const uint16_t* w_src[QW];
+#pragma unroll
+  for (int q = 0; q < QA; q++) a_src[q] = A + (long)min(m0 + 8 * (q * 4 + wave) + drow, M - 1) * lda;
+#pragma unroll
+  for (int q = 0; q < QW; q++) w_src[q] = W + (long)min(n0 + 8 * (q * 4 + wave) + drow, N - 1) * ldw;
+  auto issue = [&](int kt, int s) {
+    const int kk = kt * BK + dch * 8;
+    const int ka = kk < K ? kk : 0;
+    const uint32_t st = sbase + (uint32_t)(s * STAGE * 2);
+#pragma unroll
+    for (int q = 0; q < QA; q++) dma16(a_src[q] + ka, __builtin_amdgcn_readfirstlane(st + (q * 4 + wave) * 1024));
+#pragma unroll
+    for (int q = 0; q < QW; q++)
+      dma16(w_src[q] + kk, __builtin_amdgcn_readfirstlane(st + BM * 128 + (q * 4 + wave) * 1024));
+  };
+
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; i++)
+#pragma unroll
+    for (int j = 0; j < FM; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+#pragma unroll
+  for (int s = 0; s < S - 1; s++)
+    if (s < nk) issue(s, s);
+
+  const int c = 2 * wave + hk;  // this lane's 16-byte chunk of each 128-byte LDS row
+  for (int it = 0; it < nk; it++) {
+    wait_stages<LPS, S - 2>(nk - 1 - it);
+    __syncthreads();
+    if (it + S - 1 < nk) issue(it + S - 1, (it + S - 1) % S);
+    const uint16_t* As = smem + (it % S) * STAGE;
+    const uint16_t* Ws = As + BM * BK;
+    bf16x8 af[FM], wf[FN];
+#pragma unroll
+    for (int j = 0; j < FM; j++) {
+      const int r = j * 32 + lr;
+      af[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
+    }
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+      const int r = i * 32 + lr;
+      wf[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
+    }
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++) acc[i][j] = mfma32(wf[i], af[j], acc[i][j]);
+  }
+
+  // ---- cross-wave sum in a fixed order, ((w0 + w2) + (w1 + w3)): waves 2-3 hand their tiles to waves 0-1 through
+  // LDS, waves 0-1 write the two sums back, and every wave finishes a quarter of the groups (epilogue + store)
+  auto put = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          red[(slot * G + (i * FM + j) * 4 + g) * 64 + lane] = v;
+        }
+  };
+  __syncthreads();  // every wave is done with the ring
+  if (wave >= 2) put(wave - 2);
+  __syncthreads();
+  if (wave < 2) {
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const f32x4 v = red[(wave * G + (i * FM + j) * 4 + g) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[i][j][4 * g + e] += v[e];
+        }
+  }
+  __syncthreads();
+  if (wave < 2) put(wave);
+  __syncthreads();
+#pragma unroll
+  for (int q = wave; q < G; q += 4) {
+    const f32x4 v = red[q * 64 + lane] + red[(G + q) * 64 + lane];
+    const int i = q / (FM * 4), j = (q / 4) % FM, g = q % 4;
+    const int m = m0 + j * 32 + lr;
+    const int n = n0 + i * 32 + 8 * g + 4 * hk;
+    if (m < M && n < N) {
+      const float a4[4] = {v[0], v[1], v[2], v[3]};
+      epi4(a4, m, n, bias, R, ldr, r_rows, C, ldc, act, act_ncols);
+    }
+  }
+}
+
+struct Cfg { int bm, bn, stages, per_cu, kind; };
+// kind 0: LDS-shared tile split over the waves; kind 1: wave-split K (each wave the whole tile, a quarter of K).
+// Both stage operands through a `stages`-deep LDS ring.
+// per_cu: workgroups that fit one CU at once (LDS- or register-limited)
+constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0}, {64, 128, 4, 1, 0}, {128, 64, 4, 1, 0}, {64, 64, 4, 2, 0},
+                         {256, 128, 3, 1, 0}, {128, 256, 3, 1, 0}, {64, 64, 3, 3, 0}, {128, 128, 2, 2, 0},
+                         {64, 64, 4, 2, 1},   {64, 128, 4, 1, 1},  {128, 64, 4, 1, 1}, {64, 64, 8, 1, 1},
+                         {64, 128, 6, 1, 1},  {64, 64, 6, 1, 1},   {128, 64, 6, 1, 1}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -238,6 +398,16 @@ hipError_t launch(hipStream_t st, int splits, const uint16_t* A, long lda, const
   const int kps = (nk + splits - 1) / splits;
   hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn * splits), dim3(256), 0, st, A, lda, W,
                      ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, tm, tn, splits, kps, ws, cnt);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int S>
+hipError_t launch_ks(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* bias,
+                     const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int K, int Kw,
+                     int act, int act_ncols) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_ks_kernel<BM, BN, S>), dim3(tm * tn), dim3(256), 0, st, A, lda, W, ldw, bias, R, ldr, r_rows,
+                     C, ldc, M, N, K, Kw, act, act_ncols, tm, tn);
   return hipGetLastError();
 }
 
@@ -256,26 +426,31 @@ extern "C" int mx_gemm_cfg_tile(int cfg, int* bm, int* bn) {
   return MX_OK;
 }
 
+extern "C" int mx_gemm_cfg_kind(int cfg) {
+  if (cfg < 0 || cfg >= kNCfg) return MX_EBADCFG;
+  return kCfgs[cfg].kind;
+}
+
 // Workspace a (cfg, splits) call needs: fp32 partial tiles and one counter per output tile.
 extern "C" long mx_gemm_ws_elems(int cfg, int splits, int M, int N) {
-  if (cfg < 0 || cfg >= kNCfg || splits <= 1) return 0;
+  if (cfg < 0 || cfg >= kNCfg || splits <= 1 || kCfgs[cfg].kind) return 0;
   return tiles_of(cfg, M, N) * splits * kCfgs[cfg].bm * kCfgs[cfg].bn;
 }
 extern "C" long mx_gemm_ws_counters(int cfg, int splits, int M, int N) {
-  if (cfg < 0 || cfg >= kNCfg || splits <= 1) return 0;
+  if (cfg < 0 || cfg >= kNCfg || splits <= 1 || kCfgs[cfg].kind) return 0;
   return tiles_of(cfg, M, N);
 }
 
 // Default (cfg, splits) when the caller passes cfg < 0: minimise estimated time = rounds of workgroups over the
 // 256 CUs x per-tile time, with per-tile time ~ BM*BN*(k-steps)/efficiency. Returns cfg * 16 + splits.
 extern "C" int mx_gemm_pick(int M, int N, int Kw) {
-  static const float eff[kNCfg] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f};
+  static const float eff[kNCfg] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};
   const int nk = Kw / BK;
   int best = 0, bsplit = 1;
   float bt = 1e30f;
   for (int c = 0; c < kNCfg; c++) {
     for (int sp = 1; sp <= 8; sp *= 2) {
-      if (sp > 1 && (nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk)) break;
+      if (sp > 1 && (kCfgs[c].kind || nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk)) break;
       const long tiles = tiles_of(c, M, N) * sp;
       const long slots = 256L * kCfgs[c].per_cu;
       const long rounds = (tiles + slots - 1) / slots;
@@ -304,6 +479,7 @@ extern "C" int mx_gemm_check(int cfg, int splits, const void* A, long lda, const
   if (bias && ((uintptr_t)bias & 15)) return MX_ELAYOUT;
   if (R && (((uintptr_t)R & 7) || ldr % 4 || ldr < N)) return MX_ELAYOUT;
   if (cfg >= 0 && splits > 1) {
+    if (kCfgs[cfg].kind) return MX_ESPLIT;  // the wave-split kind splits K inside the workgroup only
     const int nk = Kw / BK, kps = (nk + splits - 1) / splits;
     if (splits > nk || (splits - 1) * kps >= nk) return MX_ESPLIT;  // every split must own >= 1 k-step
     if (!ws || !cnt) return MX_ENULL;
@@ -345,8 +521,17 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
     case 5: e = L_(128, 256, 3); break;
     case 6: e = L_(64, 64, 3); break;
     case 7: e = L_(128, 128, 2); break;
+#define W_(BM, BN, S) launch_ks<BM, BN, S>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
+    case 8: e = W_(64, 64, 4); break;
+    case 9: e = W_(64, 128, 4); break;
+    case 10: e = W_(128, 64, 4); break;
+    case 11: e = W_(64, 64, 8); break;
+    case 12: e = W_(64, 128, 6); break;
+    case 13: e = W_(64, 64, 6); break;
+    case 14: e = W_(128, 64, 6); break;
     default: return MX_EBADCFG;
   }
 #undef L_
+#undef W_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

@@ -6,6 +6,7 @@ import torch
 import torch.nn.functional as F
 
 import strix_halo_maxx_amd.ops as ops
+from strix_halo_maxx_amd import _lib
 
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
@@ -48,11 +49,13 @@ def test_gemm_bias_vs_fp32(dev, M, K, N):
     assert (y.float().cpu() - ref).abs().max().item() < 0.02 * ref.abs().max().item() + 1e-2
 
 
-@pytest.mark.parametrize("cfg", range(8))
+@pytest.mark.parametrize("cfg", range(15))
 @pytest.mark.parametrize("splits", [1, 3])
 def test_gemm_every_tile_config(dev, cfg, splits):
     """Every tile config, with and without split-K, on ragged M / N / K tails (K = 1000: the last k-step is partial
-    and reads A's padding columns against W's zero padding)."""
+    and reads A's padding columns against W's zero padding). Wave-split-K configs reject split-K."""
+    lib = _lib.load()
+    assert lib.mx_gemm_ncfg() == 15
     M, K, N = 300, 1000, 1152 + 68
     g = gen(cfg)
     x = torch.randn(M, K, generator=g).to(BF)
@@ -62,6 +65,10 @@ def test_gemm_every_tile_config(dev, cfg, splits):
     lin = ops.MxLin(w, b)
     lin.cfgs[M] = (cfg, splits)
     print(f"gemm cfg={cfg} splits={splits}", flush=True)
+    if splits > 1 and lib.mx_gemm_cfg_kind(cfg) == 1:
+        with pytest.raises(_lib.MxError, match="-3"):
+            lin(x.to(dev))
+        return
     y = lin(x.to(dev))
     assert rel(y, ref) < 5e-3
     y2 = lin(x.to(dev))  # counters re-armed: a second call gives the same bits
