@@ -73,7 +73,7 @@ def op_timing(vt, img, reps=5):
     def sym(l):
         cfg = l.cfgs.get(M) or ops._TUNED.get((M, l.N, l.Kw))
         return gemm_symbol(cfg[0])
-    attn_sym = "attn_fwd_kernel<80, 96, {}>".format("4, 1, 64" if ((T + 127) // 128) * H * B >= 512 else "1, 4, 32")
+    attn_sym = "attn_fwd_kernel<{}, {}>".format(hd, "4, 1, 64, 3" if ((T + 127) // 128) * H * B >= 512 else "1, 4, 128, 2")
     classes = {
         "ln": ("layernorm_kernel<4>", 0, lambda i, b: ops.layernorm(saved[i][0], *b["ln1"], eps=vt.eps, out=outs["h"])),
         "qkv": (sym(blocks[0]["qkv"]), 2 * M * D * 3 * D, lambda i, b: b["qkv"](saved[i][1], out=outs["qkv"])),

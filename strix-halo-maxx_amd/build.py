@@ -22,9 +22,14 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-ta
          "-packed-fp32-ops", "-Wno-unused-result", "-ffp-contract=off"]
 
 
+# Per-file extras. attn.hip: MFMA accumulators in ordinary VGPRs (the online softmax rescales and reads them with
+# VALU ops every key block; accumulation registers would need a copy each way).
+FILE_FLAGS = {"attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src):
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-I", CSRC, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-I", CSRC, "-c", src, "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in p.stderr.splitlines() if "packed-fp32-ops" not in l)
     if p.returncode != 0:

@@ -10,61 +10,76 @@
 //    cross-half exchange, and the online-softmax rescale of the output is lane-local.
 //  * O^T = V^T P^T: the score registers of S^T are, element for element, the B operand of this MFMA (the key
 //    order inside a k-group is the same permutation on both operands), so P never goes through LDS.
-//  * K is staged in LDS row-major [key][d] (row stride DK+8 bf16: conflict-free 16-byte operand reads); V is staged
-//    transposed [d][key] (row stride KB+4: conflict-free 8-byte reads). The next key block is prefetched into
-//    registers while the current one is consumed.
-//  * Workgroup = NQW query waves x NKW key waves. With NKW > 1 the key blocks are dealt round-robin to the key
-//    waves (each with its own LDS staging) and the partial (max, sum, O) of each query are merged at the end in fp32:
-//    this is how batch-1 shapes (16 heads x 729 queries = 368 query waves) still put >1000 waves on 256 CUs.
-//  * Head dim 72 pads to 80 along the QK contraction (5 k-steps) and to 96 output rows for PV (3 row tiles).
+//  * K and V blocks of KB keys are copied row-major ([key][d], 2 D bytes per row) into an S-stage LDS ring by the
+//    asynchronous LDS-DMA load, one or more blocks ahead of the MFMAs; every wave of the workgroup issues a share of
+//    each block's 16-byte chunks. The V^T operand of the PV product is read straight from the row-major block with
+//    the LDS transpose read (ds_read_b64_tr_b16). D = 64 rows are 128 bytes: their 16-byte chunks are XOR-swizzled
+//    by ((key >> 1) & 7) (the DMA fetches the global chunk that belongs at each slot) so operand reads spread over
+//    the 64 banks; D = 72 rows (144 bytes) need no swizzle.
+//  * Workgroup = NQW query waves x NKW key waves. Each KB-key block is split into NKW sub-blocks of KB / NKW keys;
+//    key wave w consumes sub-block w of every block, and the partial (max, sum, O) of each query are merged at the
+//    end in fp32. Batch-1 shapes (16 heads x 729 queries = 368 query waves) use NKW = 4 so that ~1500 waves run.
+//  * Head dim 72 pads to 80 along the QK contraction (5 k-steps; Q's padding is zero, so the neighbouring LDS bytes
+//    that K's padding reads are multiplied by 0) and to 96 output rows for PV (3 row tiles; rows >= 72 are dropped).
 // Numerics: fp32 scores and accumulators; P is rounded to bf16 before the PV product and the softmax denominator is
 // summed over those rounded values, so numerator and denominator use the same weights.
 #include "common.h"
 
 namespace {
 
-template <int DK, int DV, int NQW, int NKW, int KB>
-struct AttnSmem {
-  static constexpr int KS = DK + 8, VS = KB + 4;
-  static constexpr int GROUP = KB * KS + DV * VS;              // bf16 elements per key group
-  static constexpr int STAGE_BYTES = NKW * GROUP * 2;
-  static constexpr int COMB_BYTES = NKW > 1 ? NKW * NQW * (2 * 32 + (DV / 32) * 16 * 64) * 4 : 0;
-  static constexpr int BYTES = STAGE_BYTES > COMB_BYTES ? STAGE_BYTES : COMB_BYTES;
+template <int D, int NQW, int NKW, int KB, int S>
+struct AttnCfg {
+  static constexpr int DK = D == 72 ? 80 : 64;      // QK contraction (multiple of 16)
+  static constexpr int DV = D == 72 ? 96 : 64;      // PV output rows (multiple of 32)
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per K / V row
+  static constexpr bool SWZ = (D == 64);
+  static constexpr int KBW = KB / NKW;              // keys per key wave per block
+  static constexpr int NST = KBW / 32;              // S^T tiles per key wave per block
+  static constexpr int NCH = 2 * KB * CPR;          // K + V chunks per block
+  static constexpr int NI = (NCH + 63) / 64;        // DMA instructions per block
+  static constexpr int NIW = (NI + 3) / 4;          // ... per wave (instructions >= NI are padding)
+  // one ring stage: K block, V block, then the padding instructions' landing area, which also absorbs the last
+  // rows' over-reads (PV rows 72..95 of D = 72, QK chunk 9 of D = 72)
+  static constexpr int STAGE_B = NIW * 4 * 1024 + 1024;
+  static constexpr int RING_B = S * STAGE_B;
+  static constexpr int COMB_B = NKW > 1 ? NKW * NQW * (2 * 64 + (DV / 32) * 16 * 64) * 4 : 0;
+  static constexpr int BYTES = RING_B > COMB_B ? RING_B : COMB_B;
+  static_assert(KBW % 32 == 0 && NST >= 1, "key sub-block of whole 32-key tiles");
+  static_assert(NQW * NKW == 4, "4 waves");
+  static_assert(D == 64 || D == 72, "head dim");
 };
 
-template <int DK, int DV, int NQW, int NKW, int KB>
-__global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
+template <int D, int NQW, int NKW, int KB, int S>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(
     const uint16_t* __restrict__ Q, long sq_b, long sq_h, long sq_t,
     const uint16_t* __restrict__ K, long sk_b, long sk_h, long sk_t,
     const uint16_t* __restrict__ V, long sv_b, long sv_h, long sv_t,
     uint16_t* __restrict__ O, long so_b, long so_h, long so_t,
-    int Tq, int Tk, int D, float scale_log2, int qpos0, int causal_from) {
-  using SM = AttnSmem<DK, DV, NQW, NKW, KB>;
-  constexpr int KS = SM::KS, VS = SM::VS;
-  constexpr int GT = 64 * NQW;                    // threads per key group (they stage that group's blocks)
-  constexpr int KCH = DK / 8;                     // 16-byte chunks per staged K row
-  constexpr int KI = (KB * KCH + GT - 1) / GT;    // K chunks per thread
-  constexpr int VG = KB / 4;                      // 4-key groups per block
-  constexpr int VI = (VG * 9 + GT - 1) / GT;      // V items (4 keys x 8 d) per thread, d <= 72
-  constexpr int NST = KB / 32;                    // S^T tiles per block
-  __shared__ __attribute__((aligned(16))) uint16_t smem[SM::BYTES / 2];
+    int Tq, int Tk, int H, int nbh, float scale_log2, int qpos0, int causal_from) {
+  using C = AttnCfg<D, NQW, NKW, KB, S>;
+  constexpr int DK = C::DK, DV = C::DV, CPR = C::CPR, KBW = C::KBW, NST = C::NST, NIW = C::NIW;
+  constexpr int ROWB = 2 * D;  // bytes per staged row
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::BYTES];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qg = wave % NQW, kw = wave / NQW;
-  const int gtid = qg * 64 + lane;
   const int lr = lane & 31, hk = lane >> 5;
-  const int b = blockIdx.z, h = blockIdx.y;
-  const int qw0 = blockIdx.x * 32 * NQW + qg * 32;
+  // Tiles (query tile x, head h, batch b) in a 1-D grid. The dispatcher sends workgroup i to XCD i % 8; consecutive
+  // tile numbers (the query tiles of one head first) are placed on one XCD so each head's K / V is fetched into a
+  // single XCD's L2.
+  const int nqt = (Tq + 32 * NQW - 1) / (32 * NQW);
+  const int ntile = nqt * nbh;
+  const int per = ntile / 8, rem = ntile % 8, xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
+  const int tnum = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  const int qx = tnum % nqt, bh = tnum / nqt;
+  const int b = bh / H, h = bh % H;
+  const int qw0 = qx * 32 * NQW + qg * 32;
   const int qi = qw0 + lr;
   const int qpos = qpos0 + qi;
   const uint16_t* Qb = Q + b * sq_b + h * sq_h;
   const uint16_t* Kb = K + b * sk_b + h * sk_h;
   const uint16_t* Vb = V + b * sv_b + h * sv_h;
-  uint16_t* Ks = smem + kw * SM::GROUP;
-  uint16_t* Vt = Ks + KB * KS;
-  const int dch = D >> 3;
-
-  for (int i = gtid; i < (DV - D) * VS; i += GT) Vt[D * VS + i] = 0;
+  const uint32_t sbase = lds_off(smem);
 
   bf16x8 qf[DK / 16];
   {
@@ -80,179 +95,223 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
 
   int kend = Tk;
   if (causal_from < Tk) {
-    const int qlast = min((int)(blockIdx.x + 1) * 32 * NQW, Tq) - 1;
+    const int qlast = min((qx + 1) * 32 * NQW, Tq) - 1;
     kend = min(Tk, max(causal_from, qpos0 + qlast + 1));
   }
   const int nkb = (kend + KB - 1) / KB;
-  const int nrounds = (nkb + NKW - 1) / NKW;
 
-  // ---- staging registers for one key block of this key group
-  u32x4 kr[KI];
-  u32x4 vr[VI][4];
-  auto load_block = [&](int kb) {
-    const int k0 = kb * KB;
+  // ---- this lane's DMA chunks: instruction q = wave + 4 i of a block covers chunks 64 q .. 64 q + 63, which are all
+  // K chunks (q < KB * CPR / 64) or all V chunks; instructions q >= NI are padding and refetch the block's first chunk
+  static_assert((KB * CPR) % 64 == 0, "an instruction never straddles the K and V parts");
+  constexpr int NIK = KB * CPR / 64;  // K instructions per block
+  uint32_t doff[NIW];                 // byte offset of this lane's chunk from the block's first row
+  int dkey[NIW];                      // its key within the block
 #pragma unroll
-    for (int j = 0; j < KI; j++) {
-      const int i = gtid + j * GT;
-      const int key = i / KCH, c = i % KCH;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (i < KB * KCH && k0 + key < Tk && c < dch) v = *reinterpret_cast<const u32x4*>(Kb + (long)(k0 + key) * sk_t + c * 8);
-      kr[j] = v;
-    }
+  for (int i = 0; i < NIW; i++) {
+    const int q = wave + 4 * i;
+    const int ch = q < C::NI ? (q * 64 + lane) % (KB * CPR) : 0;
+    const int key = ch / CPR, slot = ch % CPR;
+    const int c = C::SWZ ? (slot ^ ((key >> 1) & 7)) : slot;
+    const long st_el = (q >= NIK && q < C::NI) ? sv_t : sk_t;
+    dkey[i] = key;
+    doff[i] = (uint32_t)(key * st_el * 2 + c * 16);
+  }
+  // rows past the last key are clamped to it (finite data; those keys are masked)
+  auto issue = [&](int kb, int st) {
+    const uint32_t base = sbase + (uint32_t)(st * C::STAGE_B);
+    const uint16_t* kbase = Kb + (long)kb * KB * sk_t;
+    const uint16_t* vbase = Vb + (long)kb * KB * sv_t;
+    const int lim = Tk - 1 - kb * KB;  // last valid key within the block
+    if (lim >= KB - 1) {
 #pragma unroll
-    for (int j = 0; j < VI; j++) {
-      const int i = gtid + j * GT;
-      const int g = i / 9, c = i % 9;
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int key = k0 + 4 * g + u;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (i < VG * 9 && c < dch && key < Tk) v = *reinterpret_cast<const u32x4*>(Vb + (long)key * sv_t + c * 8);
-        vr[j][u] = v;
+      for (int i = 0; i < NIW; i++) {
+        const int q = wave + 4 * i;
+        dma16s((q >= NIK && q < C::NI) ? vbase : kbase, doff[i], base + q * 1024);
       }
-    }
-  };
-  auto store_block = [&]() {
+    } else {
 #pragma unroll
-    for (int j = 0; j < KI; j++) {
-      const int i = gtid + j * GT;
-      if (i < KB * KCH) *reinterpret_cast<u32x4*>(&Ks[(i / KCH) * KS + (i % KCH) * 8]) = kr[j];
-    }
-#pragma unroll
-    for (int j = 0; j < VI; j++) {
-      const int i = gtid + j * GT;
-      const int g = i / 9, c = i % 9;
-      if (i < VG * 9 && c < dch) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const int w = e >> 1, sh = (e & 1) * 16;
-          u32x2 o;
-          o.x = ((vr[j][0][w] >> sh) & 0xffffu) | (((vr[j][1][w] >> sh) & 0xffffu) << 16);
-          o.y = ((vr[j][2][w] >> sh) & 0xffffu) | (((vr[j][3][w] >> sh) & 0xffffu) << 16);
-          *reinterpret_cast<u32x2*>(&Vt[(c * 8 + e) * VS + 4 * g]) = o;
-        }
+      for (int i = 0; i < NIW; i++) {
+        const int q = wave + 4 * i;
+        const bool isv = q >= NIK && q < C::NI;
+        const long st_el = isv ? sv_t : sk_t;
+        const int key = dkey[i];
+        const uint32_t off = doff[i] - (uint32_t)((key > lim ? key - lim : 0) * st_el * 2);
+        dma16s(isv ? vbase : kbase, off, base + q * 1024);
       }
     }
   };
 
   float m_run = -1e30f, l_run = 0.f;
+  bool first = true;  // no key block consumed yet by this wave (O and l are still zero)
   f32x16 oacc[DV / 32];
 #pragma unroll
   for (int i = 0; i < DV / 32; i++)
 #pragma unroll
     for (int e = 0; e < 16; e++) oacc[i][e] = 0.f;
 
-  if (kw < nkb) load_block(kw);
-  for (int r = 0; r < nrounds; r++) {
-    const int kb = r * NKW + kw;
-    __syncthreads();
-    if (kb < nkb) store_block();
-    __syncthreads();
-    if (kb + NKW < nkb) load_block(kb + NKW);
-    if (kb >= nkb) continue;
-    const int k0 = kb * KB;
+#pragma unroll
+  for (int s = 0; s < S - 1; s++)
+    if (s < nkb) issue(s, s);
 
-    // ---- S^T = K Q^T for NST x 32 keys
+  for (int kb = 0; kb < nkb; kb++) {
+    wait_stages<NIW, S - 2>(nkb - 1 - kb);
+    __syncthreads();
+    if (kb + S - 1 < nkb) issue(kb + S - 1, (kb + S - 1) % S);
+    const int k0 = kb * KB + kw * KBW;  // first key of this wave's sub-block
+    if (k0 >= kend) continue;
+    const uint8_t* Kst = smem + (kb % S) * C::STAGE_B + kw * KBW * ROWB;
+    const uint8_t* Vst = smem + (kb % S) * C::STAGE_B + KB * ROWB + kw * KBW * ROWB;
+
+    // ---- S^T = K Q^T for NST x 32 keys (the NST chains interleave)
     f32x16 st[NST];
-#pragma unroll
-    for (int kt = 0; kt < NST; kt++) {
-#pragma unroll
-      for (int e = 0; e < 16; e++) st[kt][e] = 0.f;
-#pragma unroll
-      for (int s = 0; s < DK / 16; s++) {
-        const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ks[(kt * 32 + lr) * KS + 16 * s + 8 * hk]));
-        st[kt] = mfma32(a, qf[s], st[kt]);
-      }
-    }
-    // ---- scale, mask, online softmax
-    const bool need_mask = (k0 + KB > Tk) || (causal_from < Tk && k0 + KB > causal_from && k0 + KB - 1 > qpos0 + qw0);
-    float mx = -1e30f;
 #pragma unroll
     for (int kt = 0; kt < NST; kt++)
 #pragma unroll
-      for (int r2 = 0; r2 < 16; r2++) {
-        float v = st[kt][r2] * scale_log2;
-        if (need_mask) {
-          const int key = k0 + kt * 32 + 8 * (r2 >> 2) + 4 * hk + (r2 & 3);
-          if (!(key < Tk && (key < causal_from || key <= qpos))) v = -INFINITY;
-        }
-        st[kt][r2] = v;
-        mx = fmaxf(mx, v);
+      for (int e = 0; e < 16; e++) st[kt][e] = 0.f;
+#pragma unroll
+    for (int s = 0; s < DK / 16; s++)
+#pragma unroll
+      for (int kt = 0; kt < NST; kt++) {
+        const int key = kt * 32 + lr;  // within the sub-block; the swizzle uses the key within the block
+        const int c = 2 * s + hk;
+        const int slot = C::SWZ ? (c ^ (((kw * KBW + key) >> 1) & 7)) : c;
+        const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(Kst + key * ROWB + slot * 16));
+        st[kt] = mfma32(a, qf[s], st[kt]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
-    m_run = mnew;
+    // ---- mask, online softmax. Scores stay unscaled until the exponent: p = exp2(scale_log2 s - m) with m the
+    // running max in scaled units. The running max is only raised (and O, l rescaled) when a query's block max
+    // exceeds it by more than 8, i.e. the exponentials of a stale max stay <= 256; the normalisation at the end is
+    // unaffected.
+    const bool need_mask = (k0 + KBW > Tk) || (causal_from < Tk && k0 + KBW > causal_from && k0 + KBW - 1 > qpos0 + qw0);
+    float mx = -INFINITY;
+    if (need_mask) {
+      const int lim = min(Tk, max(causal_from, qpos + 1));  // keys < lim are visible to this query
+#pragma unroll
+      for (int kt = 0; kt < NST; kt++)
+#pragma unroll
+        for (int r2 = 0; r2 < 16; r2++) {
+          const int key = k0 + kt * 32 + 8 * (r2 >> 2) + 4 * hk + (r2 & 3);
+          const float v = key < lim ? st[kt][r2] : -INFINITY;
+          st[kt][r2] = v;
+          mx = fmaxf(mx, v);
+        }
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < NST; kt++)
+#pragma unroll
+        for (int r2 = 0; r2 < 16; r2++) mx = fmaxf(mx, st[kt][r2]);
+    }
+    mx = halves_max(mx) * scale_log2;
+    const bool grow = mx > m_run + 8.f;
+    if (__any(grow)) {
+      const float mnew = grow ? mx : m_run;
+      if (!first) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < DV / 32; i++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) oacc[i][e] *= alpha;
+      }
+      m_run = mnew;
+    }
+    first = false;
     float sum = 0.f;
     uint32_t pk[NST][8];
 #pragma unroll
     for (int kt = 0; kt < NST; kt++)
 #pragma unroll
       for (int r2 = 0; r2 < 16; r2 += 2) {
-        const uint32_t w = pack2(__builtin_amdgcn_exp2f(st[kt][r2] - mnew), __builtin_amdgcn_exp2f(st[kt][r2 + 1] - mnew));
+        const uint32_t w = pack2(__builtin_amdgcn_exp2f(__builtin_fmaf(st[kt][r2], scale_log2, -m_run)),
+                                 __builtin_amdgcn_exp2f(__builtin_fmaf(st[kt][r2 + 1], scale_log2, -m_run)));
         sum += lo_bf(w) + hi_bf(w);
         pk[kt][r2 >> 1] = w;
       }
-    sum += __shfl_xor(sum, 32, 64);
-    l_run = l_run * alpha + sum;
-#pragma unroll
-    for (int i = 0; i < DV / 32; i++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) oacc[i][e] *= alpha;
+    l_run += halves_sum(sum);
 
-    // ---- O^T += V^T P^T ; k-step (kt, s) covers keys kt*32 + 16 s + {4hk..4hk+3, 8+4hk..8+4hk+3}
+    // ---- O^T += V^T P^T ; k-step (kt, s) covers keys kt*32 + 16 s + {4hk..4hk+3, 8+4hk..8+4hk+3}. The V^T
+    // operand comes from two transpose reads: lane j = lane & 15 of each 16-lane group points at
+    // V[first key + (j >> 2)][d0 + 4 (j & 3)], d0 = 32 dt + 16 ((lane >> 4) & 1).
+    const int jr = (lane & 15) >> 2, jc = 4 * (lane & 3) + 16 * ((lane >> 4) & 1);
 #pragma unroll
     for (int kt = 0; kt < NST; kt++)
 #pragma unroll
       for (int s = 0; s < 2; s++) {
-        u32x4 pb = {pk[kt][4 * s], pk[kt][4 * s + 1], pk[kt][4 * s + 2], pk[kt][4 * s + 3]};
+        const u32x4 pb = {pk[kt][4 * s], pk[kt][4 * s + 1], pk[kt][4 * s + 2], pk[kt][4 * s + 3]};
         const bf16x8 bp = as_bf16x8(pb);
-        const int kk = kt * 32 + 16 * s + 4 * hk;
+        const int r0 = kt * 32 + 16 * s + 4 * hk + jr;  // within the sub-block
 #pragma unroll
         for (int dt = 0; dt < DV / 32; dt++) {
-          const uint16_t* vrow = &Vt[(dt * 32 + lr) * VS + kk];
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-          u32x4 va = {lo.x, lo.y, hi.x, hi.y};
+          const int col = dt * 32 + jc;
+          u32x2 lo, hi;
+          if constexpr (C::SWZ) {
+            const int kr0 = kw * KBW + r0, kr1 = kr0 + 8;
+            lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(
+                Vst + r0 * ROWB + ((((col >> 3) ^ ((kr0 >> 1) & 7)) << 4) | ((col & 7) * 2))));
+            hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(
+                Vst + (r0 + 8) * ROWB + ((((col >> 3) ^ ((kr1 >> 1) & 7)) << 4) | ((col & 7) * 2))));
+          } else {
+            lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(Vst + r0 * ROWB + col * 2));
+            hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(Vst + (r0 + 8) * ROWB + col * 2));
+          }
+          const u32x4 va = {lo.x, lo.y, hi.x, hi.y};
           oacc[dt] = mfma32(as_bf16x8(va), bp, oacc[dt]);
         }
       }
   }
 
   if constexpr (NKW > 1) {
-    // ---- merge the key waves' partial results (fp32) through LDS
+    // ---- merge the key waves' partial results (fp32) through LDS: every key wave finishes 1 / NKW of the output
+    // rows (d) of its query tile, summing the partials in key-wave order
     constexpr int OW = (DV / 32) * 16 * 64;  // floats of O per wave
+    constexpr int NE = (DV / 32) * 16;       // O registers per lane
+    static_assert(NE % NKW == 0, "registers split evenly over the key waves");
     float* cm = reinterpret_cast<float*>(smem);
-    float* cl = cm + NKW * NQW * 32;
-    float* co = cl + NKW * NQW * 32;
+    float* cl = cm + NKW * NQW * 64;
+    float* co = cl + NKW * NQW * 64;
+    wait_vm<0>();
     __syncthreads();
     const int slot = kw * NQW + qg;
-    if (hk == 0) { cm[slot * 32 + lr] = m_run; cl[slot * 32 + lr] = l_run; }
+    cm[slot * 64 + lane] = m_run;
+    cl[slot * 64 + lane] = l_run;
 #pragma unroll
     for (int dt = 0; dt < DV / 32; dt++)
 #pragma unroll
       for (int e = 0; e < 16; e++) co[slot * OW + (dt * 16 + e) * 64 + lane] = oacc[dt][e];
     __syncthreads();
-    if (kw != 0) return;
     float M = -1e30f;
 #pragma unroll
-    for (int k = 0; k < NKW; k++) M = fmaxf(M, cm[(k * NQW + qg) * 32 + lr]);
-    float L = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DV / 32; dt++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) oacc[dt][e] = 0.f;
+    for (int k = 0; k < NKW; k++) M = fmaxf(M, cm[(k * NQW + qg) * 64 + lane]);
+    float L = 0.f, f[NKW];
 #pragma unroll
     for (int k = 0; k < NKW; k++) {
-      const int sl = k * NQW + qg;
-      const float f = __builtin_amdgcn_exp2f(cm[sl * 32 + lr] - M);
-      L += cl[sl * 32 + lr] * f;
-#pragma unroll
-      for (int dt = 0; dt < DV / 32; dt++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) oacc[dt][e] += co[sl * OW + (dt * 16 + e) * 64 + lane] * f;
+      f[k] = __builtin_amdgcn_exp2f(cm[(k * NQW + qg) * 64 + lane] - M);
+      L += cl[(k * NQW + qg) * 64 + lane] * f[k];
     }
-    l_run = L;
+    if (qi >= Tq) return;
+    const float inv = 1.f / L;
+    uint16_t* orow = O + b * so_b + (long)qi * so_t + h * so_h;
+    // this wave's share: registers r = 4 g' of 4 consecutive output rows, g' = kw, kw + NKW, ...
+#pragma unroll
+    for (int g2 = kw; g2 < NE / 4; g2 += NKW) {
+      float o4[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < NKW; k++) acc += co[(k * NQW + qg) * OW + (4 * g2 + u) * 64 + lane] * f[k];
+        o4[u] = acc * inv;
+      }
+      const int dt = g2 / 4, g = g2 % 4;
+      const int d = dt * 32 + 8 * g + 4 * hk;
+      if (d < D) {
+        u32x2 o;
+        o.x = pack2(o4[0], o4[1]);
+        o.y = pack2(o4[2], o4[3]);
+        *reinterpret_cast<u32x2*>(orow + d) = o;
+      }
+    }
+    return;
   }
 
   if (qi >= Tq) return;
@@ -280,12 +339,13 @@ struct Args {
   float sl2;
 };
 
-template <int DK, int DV, int NQW, int NKW, int KB>
+template <int D, int NQW, int NKW, int KB, int S>
 hipError_t launch(hipStream_t st, const Args& a) {
-  dim3 g((a.Tq + 32 * NQW - 1) / (32 * NQW), a.H, a.B);
-  hipLaunchKernelGGL((attn_fwd_kernel<DK, DV, NQW, NKW, KB>), g, dim3(64 * NQW * NKW), 0, st, a.Q, a.sq_b, a.sq_h,
+  const long nt = (long)((a.Tq + 32 * NQW - 1) / (32 * NQW)) * a.H * a.B;
+  if (nt > 0x7fffffffL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((attn_fwd_kernel<D, NQW, NKW, KB, S>), dim3((unsigned)nt), dim3(256), 0, st, a.Q, a.sq_b, a.sq_h,
                      a.sq_t, a.K, a.sk_b, a.sk_h, a.sk_t, a.V, a.sv_b, a.sv_h, a.sv_t, a.O, a.so_b, a.so_h, a.so_t,
-                     a.Tq, a.Tk, a.D, a.sl2, a.qpos0, a.causal_from);
+                     a.Tq, a.Tk, a.H, a.H * a.B, a.sl2, a.qpos0, a.causal_from);
   return hipGetLastError();
 }
 
@@ -312,11 +372,11 @@ extern "C" int mx_sdpa(hipStream_t st, const uint16_t* Q, long sq_b, long sq_h, 
   if ((sq_b | sq_h | sk_b | sk_h | sv_b | sv_h) % 8 || so_h % 4 || so_b % 4) return MX_ESHAPE;
   const Args a{Q, K, V, O, sq_b, sq_h, sq_t, sk_b, sk_h, sk_t, sv_b, sv_h, sv_t, so_b, so_h, so_t,
                B, H, Tq, Tk, D, qpos0, causal_from, scale * 1.4426950408889634f};
-  // many (batch, head, 128-query) tiles: 4 query waves share each staged key block; few: split the keys over
-  // 4 waves per 32 queries so the grid still fills the GPU
+  // many (batch, head, 128-query) tiles: 4 query waves share each staged key block; few: split every 128-key block
+  // over 4 key waves per 32 queries so the grid still fills the GPU
   const long wg4 = (long)((Tq + 127) / 128) * H * B;
   hipError_t e;
-  if (D == 72) e = (wg4 >= 512) ? launch<80, 96, 4, 1, 64>(st, a) : launch<80, 96, 1, 4, 32>(st, a);
-  else e = (wg4 >= 512) ? launch<64, 64, 4, 1, 64>(st, a) : launch<64, 64, 1, 4, 32>(st, a);
+  if (D == 72) e = (wg4 >= 512) ? launch<72, 4, 1, 64, 3>(st, a) : launch<72, 1, 4, 128, 2>(st, a);
+  else e = (wg4 >= 512) ? launch<64, 4, 1, 64, 3>(st, a) : launch<64, 1, 4, 128, 2>(st, a);
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

@@ -65,3 +65,64 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+
+// ---- asynchronous global -> LDS copies (LDS-DMA) and their completion waits
+#pragma clang diagnostic ignored "-Winline-asm"
+
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) void*)p);
+}
+
+// 64 lanes x 16 bytes from global (per-lane address) into LDS at m0 = lds (wave-uniform) + 16 * lane. The compiler
+// does not see the LDS write: the caller waits for it with wait_vm / wait_stages and a barrier before reading.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+// Same copy with a wave-uniform 64-bit base (SGPR pair) and a per-lane 32-bit byte offset.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint64_t bu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bu),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait until at most min(ahead, A) ring stages of LPS loads each are still in flight.
+template <int LPS, int A>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      wait_vm<A * LPS>();
+      return;
+    }
+    wait_stages<LPS, A - 1>(ahead);
+  } else {
+    wait_vm<0>();
+  }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+// LDS transpose read (ds_read_b64_tr_b16). Within each 16-lane group, lane j = a + 4 e (a, e in 0..3) supplies the
+// address of 4 consecutive bf16 of some row; lane 4 a' + b then receives element b of the reads of lanes
+// a', a' + 4, a' + 8, a' + 12 (in that order). With lane a + 4 e pointing at M[r0 + e][c0 + 4 a], every lane j of
+// the group receives the column M[r0 .. r0 + 3][c0 + j].
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// Combine the two 32-lane halves of a wave (v_permlane32_swap): every lane receives (v[l & 31], v[(l & 31) + 32]),
+// so both halves compute the same low-then-high result.
+__device__ __forceinline__ float halves_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}

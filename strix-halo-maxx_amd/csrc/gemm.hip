@@ -31,38 +31,9 @@
 // columns [K, Kw). A chunks beyond K are fetched from column 0 of the same row (finite data times W's zeros).
 #include "common.h"
 
-#pragma clang diagnostic ignored "-Winline-asm"
-
 namespace {
 
 constexpr int BK = 64;
-
-__device__ __forceinline__ uint32_t lds_off(const void* p) {
-  return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) void*)p);
-}
-
-// 64 lanes x 16 bytes from global (per-lane address) into LDS at m0 = lds (wave-uniform) + 16 * lane.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N <= 63, "vmcnt field");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// Wait until at most min(ahead, A) ring stages of LPS loads each are still in flight.
-template <int LPS, int A>
-__device__ __forceinline__ void wait_stages(int ahead) {
-  if constexpr (A > 0) {
-    if (ahead >= A) {
-      wait_vm<A * LPS>();
-      return;
-    }
-    wait_stages<LPS, A - 1>(ahead);
-  } else {
-    wait_vm<0>();
-  }
-}
 
 // Epilogue for output row m, columns n .. n+3 from fp32 sums s[0..3]: + bias, round to bf16, optional activation
 // (rounded again), optional + residual (fp32 add, rounded once more); act 3 writes the gated pair results to

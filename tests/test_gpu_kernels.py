@@ -119,7 +119,8 @@ def _sdpa_ref(q, k, v, scale, mask=None):
     return torch.softmax(s, dim=-1) @ v
 
 
-@pytest.mark.parametrize("B,H,T,D", [(1, 16, 729, 72), (2, 16, 729, 72), (1, 12, 1280, 64), (1, 32, 730, 64), (1, 4, 33, 72)])
+@pytest.mark.parametrize("B,H,T,D", [(1, 16, 729, 72), (2, 16, 729, 72), (1, 12, 1280, 64), (1, 32, 730, 64), (1, 4, 33, 72),
+                                     (6, 16, 729, 72), (5, 12, 1280, 64)])
 def test_sdpa_strided_views(dev, B, H, T, D):
     """q, k, v as strided views of a fused qkv output (the vision layout, md2fast.py:154)."""
     g = gen(B * 100 + T)

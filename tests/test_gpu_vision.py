@@ -65,14 +65,23 @@ def test_one_block_config0(dev):
     assert good, st
 
 
-def test_batch2_block_matches_batch1(dev):
-    """Batching crops stacks them as token rows; each crop's result must not depend on its batch neighbours."""
+def test_batch2_crops_independent(dev):
+    """Batching crops stacks them as token rows; a crop's result must not depend on its batch neighbours. Changing
+    crop 0 leaves crop 1's output bit-identical (same batch size, so the same kernels and tiles), and crop 1 batched
+    agrees with crop 1 alone to the per-block tolerance (batch 1 and batch 2 may pick different GEMM tilings, whose
+    summation orders can differ in the last bit)."""
     w = S.vision_weights(0, layers=1)
     x = S.activations(2, (2, 729, 1152))
     vt = md2.VisionTower(w)
     y2 = vt.block(vt.blocks[0], x.view(-1, 1152).to(dev), 2).view(2, 729, 1152).cpu()
+    xb = x.clone()
+    xb[0] = S.activations(3, (1, 729, 1152))[0]
+    y2b = vt.block(vt.blocks[0], xb.view(-1, 1152).to(dev), 2).view(2, 729, 1152).cpu()
+    assert torch.equal(y2[1], y2b[1])
+    assert not torch.equal(y2[0], y2b[0])
     y1 = vt.block(vt.blocks[0], x[1].reshape(729, 1152).to(dev), 1).view(729, 1152).cpu()
-    assert torch.equal(y2[1], y1)
+    good, st = ok(y2[1], y1)
+    assert good, st
 
 
 def test_tower_per_block_and_end_to_end(dev, full):
