@@ -30,7 +30,7 @@ def vision_flops_per_frame(layers=27, T=729, D=1152, F=4304, H=16, hd=72, Kp=588
 
 
 # LDS ring depth of each GEMM tile config (the kernel template's last argument)
-GEMM_STAGES = {0: 4, 1: 4, 2: 4, 3: 4, 4: 3, 5: 3, 6: 3, 7: 2, 8: 4, 9: 4, 10: 4, 11: 8, 12: 6, 13: 6, 14: 6}
+GEMM_STAGES = {0: 4, 1: 4, 2: 4, 3: 4, 4: 3, 5: 3, 6: 3, 7: 2, 8: 4, 9: 4, 10: 4, 11: 3, 12: 2, 13: 6, 14: 2}
 
 
 def gemm_symbol(cfg):
@@ -43,8 +43,9 @@ def gemm_symbol(cfg):
 
 
 def op_timing(vt, img, reps=5):
-    """Per-kernel launch time inside the tower: one eager pass keeps every block's real operands, then for each op
-    class a HIP graph of its 27 launches (each on its own block's weights and activations, as in the tower) is
+    """Per-kernel launch time inside the tower (its split-K form: partial GEMMs for the two residual Linears, each
+    reduced by the fused residual-LayerNorm kernel): one eager pass keeps every block's real operands, then for each
+    op class a HIP graph of its 27 launches (each on its own block's weights and activations, as in the tower) is
     replayed `reps` times between two HIP events recorded on the stream the kernels run on. Returns
     {label: [total_ms, launches, flops_per_launch, kernel symbol]}."""
     import torch
@@ -55,32 +56,43 @@ def op_timing(vt, img, reps=5):
     blocks = vt.blocks
     saved = []
     x = vt.embed(img)
-    for b in blocks:
-        h = ops.layernorm(x, *b["ln1"], eps=vt.eps)
+    h = ops.layernorm(x, *blocks[0]["ln1"], eps=vt.eps)
+    for i, b in enumerate(blocks):
         qkv = b["qkv"](h)
         q5 = qkv.view(B, T, 3, H, hd)
-        q, k, v = (q5[:, :, i].transpose(1, 2) for i in range(3))
-        a = vt.attn(q, k, v)
-        x1 = b["proj"](a.view(M, D), res=x)
-        h2 = ops.layernorm(x1, *b["ln2"], eps=vt.eps)
+        q, k, v = (q5[:, :, j].transpose(1, 2) for j in range(3))
+        a = vt.attn(q, k, v).view(M, D)
+        pp = b["proj"].partial(a)
+        x1, h2 = ops.residual_layernorm(pp, b["proj"].b, x, b["ln2"], eps=vt.eps)
         f = b["fc1"](h2, gelu=True)
-        saved.append((x, h, qkv, (q, k, v), a, x1, h2, f))
-        x = b["fc2"](f, res=x1)
+        pf = b["fc2"].partial(f)
+        nxt = blocks[i + 1]["ln1"] if i + 1 < len(blocks) else vt.post_ln
+        x2, hn = ops.residual_layernorm(pf, b["fc2"].b, x1, nxt, eps=vt.eps)
+        saved.append((x, h, (q, k, v), a, pp, x1, h2, f, pf, nxt))
+        x, h = x2, hn
     outs = {n: torch.empty(M, w, device=x.device, dtype=torch.bfloat16)
             for n, w in (("h", D), ("qkv", 3 * D), ("x", D), ("f", blocks[0]["fc1"].N))}
     a_out = torch.empty(B, T, D, device=x.device, dtype=torch.bfloat16)
+    pp_out, pf_out = torch.empty_like(saved[0][4]), torch.empty_like(saved[0][8])
 
     def sym(l):
         cfg = l.cfgs.get(M) or ops._TUNED.get((M, l.N, l.Kw))
         return gemm_symbol(cfg[0])
+
+    def psym(l):
+        cfg, sp = ops._TUNED_P[(M, l.N, l.Kw)]
+        return f"{gemm_symbol(cfg)} x{sp} splits"
     attn_sym = "attn_fwd_kernel<{}, {}>".format(hd, "4, 1, 64, 3" if ((T + 127) // 128) * H * B >= 512 else "1, 4, 128, 2")
     classes = {
-        "ln": ("layernorm_kernel<4>", 0, lambda i, b: ops.layernorm(saved[i][0], *b["ln1"], eps=vt.eps, out=outs["h"])),
         "qkv": (sym(blocks[0]["qkv"]), 2 * M * D * 3 * D, lambda i, b: b["qkv"](saved[i][1], out=outs["qkv"])),
-        "attn": (attn_sym, 4 * B * H * T * T * hd, lambda i, b: ops.sdpa(*saved[i][3], out=a_out)),
-        "proj": (sym(blocks[0]["proj"]), 2 * M * D * D, lambda i, b: b["proj"](saved[i][4].view(M, D), res=saved[i][0], out=outs["x"])),
+        "attn": (attn_sym, 4 * B * H * T * T * hd, lambda i, b: ops.sdpa(*saved[i][2], out=a_out)),
+        "proj": (psym(blocks[0]["proj"]), 2 * M * D * D, lambda i, b: b["proj"].partial(saved[i][3], out=pp_out)),
+        "res_ln2": ("residual_layernorm_kernel<3>", 0, lambda i, b: ops.residual_layernorm(
+            saved[i][4], b["proj"].b, saved[i][0], b["ln2"], eps=vt.eps, x_out=outs["x"], y_out=outs["h"])),
         "fc1": (sym(blocks[0]["fc1"]), 2 * M * D * blocks[0]["fc1"].N, lambda i, b: b["fc1"](saved[i][6], gelu=True, out=outs["f"])),
-        "fc2": (sym(blocks[0]["fc2"]), 2 * M * blocks[0]["fc2"].K * D, lambda i, b: b["fc2"](saved[i][7], res=saved[i][5], out=outs["x"])),
+        "fc2": (psym(blocks[0]["fc2"]), 2 * M * blocks[0]["fc2"].K * D, lambda i, b: b["fc2"].partial(saved[i][7], out=pf_out)),
+        "res_ln1": ("residual_layernorm_kernel<3>", 0, lambda i, b: ops.residual_layernorm(
+            saved[i][8], b["fc2"].b, saved[i][5], saved[i][9], eps=vt.eps, x_out=outs["x"], y_out=outs["h"])),
     }
     res = {}
     for name, (ksym, fl, fn) in classes.items():

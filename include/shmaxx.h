@@ -41,9 +41,16 @@ int mx_gemm_pick(int M, int N, int Kw);
 /* Number of tile configs / the (BM, BN) tile of one. Replaces bf16gemm_ncfg (i8gemm.hip:553). */
 int mx_gemm_ncfg(void);
 int mx_gemm_cfg_tile(int cfg, int* bm, int* bn);
-/* Kernel kind of a tile config: 0 = LDS-shared tile (split-K capable), 1 = wave-split K (splits must be 1), or
- * MX_EBADCFG. No counterpart in the reference (its configs are all one kind). */
+/* Kernel kind of a tile config: 0 = LDS-shared tile (split-K capable), 1 = wave-split K (splits must be 1 in
+ * mx_gemm_bf16; mx_gemm_bf16_partial splits K over workgroups), or MX_EBADCFG. No counterpart in the reference (its
+ * configs are all one kind). */
 int mx_gemm_cfg_kind(int cfg);
+/* Raw split-K partials for a kind-1 cfg: P[s][m][n] = sum over split s's k-steps of A[m,k] W[n,k] (fp32; row stride
+ * ldp, split stride p_split), no bias / activation / residual; the consumer adds the splits in order
+ * (mx_residual_layernorm). No counterpart in the reference (no split-K there): it replaces the GEMM half of the
+ * residual Linears x + proj(a) and x + fc2(f) (moondream/gpu/md2fast.py:152-157). */
+int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                         float* P, long ldp, long p_split, int M, int N, int K, int Kw);
 /* Split-K workspace a (cfg, splits) call needs: fp32 elements / tile counters. Replaces the fixed-size
  * workspace() of moondream/gpu/hgemm.py:78-83. */
 long mx_gemm_ws_elems(int cfg, int splits, int M, int N);
@@ -66,6 +73,12 @@ int mx_sdpa_check(const void* Q, long sq_t, const void* K, long sk_t, const void
  * TRecViT ln_1 / ln_2 / encoder_norm (numerics restated at tapnext/npu/pack8.py:232-238). */
 int mx_layernorm(hipStream_t st, const uint16_t* X, long ldx, const uint16_t* gamma, const uint16_t* beta, uint16_t* Y,
                  long ldy, int rows, int D, float eps);
+/* x = bf16(bf16(sum_s P[s] + bias) + R) -> Xo, then y = LayerNorm(x) -> Y (skipped when gamma is null): the
+ * epilogue of a split-K residual Linear fused with the LayerNorm that reads its output. Replaces the residual add +
+ * next _ln of the vision block loop (moondream/gpu/md2fast.py:152-157, :43-44); bias fp32 or null. */
+int mx_residual_layernorm(hipStream_t st, const float* P, int nsplit, long p_split, long ldp, const float* bias,
+                          const uint16_t* R, long ldr, uint16_t* Xo, long ldxo, const uint16_t* gamma,
+                          const uint16_t* beta, uint16_t* Y, long ldy, int rows, int D, float eps);
 /* TRecViT RMSNorm with torch's bf16 rounding; sc1 = bf16(scale + 1). Replaces temporal_pre_norm / channel_pre_norm
  * (tapnext/npu/step8.py:474, :480; numerics tapnext/npu/pack8.py:222-229). */
 int mx_rmsnorm(hipStream_t st, const uint16_t* X, long ldx, const uint16_t* sc1, uint16_t* Y, long ldy, int rows, int D,

@@ -25,9 +25,11 @@ SIGNATURES = {
     "mx_gemm_ncfg": [],
     "mx_gemm_cfg_tile": [I, ctypes.POINTER(I), ctypes.POINTER(I)],
     "mx_gemm_cfg_kind": [I],
+    "mx_gemm_bf16_partial": [P, I, I, P, L, P, L, P, L, L, I, I, I, I],
     "mx_sdpa": [P, P, L, L, L, P, L, L, L, P, L, L, L, P, L, L, L, I, I, I, I, I, F, I, I],
     "mx_sdpa_check": [P, L, P, L, P, L, P, L, I, I, I, I, I],
     "mx_layernorm": [P, P, L, P, P, P, L, I, I, F],
+    "mx_residual_layernorm": [P, P, I, L, L, P, P, L, P, L, P, P, P, L, I, I, F],
     "mx_rmsnorm": [P, P, L, P, P, L, I, I, F],
     "mx_patchify_u8": [P, P, P, L, I, I, I, I],
     "mx_rope_kv": [P, P, L, P, P, P, P, I, I, I, I, I, I, I],

@@ -38,11 +38,18 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// tanh(u) = 1 - 2 / (exp(2 u) + 1) on the hardware exp2 (v_exp_f32) and reciprocal (v_rcp_f32): saturates to +-1
+// for large |u| (exp2 -> inf / 0) and is within ~2e-7 of tanh everywhere in absolute terms, far below the bf16
+// rounding that follows every use here. A handful of VALU ops instead of a libm polynomial with range reduction.
+__device__ __forceinline__ float tanh_fast(float u) {
+  const float e = __builtin_amdgcn_exp2f(u * 2.885390081777927f);  // 2 / ln 2
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
 // GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), evaluated in fp32 like torch's
 // F.gelu(x, approximate="tanh") on a bf16 tensor (upcast, compute, round once).
 __device__ __forceinline__ float gelu_tanh(float x) {
   float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(u));
+  return 0.5f * x * (1.0f + tanh_fast(u));
 }
 // GELU, erf form (torch nn.GELU() default): 0.5 x (1 + erf(x / sqrt 2)).
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }

@@ -224,11 +224,12 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
 
 // Wave-split-K kernel (see the header): 4 waves share the LDS ring of a BM x BN tile; wave w multiplies the k
 // columns [16 w, 16 w + 16) of every 64-wide k-step into its own copy of the whole tile.
-template <int BM, int BN, int S>
-__global__ __launch_bounds__(256) void gemm_ks_kernel(
+template <int BM, int BN, int S, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_ks_kernel(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
     const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
-    uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols, int tiles_m, int tiles_n) {
+    uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols, int tiles_m, int tiles_n,
+    int splits, int kt_per_split, float* __restrict__ P, long ldp, long p_split) {
   static_assert(S >= 2, "at least a double buffer");
   constexpr int FM = BM / 32, FN = BN / 32;
   constexpr int QA = BM / 32, QW = BN / 32;  // DMA instructions per wave per stage
@@ -241,13 +242,15 @@ __global__ __launch_bounds__(256) void gemm_ks_kernel(
   uint16_t* smem = reinterpret_cast<uint16_t*>(smem_b);
   f32x4* red = reinterpret_cast<f32x4*>(smem_b);
 
-  const int nt = tiles_m * tiles_n;
+  const int nt = tiles_m * tiles_n, ntot = nt * splits;
   const int b = blockIdx.x;
-  const int per = nt / 8, rem = nt % 8, xcd = b % 8, idx = b / 8;
+  const int per = ntot / 8, rem = ntot % 8, xcd = b % 8, idx = b / 8;
   const int t = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
-  const int tile_m = t % tiles_m, tile_n = t / tiles_m;
+  const int tile = t % nt, split = t / nt;
+  const int tile_m = tile % tiles_m, tile_n = tile / tiles_m;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
-  const int nk = Kw / BK;
+  const int kt0 = split * kt_per_split;
+  const int nk = min(Kw / BK, kt0 + kt_per_split) - kt0;  // k-steps of this split
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, hk = lane >> 5;
   const uint32_t sbase = lds_off(smem);
@@ -280,13 +283,13 @@ __global__ __launch_bounds__(256) void gemm_ks_kernel(
 
 #pragma unroll
   for (int s = 0; s < S - 1; s++)
-    if (s < nk) issue(s, s);
+    if (s < nk) issue(kt0 + s, s);
 
   const int c = 2 * wave + hk;  // this lane's 16-byte chunk of each 128-byte LDS row
   for (int it = 0; it < nk; it++) {
     wait_stages<LPS, S - 2>(nk - 1 - it);
     __syncthreads();
-    if (it + S - 1 < nk) issue(it + S - 1, (it + S - 1) % S);
+    if (it + S - 1 < nk) issue(kt0 + it + S - 1, (it + S - 1) % S);
     const uint16_t* As = smem + (it % S) * STAGE;
     const uint16_t* Ws = As + BM * BK;
     bf16x8 af[FM], wf[FN];
@@ -344,8 +347,12 @@ __global__ __launch_bounds__(256) void gemm_ks_kernel(
     const int m = m0 + j * 32 + lr;
     const int n = n0 + i * 32 + 8 * g + 4 * hk;
     if (m < M && n < N) {
-      const float a4[4] = {v[0], v[1], v[2], v[3]};
-      epi4(a4, m, n, bias, R, ldr, r_rows, C, ldc, act, act_ncols);
+      if (P) {
+        *reinterpret_cast<f32x4*>(P + split * p_split + (long)m * ldp + n) = v;  // raw partial sums
+      } else {
+        const float a4[4] = {v[0], v[1], v[2], v[3]};
+        epi4(a4, m, n, bias, R, ldr, r_rows, C, ldc, act, act_ncols);
+      }
     }
   }
 }
@@ -356,8 +363,8 @@ struct Cfg { int bm, bn, stages, per_cu, kind; };
 // per_cu: workgroups that fit one CU at once (LDS- or register-limited)
 constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0}, {64, 128, 4, 1, 0}, {128, 64, 4, 1, 0}, {64, 64, 4, 2, 0},
                          {256, 128, 3, 1, 0}, {128, 256, 3, 1, 0}, {64, 64, 3, 3, 0}, {128, 128, 2, 2, 0},
-                         {64, 64, 4, 2, 1},   {64, 128, 4, 1, 1},  {128, 64, 4, 1, 1}, {64, 64, 8, 1, 1},
-                         {64, 128, 6, 1, 1},  {64, 64, 6, 1, 1},   {128, 64, 6, 1, 1}};
+                         {64, 64, 4, 2, 1},   {64, 128, 4, 1, 1},  {128, 64, 4, 1, 1}, {64, 64, 3, 3, 1},
+                         {64, 96, 2, 3, 1},   {64, 64, 6, 1, 1},   {96, 64, 2, 3, 1}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -372,13 +379,14 @@ hipError_t launch(hipStream_t st, int splits, const uint16_t* A, long lda, const
   return hipGetLastError();
 }
 
-template <int BM, int BN, int S>
+template <int BM, int BN, int S, int OCC>
 hipError_t launch_ks(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* bias,
                      const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int K, int Kw,
-                     int act, int act_ncols) {
+                     int act, int act_ncols, int splits = 1, float* P = nullptr, long ldp = 0, long p_split = 0) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_ks_kernel<BM, BN, S>), dim3(tm * tn), dim3(256), 0, st, A, lda, W, ldw, bias, R, ldr, r_rows,
-                     C, ldc, M, N, K, Kw, act, act_ncols, tm, tn);
+  const int nk = Kw / BK, kps = (nk + splits - 1) / splits;
+  hipLaunchKernelGGL((gemm_ks_kernel<BM, BN, S, OCC>), dim3(tm * tn * splits), dim3(256), 0, st, A, lda, W, ldw, bias, R, ldr,
+                     r_rows, C, ldc, M, N, K, Kw, act, act_ncols, tm, tn, splits, kps, P, ldp, p_split);
   return hipGetLastError();
 }
 
@@ -492,17 +500,49 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
     case 5: e = L_(128, 256, 3); break;
     case 6: e = L_(64, 64, 3); break;
     case 7: e = L_(128, 128, 2); break;
-#define W_(BM, BN, S) launch_ks<BM, BN, S>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
-    case 8: e = W_(64, 64, 4); break;
-    case 9: e = W_(64, 128, 4); break;
-    case 10: e = W_(128, 64, 4); break;
-    case 11: e = W_(64, 64, 8); break;
-    case 12: e = W_(64, 128, 6); break;
-    case 13: e = W_(64, 64, 6); break;
-    case 14: e = W_(128, 64, 6); break;
+#define W_(BM, BN, S, OCC) launch_ks<BM, BN, S, OCC>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
+    case 8: e = W_(64, 64, 4, 2); break;
+    case 9: e = W_(64, 128, 4, 1); break;
+    case 10: e = W_(128, 64, 4, 1); break;
+    case 11: e = W_(64, 64, 3, 3); break;
+    case 12: e = W_(64, 96, 2, 3); break;
+    case 13: e = W_(64, 64, 6, 1); break;
+    case 14: e = W_(96, 64, 2, 3); break;
     default: return MX_EBADCFG;
   }
 #undef L_
+#undef W_
+  return e == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// Raw split-K partial sums of A W^T for wave-split configs (kind 1): P[s][m][n] (fp32, row stride ldp, split stride
+// p_split) = sum over the k-steps of split s, s < splits. No bias, activation or residual: the consumer reduces the
+// splits in order (e.g. mx_residual_layernorm). No counterpart in the reference, which has no split-K.
+extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda,
+                                    const uint16_t* W, long ldw, float* P, long ldp, long p_split, int M, int N, int K,
+                                    int Kw) {
+  if (cfg < 0 || cfg >= kNCfg || kCfgs[cfg].kind != 1) return MX_EBADCFG;
+  if (!P) return MX_ENULL;
+  int rc = mx_gemm_check(cfg, 1, A, lda, W, ldw, nullptr, nullptr, 0, P, ldp, M, N, K, Kw, 0, nullptr, 0, nullptr, 0);
+  if (rc) return rc;
+  const int nk = Kw / BK;
+  if (splits < 1 || splits > nk) return MX_ESPLIT;
+  const int kps = (nk + splits - 1) / splits;
+  if ((splits - 1) * kps >= nk) return MX_ESPLIT;  // every split owns >= 1 k-step
+  if (ldp % 4 || ldp < N || ((uintptr_t)P & 15) || p_split % 4 || (splits > 1 && p_split < (long)M * ldp))
+    return MX_ELAYOUT;
+  hipError_t e;
+#define W_(BM, BN, S, OCC) launch_ks<BM, BN, S, OCC>(st, A, lda, W, ldw, nullptr, nullptr, 0, 0, nullptr, 0, M, N, K, Kw, 0, 0, splits, P, ldp, p_split)
+  switch (cfg) {
+    case 8: e = W_(64, 64, 4, 2); break;
+    case 9: e = W_(64, 128, 4, 1); break;
+    case 10: e = W_(128, 64, 4, 1); break;
+    case 11: e = W_(64, 64, 3, 3); break;
+    case 12: e = W_(64, 96, 2, 3); break;
+    case 13: e = W_(64, 64, 6, 1); break;
+    case 14: e = W_(96, 64, 2, 3); break;
+    default: return MX_EBADCFG;
+  }
 #undef W_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

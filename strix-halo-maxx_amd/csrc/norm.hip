@@ -103,6 +103,111 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   }
 }
 
+// Split-K reduction + bias + residual, then LayerNorm, one wave per row:
+//   x = bf16(bf16(sum_s P[s] + bias) + R)      (the Linear output rounded to bf16, then the fp32 residual add,
+//                                               rounded once more: torch's order for `linear(...) + res` in bf16)
+//   y = LayerNorm(x) as in layernorm_kernel (skipped when gamma is null)
+// The partials are added in split order, so the result does not depend on scheduling.
+template <int MAXC, int NS>
+__global__ __launch_bounds__(256) void residual_layernorm_kernel(
+    const float* __restrict__ P, long p_split, long ldp, const float* __restrict__ bias,
+    const uint16_t* __restrict__ R, long ldr, uint16_t* __restrict__ Xo, long ldxo, const uint16_t* __restrict__ gamma,
+    const uint16_t* __restrict__ beta, uint16_t* __restrict__ Y, long ldy, int rows, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = D >> 3;
+  // every load of the row is issued before any arithmetic (the row is latency-bound, not bandwidth-bound)
+  f32x4 pv[MAXC][NS][2];
+  u32x4 rv[MAXC];
+  f32x4 bv[MAXC][2];
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      const float* p = P + (long)row * ldp + c * 8;
+#pragma unroll
+      for (int sp = 0; sp < NS; sp++) {
+        pv[i][sp][0] = *reinterpret_cast<const f32x4*>(p + sp * p_split);
+        pv[i][sp][1] = *reinterpret_cast<const f32x4*>(p + sp * p_split + 4);
+      }
+      rv[i] = *reinterpret_cast<const u32x4*>(R + (long)row * ldr + c * 8);
+      if (bias) {
+        bv[i][0] = *reinterpret_cast<const f32x4*>(bias + c * 8);
+        bv[i][1] = *reinterpret_cast<const f32x4*>(bias + c * 8 + 4);
+      } else {
+        bv[i][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+        bv[i][1] = bv[i][0];
+      }
+    }
+  }
+  float v[MAXC][8];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) { a[e] = pv[i][0][0][e]; a[4 + e] = pv[i][0][1][e]; }
+#pragma unroll
+      for (int sp = 1; sp < NS; sp++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) { a[e] += pv[i][sp][0][e]; a[4 + e] += pv[i][sp][1][e]; }
+      if (bias) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) { a[e] += bv[i][0][e]; a[4 + e] += bv[i][1][e]; }
+      }
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[i][2 * e] = rbf(rbf(a[2 * e]) + lo_bf(rv[i][e]));
+        v[i][2 * e + 1] = rbf(rbf(a[2 * e + 1]) + hi_bf(rv[i][e]));
+        o[e] = pack2(v[i][2 * e], v[i][2 * e + 1]);
+      }
+      *reinterpret_cast<u32x4*>(Xo + (long)row * ldxo + c * 8) = o;
+#pragma unroll
+      for (int e = 0; e < 8; e++) s += v[i][e];
+    }
+  }
+  if (!gamma) return;
+  u32x4 gv[MAXC], ev[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      gv[i] = *reinterpret_cast<const u32x4*>(gamma + c * 8);
+      ev[i] = *reinterpret_cast<const u32x4*>(beta + c * 8);
+    }
+  }
+  const float mean = wave_sum(s) / (float)D;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) { const float d = v[i][e] - mean; ss += d * d; }
+    }
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
+  uint16_t* y = Y + (long)row * ldy;
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float y0 = (v[i][2 * e] - mean) * rstd * lo_bf(gv[i][e]) + lo_bf(ev[i][e]);
+        const float y1 = (v[i][2 * e + 1] - mean) * rstd * hi_bf(gv[i][e]) + hi_bf(ev[i][e]);
+        o[e] = pack2(y0, y1);
+      }
+      *reinterpret_cast<u32x4*>(y + c * 8) = o;
+    }
+  }
+}
+
 int check(const void* X, long ldx, const void* Y, long ldy, int rows, int D) {
   if (!X || !Y) return MX_ENULL;
   if (rows < 1 || D < 8 || D % 8 || D > 8192 || ldx % 8 || ldy % 8 || ldx < D || ldy < D) return MX_ESHAPE;
@@ -137,5 +242,37 @@ extern "C" int mx_rmsnorm(hipStream_t st, const uint16_t* X, long ldx, const uin
   if (nch <= 128) hipLaunchKernelGGL(rmsnorm_kernel<2>, g, dim3(256), 0, st, X, ldx, sc1, Y, ldy, rows, D, eps);
   else if (nch <= 256) hipLaunchKernelGGL(rmsnorm_kernel<4>, g, dim3(256), 0, st, X, ldx, sc1, Y, ldy, rows, D, eps);
   else hipLaunchKernelGGL(rmsnorm_kernel<16>, g, dim3(256), 0, st, X, ldx, sc1, Y, ldy, rows, D, eps);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// x = bf16(bf16(sum_s P[s] + bias) + R) -> Xo; y = LayerNorm(x; gamma, beta, eps) -> Y (skipped if gamma is null).
+// P: nsplit fp32 partial sums (split stride p_split, row stride ldp), e.g. from mx_gemm_bf16_partial. bias: fp32 or
+// null. Fuses the epilogue of a residual Linear with the LayerNorm that consumes its output (the reference runs them
+// as `x = x + proj(a)` then `ln2(x)`, moondream/gpu/md2fast.py:152-157).
+extern "C" int mx_residual_layernorm(hipStream_t st, const float* P, int nsplit, long p_split, long ldp,
+                                     const float* bias, const uint16_t* R, long ldr, uint16_t* Xo, long ldxo,
+                                     const uint16_t* gamma, const uint16_t* beta, uint16_t* Y, long ldy, int rows,
+                                     int D, float eps) {
+  if (!P || !R || !Xo) return MX_ENULL;
+  if (nsplit < 1 || rows < 1 || D < 8 || D % 8 || D > 2048) return MX_ESHAPE;
+  if (ldp % 4 || ldp < D || ldr % 8 || ldr < D || ldxo % 8 || ldxo < D || (nsplit > 1 && (p_split % 4 || p_split < (long)rows * ldp)))
+    return MX_ESHAPE;
+  if ((((uintptr_t)P | (uintptr_t)R | (uintptr_t)Xo) & 15) || (bias && ((uintptr_t)bias & 15))) return MX_ELAYOUT;
+  if (gamma) {
+    if (!beta || !Y) return MX_ENULL;
+    if (ldy % 8 || ldy < D) return MX_ESHAPE;
+    if (((uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)Y) & 15) return MX_ELAYOUT;
+  }
+  if (nsplit > 4) return MX_ESHAPE;
+  dim3 g((rows + 3) / 4);
+  const int nch = D / 8;
+#define L2_(C, NS) hipLaunchKernelGGL((residual_layernorm_kernel<C, NS>), g, dim3(256), 0, st, P, p_split, ldp, bias, R, ldr, Xo, ldxo, gamma, beta, Y, ldy, rows, D, eps)
+#define L_(C) switch (nsplit) { case 1: L2_(C, 1); break; case 2: L2_(C, 2); break; case 3: L2_(C, 3); break; default: L2_(C, 4); }
+  if (nch <= 128) { L_(2); }
+  else if (nch <= 192) { L_(3); }
+  else if (nch <= 256) { L_(4); }
+  else return MX_ESHAPE;
+#undef L2_
+#undef L_
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

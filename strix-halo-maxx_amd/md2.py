@@ -9,7 +9,11 @@ differences are MI355X-side only:
     588 -> 592), and the position embedding is added in that GEMM's epilogue (broadcast over the batch);
   * q, k, v are read by the attention kernel straight out of the fused qkv GEMM output (strided views, no copies),
     and the attention output is written in (token, head * 72) order, i.e. already "transposed back";
-  * residual adds and GELU run in the GEMM epilogues (the reference's fused_gelu / fused_res flags).
+  * residual adds and GELU run in the GEMM epilogues (the reference's fused_gelu / fused_res flags); with the
+    library's own Linear (MxLin), the two residual Linears of a block (attention proj, MLP fc2) instead run split-K
+    into fp32 partials, and one kernel adds the partials, bias and residual and applies the LayerNorm that reads the
+    result (ln2, the next block's ln1, or the final post-LN), so each residual stream row is finished and
+    normalised in a single pass.
 """
 import torch
 
@@ -44,16 +48,30 @@ class VisionTower:
             self.proj_fc1, self.proj_fc2 = lin("proj_mlp.fc1"), lin("proj_mlp.fc2")
         self.attn = attn or ops.Attn(self.H, self.T, self.hd)
         self.graphs = {}
+        # split-K residual Linears + fused residual LayerNorm when the Linear class can emit raw partial sums
+        self.splitk = hasattr(self.blocks[0]["proj"], "partial") if self.blocks else False
 
-    # ---- one pre-LN block (md2fast.py:152-157)
-    def block(self, b, x, B):
+    def _attn(self, b, h, B):
         T, H, hd, D = self.T, self.H, self.hd, self.D
-        h = ops.layernorm(x, *b["ln1"], eps=self.eps)
         qkv = b["qkv"](h)                                   # (B*T, 3D)
         q5 = qkv.view(B, T, 3, H, hd)
         q, k, v = (q5[:, :, i].transpose(1, 2) for i in range(3))   # (B, H, T, hd) strided views
-        a = self.attn(q, k, v)                              # (B, T, D)
-        x = b["proj"](a.view(B * T, D), res=x)
+        return self.attn(q, k, v).view(B * T, D)            # (B*T, D)
+
+    def _block_sk(self, b, x, h, B, next_ln):
+        """Split-K form of one block: x (residual stream) and h = ln1(x) in; the block output and next_ln(output)
+        out (the second is None when next_ln is None)."""
+        a = self._attn(b, h, B)
+        x1, h2 = ops.residual_layernorm(b["proj"].partial(a), b["proj"].b, x, b["ln2"], eps=self.eps)
+        f = b["fc1"](h2, gelu=True)
+        return ops.residual_layernorm(b["fc2"].partial(f), b["fc2"].b, x1, next_ln, eps=self.eps)
+
+    # ---- one pre-LN block (md2fast.py:152-157)
+    def block(self, b, x, B):
+        h = ops.layernorm(x, *b["ln1"], eps=self.eps)
+        if self.splitk:
+            return self._block_sk(b, x, h, B, None)[0]
+        x = b["proj"](self._attn(b, h, B), res=x)
         return b["fc2"](b["fc1"](ops.layernorm(x, *b["ln2"], eps=self.eps), gelu=True), res=x)
 
     def embed(self, img_u8):
@@ -66,9 +84,16 @@ class VisionTower:
         (or (B, 729, 2048) after the projection MLP when project=True)."""
         B = img_u8.shape[0]
         x = self.embed(img_u8)
-        for b in self.blocks:
-            x = self.block(b, x, B)
-        x = ops.layernorm(x, *self.post_ln, eps=self.eps)
+        if self.splitk:
+            h = ops.layernorm(x, *self.blocks[0]["ln1"], eps=self.eps)
+            for i, b in enumerate(self.blocks):
+                nxt = self.blocks[i + 1]["ln1"] if i + 1 < len(self.blocks) else self.post_ln
+                x, h = self._block_sk(b, x, h, B, nxt)
+            x = h
+        else:
+            for b in self.blocks:
+                x = self.block(b, x, B)
+            x = ops.layernorm(x, *self.post_ln, eps=self.eps)
         if project:
             x = self.project(x)
         return x.view(B, self.T, -1)

@@ -153,6 +153,65 @@ class MxLin:
         _lib.check(self._launch(cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws, act_cols), "mx_gemm_bf16")
         return y2.view(*x.shape[:-1], Nout) if out is None else y
 
+    def partial(self, x, out=None):
+        """Raw fp32 split-K partial sums of x W^T, shape (splits, M, N), for a consumer that adds them in order
+        together with the bias (residual_layernorm). The tile config and split count are tuned per (M, N, K)."""
+        x2 = _rows(x, self.K)
+        if x2.shape[1] != self.K:
+            raise ValueError(f"input width {x2.shape[1]} != {self.K}")
+        M = x2.shape[0]
+        cfg, sp = _partial_cfg(self, M, x2)
+        P = out if out is not None else torch.empty(sp, M, self.N, device=x2.device, dtype=torch.float32)
+        if P.shape != (sp, M, self.N) or P.stride(2) != 1:
+            raise ValueError("out must be (splits, M, N) fp32 with unit column stride")
+        _lib.check(_partial(self, cfg, sp, x2, P, M), "mx_gemm_bf16_partial")
+        return P
+
+
+_TUNED_P = {}  # (M, N, Kw) -> (cfg, splits) of the split-K partial GEMM
+
+
+def _partial(lin, cfg, sp, x2, P, M):
+    return _lib.load().mx_gemm_bf16_partial(stream(), cfg, sp, x2.data_ptr(), x2.stride(0), lin.w.data_ptr(),
+                                            lin.w.stride(0), P.data_ptr(), P.stride(1), P.stride(0), M, lin.N, lin.K,
+                                            lin.Kw)
+
+
+def _partial_cfg(lin, M, x2):
+    """(cfg, splits) for the split-K partial GEMM: every wave-split config x splits in 1..4 timed once on the real
+    operands (outside graph capture), else 64x64 tiles with 2 splits."""
+    key = (M, lin.N, lin.Kw)
+    if key in _TUNED_P:
+        return _TUNED_P[key]
+    lib = _lib.load()
+    best = (8, 2)
+    if MxLin.autotune and not torch.cuda.is_current_stream_capturing():
+        nk = lin.Kw // 64
+        bt = float("inf")
+        P = torch.empty(4, M, lin.N, device=x2.device, dtype=torch.float32)
+        for cfg in range(lib.mx_gemm_ncfg()):
+            if lib.mx_gemm_cfg_kind(cfg) != 1:
+                continue
+            for sp in (1, 2, 3, 4):
+                if sp > 1 and (nk // sp < 2 or (sp - 1) * (-(-nk // sp)) >= nk):
+                    continue
+                run = lambda: _partial(lin, cfg, sp, x2, P, M)
+                if run() != 0:
+                    continue
+                run()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(10):
+                    run()
+                e1.record()
+                e1.synchronize()
+                t = e0.elapsed_time(e1)
+                if t < bt:
+                    best, bt = (cfg, sp), t
+        del P
+    _TUNED_P[key] = best
+    return best
+
 
 def tune_gemm(lin, M, x2, y2, a, r2, ldr, r_rows, ws, reps=10):
     """Time every (tile config, split-K) candidate on the real operands; return the fastest. Runs eagerly on the
@@ -226,6 +285,21 @@ def layernorm(x, w, b, eps=1e-5, out=None):
     call("mx_layernorm", stream(), x2.data_ptr(), x2.stride(0), w.data_ptr(), b.data_ptr(), y.data_ptr(),
          y.reshape(-1, D).stride(0), x2.shape[0], D, float(eps))
     return y.view(*x.shape) if out is None else y
+
+
+def residual_layernorm(P, bias, res, ln=None, eps=1e-5, x_out=None, y_out=None):
+    """Reduce split-K partials P (splits, M, D) fp32: x = bf16(bf16(sum P + bias) + res); y = LayerNorm(x; ln) when
+    ln = (gamma, beta) is given. Returns (x, y) (y None without ln)."""
+    S, M, D = P.shape
+    r2 = _rows(res, D)
+    x = x_out if x_out is not None else torch.empty(M, D, device=P.device, dtype=BF)
+    y = None
+    if ln is not None:
+        y = y_out if y_out is not None else torch.empty(M, D, device=P.device, dtype=BF)
+    call("mx_residual_layernorm", stream(), P.data_ptr(), S, P.stride(0), P.stride(1), ptr(bias), r2.data_ptr(),
+         r2.stride(0), x.data_ptr(), x.stride(0), ptr(ln[0]) if ln else None, ptr(ln[1]) if ln else None, ptr(y),
+         y.stride(0) if y is not None else 0, M, D, float(eps))
+    return x, y
 
 
 def rmsnorm(x, sc1, eps=1e-6, out=None):

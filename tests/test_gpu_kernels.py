@@ -75,6 +75,61 @@ def test_gemm_every_tile_config(dev, cfg, splits):
     assert torch.equal(y.cpu(), y2.cpu())
 
 
+@pytest.mark.parametrize("M,K,N", [(729, 1152, 1152), (729, 4304, 1152), (300, 1000, 1220)])
+def test_gemm_partial_splits(dev, M, K, N):
+    """mx_gemm_bf16_partial, every wave-split config x 1-3 splits: the in-order fp32 sum of the partials is the fp32
+    product to accumulation accuracy (K = 1000: the last k-step is partial). Configs of the LDS-shared kind are
+    rejected."""
+    g = gen(M + K)
+    x = torch.randn(M, K, generator=g).to(BF)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    ref = x.double() @ w.double().t()
+    lin = ops.MxLin(w, None)
+    lib = _lib.load()
+    x2 = x.to(dev)
+    for cfg in range(lib.mx_gemm_ncfg()):
+        for sp in (1, 2, 3):
+            P = torch.full((sp, M, N), float("nan"), device=dev)
+            rc = ops._partial(lin, cfg, sp, x2, P, M)
+            if lib.mx_gemm_cfg_kind(cfg) != 1:
+                assert rc == -1
+                continue
+            assert rc == 0, (cfg, sp, rc)
+            Pc = P.cpu()
+            acc = Pc[0].clone()
+            for i in range(1, sp):
+                acc += Pc[i]
+            err = (acc.double() - ref).abs().max().item()
+            print(f"partial cfg={cfg} splits={sp} err={err:.2e}", flush=True)
+            assert err <= 1e-5 * ref.abs().max().item(), (cfg, sp, err)
+
+
+def test_residual_layernorm_matches_unfused(dev):
+    """x = bf16(bf16(sum P + bias) + res) bit for bit from the partials (CPU restatement, same fp32 order); the same
+    within 1 ulp of the single-pass GEMM epilogue (different summation order); y equals layernorm(x) exactly."""
+    M, K, N = 729, 1152, 1152
+    g = gen(11)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    r = (torch.randn(M, N, generator=g) * 4).to(BF).to(dev)
+    gam = (1 + 0.1 * torch.randn(N, generator=g)).to(BF).to(dev)
+    bet = (0.1 * torch.randn(N, generator=g)).to(BF).to(dev)
+    lin = ops.MxLin(w, b)
+    P = lin.partial(x)
+    xo, yo = ops.residual_layernorm(P, lin.b, r, (gam, bet), eps=1e-6)
+    xo2, none = ops.residual_layernorm(P, lin.b, r, None, eps=1e-6)
+    assert none is None and torch.equal(xo.cpu(), xo2.cpu())
+    Pc = P.cpu()
+    acc = Pc[0].clone()
+    for i in range(1, Pc.shape[0]):
+        acc += Pc[i]
+    exp = ((acc + lin.b.cpu()).to(BF).float() + r.cpu().float()).to(BF)
+    assert torch.equal(xo.cpu(), exp)
+    assert within_ulps(xo, lin(x, res=r), n=1, frac=1e-2)
+    assert torch.equal(yo.cpu(), ops.layernorm(xo, gam, bet, eps=1e-6).cpu())
+
+
 def test_gemm_epilogues_match_unfused(dev):
     """GELU applied to the bf16-rounded linear output, then + residual (md2fast.py:55-67; i8gemm.hip:378)."""
     M, K, N = 729, 1152, 4304
