@@ -85,7 +85,7 @@ def test_gemm_pick_is_a_valid_config():
         assert 0 <= cfg < lib.mx_gemm_ncfg() and sp >= 1
         bm, bn = ctypes.c_int(), ctypes.c_int()
         assert lib.mx_gemm_cfg_tile(cfg, ctypes.byref(bm), ctypes.byref(bn)) == 0
-        assert bm.value in (32, 64, 128, 256) and bn.value in (64, 128, 256)
+        assert bm.value % 32 == 0 and bn.value % 32 == 0 and 32 <= min(bm.value, bn.value) and max(bm.value, bn.value) <= 256
         assert lib.mx_gemm_cfg_kind(cfg) in (0, 1)
         assert sp == 1 or lib.mx_gemm_cfg_kind(cfg) == 0
     assert lib.mx_gemm_cfg_kind(lib.mx_gemm_ncfg()) == -1 and lib.mx_gemm_cfg_kind(-1) == -1
