@@ -58,6 +58,31 @@ __device__ __forceinline__ void ln_chunks(u32x4 (&xc)[KC], const uint16_t* gamma
   }
 }
 
+// Sum R per-lane values over the wave (R a power of two <= 64) with 6 + R - 1 - log2(R) exchanges instead of 6 R:
+// each of the first log2(R) exchanges (lane distance 32, 16, ...) halves the values a lane holds (a lane keeps the
+// half selected by its lane bit and receives its partner's copy of that half), then a butterfly over the remaining
+// lane bits completes the sums. Lane l ends with the total of value l >> (6 - log2 R).
+template <int R>
+__device__ __forceinline__ float reduce_rows(float (&v)[R], int lane) {
+  constexpr int L = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : R == 16 ? 4 : R == 32 ? 5 : 6;
+  static_assert((1 << L) == R, "R must be a power of two <= 64");
+#pragma unroll
+  for (int st = 0; st < L; st++) {
+    const int d = 32 >> st, H = R >> (st + 1);
+    const bool up = lane & d;
+#pragma unroll
+    for (int j = 0; j < H; j++) {
+      const float keep = up ? v[j + H] : v[j];
+      const float send = up ? v[j] : v[j + H];
+      v[j] = keep + __shfl_xor(send, d, 64);
+    }
+  }
+  float t = v[0];
+#pragma unroll
+  for (int d = 32 >> L; d >= 1; d >>= 1) t += __shfl_xor(t, d, 64);
+  return t;
+}
+
 template <int KC>
 __device__ __forceinline__ void load_vec(u32x4 (&xc)[KC], const uint16_t* x, int lane) {
 #pragma unroll
@@ -72,9 +97,15 @@ __global__ __launch_bounds__(256) void ln_gemv2_kernel(const uint16_t* __restric
                                                        const float* __restrict__ bias, int N, int n1,
                                                        uint16_t* __restrict__ out1, uint16_t* __restrict__ out2,
                                                        int act2) {
+  constexpr int SH = 6 - (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);  // lane >> SH = row it finishes
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * R;
   if (row0 >= N) return;
+  const int nme = row0 + (lane >> SH);  // the output row this lane completes
+  // the small operands first, so the LayerNorm runs while the weight rows stream in
+  u32x4 xc[KC];
+  load_vec<KC>(xc, x, lane);
+  const float bme = (bias && nme < N) ? bias[nme] : 0.f;
   u32x4 wv[R][KC];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -82,25 +113,23 @@ __global__ __launch_bounds__(256) void ln_gemv2_kernel(const uint16_t* __restric
 #pragma unroll
     for (int i = 0; i < KC; i++) wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (lane + 64 * i) * 8));
   }
-  u32x4 xc[KC];
-  load_vec<KC>(xc, x, lane);
   if (gamma) ln_chunks<KC>(xc, gamma, beta, eps, KC * 512, lane);
+  float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    float acc = 0.f;
+    acc[r] = 0.f;
 #pragma unroll
-    for (int i = 0; i < KC; i++) acc = dot8(wv[r][i], xc[i], acc);
-    acc = wave_sum(acc);
-    const int n = row0 + r;
-    if (lane == 0 && n < N) {
-      float v = rbf(acc + (bias ? bias[n] : 0.f));
-      if (n < n1) {
-        out1[n] = f2bf(v);
-      } else {
-        if (act2 == 1) v = gelu_tanh(v);
-        else if (act2 == 2) v = gelu_erf(v);
-        out2[n - n1] = f2bf(v);
-      }
+    for (int i = 0; i < KC; i++) acc[r] = dot8(wv[r][i], xc[i], acc[r]);
+  }
+  const float tot = reduce_rows<R>(acc, lane);
+  if ((lane & ((1 << SH) - 1)) == 0 && nme < N) {
+    float v = rbf(tot + bme);
+    if (nme < n1) {
+      out1[nme] = f2bf(v);
+    } else {
+      if (act2 == 1) v = gelu_tanh(v);
+      else if (act2 == 2) v = gelu_erf(v);
+      out2[nme - n1] = f2bf(v);
     }
   }
 }
@@ -113,9 +142,18 @@ __global__ __launch_bounds__(256) void gemv_dual_res_kernel(const uint16_t* __re
                                                             const float* __restrict__ bp,
                                                             const uint16_t* __restrict__ xres, uint16_t* __restrict__ out,
                                                             int N) {
+  // 2 R sums per wave (fc2 rows, then proj rows): lane l finishes sum l >> SH; the proj sum of row r sits 32 lanes
+  // above its fc2 sum
+  constexpr int SH = 6 - (R == 1 ? 1 : R == 2 ? 2 : R == 4 ? 3 : 4);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * R;
   if (row0 >= N) return;
+  const int nme = row0 + ((lane >> SH) & (R - 1));
+  u32x4 gc[KC1], ac[KC2];
+  load_vec<KC1>(gc, g, lane);
+  load_vec<KC2>(ac, a, lane);
+  const bool in = nme < N;
+  const float b2me = in ? b2[nme] : 0.f, bpme = in ? bp[nme] : 0.f, xme = in ? bf2f(xres[nme]) : 0.f;
   u32x4 w2[R][KC1], wp[R][KC2];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -127,23 +165,21 @@ __global__ __launch_bounds__(256) void gemv_dual_res_kernel(const uint16_t* __re
     for (int i = 0; i < KC2; i++)
       wp[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Wp + (long)n * KC2 * 512 + (lane + 64 * i) * 8));
   }
-  u32x4 gc[KC1], ac[KC2];
-  load_vec<KC1>(gc, g, lane);
-  load_vec<KC2>(ac, a, lane);
+  float acc[2 * R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    float s2 = 0.f, sp = 0.f;
+    acc[r] = 0.f;
+    acc[R + r] = 0.f;
 #pragma unroll
-    for (int i = 0; i < KC1; i++) s2 = dot8(w2[r][i], gc[i], s2);
+    for (int i = 0; i < KC1; i++) acc[r] = dot8(w2[r][i], gc[i], acc[r]);
 #pragma unroll
-    for (int i = 0; i < KC2; i++) sp = dot8(wp[r][i], ac[i], sp);
-    s2 = wave_sum(s2);
-    sp = wave_sum(sp);
-    const int n = row0 + r;
-    if (lane == 0 && n < N) {
-      const float pr = rbf(rbf(sp + bp[n]) + bf2f(xres[n]));
-      out[n] = f2bf(rbf(s2 + b2[n]) + pr);
-    }
+    for (int i = 0; i < KC2; i++) acc[R + r] = dot8(wp[r][i], ac[i], acc[R + r]);
+  }
+  const float tot = reduce_rows<2 * R>(acc, lane);      // lanes < 32: fc2 sums, lanes >= 32: proj sums
+  const float sp = __shfl_xor(tot, 32, 64);
+  if (lane < 32 && (lane & ((1 << SH) - 1)) == 0 && in) {
+    const float pr = rbf(rbf(sp + bpme) + xme);
+    out[nme] = f2bf(rbf(tot + b2me) + pr);
   }
 }
 
@@ -164,11 +200,16 @@ __global__ __launch_bounds__(256) void ln_gemv_argmax_kernel(const uint16_t* __r
                                                              const float* __restrict__ bias, int N,
                                                              uint16_t* __restrict__ logits,
                                                              unsigned long long* __restrict__ part) {
+  constexpr int SH = 6 - (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);
   __shared__ unsigned long long sbest[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * R;
   unsigned long long best = 0ull;
   if (row0 < N) {
+    const int nme = row0 + (lane >> SH);
+    u32x4 xc[KC];
+    load_vec<KC>(xc, x, lane);
+    const float bme = nme < N ? bias[nme] : 0.f;
     u32x4 wv[R][KC];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -176,22 +217,24 @@ __global__ __launch_bounds__(256) void ln_gemv_argmax_kernel(const uint16_t* __r
 #pragma unroll
       for (int i = 0; i < KC; i++) wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (lane + 64 * i) * 8));
     }
-    u32x4 xc[KC];
-    load_vec<KC>(xc, x, lane);
     ln_chunks<KC>(xc, gamma, beta, eps, KC * 512, lane);
+    float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      float acc = 0.f;
+      acc[r] = 0.f;
 #pragma unroll
-      for (int i = 0; i < KC; i++) acc = dot8(wv[r][i], xc[i], acc);
-      acc = wave_sum(acc);
-      const int n = row0 + r;
-      if (n < N) {
-        const float v = rbf(acc + bias[n]);
-        if (logits && lane == 0) logits[n] = f2bf(v);
-        const unsigned long long k = amax_key(v, n);
-        best = k > best ? k : best;
-      }
+      for (int i = 0; i < KC; i++) acc[r] = dot8(wv[r][i], xc[i], acc[r]);
+    }
+    const float tot = reduce_rows<R>(acc, lane);
+    if (nme < N) {
+      const float v = rbf(tot + bme);
+      if (logits && (lane & ((1 << SH) - 1)) == 0) logits[nme] = f2bf(v);
+      best = amax_key(v, nme);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const unsigned long long t = __shfl_xor(best, o, 64);
+      best = t > best ? t : best;
     }
   }
   if (lane == 0) sbest[wave] = best;
