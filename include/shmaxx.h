@@ -116,9 +116,10 @@ int mx_lm_argmax_nparts(int N);
  * x = wte[token]. Replaces the host-side argmax + F.embedding of a greedy step (md2fast.py:209). */
 int mx_embed_step(hipStream_t st, const unsigned long long* part, int nparts, const uint16_t* wte, int D, int* state,
                   int pos_base, int* tokens, uint16_t* x);
-/* One decode token: rope of q and k at pos = state[1], K/V append at pos, split-KV (S splits) attention over keys
- * 0..pos into out (H * 64). ws >= H * S * 66 floats, cnt >= H ints (zero before first use, left zero). Replaces the
- * SDPA over the KV cache of md2fast.py:185 for one query. */
+/* One decode token: rope of q and k at pos = state[1], K/V append at pos, attention over keys 0..pos into out
+ * (H * 64): one workgroup per head, 16 waves with a one-pass online softmax each, merged in LDS. S, ws and cnt
+ * are unused (ws / cnt may be null; kept for ABI stability). Replaces the SDPA over the KV cache of md2fast.py:185 for one
+ * query. */
 int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H, int ctx,
                    const int* state, int S, float scale, float* ws, int* cnt, uint16_t* out);
 

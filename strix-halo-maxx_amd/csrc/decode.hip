@@ -4,8 +4,8 @@
 // 2 per token, all replayed from one HIP graph, with the step's position and the token living in device memory:
 //   ln_gemv2      h = LN(x) (recomputed per wave from the 4 KB row), [qkv | fc1] = h [Wqkv | Wfc1]^T + b, GELU on
 //                 the fc1 part (the reference's qkv and fc1 both read the same LN output, md2fast.py:173-198)
-//   decode_attn   rope on q / k of the new token, K/V append at `pos`, split-KV attention over keys 0..pos, then a
-//                 small per-head merge kernel
+//   decode_attn   rope on q / k of the new token, K/V append at `pos`, attention over keys 0..pos: one workgroup per
+//                 head, a one-pass online softmax per wave, the 16 waves merged in LDS
 //   gemv_dual_res x' = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)): the parallel residual of
 //                 md2fast.py:198 with the reference's rounding order, both GEMVs in one pass over [Wfc2 | Wproj]
 //   ln_gemv_argmax  logits = LN(x) Wlm^T + b (bf16, as the reference's bf16 lm_head) and a per-workgroup argmax
@@ -281,24 +281,24 @@ __global__ __launch_bounds__(1024) void embed_step_kernel(const unsigned long lo
 }
 
 // ---------------------------------------------------------------------------------------------- decode attention
-constexpr int DA_MAXK = 1024;  // keys per split held in LDS
-constexpr int DA_UNROLL = 4;   // key rounds (32 keys each) whose loads are issued together
+constexpr int DA_W = 16;       // waves per head (one 1024-thread workgroup per head)
+constexpr int DA_UNROLL = 8;   // key rounds (8 keys per wave each) whose K and V loads are issued together
 
-__global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
-                                                          uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-                                                          int H, int ctx, const int* __restrict__ state, int S,
-                                                          float scale_log2, float* __restrict__ ws) {
-  __shared__ float sc[DA_MAXK];
+// One workgroup per head. Wave w takes keys w * 8 + (lane >> 3) + 128 r, 8 lanes per key (lane & 7 -> dims
+// 8 (lane & 7) .. +7), and runs an online softmax over them in one pass: the K and V rows of DA_UNROLL rounds are
+// loaded together, scores reduced within each 8-lane group, the wave's running max raised (and its O, l rescaled)
+// per batch. The 16 waves' (m, l, O) are merged in LDS. P is rounded to bf16 and l sums the rounded values.
+__global__ __launch_bounds__(1024) void decode_attn_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
+                                                           uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                           int H, int ctx, const int* __restrict__ state,
+                                                           float scale_log2, uint16_t* __restrict__ out) {
   __shared__ float qs[64];
   __shared__ uint16_t knew[64], vnew[64];
-  __shared__ float red[8];
-  __shared__ float osum[4][64];
-  const int h = blockIdx.x, split = blockIdx.y;
+  __shared__ float rec[DA_W][66];  // (m, l, o[64]) of each wave
+  const int h = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = state[1];
   const int L = pos + 1;
-  const int chunk = (L + S - 1) / S;
-  const int k0 = split * chunk, k1 = min(L, k0 + chunk);
   const float* cp = cs + (long)pos * 32;
   const uint16_t* src = qkv + h * 64;
   const uint16_t* ksrc = qkv + H * 64 + h * 64;
@@ -324,29 +324,33 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
     vnew[d] = vsrc[d];
   }
   __syncthreads();
-  const bool has_new = (k0 <= pos && pos < k1);
-  if (has_new && tid < 64) {  // the split that owns key `pos` appends it to the cache (and uses it from LDS)
+  if (tid < 64) {  // append the new token's K / V to the cache (this step reads them from LDS)
     kc[((long)h * ctx + pos) * 64 + tid] = knew[tid];
     vc[((long)h * ctx + pos) * 64 + tid] = vnew[tid];
   }
-  // ---- scores: 8 lanes per key (lane % 8 -> dims 8 (lane % 8) ..), 8 keys per wave per round, DA_UNROLL rounds
-  // of loads in flight
   const int sub = lane & 7, kg = lane >> 3;
   float qv[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) qv[e] = qs[sub * 8 + e];
-  float mloc = -1e30f;
-  for (int base = k0 + wave * 8 + kg; base < k1; base += 32 * DA_UNROLL) {
-    u32x4 kk[DA_UNROLL];
+  float m_run = -1e30f, l_run = 0.f;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // the loop bound is wave-uniform (every lane takes part in the wave-wide max); keys past L are masked
+  for (int b0 = wave * 8; b0 < L; b0 += 8 * DA_W * DA_UNROLL) {
+    const int base = b0 + kg;
+    u32x4 kk[DA_UNROLL], vv[DA_UNROLL];
 #pragma unroll
     for (int u = 0; u < DA_UNROLL; u++) {
-      const int key = base + 32 * u;
-      kk[u] = (key < k1 && key != pos) ? *reinterpret_cast<const u32x4*>(kh + (long)key * 64 + sub * 8)
-                                       : *reinterpret_cast<const u32x4*>(&knew[sub * 8]);
+      const int key = base + 8 * DA_W * u;
+      const bool cached = key < L && key != pos;
+      kk[u] = cached ? *reinterpret_cast<const u32x4*>(kh + (long)key * 64 + sub * 8)
+                     : *reinterpret_cast<const u32x4*>(&knew[sub * 8]);
+      vv[u] = cached ? *reinterpret_cast<const u32x4*>(vh + (long)key * 64 + sub * 8)
+                     : *reinterpret_cast<const u32x4*>(&vnew[sub * 8]);
     }
+    float sv[DA_UNROLL];
+    float mb = -1e30f;
 #pragma unroll
     for (int u = 0; u < DA_UNROLL; u++) {
-      const int key = base + 32 * u;
       float s = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -356,75 +360,57 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(const uint16_t* __rest
       s += __shfl_xor(s, 1, 64);
       s += __shfl_xor(s, 2, 64);
       s += __shfl_xor(s, 4, 64);
-      s *= scale_log2;
-      if (key < k1) {
-        if (sub == 0) sc[key - k0] = s;
-        mloc = fmaxf(mloc, s);
-      }
+      s = (base + 8 * DA_W * u < L) ? s * scale_log2 : -INFINITY;
+      sv[u] = s;
+      mb = fmaxf(mb, s);
     }
-  }
-  mloc = wave_max(mloc);
-  if (lane == 0) red[wave] = mloc;
-  __syncthreads();
-  const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // ---- P (rounded to bf16) and PV with the same key mapping
-  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-  for (int base = k0 + wave * 8 + kg; base < k1; base += 32 * DA_UNROLL) {
-    u32x4 vv[DA_UNROLL];
+    mb = wave_max(mb);
+    if (mb > m_run) {  // wave-uniform
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mb);
+      l_run *= alpha;
 #pragma unroll
-    for (int u = 0; u < DA_UNROLL; u++) {
-      const int key = base + 32 * u;
-      vv[u] = (key < k1 && key != pos) ? *reinterpret_cast<const u32x4*>(vh + (long)key * 64 + sub * 8)
-                                       : *reinterpret_cast<const u32x4*>(&vnew[sub * 8]);
+      for (int e = 0; e < 8; e++) o[e] *= alpha;
+      m_run = mb;
     }
 #pragma unroll
     for (int u = 0; u < DA_UNROLL; u++) {
-      const int key = base + 32 * u;
-      if (key < k1) {
-        const float p = rbf(__builtin_amdgcn_exp2f(sc[key - k0] - m));
-        if (sub == 0) lsum += p;
+      const float p = rbf(__builtin_amdgcn_exp2f(sv[u] - m_run));
+      if (sub == 0) l_run += p;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          o[2 * e] = __builtin_fmaf(p, lo_bf(vv[u][e]), o[2 * e]);
-          o[2 * e + 1] = __builtin_fmaf(p, hi_bf(vv[u][e]), o[2 * e + 1]);
-        }
+      for (int e = 0; e < 4; e++) {
+        o[2 * e] = __builtin_fmaf(p, lo_bf(vv[u][e]), o[2 * e]);
+        o[2 * e + 1] = __builtin_fmaf(p, hi_bf(vv[u][e]), o[2 * e + 1]);
       }
     }
   }
-  // reduce over the 8 key groups of the wave, then over the 4 waves
+  // reduce over the 8 key groups of the wave
 #pragma unroll
   for (int e = 0; e < 8; e++) {
     o[e] += __shfl_xor(o[e], 8, 64);
     o[e] += __shfl_xor(o[e], 16, 64);
     o[e] += __shfl_xor(o[e], 32, 64);
   }
-  lsum = wave_sum(lsum);
+  l_run = wave_sum(l_run);
   if (kg == 0) {
 #pragma unroll
-    for (int e = 0; e < 8; e++) osum[wave][sub * 8 + e] = o[e];
+    for (int e = 0; e < 8; e++) rec[wave][2 + sub * 8 + e] = o[e];
   }
-  if (lane == 0) red[4 + wave] = lsum;
+  if (lane == 0) { rec[wave][0] = m_run; rec[wave][1] = l_run; }
   __syncthreads();
-  float* rec = ws + ((long)h * S + split) * 66;  // (m, l, o[64]) of this split, merged by decode_combine_kernel
-  if (tid < 64) rec[2 + tid] = osum[0][tid] + osum[1][tid] + osum[2][tid] + osum[3][tid];
-  if (tid == 0) { rec[0] = (k1 > k0) ? m : -1e30f; rec[1] = red[4] + red[5] + red[6] + red[7]; }
-}
-
-// merge the S split partials of each head: out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
-__global__ __launch_bounds__(64) void decode_combine_kernel(const float* __restrict__ ws, int S,
-                                                            uint16_t* __restrict__ out) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  const float* base = ws + (long)h * S * 66;
-  float M = -1e30f;
-  for (int sp = 0; sp < S; sp++) M = fmaxf(M, base[sp * 66]);
-  float Lt = 0.f, acc = 0.f;
-  for (int sp = 0; sp < S; sp++) {
-    const float f = __builtin_amdgcn_exp2f(base[sp * 66] - M);
-    Lt += base[sp * 66 + 1] * f;
-    acc += base[sp * 66 + 2 + d] * f;
+  // ---- merge the waves: out = sum_w o_w 2^(m_w - M) / sum_w l_w 2^(m_w - M)
+  if (tid < 64) {
+    float M = -1e30f;
+#pragma unroll
+    for (int w = 0; w < DA_W; w++) M = fmaxf(M, rec[w][0]);
+    float Lt = 0.f, acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < DA_W; w++) {
+      const float f = __builtin_amdgcn_exp2f(rec[w][0] - M);
+      Lt += rec[w][1] * f;
+      acc += rec[w][2 + tid] * f;
+    }
+    out[h * 64 + tid] = f2bf(acc / Lt);
   }
-  out[h * 64 + d] = f2bf(acc / Lt);
 }
 
 }  // namespace
@@ -489,12 +475,12 @@ extern "C" int mx_embed_step(hipStream_t st, const unsigned long long* part, int
 // the split-KV pass and the per-head merge (a kernel boundary instead of a device-scope fence + counter).
 extern "C" int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H,
                               int ctx, const int* state, int S, float scale, float* ws, int* cnt, uint16_t* out) {
+  (void)S;
+  (void)ws;
   (void)cnt;
-  if (!qkv || !cs || !kc || !vc || !state || !ws || !out) return MX_ENULL;
-  if (H < 1 || S < 1 || ctx < 1 || (ctx + S - 1) / S > DA_MAXK) return MX_ESHAPE;
-  hipLaunchKernelGGL(decode_attn_kernel, dim3(H, S), dim3(256), 0, st, qkv, cs, kc, vc, H, ctx, state, S,
-                     scale * 1.4426950408889634f, ws);
-  if (hipGetLastError() != hipSuccess) return MX_ELAUNCH;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(H), dim3(64), 0, st, ws, S, out);
+  if (!qkv || !cs || !kc || !vc || !state || !out) return MX_ENULL;
+  if (H < 1 || ctx < 1) return MX_ESHAPE;
+  hipLaunchKernelGGL(decode_attn_kernel, dim3(H), dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state,
+                     scale * 1.4426950408889634f, out);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

@@ -22,7 +22,7 @@ BOS = 50256  # moondream2's tokenizer bos_id (the Phi / GPT-2 <|endoftext|> id)
 
 
 class TextDecoder:
-    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", ctx=1024, attn_splits=16):
+    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", ctx=1024, attn_splits=4):
         c = TXT
         self.dev = torch.device(device)
         self.D, self.H, self.hd, self.eps = c["dim"], c["heads"], c["hd"], c["ln_eps"]
