@@ -42,12 +42,10 @@ def gemm_symbol(cfg):
     return f"gemm_bf16_kernel<{bm}, {bn}, 2, 2, {GEMM_STAGES[cfg]}>"
 
 
-def op_timing(vt, img, reps=5):
-    """Per-kernel launch time inside the tower (its split-K form: partial GEMMs for the two residual Linears, each
-    reduced by the fused residual-LayerNorm kernel): one eager pass keeps every block's real operands, then for each
-    op class a HIP graph of its 27 launches (each on its own block's weights and activations, as in the tower) is
-    replayed `reps` times between two HIP events recorded on the stream the kernels run on. Returns
-    {label: [total_ms, launches, flops_per_launch, kernel symbol]}."""
+def op_classes(vt, img):
+    """The tower's batch-1 op classes (its split-K form: partial GEMMs for the two residual Linears, each reduced by
+    the fused residual-LayerNorm kernel) as {label: (kernel symbol, flops per launch, fn(i, block))}; one eager pass
+    keeps every block's real operands, and fn(i, block) relaunches op `label` of block i on them."""
     import torch
     import strix_halo_maxx_amd.ops as ops
     B = img.shape[0]
@@ -94,6 +92,16 @@ def op_timing(vt, img, reps=5):
         "res_ln1": ("residual_layernorm_kernel<3>", 0, lambda i, b: ops.residual_layernorm(
             saved[i][8], b["fc2"].b, saved[i][5], saved[i][9], eps=vt.eps, x_out=outs["x"], y_out=outs["h"])),
     }
+    return classes
+
+
+def op_timing(vt, img, reps=5):
+    """Per-kernel launch time inside the tower: for each op class of op_classes a HIP graph of its 27 launches (each
+    on its own block's weights and activations, as in the tower) is replayed `reps` times between two HIP events
+    recorded on the stream the kernels run on. Returns {label: [total_ms, launches, flops_per_launch, symbol]}."""
+    import torch
+    classes = op_classes(vt, img)
+    blocks = vt.blocks
     res = {}
     for name, (ksym, fl, fn) in classes.items():
         g = torch.cuda.CUDAGraph()
@@ -112,6 +120,52 @@ def op_timing(vt, img, reps=5):
         res[name] = [e0.elapsed_time(e1), n, fl, ksym]
         del g
     return res
+
+
+def traffic_probe(vt, img, reps=3):
+    """Eager launches for HBM-traffic counters (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, on this mode): after two
+    passes of the tower and the eager pass that keeps every block's operands, a marker fill of 12345 floats, then each
+    op class of the tower's batch-1 path
+    launched `reps` x 27 times on its own blocks' operands (the op_timing classes, in order), then a marker fill of
+    23456 floats and the calibration: `reps` device copies of 256 MiB (known traffic: 256 MiB read + 256 MiB
+    written each). Traffic per launch = counter per dispatch x (256 MiB / the counter of one calibration copy)."""
+    import torch
+    vt(img)
+    vt(img)
+    classes = op_classes(vt, img)
+    torch.cuda.synchronize()
+    torch.full((12345,), 1.0, device=img.device)
+    for name, (ksym, fl, fn) in classes.items():
+        for _ in range(reps):
+            for i, b in enumerate(vt.blocks):
+                fn(i, b)
+        torch.cuda.synchronize()
+    torch.full((23456,), 1.0, device=img.device)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=img.device)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("[bench] traffic probe done: " + ", ".join(f"{k}={v[0]}" for k, v in classes.items()), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "vision_tower_b1_hbm_traffic.md")
+
+
+def measured_traffic(label, sym):
+    """HBM bytes per launch of op `label` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (the JSON
+    block of profiles/vision_tower_b1_hbm_traffic.md), if it was measured on the same kernel; else (None, reason)."""
+    try:
+        txt = open(TRAFFIC_FILE).read()
+        blob = json.loads(txt.split("```json", 1)[1].split("```", 1)[0])
+    except (OSError, IndexError, ValueError):
+        return None, "no committed traffic summary"
+    e = blob.get("ops", {}).get(label)
+    if not e:
+        return None, f"op {label} not in the committed traffic summary"
+    if e.get("kernel") != sym:
+        return None, f"committed summary measured {e.get('kernel')}, this run picked {sym}"
+    return int(e["bytes_per_launch"]), os.path.relpath(TRAFFIC_FILE, os.path.dirname(TRAFFIC_FILE) + "/..")
 
 
 def cpu_baseline(budget_s=20.0):
@@ -252,6 +306,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--extra", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only the eager launches that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count (see traffic_probe)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (every workload here fits one GPU's "
@@ -266,6 +322,10 @@ def main():
     w = S.vision_weights(0)
     vt = md2.VisionTower(w, device=dev)
     img = S.images_u8(1, 1).to(dev)
+    if a.traffic_probe:
+        with torch.inference_mode():
+            traffic_probe(vt, img)
+        return
     print(f"[bench] tower batch 1: warmup {a.warmup}, steps {a.steps}", file=sys.stderr, flush=True)
     with torch.inference_mode():
         s = tower_time(vt, img, a.steps, a.warmup)
@@ -274,8 +334,10 @@ def main():
     label, (tot_ms, n, fl, sym) = max(agg.items(), key=lambda kv: kv[1][0])
     avg_s = tot_ms / n / 1e3
     achieved = fl / avg_s
+    traffic, tsrc = measured_traffic(label, sym)
     roof = {"bound": "mfma", "kernel": sym, "op": label, "achieved": round(achieved / 1e12, 1),
-            "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
+            "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": traffic,
+            "traffic_source": tsrc,
             "avg_launch_us": round(avg_s * 1e6, 2), "launches_timed": n, "flops_per_launch": fl,
             "per_op_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in agg.items()},
             "per_op_kernel": {k: v[3] for k, v in agg.items()}}

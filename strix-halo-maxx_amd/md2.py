@@ -48,8 +48,11 @@ class VisionTower:
             self.proj_fc1, self.proj_fc2 = lin("proj_mlp.fc1"), lin("proj_mlp.fc2")
         self.attn = attn or ops.Attn(self.H, self.T, self.hd)
         self.graphs = {}
-        # split-K residual Linears + fused residual LayerNorm when the Linear class can emit raw partial sums
+        # split-K residual Linears + fused residual LayerNorm when the Linear class can emit raw partial sums and the
+        # batch is small (a few crops: too few output tiles to fill the GPU otherwise; large batches have enough
+        # tiles, and there the fp32 partials would only add traffic)
         self.splitk = hasattr(self.blocks[0]["proj"], "partial") if self.blocks else False
+        self.splitk_max_rows = 8192
 
     def _attn(self, b, h, B):
         T, H, hd, D = self.T, self.H, self.hd, self.D
@@ -67,9 +70,12 @@ class VisionTower:
         return ops.residual_layernorm(b["fc2"].partial(f), b["fc2"].b, x1, next_ln, eps=self.eps)
 
     # ---- one pre-LN block (md2fast.py:152-157)
+    def _use_splitk(self, B):
+        return self.splitk and B * self.T <= self.splitk_max_rows
+
     def block(self, b, x, B):
         h = ops.layernorm(x, *b["ln1"], eps=self.eps)
-        if self.splitk:
+        if self._use_splitk(B):
             return self._block_sk(b, x, h, B, None)[0]
         x = b["proj"](self._attn(b, h, B), res=x)
         return b["fc2"](b["fc1"](ops.layernorm(x, *b["ln2"], eps=self.eps), gelu=True), res=x)
@@ -84,7 +90,7 @@ class VisionTower:
         (or (B, 729, 2048) after the projection MLP when project=True)."""
         B = img_u8.shape[0]
         x = self.embed(img_u8)
-        if self.splitk:
+        if self._use_splitk(B):
             h = ops.layernorm(x, *self.blocks[0]["ln1"], eps=self.eps)
             for i, b in enumerate(self.blocks):
                 nxt = self.blocks[i + 1]["ln1"] if i + 1 < len(self.blocks) else self.post_ln

@@ -8,6 +8,9 @@ They keep the reference's operator protocol so the per-model forwards read like 
 Every call launches asynchronously on torch's current stream; nothing here synchronises, so a forward made of these
 calls can be captured into a HIP graph.
 """
+import json
+import os
+
 import torch
 
 from . import _lib
@@ -62,6 +65,25 @@ class Workspace:
 
 _TUNED = {}  # (M, N, Kw) -> (cfg, splits), shared by every layer of that shape
 
+# Fixed tile table for MI355X (built by `python -m strix_halo_maxx_amd.tune` from in-context timings: each shape timed
+# on the sequence of launches it runs in, with its real cache state). Shapes it lists skip the autotuner, so every
+# process runs the same kernels; the reference's pick_cfg has the same two tiers (FIXED table, then timing,
+# moondream/gpu/hgemm.py:47-76).
+_TABLE_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_table_gfx950.json")
+
+
+def _load_table():
+    try:
+        with open(_TABLE_FILE) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return {}, {}
+    conv = lambda m: {tuple(int(v) for v in k.split(",")): tuple(int(v) for v in c) for k, c in m.items()}
+    return conv(d.get("fused", {})), conv(d.get("partial", {}))
+
+
+_FIXED, _FIXED_P = _load_table()
+
 
 def _ws_need(cfg, splits, M, N):
     lib = _lib.load()
@@ -80,6 +102,7 @@ class MxLin:
     fused_gelu = True
     fused_res = True
     autotune = True
+    use_table = True
 
     def __init__(self, weight, bias, dtype=BF, device="cuda"):
         assert dtype == BF, "bf16 only"
@@ -109,6 +132,9 @@ class MxLin:
     def _pick(self, M, x2, y2, a, r2, ldr, r_rows, ws):
         key = (M, self.N, self.Kw)
         if key in _TUNED:
+            return _TUNED[key]
+        if MxLin.use_table and key in _FIXED:
+            _TUNED[key] = _FIXED[key]
             return _TUNED[key]
         lib = _lib.load()
         if not MxLin.autotune or torch.cuda.is_current_stream_capturing():
@@ -182,6 +208,9 @@ def _partial_cfg(lin, M, x2):
     operands (outside graph capture), else 64x64 tiles with 2 splits."""
     key = (M, lin.N, lin.Kw)
     if key in _TUNED_P:
+        return _TUNED_P[key]
+    if MxLin.use_table and key in _FIXED_P:
+        _TUNED_P[key] = _FIXED_P[key]
         return _TUNED_P[key]
     lib = _lib.load()
     best = (8, 2)
