@@ -99,17 +99,18 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N <= 63, "vmcnt field");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// Wait until at most min(ahead, A) ring stages of LPS loads each are still in flight.
-template <int LPS, int A>
+// Wait until at most E + min(ahead, A) * LPS loads are still in flight: ring stages of LPS loads each, plus E loads
+// issued after the awaited stage's own (in the same issue call).
+template <int LPS, int A, int E = 0>
 __device__ __forceinline__ void wait_stages(int ahead) {
   if constexpr (A > 0) {
     if (ahead >= A) {
-      wait_vm<A * LPS>();
+      wait_vm<E + A * LPS>();
       return;
     }
-    wait_stages<LPS, A - 1>(ahead);
+    wait_stages<LPS, A - 1, E>(ahead);
   } else {
-    wait_vm<0>();
+    wait_vm<E>();
   }
 }
 

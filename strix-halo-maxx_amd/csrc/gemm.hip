@@ -35,41 +35,113 @@ namespace {
 
 constexpr int BK = 64;
 
-// Epilogue for output row m, columns n .. n+3 from fp32 sums s[0..3]: + bias, round to bf16, optional activation
-// (rounded again), optional + residual (fp32 add, rounded once more); act 3 writes the gated pair results to
-// columns n / 2, n / 2 + 1.
-__device__ __forceinline__ void epi4(const float* s, int m, int n, const float* __restrict__ bias,
-                                     const uint16_t* __restrict__ R, long ldr, int r_rows, uint16_t* __restrict__ C,
-                                     long ldc, int act, int act_ncols) {
+// Tile order. Dispatch sends workgroup b to XCD (b % 8), so each XCD is given a contiguous run of the tile sequence
+// (split-major, then tile). Inside a run, tiles go in groups of GM row panels, column-major within a group: the 32
+// workgroups an XCD runs at once then share GM panels of A and a few panels of W in that XCD's L2, instead of
+// sweeping every row panel of A past one W panel. Grids with at most GM row panels keep plain column-major order.
+constexpr int GM = 8;
+__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int splits, int& tm, int& tn, int& split) {
+  const int nt = tiles_m * tiles_n, ntot = nt * splits;
+  const int per = ntot / 8, rem = ntot % 8, xcd = b % 8, idx = b / 8;
+  const int t = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  const int tile = t % nt;
+  split = t / nt;
+  const int grp = tile / (GM * tiles_n), first = grp * GM, gs = min(tiles_m - first, GM);
+  const int r = tile - grp * GM * tiles_n;
+  tm = first + r % gs;
+  tn = r / gs;
+}
+
+// Epilogue of one 4-column group (output row m, columns n .. n+3) from fp32 sums s: + bias, round to bf16, activation
+// ACT (1 GELU-tanh, 2 GELU-erf; rounded again; skipped for columns >= act_ncols when act_ncols > 0), + residual
+// (fp32 add, rounded once more). ACT 3 is the gated GELU of interleaved (gate, up) column pairs, written to columns
+// n / 2, n / 2 + 1. Bias and residual come in as operands: callers load every group's before their first store, so
+// no store has to wait behind a load issued after an earlier store (vmcnt counts both).
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+template <int ACT>
+__device__ __forceinline__ u32x2 epi_val(const f32x4& s, const f32x4& bv, const u32x2& rv, bool has_r, int n,
+                                         int act_ncols) {
   float v[4];
-  f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-  if (bias) bv = *reinterpret_cast<const f32x4*>(bias + n);
 #pragma unroll
   for (int e = 0; e < 4; e++) v[e] = rbf(s[e] + bv[e]);
-  if (act == 3) {
-    // gated GELU on interleaved (gate, up) column pairs -> output column n / 2 + {0, 1}
-    const uint32_t o = pack2(rbf(gelu_tanh(v[0])) * v[1], rbf(gelu_tanh(v[2])) * v[3]);
-    *reinterpret_cast<uint32_t*>(C + (long)m * ldc + (n >> 1)) = o;
-    return;
-  }
-  if (act_ncols > 0 && n >= act_ncols) {
-    // no activation on this column range
-  } else if (act == 1) {
-#pragma unroll
-    for (int e = 0; e < 4; e++) v[e] = rbf(gelu_tanh(v[e]));
-  } else if (act == 2) {
-#pragma unroll
-    for (int e = 0; e < 4; e++) v[e] = rbf(gelu_erf(v[e]));
-  }
-  if (R) {
-    const int rm = r_rows > 0 ? m % r_rows : m;
-    const u32x2 rr = *reinterpret_cast<const u32x2*>(R + (long)rm * ldr + n);
-    v[0] += lo_bf(rr.x); v[1] += hi_bf(rr.x); v[2] += lo_bf(rr.y); v[3] += hi_bf(rr.y);
-  }
   u32x2 o;
-  o.x = pack2(v[0], v[1]);
-  o.y = pack2(v[2], v[3]);
-  *reinterpret_cast<u32x2*>(C + (long)m * ldc + n) = o;
+  if constexpr (ACT == 3) {
+    o.x = pack2(rbf(gelu_tanh(v[0])) * v[1], rbf(gelu_tanh(v[2])) * v[3]);
+    o.y = 0;
+  } else {
+    if constexpr (ACT == 1 || ACT == 2) {
+      if (act_ncols <= 0 || n < act_ncols) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = rbf(ACT == 1 ? gelu_tanh(v[e]) : gelu_erf(v[e]));
+      }
+    }
+    if (has_r) {
+      v[0] += lo_bf(rv.x);
+      v[1] += hi_bf(rv.x);
+      v[2] += lo_bf(rv.y);
+      v[3] += hi_bf(rv.y);
+    }
+    o.x = pack2(v[0], v[1]);
+    o.y = pack2(v[2], v[3]);
+  }
+  return o;
+}
+// Group result into the LDS staging tile (row pitch SP elements) at tile row r, tile column c (ACT 3: column c / 2).
+template <int ACT, int SP>
+__device__ __forceinline__ void stage_val(uint16_t* st, int r, int c, const u32x2& o) {
+  if constexpr (ACT == 3)
+    *reinterpret_cast<uint32_t*>(st + r * SP + (c >> 1)) = o.x;
+  else
+    *reinterpret_cast<u32x2*>(st + r * SP + c) = o;
+}
+// Staged ROWS x COLS tile (LDS, row pitch PITCH elements of T) -> C[m0 + r][c0 + c], rows < M, columns < Ncols.
+// The workgroup's 256 threads take consecutive 16-byte chunks of consecutive rows, so each wave store covers whole
+// cache lines (the MFMA layout alone would write 16-32 bytes into each of 32 lines per store).
+template <int ROWS, int COLS, int PITCH, typename T>
+__device__ __forceinline__ void store_staged(const T* st, T* __restrict__ C, long ldc, int m0, int c0, int M, int Ncols,
+                                             int tid) {
+  constexpr int EPC = 16 / sizeof(T), CPR = (COLS + EPC - 1) / EPC, TOT = ROWS * CPR;
+  const bool a16 = ((ldc * (long)sizeof(T)) % 16 == 0) && ((uintptr_t)C % 16 == 0) && ((c0 * (int)sizeof(T)) % 16 == 0);
+#pragma unroll
+  for (int idx0 = 0; idx0 < TOT; idx0 += 256) {
+    const int idx = idx0 + tid;
+    if (idx < TOT) {
+      const int r = idx / CPR, cc = idx % CPR;
+      const int m = m0 + r, n = c0 + cc * EPC;
+      if (m < M && n < Ncols) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * PITCH + cc * EPC);
+        T* dst = C + (long)m * ldc + n;
+        if (n + EPC <= Ncols && a16) {
+          *reinterpret_cast<u32x4*>(dst) = v;
+        } else {
+          *reinterpret_cast<u32x2*>(dst) = u32x2{v.x, v.y};
+          if (n + EPC <= Ncols) *reinterpret_cast<u32x2*>(dst + EPC / 2) = u32x2{v.z, v.w};
+        }
+      }
+    }
+  }
+}
+// Group operands, read from clamped (always valid) addresses; values of out-of-range groups are never stored.
+__device__ __forceinline__ f32x4 bias4(const float* __restrict__ bias, int n, int N) {
+  return *reinterpret_cast<const f32x4*>(bias + min(n, N - 4));
+}
+__device__ __forceinline__ u32x2 res4(const uint16_t* __restrict__ R, long ldr, int r_rows, int m, int n, int M, int N) {
+  int rm = min(m, M - 1);
+  if (r_rows > 0) rm %= r_rows;
+  return *reinterpret_cast<const u32x2*>(R + (long)rm * ldr + min(n, N - 4));
+}
+// Run f(IntC<act>) for the runtime activation code act (0..3).
+template <typename F>
+__device__ __forceinline__ void with_act(int act, F&& f) {
+  switch (act) {
+    case 1: f(IntC<1>{}); break;
+    case 2: f(IntC<2>{}); break;
+    case 3: f(IntC<3>{}); break;
+    default: f(IntC<0>{}); break;
+  }
 }
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -89,13 +161,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
   __shared__ __attribute__((aligned(1024))) uint16_t smem[S * STAGE];
   __shared__ int s_last;
 
-  // ---- XCD-aware order over (split, tile_n, tile_m): dispatch sends workgroup b to XCD (b % 8).
-  const int nt = tiles_m * tiles_n * splits;
-  const int b = blockIdx.x;
-  const int per = nt / 8, rem = nt % 8, xcd = b % 8, idx = b / 8;
-  const int t = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
-  const int tile = t % (tiles_m * tiles_n), split = t / (tiles_m * tiles_n);
-  const int tile_m = tile % tiles_m, tile_n = tile / tiles_m;
+  int tile_m, tile_n, split;
+  tile_of(blockIdx.x, tiles_m, tiles_n, splits, tile_m, tile_n, split);
+  const int tile = tile_n * tiles_m + tile_m;  // split-K workspace slot
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   const int nk_all = Kw / BK;
   const int kt0 = split * kt_per_split;
@@ -204,22 +272,52 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     if (tid == 0) cnt[tile] = 0;
   }
 
-  // ---- epilogue: lane holds output row m, columns n .. n+3 for each 8-row group g of the MFMA result
+  // ---- epilogue: lane holds output row m, columns n .. n+3 for each 8-row group g of the MFMA result. Every bias and
+  // residual load is issued before the first store.
+  f32x4 bv[FN][4];
+  u32x2 rv[FN][FM][4];
 #pragma unroll
-  for (int i = 0; i < FN; i++) {
+  for (int i = 0; i < FN; i++)
 #pragma unroll
-    for (int j = 0; j < FM; j++) {
-      const int m = m0 + wm * WTM + j * 32 + lr;
-      if (m >= M) continue;
+    for (int g = 0; g < 4; g++) bv[i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (bias) {
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int n = n0 + wn * WTN + i * 32 + 8 * g + 4 * hk;
-        if (n >= N) continue;
-        const float a4[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-        epi4(a4, m, n, bias, R, ldr, r_rows, C, ldc, act, act_ncols);
-      }
-    }
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) bv[i][g] = bias4(bias, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N);
   }
+  if (R) {
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          rv[i][j][g] = res4(R, ldr, r_rows, m0 + wm * WTM + j * 32 + lr, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, M, N);
+  }
+  // results go through an LDS staging tile (the ring is free once every wave is past its last k-step)
+  constexpr int SP = BN + 8;
+  static_assert(BM * SP <= S * STAGE, "staging tile fits the ring");
+  __syncthreads();
+  with_act(act, [&](auto ac) {
+    constexpr int ACT = decltype(ac)::value;
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int c = wn * WTN + i * 32 + 8 * g + 4 * hk;
+          const f32x4 a4 = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          stage_val<ACT, SP>(smem, wm * WTM + j * 32 + lr, c,
+                             epi_val<ACT>(a4, bv[i][g], rv[i][j][g], R != nullptr, n0 + c, act_ncols));
+        }
+  });
+  __syncthreads();
+  if (act == 3)
+    store_staged<BM, BN / 2, SP>(smem, C, ldc, m0, n0 / 2, M, N / 2, tid);
+  else
+    store_staged<BM, BN, SP>(smem, C, ldc, m0, n0, M, N, tid);
 }
 
 // Wave-split-K kernel (see the header): 4 waves share the LDS ring of a BM x BN tile; wave w multiplies the k
@@ -242,12 +340,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_ks_kernel(
   uint16_t* smem = reinterpret_cast<uint16_t*>(smem_b);
   f32x4* red = reinterpret_cast<f32x4*>(smem_b);
 
-  const int nt = tiles_m * tiles_n, ntot = nt * splits;
-  const int b = blockIdx.x;
-  const int per = ntot / 8, rem = ntot % 8, xcd = b % 8, idx = b / 8;
-  const int t = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
-  const int tile = t % nt, split = t / nt;
-  const int tile_m = tile % tiles_m, tile_n = tile / tiles_m;
+  int tile_m, tile_n, split;
+  tile_of(blockIdx.x, tiles_m, tiles_n, splits, tile_m, tile_n, split);
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   const int kt0 = split * kt_per_split;
   const int nk = min(Kw / BK, kt0 + kt_per_split) - kt0;  // k-steps of this split
@@ -340,21 +434,60 @@ __global__ __launch_bounds__(256, OCC) void gemm_ks_kernel(
   __syncthreads();
   if (wave < 2) put(wave);
   __syncthreads();
+  // this wave's groups q = wave + 4 t: sums, then (fused epilogue) every bias / residual load before the first store
+  constexpr int GW = G / 4;
+  static_assert(G % 4 == 0, "groups split evenly over the waves");
+  f32x4 vs[GW];
 #pragma unroll
-  for (int q = wave; q < G; q += 4) {
-    const f32x4 v = red[q * 64 + lane] + red[(G + q) * 64 + lane];
-    const int i = q / (FM * 4), j = (q / 4) % FM, g = q % 4;
-    const int m = m0 + j * 32 + lr;
-    const int n = n0 + i * 32 + 8 * g + 4 * hk;
-    if (m < M && n < N) {
-      if (P) {
-        *reinterpret_cast<f32x4*>(P + split * p_split + (long)m * ldp + n) = v;  // raw partial sums
-      } else {
-        const float a4[4] = {v[0], v[1], v[2], v[3]};
-        epi4(a4, m, n, bias, R, ldr, r_rows, C, ldc, act, act_ncols);
-      }
-    }
+  for (int t = 0; t < GW; t++) {
+    const int q = wave + 4 * t;
+    vs[t] = red[q * 64 + lane] + red[(G + q) * 64 + lane];
   }
+  auto row_of = [&](int t) { return m0 + ((wave + 4 * t) / 4) % FM * 32 + lr; };
+  auto col_of = [&](int t) {
+    const int q = wave + 4 * t;
+    return n0 + q / (FM * 4) * 32 + 8 * (q % 4) + 4 * hk;
+  };
+  __syncthreads();  // every wave has its sums: the LDS becomes the staging tile
+  if (P) {
+    // raw fp32 partial sums, staged like the bf16 results
+    constexpr int SPF = BN + 4;
+    static_assert(BM * SPF * 4 <= sizeof(smem_b), "fp32 staging tile fits");
+    float* stf = reinterpret_cast<float*>(smem_b);
+#pragma unroll
+    for (int t = 0; t < GW; t++)
+      *reinterpret_cast<f32x4*>(stf + (row_of(t) - m0) * SPF + (col_of(t) - n0)) = vs[t];
+    __syncthreads();
+    store_staged<BM, BN, SPF>(stf, P + split * p_split, ldp, m0, n0, M, N, tid);
+    return;
+  }
+  f32x4 bv[GW];
+  u32x2 rv[GW];
+#pragma unroll
+  for (int t = 0; t < GW; t++) bv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (bias) {
+#pragma unroll
+    for (int t = 0; t < GW; t++) bv[t] = bias4(bias, col_of(t), N);
+  }
+  if (R) {
+#pragma unroll
+    for (int t = 0; t < GW; t++) rv[t] = res4(R, ldr, r_rows, row_of(t), col_of(t), M, N);
+  }
+  constexpr int SP = BN + 8;
+  static_assert(BM * SP * 2 <= sizeof(smem_b), "staging tile fits");
+  with_act(act, [&](auto ac) {
+    constexpr int ACT = decltype(ac)::value;
+#pragma unroll
+    for (int t = 0; t < GW; t++) {
+      const int n = col_of(t);
+      stage_val<ACT, SP>(smem, row_of(t) - m0, n - n0, epi_val<ACT>(vs[t], bv[t], rv[t], R != nullptr, n, act_ncols));
+    }
+  });
+  __syncthreads();
+  if (act == 3)
+    store_staged<BM, BN / 2, SP>(smem, C, ldc, m0, n0 / 2, M, N / 2, tid);
+  else
+    store_staged<BM, BN, SP>(smem, C, ldc, m0, n0, M, N, tid);
 }
 
 struct Cfg { int bm, bn, stages, per_cu, kind; };
