@@ -55,8 +55,7 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int spl
 // Epilogue of one 4-column group (output row m, columns n .. n+3) from fp32 sums s: + bias, round to bf16, activation
 // ACT (1 GELU-tanh, 2 GELU-erf; rounded again; skipped for columns >= act_ncols when act_ncols > 0), + residual
 // (fp32 add, rounded once more). ACT 3 is the gated GELU of interleaved (gate, up) column pairs, written to columns
-// n / 2, n / 2 + 1. Bias and residual come in as operands: callers load every group's before their first store, so
-// no store has to wait behind a load issued after an earlier store (vmcnt counts both).
+// n / 2, n / 2 + 1.
 template <int V>
 struct IntC {
   static constexpr int value = V;
@@ -100,13 +99,13 @@ __device__ __forceinline__ void stage_val(uint16_t* st, int r, int c, const u32x
 // Staged ROWS x COLS tile (LDS, row pitch PITCH elements of T) -> C[m0 + r][c0 + c], rows < M, columns < Ncols.
 // The workgroup's 256 threads take consecutive 16-byte chunks of consecutive rows, so each wave store covers whole
 // cache lines (the MFMA layout alone would write 16-32 bytes into each of 32 lines per store).
-template <int ROWS, int COLS, int PITCH, typename T>
+template <int ROWS, int COLS, int PITCH, int NT = 256, typename T>
 __device__ __forceinline__ void store_staged(const T* st, T* __restrict__ C, long ldc, int m0, int c0, int M, int Ncols,
                                              int tid) {
   constexpr int EPC = 16 / sizeof(T), CPR = (COLS + EPC - 1) / EPC, TOT = ROWS * CPR;
   const bool a16 = ((ldc * (long)sizeof(T)) % 16 == 0) && ((uintptr_t)C % 16 == 0) && ((c0 * (int)sizeof(T)) % 16 == 0);
 #pragma unroll
-  for (int idx0 = 0; idx0 < TOT; idx0 += 256) {
+  for (int idx0 = 0; idx0 < TOT; idx0 += NT) {
     const int idx = idx0 + tid;
     if (idx < TOT) {
       const int r = idx / CPR, cc = idx % CPR;
@@ -116,9 +115,12 @@ __device__ __forceinline__ void store_staged(const T* st, T* __restrict__ C, lon
         T* dst = C + (long)m * ldc + n;
         if (n + EPC <= Ncols && a16) {
           *reinterpret_cast<u32x4*>(dst) = v;
-        } else {
-          *reinterpret_cast<u32x2*>(dst) = u32x2{v.x, v.y};
-          if (n + EPC <= Ncols) *reinterpret_cast<u32x2*>(dst + EPC / 2) = u32x2{v.z, v.w};
+        } else {  // unaligned row or the row's tail: 4-byte words (callers keep rows 4-byte aligned)
+          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+          const int nw = min(4, (Ncols - n) * (int)sizeof(T) / 4);
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (e < nw) reinterpret_cast<uint32_t*>(dst)[e] = w[e];
         }
       }
     }
@@ -145,20 +147,27 @@ __device__ __forceinline__ void with_act(int act, F&& f) {
 }
 
 template <int BM, int BN, int WGM, int WGN, int S>
-__global__ __launch_bounds__(256) void gemm_bf16_kernel(
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
     const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
     uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols,
-    int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt) {
-  static_assert(WGM * WGN == 4, "4 waves per workgroup");
+    int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt,
+    float* __restrict__ P, long ldp, long p_split) {
+  constexpr int NW = WGM * WGN, NT = 64 * NW;
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
   static_assert(S >= 2, "at least a double buffer");
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int QA = BM / 32, QW = BN / 32;  // DMA instructions per wave per stage
+  constexpr int QA = BM / (8 * NW), QW = BN / (8 * NW);  // DMA instructions per wave per stage
+  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "whole DMA instructions per wave");
   constexpr int LPS = QA + QW;
   constexpr int STAGE = (BM + BN) * BK;      // elements per ring stage
   static_assert(FM >= 1 && FN >= 1 && QA >= 1 && QW >= 1, "tile too small");
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[S * STAGE];
+  constexpr int SP = BN + 8;  // row pitch of the epilogue's staging tile (reuses the ring)
+  constexpr int SPF = BN + 4;  // row pitch of the fp32 staging tile of the partial-sum mode (4-wave tiles)
+  constexpr int SMEM0 = S * STAGE > BM * SP ? S * STAGE : BM * SP;
+  constexpr int SMEM = NW == 4 && BM * SPF * 2 > SMEM0 ? BM * SPF * 2 : SMEM0;
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
   __shared__ int s_last;
 
   int tile_m, tile_n, split;
@@ -180,12 +189,12 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
   const uint16_t* w_src[QW];
 #pragma unroll
   for (int q = 0; q < QA; q++) {
-    const int gm = min(m0 + 8 * (q * 4 + wave) + drow, M - 1);
+    const int gm = min(m0 + 8 * (q * NW + wave) + drow, M - 1);
     a_src[q] = A + (long)gm * lda;
   }
 #pragma unroll
   for (int q = 0; q < QW; q++) {
-    const int gn = min(n0 + 8 * (q * 4 + wave) + drow, N - 1);
+    const int gn = min(n0 + 8 * (q * NW + wave) + drow, N - 1);
     w_src[q] = W + (long)gn * ldw;
   }
   auto issue = [&](int kt, int s) {
@@ -193,10 +202,10 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     const int ka = kk < K ? kk : 0;
     const uint32_t st = sbase + (uint32_t)(s * STAGE * 2);
 #pragma unroll
-    for (int q = 0; q < QA; q++) dma16(a_src[q] + ka, __builtin_amdgcn_readfirstlane(st + (q * 4 + wave) * 1024));
+    for (int q = 0; q < QA; q++) dma16(a_src[q] + ka, __builtin_amdgcn_readfirstlane(st + (q * NW + wave) * 1024));
 #pragma unroll
     for (int q = 0; q < QW; q++)
-      dma16(w_src[q] + kk, __builtin_amdgcn_readfirstlane(st + BM * 128 + (q * 4 + wave) * 1024));
+      dma16(w_src[q] + kk, __builtin_amdgcn_readfirstlane(st + BM * 128 + (q * NW + wave) * 1024));
   };
 
   f32x16 acc[FN][FM];
@@ -239,8 +248,29 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     }
   }
 
-  // ---- split-K: partial tile to the workspace; the last split to arrive reduces in split order
-  if (splits > 1) {
+  // ---- partial-sum mode (mx_gemm_bf16_partial): this split's raw fp32 sums to its slab of P, staged like the bf16
+  // results; no bias, activation or residual
+  if constexpr (NW == 4) {
+    if (P) {
+      float* stf = reinterpret_cast<float*>(smem);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++)
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+            *reinterpret_cast<f32x4*>(stf + (wm * WTM + j * 32 + lr) * SPF + wn * WTN + i * 32 + 8 * g + 4 * hk) =
+                f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+      __syncthreads();
+      store_staged<BM, BN, SPF, NT>(stf, P + split * p_split, ldp, m0, n0, M, N, tid);
+      return;
+    }
+  }
+
+  // ---- split-K: partial tile to the workspace; the last split to arrive reduces in split order (4-wave tiles only:
+  // the 8-wave tiles serve grids large enough without it)
+  if (NW == 4 && splits > 1) {
     constexpr int TE = BM * BN;
     float* mine = ws + (long)(tile * splits + split) * TE;
 #pragma unroll
@@ -272,32 +302,29 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
     if (tid == 0) cnt[tile] = 0;
   }
 
-  // ---- epilogue: lane holds output row m, columns n .. n+3 for each 8-row group g of the MFMA result. Every bias and
-  // residual load is issued before the first store.
+  // ---- epilogue: lane holds output row m, columns n .. n+3 for each 8-row group g of the MFMA result. Results go
+  // through an LDS staging tile (the ring is free once every wave is past its last k-step) and reach C only in the
+  // final copy, so the bias / residual loads here never queue behind stores. They are all issued up front (one
+  // latency for the lot) where the registers allow: always for the bias, for the residual on 4-wave tiles.
+  constexpr bool HOIST_R = FN * FM <= 4;
   f32x4 bv[FN][4];
-  u32x2 rv[FN][FM][4];
+  u32x2 rv[HOIST_R ? FN : 1][HOIST_R ? FM : 1][4];
 #pragma unroll
   for (int i = 0; i < FN; i++)
 #pragma unroll
-    for (int g = 0; g < 4; g++) bv[i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (bias) {
+    for (int g = 0; g < 4; g++)
+      bv[i][g] = bias ? bias4(bias, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N) : f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (HOIST_R) {
+    if (R) {
 #pragma unroll
-    for (int i = 0; i < FN; i++)
+      for (int i = 0; i < FN; i++)
 #pragma unroll
-      for (int g = 0; g < 4; g++) bv[i][g] = bias4(bias, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N);
+        for (int j = 0; j < FM; j++)
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+            rv[i][j][g] = res4(R, ldr, r_rows, m0 + wm * WTM + j * 32 + lr, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, M, N);
+    }
   }
-  if (R) {
-#pragma unroll
-    for (int i = 0; i < FN; i++)
-#pragma unroll
-      for (int j = 0; j < FM; j++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-          rv[i][j][g] = res4(R, ldr, r_rows, m0 + wm * WTM + j * 32 + lr, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, M, N);
-  }
-  // results go through an LDS staging tile (the ring is free once every wave is past its last k-step)
-  constexpr int SP = BN + 8;
-  static_assert(BM * SP <= S * STAGE, "staging tile fits the ring");
   __syncthreads();
   with_act(act, [&](auto ac) {
     constexpr int ACT = decltype(ac)::value;
@@ -307,17 +334,21 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(
       for (int j = 0; j < FM; j++)
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-          const int c = wn * WTN + i * 32 + 8 * g + 4 * hk;
+          const int r = wm * WTM + j * 32 + lr, c = wn * WTN + i * 32 + 8 * g + 4 * hk;
+          u32x2 rg = {0u, 0u};
+          if constexpr (HOIST_R)
+            rg = rv[i][j][g];
+          else if (R)
+            rg = res4(R, ldr, r_rows, m0 + r, n0 + c, M, N);
           const f32x4 a4 = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          stage_val<ACT, SP>(smem, wm * WTM + j * 32 + lr, c,
-                             epi_val<ACT>(a4, bv[i][g], rv[i][j][g], R != nullptr, n0 + c, act_ncols));
+          stage_val<ACT, SP>(smem, r, c, epi_val<ACT>(a4, bv[i][g], rg, R != nullptr, n0 + c, act_ncols));
         }
   });
   __syncthreads();
   if (act == 3)
-    store_staged<BM, BN / 2, SP>(smem, C, ldc, m0, n0 / 2, M, N / 2, tid);
+    store_staged<BM, BN / 2, SP, NT>(smem, C, ldc, m0, n0 / 2, M, N / 2, tid);
   else
-    store_staged<BM, BN, SP>(smem, C, ldc, m0, n0, M, N, tid);
+    store_staged<BM, BN, SP, NT>(smem, C, ldc, m0, n0, M, N, tid);
 }
 
 // Wave-split-K kernel (see the header): 4 waves share the LDS ring of a BM x BN tile; wave w multiplies the k
@@ -461,17 +492,13 @@ __global__ __launch_bounds__(256, OCC) void gemm_ks_kernel(
     store_staged<BM, BN, SPF>(stf, P + split * p_split, ldp, m0, n0, M, N, tid);
     return;
   }
+  // every bias / residual load issued before the first use (one latency for the lot)
   f32x4 bv[GW];
   u32x2 rv[GW];
 #pragma unroll
-  for (int t = 0; t < GW; t++) bv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (bias) {
-#pragma unroll
-    for (int t = 0; t < GW; t++) bv[t] = bias4(bias, col_of(t), N);
-  }
-  if (R) {
-#pragma unroll
-    for (int t = 0; t < GW; t++) rv[t] = res4(R, ldr, r_rows, row_of(t), col_of(t), M, N);
+  for (int t = 0; t < GW; t++) {
+    bv[t] = bias ? bias4(bias, col_of(t), N) : f32x4{0.f, 0.f, 0.f, 0.f};
+    rv[t] = R ? res4(R, ldr, r_rows, row_of(t), col_of(t), M, N) : u32x2{0u, 0u};
   }
   constexpr int SP = BN + 8;
   static_assert(BM * SP * 2 <= sizeof(smem_b), "staging tile fits");
@@ -490,25 +517,29 @@ __global__ __launch_bounds__(256, OCC) void gemm_ks_kernel(
     store_staged<BM, BN, SP>(smem, C, ldc, m0, n0, M, N, tid);
 }
 
-struct Cfg { int bm, bn, stages, per_cu, kind; };
+struct Cfg { int bm, bn, stages, per_cu, kind, waves; };
 // kind 0: LDS-shared tile split over the waves; kind 1: wave-split K (each wave the whole tile, a quarter of K).
 // Both stage operands through a `stages`-deep LDS ring.
 // per_cu: workgroups that fit one CU at once (LDS- or register-limited)
-constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0}, {64, 128, 4, 1, 0}, {128, 64, 4, 1, 0}, {64, 64, 4, 2, 0},
-                         {256, 128, 3, 1, 0}, {128, 256, 3, 1, 0}, {64, 64, 3, 3, 0}, {128, 128, 2, 2, 0},
-                         {64, 64, 4, 2, 1},   {64, 128, 4, 1, 1},  {128, 64, 4, 1, 1}, {64, 64, 3, 3, 1},
-                         {64, 96, 2, 3, 1},   {64, 64, 6, 1, 1},   {96, 64, 2, 3, 1}};
+constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0, 4}, {64, 128, 4, 1, 0, 4}, {128, 64, 4, 1, 0, 4}, {64, 64, 4, 2, 0, 4},
+                         {256, 128, 3, 1, 0, 4}, {128, 256, 3, 1, 0, 4}, {64, 64, 3, 3, 0, 4}, {128, 128, 2, 2, 0, 4},
+                         {64, 64, 4, 2, 1, 4},   {64, 128, 4, 1, 1, 4},  {128, 64, 4, 1, 1, 4}, {64, 64, 3, 3, 1, 4},
+                         {64, 96, 2, 3, 1, 4},   {64, 64, 6, 1, 1, 4},   {96, 64, 2, 3, 1, 4},
+                         // 8-wave tiles for large grids: 2 waves per SIMD hide each other's LDS reads and barriers
+                         {256, 256, 2, 1, 0, 8}, {256, 128, 3, 1, 0, 8}, {128, 256, 3, 1, 0, 8}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int BM, int BN, int WGM, int WGN, int S>
 hipError_t launch(hipStream_t st, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
                   const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N,
-                  int K, int Kw, int act, int act_ncols, float* ws, int* cnt) {
+                  int K, int Kw, int act, int act_ncols, float* ws, int* cnt, float* P = nullptr, long ldp = 0,
+                  long p_split = 0) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   const int nk = Kw / BK;
   const int kps = (nk + splits - 1) / splits;
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn * splits), dim3(256), 0, st, A, lda, W,
-                     ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, tm, tn, splits, kps, ws, cnt);
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn * splits), dim3(64 * WGM * WGN), 0, st, A, lda, W,
+                     ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, tm, tn, splits, kps, ws, cnt, P,
+                     ldp, p_split);
   return hipGetLastError();
 }
 
@@ -556,13 +587,15 @@ extern "C" long mx_gemm_ws_counters(int cfg, int splits, int M, int N) {
 // Default (cfg, splits) when the caller passes cfg < 0: minimise estimated time = rounds of workgroups over the
 // 256 CUs x per-tile time, with per-tile time ~ BM*BN*(k-steps)/efficiency. Returns cfg * 16 + splits.
 extern "C" int mx_gemm_pick(int M, int N, int Kw) {
-  static const float eff[kNCfg] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};
+  static const float eff[kNCfg] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f,
+                                   1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f};
   const int nk = Kw / BK;
   int best = 0, bsplit = 1;
   float bt = 1e30f;
   for (int c = 0; c < kNCfg; c++) {
     for (int sp = 1; sp <= 8; sp *= 2) {
-      if (sp > 1 && (kCfgs[c].kind || nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk)) break;
+      if (sp > 1 && (kCfgs[c].kind || kCfgs[c].waves != 4 || nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk))
+        break;
       const long tiles = tiles_of(c, M, N) * sp;
       const long slots = 256L * kCfgs[c].per_cu;
       const long rounds = (tiles + slots - 1) / slots;
@@ -591,7 +624,7 @@ extern "C" int mx_gemm_check(int cfg, int splits, const void* A, long lda, const
   if (bias && ((uintptr_t)bias & 15)) return MX_ELAYOUT;
   if (R && (((uintptr_t)R & 7) || ldr % 4 || ldr < N)) return MX_ELAYOUT;
   if (cfg >= 0 && splits > 1) {
-    if (kCfgs[cfg].kind) return MX_ESPLIT;  // the wave-split kind splits K inside the workgroup only
+    if (kCfgs[cfg].kind || kCfgs[cfg].waves != 4) return MX_ESPLIT;  // 4-wave kind-0 tiles only
     const int nk = Kw / BK, kps = (nk + splits - 1) / splits;
     if (splits > nk || (splits - 1) * kps >= nk) return MX_ESPLIT;  // every split must own >= 1 k-step
     if (!ws || !cnt) return MX_ENULL;
@@ -633,6 +666,9 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
     case 5: e = L_(128, 256, 3); break;
     case 6: e = L_(64, 64, 3); break;
     case 7: e = L_(128, 128, 2); break;
+    case 15: e = launch<256, 256, 2, 4, 2>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
+    case 16: e = launch<256, 128, 4, 2, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
+    case 17: e = launch<128, 256, 2, 4, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
 #define W_(BM, BN, S, OCC) launch_ks<BM, BN, S, OCC>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
     case 8: e = W_(64, 64, 4, 2); break;
     case 9: e = W_(64, 128, 4, 1); break;
@@ -654,7 +690,7 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
 extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda,
                                     const uint16_t* W, long ldw, float* P, long ldp, long p_split, int M, int N, int K,
                                     int Kw) {
-  if (cfg < 0 || cfg >= kNCfg || kCfgs[cfg].kind != 1) return MX_EBADCFG;
+  if (cfg < 0 || cfg >= kNCfg || kCfgs[cfg].waves != 4) return MX_EBADCFG;
   if (!P) return MX_ENULL;
   int rc = mx_gemm_check(cfg, 1, A, lda, W, ldw, nullptr, nullptr, 0, P, ldp, M, N, K, Kw, 0, nullptr, 0, nullptr, 0);
   if (rc) return rc;
@@ -666,7 +702,16 @@ extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const u
     return MX_ELAYOUT;
   hipError_t e;
 #define W_(BM, BN, S, OCC) launch_ks<BM, BN, S, OCC>(st, A, lda, W, ldw, nullptr, nullptr, 0, 0, nullptr, 0, M, N, K, Kw, 0, 0, splits, P, ldp, p_split)
+#define L_(BM, BN, S) launch<BM, BN, 2, 2, S>(st, splits, A, lda, W, ldw, nullptr, nullptr, 0, 0, nullptr, 0, M, N, K, Kw, 0, 0, nullptr, nullptr, P, ldp, p_split)
   switch (cfg) {
+    case 0: e = L_(128, 128, 4); break;
+    case 1: e = L_(64, 128, 4); break;
+    case 2: e = L_(128, 64, 4); break;
+    case 3: e = L_(64, 64, 4); break;
+    case 4: e = L_(256, 128, 3); break;
+    case 5: e = L_(128, 256, 3); break;
+    case 6: e = L_(64, 64, 3); break;
+    case 7: e = L_(128, 128, 2); break;
     case 8: e = W_(64, 64, 4, 2); break;
     case 9: e = W_(64, 128, 4, 1); break;
     case 10: e = W_(128, 64, 4, 1); break;
@@ -677,5 +722,6 @@ extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const u
     default: return MX_EBADCFG;
   }
 #undef W_
+#undef L_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

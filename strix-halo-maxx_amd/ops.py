@@ -204,8 +204,8 @@ def _partial(lin, cfg, sp, x2, P, M):
 
 
 def _partial_cfg(lin, M, x2):
-    """(cfg, splits) for the split-K partial GEMM: every wave-split config x splits in 1..4 timed once on the real
-    operands (outside graph capture), else 64x64 tiles with 2 splits."""
+    """(cfg, splits) for the split-K partial GEMM: every config with a partial-sum mode x splits in 1..4 timed once on
+    the real operands (outside graph capture), else 64x64 tiles with 2 splits."""
     key = (M, lin.N, lin.Kw)
     if key in _TUNED_P:
         return _TUNED_P[key]
@@ -219,8 +219,6 @@ def _partial_cfg(lin, M, x2):
         bt = float("inf")
         P = torch.empty(4, M, lin.N, device=x2.device, dtype=torch.float32)
         for cfg in range(lib.mx_gemm_ncfg()):
-            if lib.mx_gemm_cfg_kind(cfg) != 1:
-                continue
             for sp in (1, 2, 3, 4):
                 if sp > 1 and (nk // sp < 2 or (sp - 1) * (-(-nk // sp)) >= nk):
                     continue

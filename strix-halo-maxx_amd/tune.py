@@ -94,13 +94,13 @@ def tune_tower_b1(reps, log):
             yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
             best, bt = None, float("inf")
             for cfg in range(ncfg):
-                if lib.mx_gemm_cfg_kind(cfg) != 1:
-                    continue
                 for sp in (1, 2, 3, 4):
                     if sp > 1 and (nk // sp < 2 or (sp - 1) * (-(-nk // sp)) >= nk):
                         continue
-                    ops._TUNED_P[key] = (cfg, sp)
                     P = torch.empty(sp, M, lin0.N, device=dev, dtype=torch.float32)
+                    if ops._partial(lin0, cfg, sp, ops._rows(saved[0][inp], lin0.K), P, M) != 0:
+                        continue  # no partial-sum mode for this config
+                    ops._TUNED_P[key] = (cfg, sp)
 
                     def run():
                         for i, b in enumerate(blocks):

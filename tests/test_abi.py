@@ -117,8 +117,8 @@ def test_other_entry_points_refuse_bad_shapes():
     assert lib.mx_decode_attn(None, A16, A16, A16, A16, 32, 1024, A16, 8, 0.125, None, None, None) == -6
     assert lib.mx_residual_layernorm(None, A16, 5, 0, 1152, None, A16, 1152, A16, 1152, None, None, None, 0,
                                      729, 1152, 1e-6) == -2                       # more than 4 splits
-    assert lib.mx_gemm_bf16_partial(None, 3, 2, A16, 1152, A16, 1152, A16, 1152, 729 * 1152, 729, 1152,
-                                    1152, 1152) == -1                            # not a wave-split cfg
+    assert lib.mx_gemm_bf16_partial(None, 15, 2, A16, 1152, A16, 1152, A16, 1152, 729 * 1152, 729, 1152,
+                                    1152, 1152) == -1                            # an 8-wave cfg
     assert lib.mx_ssm_step(None, A16, A16, A16, A16, 1536, A16, 1536, A16, A16, A16, A16, A16, A16, A16, A16, A16,
                            A16, 768, 1280, 700) == -2                                 # C not a multiple of 64
     assert lib.mx_rglru_scan(None, A16, A16, A16, 4, 1280, 700, A16, 1536, 0, A16, 768, 0) == -2

@@ -49,13 +49,16 @@ def test_gemm_bias_vs_fp32(dev, M, K, N):
     assert (y.float().cpu() - ref).abs().max().item() < 0.02 * ref.abs().max().item() + 1e-2
 
 
-@pytest.mark.parametrize("cfg", range(15))
+NCFG = 18  # tile configs the library exports
+
+
+@pytest.mark.parametrize("cfg", range(NCFG))
 @pytest.mark.parametrize("splits", [1, 3])
 def test_gemm_every_tile_config(dev, cfg, splits):
     """Every tile config, with and without split-K, on ragged M / N / K tails (K = 1000: the last k-step is partial
-    and reads A's padding columns against W's zero padding). Wave-split-K configs reject split-K."""
+    and reads A's padding columns against W's zero padding). Wave-split-K and 8-wave configs reject split-K."""
     lib = _lib.load()
-    assert lib.mx_gemm_ncfg() == 15
+    assert lib.mx_gemm_ncfg() == NCFG
     M, K, N = 300, 1000, 1152 + 68
     g = gen(cfg)
     x = torch.randn(M, K, generator=g).to(BF)
@@ -65,7 +68,7 @@ def test_gemm_every_tile_config(dev, cfg, splits):
     lin = ops.MxLin(w, b)
     lin.cfgs[M] = (cfg, splits)
     print(f"gemm cfg={cfg} splits={splits}", flush=True)
-    if splits > 1 and lib.mx_gemm_cfg_kind(cfg) == 1:
+    if splits > 1 and (lib.mx_gemm_cfg_kind(cfg) == 1 or cfg >= 15):
         with pytest.raises(_lib.MxError, match="-3"):
             lin(x.to(dev))
         return
@@ -77,9 +80,8 @@ def test_gemm_every_tile_config(dev, cfg, splits):
 
 @pytest.mark.parametrize("M,K,N", [(729, 1152, 1152), (729, 4304, 1152), (300, 1000, 1220)])
 def test_gemm_partial_splits(dev, M, K, N):
-    """mx_gemm_bf16_partial, every wave-split config x 1-3 splits: the in-order fp32 sum of the partials is the fp32
-    product to accumulation accuracy (K = 1000: the last k-step is partial). Configs of the LDS-shared kind are
-    rejected."""
+    """mx_gemm_bf16_partial, every 4-wave config x 1-3 splits: the in-order fp32 sum of the partials is the fp32
+    product to accumulation accuracy (K = 1000: the last k-step is partial). 8-wave configs are rejected."""
     g = gen(M + K)
     x = torch.randn(M, K, generator=g).to(BF)
     w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
@@ -91,7 +93,7 @@ def test_gemm_partial_splits(dev, M, K, N):
         for sp in (1, 2, 3):
             P = torch.full((sp, M, N), float("nan"), device=dev)
             rc = ops._partial(lin, cfg, sp, x2, P, M)
-            if lib.mx_gemm_cfg_kind(cfg) != 1:
+            if cfg >= 15:  # 8-wave configs have no partial-sum mode
                 assert rc == -1
                 continue
             assert rc == 0, (cfg, sp, rc)
@@ -130,16 +132,28 @@ def test_residual_layernorm_matches_unfused(dev):
     assert torch.equal(yo.cpu(), ops.layernorm(xo, gam, bet, eps=1e-6).cpu())
 
 
-def test_gemm_epilogues_match_unfused(dev):
-    """GELU applied to the bf16-rounded linear output, then + residual (md2fast.py:55-67; i8gemm.hip:378)."""
-    M, K, N = 729, 1152, 4304
+@pytest.mark.parametrize("cfg", [None, 0, 7, 8, 12, 15, 16, 17])
+def test_gemm_epilogues_match_unfused(dev, cfg):
+    """GELU applied to the bf16-rounded linear output, then + residual (md2fast.py:55-67; i8gemm.hip:378); the gated
+    GELU of interleaved (gate, up) columns and the column-limited activation; per tile config (None: the tuned one),
+    N = 4300 leaves a partial last column tile and an 8-column chunk with 4 valid columns."""
+    M, K, N = 729, 1152, 4300
     g = gen(3)
     x = torch.randn(M, K, generator=g).to(BF).to(dev)
     w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
     b = (torch.randn(N, generator=g) * 0.02).to(BF)
     r = torch.randn(M, N, generator=g).to(BF).to(dev)
     lin = ops.MxLin(w, b)
+    if cfg is not None:
+        lin.cfgs[M] = (cfg, 1)
+    print(f"epilogues cfg={cfg}", flush=True)
     y0 = lin(x).cpu()
+    y_g = lin(x, act="glu").cpu()
+    exp_g = (F.gelu(y0[:, 0::2].float(), approximate="tanh").to(BF).float() * y0[:, 1::2].float()).to(BF)
+    assert y_g.shape == (M, N // 2) and within_ulps(y_g, exp_g)
+    y_c = lin(x, gelu=True, act_cols=1024).cpu()
+    assert torch.equal(y_c[:, 1024:], y0[:, 1024:])
+    assert within_ulps(y_c[:, :1024], F.gelu(y0[:, :1024].float(), approximate="tanh").to(BF))
     y_t = lin(x, gelu=True).cpu()
     y_e = lin(x, act="erf").cpu()
     y_r = lin(x, res=r).cpu()
