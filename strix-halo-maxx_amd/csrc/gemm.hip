@@ -146,6 +146,18 @@ __device__ __forceinline__ void with_act(int act, F&& f) {
   }
 }
 
+// Scheduling groups for one substep of the software pipeline: R LDS reads (of the next substep's fragments), each
+// followed by its share of the F MFMAs (of this substep), so the reads are spread under the matrix work.
+template <int R, int F, int r = 0>
+__device__ __forceinline__ void interleave_reads_mfma() {
+  if constexpr (r < R) {
+    constexpr int n = F * (r + 1) / R - F * r / R;
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+    if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x008, n, 0);  // then n MFMAs
+    interleave_reads_mfma<R, F, r + 1>();
+  }
+}
+
 template <int BM, int BN, int WGM, int WGN, int S>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
@@ -166,7 +178,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
   constexpr int SP = BN + 8;  // row pitch of the epilogue's staging tile (reuses the ring)
   constexpr int SPF = BN + 4;  // row pitch of the fp32 staging tile of the partial-sum mode (4-wave tiles)
   constexpr int SMEM0 = S * STAGE > BM * SP ? S * STAGE : BM * SP;
-  constexpr int SMEM = NW == 4 && BM * SPF * 2 > SMEM0 ? BM * SPF * 2 : SMEM0;
+  // partial-sum mode and in-kernel split-K: 4-wave tiles whose fp32 staging tile fits the LDS
+  constexpr bool PSUM = NW == 4 && BM * BN <= 128 * 256;
+  constexpr int SMEM = PSUM && BM * SPF * 2 > SMEM0 ? BM * SPF * 2 : SMEM0;
   __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
   __shared__ int s_last;
 
@@ -216,41 +230,71 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
+  // Software pipeline. Operand fragments are double-buffered in registers: while the MFMAs of 16-wide substep s
+  // run, the LDS reads of substep s + 1 are in flight (one read between every few MFMAs). The ring slot of k-step it
+  // is refilled (stage it + S) right after the barrier that ends its last reads, and that barrier, the refill and the
+  // first reads of k-step it + 1 all sit under the MFMAs of k-step it's last substep. So the prologue fills all S
+  // slots and S - 1 stages stay in flight behind the one being consumed.
+  bf16x8 af[2][FM], wf[2][FN];
+  auto read_frags = [&](int buf, const uint16_t* As, int s) {
+    const uint16_t* Ws = As + BM * BK;
+    const int c = 2 * s + hk;
 #pragma unroll
-  for (int s = 0; s < S - 1; s++)
+    for (int i = 0; i < FM; i++) {
+      const int r = wm * WTM + i * 32 + lr;
+      af[buf][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
+    }
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+      const int r = wn * WTN + i * 32 + lr;
+      wf[buf][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
+    }
+  };
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++) acc[i][j] = mfma32(wf[buf][i], af[buf][j], acc[i][j]);
+  };
+  // interleave the FM + FN reads of the next substep with the FM * FN MFMAs of this one
+  auto interleave = [&]() {
+#ifndef GEMM_NO_INTERLEAVE
+    interleave_reads_mfma<FM + FN, FM * FN>();
+#endif
+  };
+
+#pragma unroll
+  for (int s = 0; s < S; s++)
     if (s < nkl) issue(kt0 + s, s);
+  wait_stages<LPS, S - 1>(nkl - 1);  // stage 0 has landed
+  __syncthreads();
+  read_frags(0, smem, 0);
 
   for (int it = 0; it < nkl; it++) {
-    // stage `it` has landed once at most (stages issued after it) x LPS loads are still in flight
-    wait_stages<LPS, S - 2>(nkl - 1 - it);
-    __syncthreads();
-    if (it + S - 1 < nkl) issue(kt0 + it + S - 1, (it + S - 1) % S);
     const uint16_t* As = smem + (it % S) * STAGE;
-    const uint16_t* Ws = As + BM * BK;
 #pragma unroll
-    for (int s = 0; s < BK / 16; s++) {
-      const int c = 2 * s + hk;
-      bf16x8 af[FM], wf[FN];
-#pragma unroll
-      for (int i = 0; i < FM; i++) {
-        const int r = wm * WTM + i * 32 + lr;
-        af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
-      }
-#pragma unroll
-      for (int i = 0; i < FN; i++) {
-        const int r = wn * WTN + i * 32 + lr;
-        wf[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
-      }
-#pragma unroll
-      for (int i = 0; i < FN; i++)
-#pragma unroll
-        for (int j = 0; j < FM; j++) acc[i][j] = mfma32(wf[i], af[j], acc[i][j]);
+    for (int s = 0; s < BK / 16 - 1; s++) {
+      read_frags((s + 1) & 1, As, s + 1);
+      mfmas(s & 1);
+      interleave();
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // stage it + 1 has landed once at most (stages issued after it) x LPS loads are still in flight; the barrier
+    // also ends every wave's reads of slot it % S, which is refilled with stage it + S. On the last k-step nothing is
+    // in flight and the reads below fetch a stale slot that is never used: one copy of the MFMAs, no branch around
+    // them (two copies would make the register allocator keep two accumulator sets).
+    wait_stages<LPS, S - 2>(nkl - 2 - it);
+    __syncthreads();
+    if (it + S < nkl) issue(kt0 + it + S, it % S);
+    read_frags(0, smem + ((it + 1) % S) * STAGE, 0);
+    mfmas(1);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // ---- partial-sum mode (mx_gemm_bf16_partial): this split's raw fp32 sums to its slab of P, staged like the bf16
   // results; no bias, activation or residual
-  if constexpr (NW == 4) {
+  if constexpr (PSUM) {
     if (P) {
       float* stf = reinterpret_cast<float*>(smem);
       __syncthreads();
@@ -270,7 +314,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
 
   // ---- split-K: partial tile to the workspace; the last split to arrive reduces in split order (4-wave tiles only:
   // the 8-wave tiles serve grids large enough without it)
-  if (NW == 4 && splits > 1) {
+  if (PSUM && splits > 1) {
     constexpr int TE = BM * BN;
     float* mine = ws + (long)(tile * splits + split) * TE;
 #pragma unroll
@@ -526,7 +570,9 @@ constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0, 4}, {64, 128, 4, 1, 0, 4}, {128, 64
                          {64, 64, 4, 2, 1, 4},   {64, 128, 4, 1, 1, 4},  {128, 64, 4, 1, 1, 4}, {64, 64, 3, 3, 1, 4},
                          {64, 96, 2, 3, 1, 4},   {64, 64, 6, 1, 1, 4},   {96, 64, 2, 3, 1, 4},
                          // 8-wave tiles for large grids: 2 waves per SIMD hide each other's LDS reads and barriers
-                         {256, 256, 2, 1, 0, 8}, {256, 128, 3, 1, 0, 8}, {128, 256, 3, 1, 0, 8}};
+                         {256, 256, 2, 1, 0, 8}, {256, 128, 3, 1, 0, 8}, {128, 256, 3, 1, 0, 8},
+                         // 4 waves of 128 x 128: 8 LDS reads per 16 MFMAs (LDS traffic at 3/4 of the MFMA time)
+                         {256, 256, 2, 1, 0, 4}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -552,6 +598,13 @@ hipError_t launch_ks(hipStream_t st, const uint16_t* A, long lda, const uint16_t
   hipLaunchKernelGGL((gemm_ks_kernel<BM, BN, S, OCC>), dim3(tm * tn * splits), dim3(256), 0, st, A, lda, W, ldw, bias, R, ldr,
                      r_rows, C, ldc, M, N, K, Kw, act, act_ncols, tm, tn, splits, kps, P, ldp, p_split);
   return hipGetLastError();
+}
+
+// configs with a partial-sum mode (mx_gemm_bf16_partial) and in-kernel split-K: every wave-split config, and the
+// 4-wave kind-0 tiles whose fp32 staging tile fits the LDS (the kernel's PSUM)
+bool psum_ok(int cfg) {
+  const Cfg& c = kCfgs[cfg];
+  return c.kind == 1 || (c.waves == 4 && c.bm * c.bn <= 128 * 256);
 }
 
 long tiles_of(int cfg, int M, int N) {
@@ -588,13 +641,13 @@ extern "C" long mx_gemm_ws_counters(int cfg, int splits, int M, int N) {
 // 256 CUs x per-tile time, with per-tile time ~ BM*BN*(k-steps)/efficiency. Returns cfg * 16 + splits.
 extern "C" int mx_gemm_pick(int M, int N, int Kw) {
   static const float eff[kNCfg] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f,
-                                   1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f};
+                                   1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f, 1.4f};
   const int nk = Kw / BK;
   int best = 0, bsplit = 1;
   float bt = 1e30f;
   for (int c = 0; c < kNCfg; c++) {
     for (int sp = 1; sp <= 8; sp *= 2) {
-      if (sp > 1 && (kCfgs[c].kind || kCfgs[c].waves != 4 || nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk))
+      if (sp > 1 && (kCfgs[c].kind || !psum_ok(c) || nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk))
         break;
       const long tiles = tiles_of(c, M, N) * sp;
       const long slots = 256L * kCfgs[c].per_cu;
@@ -624,7 +677,7 @@ extern "C" int mx_gemm_check(int cfg, int splits, const void* A, long lda, const
   if (bias && ((uintptr_t)bias & 15)) return MX_ELAYOUT;
   if (R && (((uintptr_t)R & 7) || ldr % 4 || ldr < N)) return MX_ELAYOUT;
   if (cfg >= 0 && splits > 1) {
-    if (kCfgs[cfg].kind || kCfgs[cfg].waves != 4) return MX_ESPLIT;  // 4-wave kind-0 tiles only
+    if (kCfgs[cfg].kind || !psum_ok(cfg)) return MX_ESPLIT;  // 4-wave kind-0 tiles up to 128 x 256 only
     const int nk = Kw / BK, kps = (nk + splits - 1) / splits;
     if (splits > nk || (splits - 1) * kps >= nk) return MX_ESPLIT;  // every split must own >= 1 k-step
     if (!ws || !cnt) return MX_ENULL;
@@ -669,6 +722,7 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
     case 15: e = launch<256, 256, 2, 4, 2>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 16: e = launch<256, 128, 4, 2, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 17: e = launch<128, 256, 2, 4, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
+    case 18: e = L_(256, 256, 2); break;
 #define W_(BM, BN, S, OCC) launch_ks<BM, BN, S, OCC>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
     case 8: e = W_(64, 64, 4, 2); break;
     case 9: e = W_(64, 128, 4, 1); break;
@@ -690,7 +744,7 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
 extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda,
                                     const uint16_t* W, long ldw, float* P, long ldp, long p_split, int M, int N, int K,
                                     int Kw) {
-  if (cfg < 0 || cfg >= kNCfg || kCfgs[cfg].waves != 4) return MX_EBADCFG;
+  if (cfg < 0 || cfg >= kNCfg || !psum_ok(cfg)) return MX_EBADCFG;
   if (!P) return MX_ENULL;
   int rc = mx_gemm_check(cfg, 1, A, lda, W, ldw, nullptr, nullptr, 0, P, ldp, M, N, K, Kw, 0, nullptr, 0, nullptr, 0);
   if (rc) return rc;

@@ -49,7 +49,7 @@ def test_gemm_bias_vs_fp32(dev, M, K, N):
     assert (y.float().cpu() - ref).abs().max().item() < 0.02 * ref.abs().max().item() + 1e-2
 
 
-NCFG = 18  # tile configs the library exports
+NCFG = 19  # tile configs the library exports
 
 
 @pytest.mark.parametrize("cfg", range(NCFG))
