@@ -182,7 +182,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
   constexpr bool PSUM = NW == 4 && BM * BN <= 128 * 256;
   constexpr int SMEM = PSUM && BM * SPF * 2 > SMEM0 ? BM * SPF * 2 : SMEM0;
   __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
-  __shared__ int s_last;
 
   int tile_m, tile_n, split;
   tile_of(blockIdx.x, tiles_m, tiles_n, splits, tile_m, tile_n, split);
@@ -325,9 +324,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
         for (int e = 0; e < 16; e++) mine[(((wave * FN + i) * FM + j) * 16 + e) * 64 + lane] = acc[i][j][e];
     __threadfence();
     __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&cnt[tile], 1) == splits - 1);
+    // the arrival flag lives in the ring's last 4 bytes: every wave is past its last LDS read here
+    int* s_last = reinterpret_cast<int*>(smem + SMEM - 2);
+    if (tid == 0) *s_last = (atomicAdd(&cnt[tile], 1) == splits - 1);
     __syncthreads();
-    if (!s_last) return;
+    if (!*s_last) return;
     __threadfence();
 #pragma unroll
     for (int i = 0; i < FN; i++)
@@ -450,32 +451,58 @@ __global__ __launch_bounds__(256, OCC) void gemm_ks_kernel(
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-#pragma unroll
-  for (int s = 0; s < S - 1; s++)
-    if (s < nk) issue(kt0 + s, s);
-
+  // Software pipeline, as in gemm_bf16_kernel: this wave's fragments of k-step it + 1 are read (into the other
+  // register buffer) while the MFMAs of k-step it run, so the LDS latency, the barrier and the slot refill sit under
+  // the matrix work. The prologue fills all S slots; the reads after the last k-step fetch a stale slot that is never
+  // used. The loop runs k-steps in pairs so both register buffers have compile-time indices; when nk is odd the
+  // second step of the last pair multiplies zeroed fragments (adds exact zeros) instead of branching around the
+  // MFMAs (one copy of the MFMAs keeps one set of accumulator registers).
   const int c = 2 * wave + hk;  // this lane's 16-byte chunk of each 128-byte LDS row
-  for (int it = 0; it < nk; it++) {
-    wait_stages<LPS, S - 2>(nk - 1 - it);
-    __syncthreads();
-    if (it + S - 1 < nk) issue(kt0 + it + S - 1, (it + S - 1) % S);
-    const uint16_t* As = smem + (it % S) * STAGE;
+  bf16x8 af[2][FM], wf[2][FN];
+  auto read_frags = [&](int buf, const uint16_t* As) {
     const uint16_t* Ws = As + BM * BK;
-    bf16x8 af[FM], wf[FN];
 #pragma unroll
     for (int j = 0; j < FM; j++) {
       const int r = j * 32 + lr;
-      af[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
+      af[buf][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
     }
 #pragma unroll
     for (int i = 0; i < FN; i++) {
       const int r = i * 32 + lr;
-      wf[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
+      wf[buf][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
     }
+  };
+  auto step = [&](auto cur_c, int it) {
+    constexpr int CUR = decltype(cur_c)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    // stage it + 1 has landed once at most (stages issued after it) x LPS loads are still in flight; the barrier ends
+    // every wave's reads of slot it % S, which is refilled with stage it + S
+    wait_stages<LPS, S - 2>(nk - 2 - it);
+    __syncthreads();
+    if (it + S < nk) issue(kt0 + it + S, it % S);
+    if (it >= nk) {  // the padding step of an odd nk: zero operands
+#pragma unroll
+      for (int j = 0; j < FM; j++) af[CUR][j] = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+      for (int i = 0; i < FN; i++) wf[CUR][i] = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+    }
+    read_frags(CUR ^ 1, smem + ((it + 1) % S) * STAGE);
 #pragma unroll
     for (int i = 0; i < FN; i++)
 #pragma unroll
-      for (int j = 0; j < FM; j++) acc[i][j] = mfma32(wf[i], af[j], acc[i][j]);
+      for (int j = 0; j < FM; j++) acc[i][j] = mfma32(wf[CUR][i], af[CUR][j], acc[i][j]);
+    interleave_reads_mfma<FM + FN, FM * FN>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int s = 0; s < S; s++)
+    if (s < nk) issue(kt0 + s, s);
+  wait_stages<LPS, S - 1>(nk - 1);  // stage 0 has landed
+  __syncthreads();
+  read_frags(0, smem);
+  for (int it = 0; it < nk; it += 2) {
+    step(IntC<0>{}, it);
+    step(IntC<1>{}, it + 1);
   }
 
   // ---- cross-wave sum in a fixed order, ((w0 + w2) + (w1 + w3)): waves 2-3 hand their tiles to waves 0-1 through
