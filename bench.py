@@ -48,7 +48,8 @@ def gemm_symbol(cfg):
 
 def op_classes(vt, img):
     """The tower's batch-1 op classes (its split-K form: partial GEMMs for the two residual Linears, each reduced by
-    the fused residual-LayerNorm kernel) as {label: (kernel symbol, flops per launch, fn(i, block))}; one eager pass
+    the fused residual-LayerNorm kernel) as {label: (kernel symbol, flops per launch, algorithmic HBM bytes per launch,
+    fn(i, block))}; one eager pass
     keeps every block's real operands, and fn(i, block) relaunches op `label` of block i on them."""
     import torch
     import strix_halo_maxx_amd.ops as ops
@@ -85,15 +86,22 @@ def op_classes(vt, img):
         cfg, sp = ops._TUNED_P[(M, l.N, l.Kw)]
         return f"{gemm_symbol(cfg)} x{sp} splits"
     attn_sym = "attn_fwd_kernel<{}, {}>".format(hd, "4, 1, 64, 3" if ((T + 127) // 128) * H * B >= 512 else "1, 4, 128, 2")
+    F, Kw2 = blocks[0]["fc1"].N, blocks[0]["fc2"].Kw
+    sp_proj, sp_fc2 = saved[0][4].shape[0], saved[0][8].shape[0]
+    # algorithmic HBM bytes per launch: every operand once (bf16 activations / weights, fp32 split-K partials)
     classes = {
-        "qkv": (sym(blocks[0]["qkv"]), 2 * M * D * 3 * D, lambda i, b: b["qkv"](saved[i][1], out=outs["qkv"])),
-        "attn": (attn_sym, 4 * B * H * T * T * hd, lambda i, b: ops.sdpa(*saved[i][2], out=a_out)),
-        "proj": (psym(blocks[0]["proj"]), 2 * M * D * D, lambda i, b: b["proj"].partial(saved[i][3], out=pp_out)),
-        "res_ln2": ("residual_layernorm_kernel<3>", 0, lambda i, b: ops.residual_layernorm(
+        "qkv": (sym(blocks[0]["qkv"]), 2 * M * D * 3 * D, 2 * (M * D + 3 * D * D + M * 3 * D),
+                lambda i, b: b["qkv"](saved[i][1], out=outs["qkv"])),
+        "attn": (attn_sym, 4 * B * H * T * T * hd, 8 * M * D, lambda i, b: ops.sdpa(*saved[i][2], out=a_out)),
+        "proj": (psym(blocks[0]["proj"]), 2 * M * D * D, 2 * (M * D + D * D) + 4 * sp_proj * M * D,
+                 lambda i, b: b["proj"].partial(saved[i][3], out=pp_out)),
+        "res_ln2": ("residual_layernorm_kernel<3>", 0, (4 * sp_proj + 6) * M * D, lambda i, b: ops.residual_layernorm(
             saved[i][4], b["proj"].b, saved[i][0], b["ln2"], eps=vt.eps, x_out=outs["x"], y_out=outs["h"])),
-        "fc1": (sym(blocks[0]["fc1"]), 2 * M * D * blocks[0]["fc1"].N, lambda i, b: b["fc1"](saved[i][6], gelu=True, out=outs["f"])),
-        "fc2": (psym(blocks[0]["fc2"]), 2 * M * blocks[0]["fc2"].K * D, lambda i, b: b["fc2"].partial(saved[i][7], out=pf_out)),
-        "res_ln1": ("residual_layernorm_kernel<3>", 0, lambda i, b: ops.residual_layernorm(
+        "fc1": (sym(blocks[0]["fc1"]), 2 * M * D * F, 2 * (M * D + F * D + M * F),
+                lambda i, b: b["fc1"](saved[i][6], gelu=True, out=outs["f"])),
+        "fc2": (psym(blocks[0]["fc2"]), 2 * M * blocks[0]["fc2"].K * D, 2 * (M * F + D * Kw2) + 4 * sp_fc2 * M * D,
+                lambda i, b: b["fc2"].partial(saved[i][7], out=pf_out)),
+        "res_ln1": ("residual_layernorm_kernel<3>", 0, (4 * sp_fc2 + 6) * M * D, lambda i, b: ops.residual_layernorm(
             saved[i][8], b["fc2"].b, saved[i][5], saved[i][9], eps=vt.eps, x_out=outs["x"], y_out=outs["h"])),
     }
     return classes
@@ -107,7 +115,7 @@ def op_timing(vt, img, reps=5):
     classes = op_classes(vt, img)
     blocks = vt.blocks
     res = {}
-    for name, (ksym, fl, fn) in classes.items():
+    for name, (ksym, fl, _, fn) in classes.items():
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for i, b in enumerate(blocks):
@@ -139,7 +147,7 @@ def traffic_probe(vt, img, reps=3):
     classes = op_classes(vt, img)
     torch.cuda.synchronize()
     torch.full((12345,), 1.0, device=img.device)
-    for name, (ksym, fl, fn) in classes.items():
+    for name, (ksym, fl, _, fn) in classes.items():
         for _ in range(reps):
             for i, b in enumerate(vt.blocks):
                 fn(i, b)
@@ -151,6 +159,91 @@ def traffic_probe(vt, img, reps=3):
         dst.copy_(src)
     torch.cuda.synchronize()
     print("[bench] traffic probe done: " + ", ".join(f"{k}={v[0]}" for k, v in classes.items()), flush=True)
+
+
+def _pmc_sequence(path, counter):
+    """[(kernel name, counter value)] per dispatch, in dispatch order, from a rocprofv3 counter_collection CSV."""
+    import csv
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            d = int(r["Dispatch_Id"])
+            k, v = per.get(d, (r["Kernel_Name"], 0.0))
+            per[d] = (k, v + float(r["Counter_Value"]))
+    return [per[d] for d in sorted(per)]
+
+
+def summarize_traffic(fetch_csv, write_csv, reps=3):
+    """Markdown summary (with the JSON block measured_traffic reads) of the two rocprofv3 --pmc passes (FETCH_SIZE,
+    WRITE_SIZE) over `bench.py --traffic-probe`: the op-class dispatches sit between the run's last two marker fills,
+    the calibration copies follow the second."""
+    import torch
+    import strix_halo_maxx_amd.md2 as md2
+    import strix_halo_maxx_amd.synth as S
+    vt = md2.VisionTower(S.vision_weights(0), device=torch.device("cuda:0"))
+    img = S.images_u8(1, 1).to("cuda:0")
+    with torch.inference_mode():
+        vt(img)
+        classes = op_classes(vt, img)
+    nblk = len(vt.blocks)
+    per = reps * nblk
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        seq = _pmc_sequence(path, counter)
+        fills = [i for i, (k, _) in enumerate(seq) if "FillFunctor" in k]
+        m0, m1 = fills[-2], fills[-1]
+        probe, calib = seq[m0 + 1:m1], seq[m1 + 1:]
+        if len(probe) != per * len(classes) or len(calib) < reps:
+            raise RuntimeError(f"{counter}: {len(probe)} probe dispatches, {len(calib)} calibration dispatches")
+        out[counter] = (probe, [v for _, v in calib[-reps:]])
+    fcal, wcal = (sum(out[c][1]) / reps for c in ("FETCH_SIZE", "WRITE_SIZE"))
+    copy_b = 256 << 20
+    ff, wf = copy_b / (fcal * 1024), copy_b / (wcal * 1024)
+    blob = {"calibration": {"copy_bytes_each_way": copy_b, "fetch_kib": round(fcal, 1), "write_kib": round(wcal, 1),
+                            "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)}, "ops": {}}
+    rows = []
+    for j, (label, (ksym, fl, algo, _)) in enumerate(classes.items()):
+        fk = [v for _, v in out["FETCH_SIZE"][0][j * per:(j + 1) * per]]
+        wk = [v for _, v in out["WRITE_SIZE"][0][j * per:(j + 1) * per]]
+        names = {k for k, _ in out["FETCH_SIZE"][0][j * per:(j + 1) * per]}
+        symbol = ksym.split(" x")[0]
+        base = symbol.split("<")[0]
+        if len(names) != 1 or base not in next(iter(names)):
+            raise RuntimeError(f"{label}: dispatches {names} do not match {symbol}")
+        fkib, wkib = sum(fk) / per, sum(wk) / per
+        tb = int(fkib * 1024 * ff + wkib * 1024 * wf)
+        blob["ops"][label] = {"kernel": ksym, "symbol": symbol, "fetch_kib": round(fkib, 1),
+                              "write_kib": round(wkib, 1), "bytes_per_launch": tb, "algorithmic_bytes": algo}
+        rows.append(f"| {label} | `{ksym}` | {fkib:,.1f} | {wkib:,.1f} | {fkib * 1024 * ff / 1e6:.2f} | "
+                    f"{wkib * 1024 * wf / 1e6:.2f} | {tb / 1e6:.2f} | {algo / 1e6:.2f} | {tb / algo:.2f} |")
+    head = ["| op | kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | read MB | written MB | traffic MB | algorithmic MB | ratio |",
+            "|---|---|---|---|---|---|---|---|---|"]
+    return (f"Calibration (plain copy of 256 MiB = {copy_b:,} B read + the same written): FETCH_SIZE reads "
+            f"{fcal:,.1f} KiB per copy, WRITE_SIZE {wcal:,.1f} KiB. Bytes = FETCH_SIZE x 1024 x {ff:.4f} + "
+            f"WRITE_SIZE x 1024 x {wf:.4f}.\n\n" + "\n".join(head + rows) +
+            "\n\nbench.py reads the JSON block below (`traffic` of the roofline line, when its dominant op ran the same "
+            "kernel):\n\n```json\n" + json.dumps(blob, indent=1) + "\n```\n")
+
+
+def summarize_trace(trace_csv, top=30):
+    """Kernel-trace rows grouped by (kernel, workgroups x threads): calls, mean / median / total duration."""
+    import csv
+    groups = {}
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            k = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "")
+            k = k[:k.index("(")] if "(" in k and "<" not in k[:k.index("(")] else k[:k.rfind(">") + 1] if ">" in k else k
+            wg = int(r["Workgroup_Size_X"])
+            key = (k[:58], int(r["Grid_Size_X"]) // wg, wg)
+            groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = [f"{'kernel':58s} {'workgroups':>12s} {'calls':>6s} {'mean_us':>9s} {'median_us':>9s} {'total_ms':>9s}"]
+    for (k, g, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        d.sort()
+        lines.append(f"{k:58s} {f'{g}x{wg}':>12s} {len(d):6d} {sum(d) / len(d):9.2f} {d[len(d) // 2]:9.2f} "
+                     f"{sum(d) / 1e3:9.2f}")
+    return "\n".join(lines)
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "vision_tower_b1_hbm_traffic.md")
@@ -312,7 +405,16 @@ def main():
     ap.add_argument("--extra", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the eager launches that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count (see traffic_probe)")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the traffic summary of two --pmc passes over --traffic-probe (see summarize_traffic)")
+    ap.add_argument("--summarize-trace", metavar="TRACE_CSV", help="print a rocprofv3 kernel trace grouped by kernel")
     a = ap.parse_args()
+    if a.summarize_trace:
+        print(summarize_trace(a.summarize_trace))
+        return
+    if a.summarize_traffic:
+        print(summarize_traffic(*a.summarize_traffic))
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (every workload here fits one GPU's "
               "288 GB; the sharding plan is design-only). Run with --gpus 1.", file=sys.stderr)
