@@ -289,16 +289,17 @@ def cpu_baseline(budget_s=20.0):
                       f"median of {n} frames after 1 warm-up, torch.set_num_threads({threads})"}
 
 
-def decode_bench(steps_tokens=128):
+def decode_bench(steps_tokens=128, w8a8=False):
     """Config 2: prefill (1 + 729 image tokens mask-free, then 64 prompt ids) + greedy decode on one HIP graph per
     step. Returns prefill ms, decode tok/s and the decode step's HBM roofline (algorithmic bytes = every weight once
-    + the KV cache read per token)."""
+    + the KV cache read per token). w8a8: the reference's default W8A8 text linears (int8 weights and activations;
+    the LM head stays bf16), reported beside the bf16 figures, never as them."""
     import torch
     import strix_halo_maxx_amd.md2text as mt
     import strix_halo_maxx_amd.synth as S
     dev = torch.device("cuda:0")
     w = S.text_weights(0)
-    dec = mt.TextDecoder(w, device=dev, ctx=1024)
+    dec = mt.TextDecoder(w, device=dev, ctx=1024, w8a8=w8a8)
     del w
     img = S.activations(3, (729, 2048), "img").to(dev)
     prompt = S.prompt_ids(4, 64)
@@ -318,7 +319,8 @@ def decode_bench(steps_tokens=128):
     t_dec = (time.perf_counter() - t0) / (steps_tokens - 1)
     c = S.TXT
     D, F, L, V = c["dim"], c["ff"], c["layers"], c["vocab"]
-    wbytes = 2 * (L * (3 * D * D + D * D + 2 * D * F) + V * D)
+    lin = L * (3 * D * D + D * D + 2 * D * F)  # text Linear weights: bf16, or int8 + fp32 per-row scales (W8A8)
+    wbytes = (lin + 4 * L * (3 * D + D + F + D) if w8a8 else 2 * lin) + 2 * V * D
     ctx_mid = dec.pos_base + steps_tokens // 2
     kvbytes = 2 * 2 * L * ctx_mid * D
     bpt = wbytes + kvbytes
@@ -328,7 +330,8 @@ def decode_bench(steps_tokens=128):
                                 "unit": "GB/s", "frac": round(bpt / t_dec / PEAK_HBM, 4),
                                 "bytes_per_token": bpt},
             "workload": "moondream2 text decoder, 24 layers, prefill 730 + 64 tokens, greedy "
-                        f"{steps_tokens} tokens, batch 1, one HIP graph per decode step"}
+                        f"{steps_tokens} tokens, batch 1, one HIP graph per decode step"
+                        + (", W8A8 text Linears (int8 weights / activations, bf16 LM head)" if w8a8 else "")}
 
 
 def trecvit_bench(frames=64, clip=16):
@@ -471,6 +474,10 @@ def main():
     print("[bench] decoder", file=sys.stderr, flush=True)
     with torch.inference_mode():
         out.setdefault("extra", {})["decoder"] = decode_bench()
+    torch.cuda.empty_cache()
+    print("[bench] decoder w8a8", file=sys.stderr, flush=True)
+    with torch.inference_mode():
+        out["extra"]["decoder_w8a8"] = decode_bench(w8a8=True)
     torch.cuda.empty_cache()
     print("[bench] trecvit", file=sys.stderr, flush=True)
     with torch.inference_mode():

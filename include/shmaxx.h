@@ -52,6 +52,27 @@ int mx_gemm_cfg_kind(int cfg);
  * residual Linears x + proj(a) and x + fc2(f) (moondream/gpu/md2fast.py:152-157). */
 int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
                          float* P, long ldp, long p_split, int M, int N, int K, int Kw);
+
+/* ============================================================================================ W8A8 (int8 MFMA)
+ * Per-token int8 quantisation of bf16 activations: s[m] = max(max_k |x[m,k]|, 1e-5) / 127 and
+ * q[m,k] = trunc(x / s + 0.5 sign) (round half away from zero), fp32 math with IEEE division. K % 8 == 0; strides in
+ * elements (ldx bf16, ldq int8 bytes; multiples of 8). Replaces the reference's _quant_rows / quant_rows
+ * (moondream/gpu/tgemm.py:81-91, hgemm.py:10-16). */
+int mx_quant_rows_i8(hipStream_t st, const uint16_t* x, long ldx, int8_t* q, long ldq, float* s, int M, int K);
+/* Per-output-channel int8 quantisation of a bf16 weight: s[n] = max(max_k |w[n,k]|, 1e-8) / 127 and
+ * q[n,k] = clamp(round-half-even(w / s), -127, 127), fp32 with IEEE division (columns past K of q untouched).
+ * Replaces the weight quantisation of HI8Lin.__init__ (moondream/gpu/hgemm.py:101-106). */
+int mx_quant_weight_i8(hipStream_t st, const uint16_t* w, long ldw, int8_t* q, long ldq, float* s, int N, int K);
+/* W8A8 GEMM: C = bf16(act(((float)(A W^T) * sa[m]) * sw[n] + bias[n])) [then + R, rounded again]: A (M, K) and
+ * W (N, Kw) int8, row strides lda / ldw in BYTES (multiples of 16), K % 16 == 0, Kw % 128 == 0, W zero in columns
+ * [K, Kw); sa / sw fp32 per-row / per-column scales; act 0 none, 1 GELU-tanh, 2 GELU-erf, applied to the fp32 value
+ * before the one bf16 rounding. With P (int32, row stride ldp elements) the raw accumulators are written instead and
+ * sa / sw / bias / R / C are ignored (cfg must then have a partial-sum mode). cfg: a kind-0 tile config
+ * (mx_gemm_cfg_kind == 0). Replaces i8gemm_launch (moondream/gpu/hip/i8gemm.hip:480) with its epilogue
+ * (i8gemm.hip:181-197); the fused residual stands for the reference's separate bf16 add (md2fast.py:55-67). */
+int mx_gemm_i8(hipStream_t st, int cfg, const int8_t* A, long lda, const int8_t* W, long ldw, const float* sa,
+               const float* sw, const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M,
+               int N, int K, int Kw, int act, int32_t* P, long ldp);
 /* Split-K workspace a (cfg, splits) call needs: fp32 elements / tile counters. Replaces the fixed-size
  * workspace() of moondream/gpu/hgemm.py:78-83. */
 long mx_gemm_ws_elems(int cfg, int splits, int M, int N);
@@ -107,6 +128,18 @@ int mx_ln_gemv2(hipStream_t st, const uint16_t* x, const uint16_t* gamma, const 
  * (mlp(..., res=lin_res(proj, a, x))) for one token, both GEMVs in one pass. */
 int mx_gemv_dual_res(hipStream_t st, const uint16_t* g, const uint16_t* W2, const float* b2, int K2, const uint16_t* a,
                      const uint16_t* Wp, const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N);
+/* W8A8 forms of the two decode GEMVs (the reference's HI8Lin text linears at batch 1, moondream/gpu/hgemm.py:95-137):
+ * every wave quantises the whole activation row per token (tgemm.py:81-91), int8 dot products sum exactly in int32,
+ * then the fp32 dequant ((acc * s) * sw[n]) + bias[n] and any GELU before one bf16 rounding (i8gemm.hip:181-197).
+ * mx_ln_gemv2_i8: LN fused in front (gamma = beta = null: none); Wq int8 (N, ldw bytes, ldw % 16 == 0); K 2048 / 1024.
+ * mx_gemv_dual_res_i8: out = bf16(bf16(fc2(g)) + bf16(bf16(proj(a)) + xres)), W2 (N, K2) and Wp (N, Kp) int8
+ * contiguous, (K2, Kp) = (8192, 2048) or (4096, 1024). */
+int mx_ln_gemv2_i8(hipStream_t st, const uint16_t* x, const uint16_t* gamma, const uint16_t* beta, float eps,
+                   const int8_t* Wq, long ldw, const float* sw, const float* bias, int N, int K, int n1, uint16_t* out1,
+                   uint16_t* out2, int act2);
+int mx_gemv_dual_res_i8(hipStream_t st, const uint16_t* g, const int8_t* W2, const float* sw2, const float* b2, int K2,
+                        const uint16_t* a, const int8_t* Wp, const float* swp, const float* bp, int Kp,
+                        const uint16_t* xres, uint16_t* out, int N);
 /* LM head: logits = LN(x) W^T + b (bf16; written when logits != null) and one argmax key per workgroup in part
  * (first index wins ties). Replaces the lm_head / lm_small call and the argmax of md2fast.py:212, :281. */
 int mx_ln_gemv_argmax(hipStream_t st, const uint16_t* x, const uint16_t* gamma, const uint16_t* beta, float eps,

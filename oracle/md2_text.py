@@ -13,6 +13,18 @@ Restates moondream/gpu/md2fast.py:
 Greedy decode (ours; not in the reference snapshot): each step feeds argmax(logits) (torch.argmax: first index among
 equal maxima) at the next position, attending to every cached key (no mask needed: a single query at the end).
 freqs_cis uses theta = 10000 (moondream's value; not present in the snapshot: parity unpinned for theta itself).
+
+W8A8 text linears (Text(..., w8a8=True)), the reference's default text path (bench.py:20 --tlin HI8Lin):
+  * quant_weight: per-output-channel scale amax / 127 (amax clamped >= 1e-8), round half to even, clamp +-127
+                                                                    hgemm.py:101-106 (HI8Lin.__init__)
+  * quant_rows: per-token scale max(amax, 1e-5) / 127, v = x / s, q = trunc(v + 0.5 sign(v)) (half away from zero)
+                                                                    tgemm.py:81-91 (_quant_rows), hgemm.py:10-16
+  * i8_linear: int32 sum of q . wq, then fp32 ((acc * s_x) * s_w) + bias (bias fp32, hgemm.py:116), GELU-tanh on that
+    fp32 value when fused (fused_gelu = True), one bf16 rounding   i8gemm.hip:181-197
+  * the layer: LN output quantised once and shared by qkv and fc1 (SHARE_QUANT, md2fast.py:52,174); proj and fc2
+    quantise their own inputs; residuals added in bf16 outside the GEMM (fused_res = False: lin_res / mlp,
+    md2fast.py:55-67)
+The LM head stays a bf16 Linear (md2fast.py:115).
 """
 import torch
 import torch.nn.functional as F
@@ -39,10 +51,40 @@ def rope(x, cos, sin):
     return torch.cat([o.to(x.dtype), xp], dim=-1)
 
 
+def quant_weight(w):
+    """hgemm.py:101-106: (N, K) bf16 weight -> int8 (N, K), fp32 per-row scale."""
+    wf = w.float()
+    s = wf.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+    return (wf / s[:, None]).round().clamp(-127, 127).to(torch.int8), s
+
+
+def quant_rows(x):
+    """tgemm.py:81-91: per-row dynamic int8 quantisation of a bf16 (M, K) activation -> (int8 (M, K), fp32 (M,))."""
+    xf = x.float()
+    s = xf.abs().amax(dim=-1).clamp_min(1e-5) / 127.0
+    v = xf / s[:, None]
+    q = torch.trunc(v + torch.where(v >= 0, 0.5, -0.5)).to(torch.int32)
+    return q.to(torch.int8), s
+
+
+def i8_linear(q, sx, wq, sw, bias, gelu_tanh=False):
+    """i8gemm.hip:181-197: exact int32 accumulation (int64 matmul here), fp32 ((acc * s_x) * s_w) + b, optional GELU
+    on the fp32 value, one bf16 rounding. q (M, K) int8, wq (N, K) int8."""
+    acc = (q.long() @ wq.long().t()).to(torch.int32)
+    v = acc.float() * sx[:, None]
+    v = v * sw[None, :]
+    if bias is not None:
+        v = v + bias.float()[None, :]
+    if gelu_tanh:
+        v = gelu(v)
+    return v.to(BF)
+
+
 class Text:
-    def __init__(self, w, ctx, freqs, bos=50256, H=32):
+    def __init__(self, w, ctx, freqs, bos=50256, H=32, w8a8=False):
         self.w = w
         self.H = H
+        self.w8a8 = w8a8
         self.D = w["wte"].shape[1]
         self.hd = self.D // H
         n = 0
@@ -53,6 +95,20 @@ class Text:
         self.vc = [torch.zeros(1, H, ctx, self.hd, dtype=BF) for _ in range(n)]
         self.cos, self.sin = freqs[..., 0].contiguous(), freqs[..., 1].contiguous()
         self.bos = bos
+        if w8a8:
+            self.q = {f"blocks.{i}.{m}": quant_weight(w[f"blocks.{i}.{m}.weight"])
+                      for i in range(n) for m in ("attn.qkv", "attn.proj", "mlp.fc1", "mlp.fc2")}
+
+    def _lin(self, name, x, pre=None, gelu_tanh=False):
+        """A text Linear: bf16 F.linear (+ separate GELU), or the W8A8 path (pre = the shared quantised input)."""
+        w = self.w
+        if not self.w8a8:
+            y = F.linear(x, w[name + ".weight"], w[name + ".bias"])
+            return gelu(y) if gelu_tanh else y
+        shp = x.shape
+        q, sx = pre if pre is not None else quant_rows(x.reshape(-1, shp[-1]))
+        wq, sw = self.q[name]
+        return i8_linear(q, sx, wq, sw, w[name + ".bias"], gelu_tanh).view(*shp[:-1], wq.shape[0])
 
     def layers(self, x, pos0, mask):
         """md2fast.py:169-199 (fuse=False). x (1, n, D)."""
@@ -62,7 +118,8 @@ class Text:
         for i in range(self.n):
             p = f"blocks.{i}."
             h = ln(x, w[p + "ln.weight"], w[p + "ln.bias"])
-            qkv = F.linear(h, w[p + "attn.qkv.weight"], w[p + "attn.qkv.bias"])
+            pre = quant_rows(h.reshape(n, -1)) if self.w8a8 else None  # shared by qkv and fc1 (md2fast.py:174)
+            qkv = self._lin(p + "attn.qkv", h, pre)
             q, k, v = qkv.split([H * hd] * 3, dim=-1)
             q = rope(q.view(1, n, H, hd).transpose(1, 2), cos, sin)
             k = rope(k.view(1, n, H, hd).transpose(1, 2), cos, sin)
@@ -74,9 +131,8 @@ class Text:
             else:
                 a = F.scaled_dot_product_attention(q, self.kc[i][:, :, :pos0 + n], self.vc[i][:, :, :pos0 + n], attn_mask=mask)
             a = a.transpose(1, 2).reshape(1, n, H * hd)
-            res = F.linear(a, w[p + "attn.proj.weight"], w[p + "attn.proj.bias"]) + x
-            x = F.linear(gelu(F.linear(h, w[p + "mlp.fc1.weight"], w[p + "mlp.fc1.bias"])),
-                         w[p + "mlp.fc2.weight"], w[p + "mlp.fc2.bias"]) + res
+            res = self._lin(p + "attn.proj", a) + x
+            x = self._lin(p + "mlp.fc2", self._lin(p + "mlp.fc1", h, pre, gelu_tanh=True)) + res
         return x
 
     def logits(self, x_last):

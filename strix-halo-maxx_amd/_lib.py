@@ -26,6 +26,9 @@ SIGNATURES = {
     "mx_gemm_cfg_tile": [I, ctypes.POINTER(I), ctypes.POINTER(I)],
     "mx_gemm_cfg_kind": [I],
     "mx_gemm_bf16_partial": [P, I, I, P, L, P, L, P, L, L, I, I, I, I],
+    "mx_gemm_i8": [P, I, P, L, P, L, P, P, P, P, L, I, P, L, I, I, I, I, I, P, L],
+    "mx_quant_rows_i8": [P, P, L, P, L, P, I, I],
+    "mx_quant_weight_i8": [P, P, L, P, L, P, I, I],
     "mx_sdpa": [P, P, L, L, L, P, L, L, L, P, L, L, L, P, L, L, L, I, I, I, I, I, F, I, I],
     "mx_sdpa_check": [P, L, P, L, P, L, P, L, I, I, I, I, I],
     "mx_layernorm": [P, P, L, P, P, P, L, I, I, F],
@@ -35,6 +38,8 @@ SIGNATURES = {
     "mx_rope_kv": [P, P, L, P, P, P, P, I, I, I, I, I, I, I],
     "mx_ln_gemv2": [P, P, P, P, F, P, L, P, I, I, I, P, P, I],
     "mx_gemv_dual_res": [P, P, P, P, I, P, P, P, I, P, P, I],
+    "mx_ln_gemv2_i8": [P, P, P, P, F, P, L, P, P, I, I, I, P, P, I],
+    "mx_gemv_dual_res_i8": [P, P, P, P, P, I, P, P, P, P, I, P, P, I],
     "mx_lm_argmax_nparts": [I],
     "mx_ln_gemv_argmax": [P, P, P, P, F, P, L, P, I, I, P, P, I],
     "mx_embed_step": [P, P, I, P, I, P, I, P, P],

@@ -183,6 +183,220 @@ __global__ __launch_bounds__(256) void gemv_dual_res_kernel(const uint16_t* __re
   }
 }
 
+// ---------------------------------------------------------------------------------------------- W8A8 GEMVs
+// The reference's W8A8 text linears (moondream/gpu/hgemm.py:95-137) at batch 1: int8 weight rows (per-row scale sw),
+// the activation row quantised per token (s = max(amax, 1e-5) / 127, q = trunc(v + 0.5 sign), tgemm.py:81-91) by every
+// wave from the whole row it holds, int8 dot products (v_dot4) summed exactly in int32, then the fp32 dequant
+// ((acc * s) * sw) + b and any GELU on that fp32 value before the one bf16 rounding (i8gemm.hip:181-197).
+// Layout: a row of K int8 is K / 16 chunks of 16 bytes; lane l holds chunks l + 64 j (j < KI), i.e. elements
+// 16 (l + 64 j) .. +15, and loads the activation values at the same positions (two 8-wide bf16 chunks per int8 chunk).
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+// Exact int32 sum over the wave of R per-lane values (the reduce_rows exchange pattern); lane l ends with the total of
+// value l >> (6 - log2 R).
+template <int R>
+__device__ __forceinline__ int reduce_rows_i(int (&v)[R], int lane) {
+  constexpr int L = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : R == 16 ? 4 : R == 32 ? 5 : 6;
+  static_assert((1 << L) == R, "R must be a power of two <= 64");
+#pragma unroll
+  for (int st = 0; st < L; st++) {
+    const int d = 32 >> st, H = R >> (st + 1);
+    const bool up = lane & d;
+#pragma unroll
+    for (int j = 0; j < H; j++) {
+      const int keep = up ? v[j + H] : v[j];
+      const int send = up ? v[j] : v[j + H];
+      v[j] = keep + __shfl_xor(send, d, 64);
+    }
+  }
+  int t = v[0];
+#pragma unroll
+  for (int d = 32 >> L; d >= 1; d >>= 1) t += __shfl_xor(t, d, 64);
+  return t;
+}
+
+// The activation row in int8-chunk order: xc[2 j], xc[2 j + 1] = bf16 elements 16 (lane + 64 j) .. +7, +8 .. +15.
+template <int KI>
+__device__ __forceinline__ void load_vec_i8order(u32x4 (&xc)[2 * KI], const uint16_t* x, int lane) {
+#pragma unroll
+  for (int j = 0; j < KI; j++) {
+    xc[2 * j] = *reinterpret_cast<const u32x4*>(x + (lane + 64 * j) * 16);
+    xc[2 * j + 1] = *reinterpret_cast<const u32x4*>(x + (lane + 64 * j) * 16 + 8);
+  }
+}
+
+// Per-token quantisation of the row held as in load_vec_i8order (every lane ends with the same scale); returns s.
+template <int KI>
+__device__ __forceinline__ float quant_row_i8(const u32x4 (&xc)[2 * KI], i32x4v (&q)[KI]) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 2 * KI; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) amax = fmaxf(amax, fmaxf(fabsf(lo_bf(xc[i][e])), fabsf(hi_bf(xc[i][e]))));
+  amax = wave_max(amax);
+  const float s = fmaxf(amax, 1e-5f) / 127.0f;
+#pragma unroll
+  for (int j = 0; j < KI; j++)
+#pragma unroll
+    for (int w = 0; w < 4; w++) {  // int32 word w of chunk j: elements 4 w .. 4 w + 3
+      uint32_t word = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const int e = 4 * w + b;  // element within the 16-wide chunk
+        const uint32_t u = xc[2 * j + (e >> 3)][(e & 7) >> 1];
+        const float f = (e & 1) ? hi_bf(u) : lo_bf(u);
+        const float t = f / s;
+        const int qi = (int)(t + (t >= 0.f ? 0.5f : -0.5f));
+        word |= ((uint32_t)qi & 0xffu) << (8 * b);
+      }
+      q[j][w] = (int)word;
+    }
+  return s;
+}
+
+__device__ __forceinline__ int dot16_i8(const i32x4v& a, const u32x4& b, int acc) {
+#pragma unroll
+  for (int w = 0; w < 4; w++) acc = __builtin_amdgcn_sdot4(a[w], (int)b[w], acc, false);
+  return acc;
+}
+
+// LN (fp32 statistics, one rounding) of a row held in int8-chunk order, gamma / beta read at the same positions.
+template <int KI>
+__device__ __forceinline__ void ln_i8order(u32x4 (&xc)[2 * KI], const uint16_t* gamma, const uint16_t* beta, float eps,
+                                           int K, int lane) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 2 * KI; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) s += lo_bf(xc[i][e]) + hi_bf(xc[i][e]);
+  const float mean = wave_sum(s) / (float)K;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 2 * KI; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float d0 = lo_bf(xc[i][e]) - mean, d1 = hi_bf(xc[i][e]) - mean;
+      ss += d0 * d0 + d1 * d1;
+    }
+  const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)K + eps);
+#pragma unroll
+  for (int i = 0; i < 2 * KI; i++) {
+    const int off = (lane + 64 * (i >> 1)) * 16 + 8 * (i & 1);
+    const u32x4 g = *reinterpret_cast<const u32x4*>(gamma + off);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(beta + off);
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      xc[i][e] = pack2((lo_bf(xc[i][e]) - mean) * rstd * lo_bf(g[e]) + lo_bf(b[e]),
+                       (hi_bf(xc[i][e]) - mean) * rstd * hi_bf(g[e]) + hi_bf(b[e]));
+  }
+}
+
+// [qkv | fc1] = dequant(quant(LN(x)) . Wq^T); out1 = rows < n1 (bf16), out2 = GELU rows >= n1 (act2 1 tanh, 2 erf)
+template <int KI, int R>
+__global__ __launch_bounds__(256) void ln_gemv2_i8_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ gamma,
+                                                          const uint16_t* __restrict__ beta, float eps,
+                                                          const int8_t* __restrict__ Wq, long ldw,
+                                                          const float* __restrict__ sw, const float* __restrict__ bias,
+                                                          int N, int n1, uint16_t* __restrict__ out1,
+                                                          uint16_t* __restrict__ out2, int act2) {
+  constexpr int SH = 6 - (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  if (row0 >= N) return;
+  const int nme = row0 + (lane >> SH);
+  u32x4 xc[2 * KI];
+  load_vec_i8order<KI>(xc, x, lane);
+  const float bme = (bias && nme < N) ? bias[nme] : 0.f, swme = nme < N ? sw[nme] : 0.f;
+  u32x4 wv[R][KI];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int8_t* wr = Wq + (long)min(row0 + r, N - 1) * ldw;
+#pragma unroll
+    for (int j = 0; j < KI; j++) wv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (lane + 64 * j) * 16));
+  }
+  if (gamma) ln_i8order<KI>(xc, gamma, beta, eps, KI * 1024, lane);
+  i32x4v q[KI];
+  const float sx = quant_row_i8<KI>(xc, q);
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    acc[r] = 0;
+#pragma unroll
+    for (int j = 0; j < KI; j++) acc[r] = dot16_i8(q[j], wv[r][j], acc[r]);
+  }
+  const int tot = reduce_rows_i<R>(acc, lane);
+  if ((lane & ((1 << SH) - 1)) == 0 && nme < N) {
+    const float t = (float)tot * sx;
+    float v = t * swme + bme;
+    if (nme < n1) {
+      out1[nme] = f2bf(v);
+    } else {
+      if (act2 == 1) v = gelu_tanh(v);
+      else if (act2 == 2) v = gelu_erf(v);
+      out2[nme - n1] = f2bf(v);
+    }
+  }
+}
+
+// x' = bf16(bf16(fc2(g)) + bf16(bf16(proj(a)) + x)) with both Linears W8A8 (the parallel residual of
+// md2fast.py:198 through lin_res / mlp with fused_res off)
+template <int KI1, int KI2, int R>
+__global__ __launch_bounds__(256) void gemv_dual_res_i8_kernel(
+    const uint16_t* __restrict__ g, const int8_t* __restrict__ W2, const float* __restrict__ sw2,
+    const float* __restrict__ b2, const uint16_t* __restrict__ a, const int8_t* __restrict__ Wp,
+    const float* __restrict__ swp, const float* __restrict__ bp, const uint16_t* __restrict__ xres,
+    uint16_t* __restrict__ out, int N) {
+  constexpr int SH = 6 - (R == 1 ? 1 : R == 2 ? 2 : R == 4 ? 3 : 4);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  if (row0 >= N) return;
+  const int nme = row0 + ((lane >> SH) & (R - 1));
+  const bool in = nme < N;
+  u32x4 w2[R][KI1], wp[R][KI2];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int n = min(row0 + r, N - 1);
+#pragma unroll
+    for (int j = 0; j < KI1; j++)
+      w2[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W2 + (long)n * KI1 * 1024 + (lane + 64 * j) * 16));
+#pragma unroll
+    for (int j = 0; j < KI2; j++)
+      wp[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Wp + (long)n * KI2 * 1024 + (lane + 64 * j) * 16));
+  }
+  const float b2me = in ? b2[nme] : 0.f, bpme = in ? bp[nme] : 0.f, xme = in ? bf2f(xres[nme]) : 0.f;
+  const float sw2me = in ? sw2[nme] : 0.f, swpme = in ? swp[nme] : 0.f;
+  i32x4v qg[KI1], qa[KI2];
+  float sg, sa;
+  {
+    u32x4 gc[2 * KI1];
+    load_vec_i8order<KI1>(gc, g, lane);
+    sg = quant_row_i8<KI1>(gc, qg);
+  }
+  {
+    u32x4 ac[2 * KI2];
+    load_vec_i8order<KI2>(ac, a, lane);
+    sa = quant_row_i8<KI2>(ac, qa);
+  }
+  int acc[2 * R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    acc[r] = 0;
+    acc[R + r] = 0;
+#pragma unroll
+    for (int j = 0; j < KI1; j++) acc[r] = dot16_i8(qg[j], w2[r][j], acc[r]);
+#pragma unroll
+    for (int j = 0; j < KI2; j++) acc[R + r] = dot16_i8(qa[j], wp[r][j], acc[R + r]);
+  }
+  const int tot = reduce_rows_i<2 * R>(acc, lane);  // lanes < 32: fc2 sums, lanes >= 32: proj sums
+  const int sp = __shfl_xor(tot, 32, 64);
+  if (lane < 32 && (lane & ((1 << SH) - 1)) == 0 && in) {
+    const float tf = (float)tot * sg, tp = (float)sp * sa;
+    const float vf = tf * sw2me + b2me, vp = tp * swpme + bpme;
+    out[nme] = f2bf(rbf(vf) + rbf(rbf(vp) + xme));
+  }
+}
+
 // ---------------------------------------------------------------------------------------------- lm head + argmax
 // Argmax key: orderable bits of the bf16 logit in the high word, (0xffffffff - index) in the low word, so the
 // largest key is the largest logit and, among equal logits, the smallest index.
@@ -482,5 +696,41 @@ extern "C" int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* 
   if (H < 1 || ctx < 1) return MX_ESHAPE;
   hipLaunchKernelGGL(decode_attn_kernel, dim3(H), dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state,
                      scale * 1.4426950408889634f, out);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// W8A8 [qkv | fc1] GEMV with the LayerNorm fused (gamma = beta = null: none): the LN output is quantised per token,
+// Wq int8 (N, ldw bytes), sw / bias fp32 per row. K = 2048 or 1024. Replaces HI8Lin on the shared quantised LN output
+// (md2fast.py:174-198) for one token.
+extern "C" int mx_ln_gemv2_i8(hipStream_t st, const uint16_t* x, const uint16_t* gamma, const uint16_t* beta, float eps,
+                              const int8_t* Wq, long ldw, const float* sw, const float* bias, int N, int K, int n1,
+                              uint16_t* out1, uint16_t* out2, int act2) {
+  if (!x || !Wq || !sw || !out1 || (n1 < N && !out2)) return MX_ENULL;
+  if ((gamma == nullptr) != (beta == nullptr)) return MX_ENULL;
+  if (N < 1 || n1 < 0 || n1 > N || ldw < K || ldw % 16 || act2 < 0 || act2 > 2) return MX_ESHAPE;
+  if (((uintptr_t)x | (uintptr_t)Wq) & 15) return MX_ELAYOUT;
+  constexpr int R = 8;
+  const dim3 g((N + 4 * R - 1) / (4 * R));
+  if (K == 2048) hipLaunchKernelGGL((ln_gemv2_i8_kernel<2, R>), g, dim3(256), 0, st, x, gamma, beta, eps, Wq, ldw, sw, bias, N, n1, out1, out2, act2);
+  else if (K == 1024) hipLaunchKernelGGL((ln_gemv2_i8_kernel<1, R>), g, dim3(256), 0, st, x, gamma, beta, eps, Wq, ldw, sw, bias, N, n1, out1, out2, act2);
+  else return MX_ESHAPE;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// W8A8 fc2 (K2 = 8192 / 4096) and proj (Kp = 2048 / 1024) GEMVs + both residual adds: out = bf16(bf16(fc2(g)) +
+// bf16(bf16(proj(a)) + xres)); W2 (N, K2) and Wp (N, Kp) int8, contiguous rows.
+extern "C" int mx_gemv_dual_res_i8(hipStream_t st, const uint16_t* g, const int8_t* W2, const float* sw2,
+                                   const float* b2, int K2, const uint16_t* a, const int8_t* Wp, const float* swp,
+                                   const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N) {
+  if (!g || !W2 || !sw2 || !b2 || !a || !Wp || !swp || !bp || !xres || !out) return MX_ENULL;
+  if (N < 1) return MX_ESHAPE;
+  if (((uintptr_t)g | (uintptr_t)W2 | (uintptr_t)a | (uintptr_t)Wp) & 15) return MX_ELAYOUT;
+  constexpr int R = 2;
+  const dim3 gr((N + 4 * R - 1) / (4 * R));
+  if (K2 == 8192 && Kp == 2048)
+    hipLaunchKernelGGL((gemv_dual_res_i8_kernel<8, 2, R>), gr, dim3(256), 0, st, g, W2, sw2, b2, a, Wp, swp, bp, xres, out, N);
+  else if (K2 == 4096 && Kp == 1024)
+    hipLaunchKernelGGL((gemv_dual_res_i8_kernel<4, 1, R>), gr, dim3(256), 0, st, g, W2, sw2, b2, a, Wp, swp, bp, xres, out, N);
+  else return MX_ESHAPE;
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

@@ -60,10 +60,33 @@ template <int V>
 struct IntC {
   static constexpr int value = V;
 };
-template <int ACT>
+// I8: s holds int32 accumulator bits; the linear output is ((float)acc * sa) * sw + bias in fp32 and any GELU applies
+// to that fp32 value before the one bf16 rounding (the W8A8 epilogue); a residual is then added to the rounded value.
+template <int ACT, bool I8 = false>
 __device__ __forceinline__ u32x2 epi_val(const f32x4& s, const f32x4& bv, const u32x2& rv, bool has_r, int n,
-                                         int act_ncols) {
+                                         int act_ncols, float sa = 0.f, const f32x4& sw = f32x4{0.f, 0.f, 0.f, 0.f}) {
   float v[4];
+  if constexpr (I8) {
+    static_assert(ACT != 3, "no gated GELU in the int8 path");
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float t = (float)__float_as_int(s[e]) * sa;
+      v[e] = t * sw[e] + bv[e];
+    }
+    if constexpr (ACT == 1 || ACT == 2) {
+      if (act_ncols <= 0 || n < act_ncols) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = ACT == 1 ? gelu_tanh(v[e]) : gelu_erf(v[e]);
+      }
+    }
+    if (has_r) {
+      v[0] = rbf(v[0]) + lo_bf(rv.x);
+      v[1] = rbf(v[1]) + hi_bf(rv.x);
+      v[2] = rbf(v[2]) + lo_bf(rv.y);
+      v[3] = rbf(v[3]) + hi_bf(rv.y);
+    }
+    return u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+  }
 #pragma unroll
   for (int e = 0; e < 4; e++) v[e] = rbf(s[e] + bv[e]);
   u32x2 o;
@@ -158,13 +181,17 @@ __device__ __forceinline__ void interleave_reads_mfma() {
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int S>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
+// The kernel body, shared by the bf16 GEMM and the W8A8 int8 GEMM (I8). In the int8 form A and W hold int8 values and
+// every K / stride argument counts 16-bit units (2 int8): an LDS row is still 128 bytes (128 int8 of one k-step), a
+// fragment is still 16 bytes (16 consecutive k for the 32x32x32 int8 MFMA instead of 8 for the 32x32x16 bf16 one), so
+// the DMA, swizzle and pipeline are unchanged; the accumulators hold int32 bits.
+template <int BM, int BN, int WGM, int WGN, int S, bool I8>
+__device__ __forceinline__ void gemm_body(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
     const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
     uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols,
     int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt,
-    float* __restrict__ P, long ldp, long p_split) {
+    float* __restrict__ P, long ldp, long p_split, const float* __restrict__ sa, const float* __restrict__ sw) {
   constexpr int NW = WGM * WGN, NT = 64 * NW;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
   static_assert(S >= 2, "at least a double buffer");
@@ -253,7 +280,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
 #pragma unroll
     for (int i = 0; i < FN; i++)
 #pragma unroll
-      for (int j = 0; j < FM; j++) acc[i][j] = mfma32(wf[buf][i], af[buf][j], acc[i][j]);
+      for (int j = 0; j < FM; j++) {
+        if constexpr (I8) {
+          typedef int i32x4 __attribute__((ext_vector_type(4)));
+          typedef int i32x16 __attribute__((ext_vector_type(16)));
+          acc[i][j] = __builtin_bit_cast(f32x16, __builtin_amdgcn_mfma_i32_32x32x32_i8(
+              __builtin_bit_cast(i32x4, wf[buf][i]), __builtin_bit_cast(i32x4, af[buf][j]),
+              __builtin_bit_cast(i32x16, acc[i][j]), 0, 0, 0));
+        } else {
+          acc[i][j] = mfma32(wf[buf][i], af[buf][j], acc[i][j]);
+        }
+      }
   };
   // interleave the FM + FN reads of the next substep with the FM * FN MFMAs of this one
   auto interleave = [&]() {
@@ -313,7 +350,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
 
   // ---- split-K: partial tile to the workspace; the last split to arrive reduces in split order (4-wave tiles only:
   // the 8-wave tiles serve grids large enough without it)
-  if (PSUM && splits > 1) {
+  if (PSUM && !I8 && splits > 1) {
     constexpr int TE = BM * BN;
     float* mine = ws + (long)(tile * splits + split) * TE;
 #pragma unroll
@@ -353,6 +390,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
   // latency for the lot) where the registers allow: always for the bias, for the residual on 4-wave tiles.
   constexpr bool HOIST_R = FN * FM <= 4;
   f32x4 bv[FN][4];
+  f32x4 swv[I8 ? FN : 1][4];
+  float sav[I8 ? FM : 1];
+  if constexpr (I8) {
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) swv[i][g] = bias4(sw, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N);
+#pragma unroll
+    for (int j = 0; j < FM; j++) sav[j] = sa[min(m0 + wm * WTM + j * 32 + lr, M - 1)];
+  }
   u32x2 rv[HOIST_R ? FN : 1][HOIST_R ? FM : 1][4];
 #pragma unroll
   for (int i = 0; i < FN; i++)
@@ -386,7 +433,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
           else if (R)
             rg = res4(R, ldr, r_rows, m0 + r, n0 + c, M, N);
           const f32x4 a4 = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          stage_val<ACT, SP>(smem, r, c, epi_val<ACT>(a4, bv[i][g], rg, R != nullptr, n0 + c, act_ncols));
+          if constexpr (I8) {
+            if constexpr (ACT != 3)
+              stage_val<ACT, SP>(smem, r, c, epi_val<ACT, true>(a4, bv[i][g], rg, R != nullptr, n0 + c, act_ncols,
+                                                                 sav[j], swv[i][g]));
+          } else {
+            stage_val<ACT, SP>(smem, r, c, epi_val<ACT>(a4, bv[i][g], rg, R != nullptr, n0 + c, act_ncols));
+          }
         }
   });
   __syncthreads();
@@ -394,6 +447,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
     store_staged<BM, BN / 2, SP, NT>(smem, C, ldc, m0, n0 / 2, M, N / 2, tid);
   else
     store_staged<BM, BN, SP, NT>(smem, C, ldc, m0, n0, M, N, tid);
+}
+
+template <int BM, int BN, int WGM, int WGN, int S>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
+    const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
+    const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
+    uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols,
+    int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt,
+    float* __restrict__ P, long ldp, long p_split) {
+  gemm_body<BM, BN, WGM, WGN, S, false>(A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols,
+                                        tiles_m, tiles_n, splits, kt_per_split, ws, cnt, P, ldp, p_split, nullptr,
+                                        nullptr);
+}
+
+// W8A8: C = epi(((float)(Aq Wq^T) * sa[m]) * sw[n] + bias[n]) (K, Kw, lda, ldw in 16-bit units); P (raw int32
+// accumulators) when given
+template <int BM, int BN, int WGM, int WGN, int S>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_i8_kernel(
+    const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw, const float* __restrict__ sa,
+    const float* __restrict__ sw, const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr,
+    int r_rows, uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols, int tiles_m,
+    int tiles_n, float* __restrict__ P, long ldp) {
+  gemm_body<BM, BN, WGM, WGN, S, true>(A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols,
+                                       tiles_m, tiles_n, 1, Kw / BK, nullptr, nullptr, P, ldp, 0, sa, sw);
 }
 
 // Wave-split-K kernel (see the header): 4 waves share the LDS ring of a BM x BN tile; wave w multiplies the k
@@ -634,6 +711,16 @@ bool psum_ok(int cfg) {
   return c.kind == 1 || (c.waves == 4 && c.bm * c.bn <= 128 * 256);
 }
 
+template <int BM, int BN, int WGM, int WGN, int S>
+hipError_t launch_i8(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* sa,
+                     const float* sw, const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C,
+                     long ldc, int M, int N, int K, int Kw, int act, float* P, long ldp) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn), dim3(64 * WGM * WGN), 0, st, A, lda, W,
+                     ldw, sa, sw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, 0, tm, tn, P, ldp);
+  return hipGetLastError();
+}
+
 long tiles_of(int cfg, int M, int N) {
   return (long)((M + kCfgs[cfg].bm - 1) / kCfgs[cfg].bm) * ((N + kCfgs[cfg].bn - 1) / kCfgs[cfg].bn);
 }
@@ -804,5 +891,53 @@ extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const u
   }
 #undef W_
 #undef L_
+  return e == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// W8A8 GEMM (the reference's HI8Lin path, moondream/gpu/hgemm.py:95-137 / i8gemm.hip:91-201 with bias, optional GELU
+// and, beyond the reference, an optional fused residual): C = bf16(gelu?(((float)(A W^T) * sa[m]) * sw[n] + bias[n]))
+// [+ R, rounded again]. A (M, K) and W (N, Kw) are int8 with row strides lda / ldw in bytes; W holds zeros in columns
+// [K, Kw); sa (M) and sw (N) are the fp32 row / column scales. With P, the raw int32 accumulators go to P (row stride
+// ldp elements) instead: no scales, bias, activation or C. cfg: a kind-0 tile config (mx_gemm_cfg_kind 0; P needs
+// one with a partial-sum mode); act: 0 none, 1 GELU-tanh, 2 GELU-erf. No split-K.
+extern "C" int mx_gemm_i8(hipStream_t st, int cfg, const int8_t* A, long lda, const int8_t* W, long ldw,
+                          const float* sa, const float* sw, const float* bias, const uint16_t* R, long ldr, int r_rows,
+                          uint16_t* C, long ldc, int M, int N, int K, int Kw, int act, int32_t* P, long ldp) {
+  if (!A || !W) return MX_ENULL;
+  if (!P && (!C || !sa || !sw)) return MX_ENULL;
+  if (cfg < 0 || cfg >= kNCfg || kCfgs[cfg].kind != 0) return MX_EBADCFG;
+  if (P && !psum_ok(cfg)) return MX_EBADCFG;
+  if (act < 0 || act > 2) return MX_EBADCFG;
+  if (M < 1 || N < 1 || N % 4 || K < 16 || K % 16 || Kw % 128 || Kw < K) return MX_ESHAPE;
+  if (lda % 16 || lda < K || ldw % 16 || ldw < Kw || r_rows < 0) return MX_ESHAPE;
+  if (((uintptr_t)A | (uintptr_t)W) & 15) return MX_ELAYOUT;
+  if (P) {
+    if (ldp % 4 || ldp < N || ((uintptr_t)P & 15)) return MX_ELAYOUT;
+  } else {
+    if (ldc % 4 || ldc < N || ((uintptr_t)C & 7)) return MX_ESHAPE;
+    if (((uintptr_t)sw & 15) || (bias && ((uintptr_t)bias & 15))) return MX_ELAYOUT;
+    if (R && (((uintptr_t)R & 7) || ldr % 4 || ldr < N)) return MX_ELAYOUT;
+  }
+  const uint16_t* A16 = reinterpret_cast<const uint16_t*>(A);
+  const uint16_t* W16 = reinterpret_cast<const uint16_t*>(W);
+  float* Pf = reinterpret_cast<float*>(P);
+  hipError_t e;
+#define I_(BM, BN, WGM, WGN, S) launch_i8<BM, BN, WGM, WGN, S>(st, A16, lda / 2, W16, ldw / 2, sa, sw, bias, R, ldr, r_rows, C, ldc, M, N, K / 2, Kw / 2, act, Pf, ldp)
+  switch (cfg) {
+    case 0: e = I_(128, 128, 2, 2, 4); break;
+    case 1: e = I_(64, 128, 2, 2, 4); break;
+    case 2: e = I_(128, 64, 2, 2, 4); break;
+    case 3: e = I_(64, 64, 2, 2, 4); break;
+    case 4: e = I_(256, 128, 2, 2, 3); break;
+    case 5: e = I_(128, 256, 2, 2, 3); break;
+    case 6: e = I_(64, 64, 2, 2, 3); break;
+    case 7: e = I_(128, 128, 2, 2, 2); break;
+    case 15: e = I_(256, 256, 2, 4, 2); break;
+    case 16: e = I_(256, 128, 4, 2, 3); break;
+    case 17: e = I_(128, 256, 2, 4, 3); break;
+    case 18: e = I_(256, 256, 2, 2, 2); break;
+    default: return MX_EBADCFG;
+  }
+#undef I_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

@@ -22,7 +22,9 @@ BOS = 50256  # moondream2's tokenizer bos_id (the Phi / GPT-2 <|endoftext|> id)
 
 
 class TextDecoder:
-    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", ctx=1024, attn_splits=4):
+    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", ctx=1024, attn_splits=4, w8a8=False):
+        """w8a8: the four text Linears of every layer run the reference's W8A8 path (its default text linear class,
+        HI8Lin, moondream/gpu/bench.py:20) in prefill and decode; the LM head stays bf16 (md2fast.py:115)."""
         c = TXT
         self.dev = torch.device(device)
         self.D, self.H, self.hd, self.eps = c["dim"], c["heads"], c["hd"], c["ln_eps"]
@@ -35,20 +37,32 @@ class TextDecoder:
         n = 0
         while f"blocks.{n}.ln.weight" in weights:
             n += 1
+        self.w8a8 = w8a8
         self.blocks = []
         for i in range(n):
             p = f"blocks.{i}."
             # [Wqkv | Wfc1] stored once, fused: the decode GEMV streams both in one pass; the prefill GEMMs use row
-            # slices of the same storage
+            # slices of the same storage (int8 with per-row scales in the W8A8 form: a row's scale is its own, so the
+            # fused quantisation equals quantising qkv and fc1 separately)
             wqf = torch.cat([weights[p + "attn.qkv.weight"], weights[p + "mlp.fc1.weight"]]).to(dev, BF).contiguous()
             bqf = torch.cat([weights[p + "attn.qkv.bias"], weights[p + "mlp.fc1.bias"]]).to(dev, torch.float32).contiguous()
             nq = weights[p + "attn.qkv.weight"].shape[0]
-            blk = dict(ln=(g(p + "ln.weight"), g(p + "ln.bias")), wqf=wqf, bqf=bqf, nq=nq,
-                       qkv=lin_cls(wqf[:nq], bqf[:nq], BF), fc1=lin_cls(wqf[nq:], bqf[nq:], BF),
-                       proj=lin_cls(weights[p + "attn.proj.weight"], weights[p + "attn.proj.bias"], BF),
-                       fc2=lin_cls(weights[p + "mlp.fc2.weight"], weights[p + "mlp.fc2.bias"], BF))
-            blk["wp"], blk["bp"] = blk["proj"].w, f32(p + "attn.proj.bias")
-            blk["w2"], blk["b2"] = blk["fc2"].w, f32(p + "mlp.fc2.bias")
+            blk = dict(ln=(g(p + "ln.weight"), g(p + "ln.bias")), bqf=bqf, nq=nq)
+            if w8a8:
+                wq, sq = ops.MxI8Lin.quantize_weight(wqf)
+                del wqf
+                blk.update(wqf=wq, sqf=sq, qkv=ops.MxI8Lin.from_quantized(wq[:nq], sq[:nq], bqf[:nq]),
+                           fc1=ops.MxI8Lin.from_quantized(wq[nq:], sq[nq:], bqf[nq:]),
+                           proj=ops.MxI8Lin(weights[p + "attn.proj.weight"], weights[p + "attn.proj.bias"], BF, dev),
+                           fc2=ops.MxI8Lin(weights[p + "mlp.fc2.weight"], weights[p + "mlp.fc2.bias"], BF, dev))
+                blk["wp"], blk["swp"] = blk["proj"].wq, blk["proj"].sw
+                blk["w2"], blk["sw2"] = blk["fc2"].wq, blk["fc2"].sw
+            else:
+                blk.update(wqf=wqf, qkv=lin_cls(wqf[:nq], bqf[:nq], BF), fc1=lin_cls(wqf[nq:], bqf[nq:], BF),
+                           proj=lin_cls(weights[p + "attn.proj.weight"], weights[p + "attn.proj.bias"], BF),
+                           fc2=lin_cls(weights[p + "mlp.fc2.weight"], weights[p + "mlp.fc2.bias"], BF))
+                blk["wp"], blk["w2"] = blk["proj"].w, blk["fc2"].w
+            blk["bp"], blk["b2"] = f32(p + "attn.proj.bias"), f32(p + "mlp.fc2.bias")
             self.blocks.append(blk)
         self.post_ln = (g("post_ln.weight"), g("post_ln.bias"))
         self.w_lm, self.b_lm = g("lm_head.weight"), f32("lm_head.bias")
@@ -81,13 +95,15 @@ class TextDecoder:
         Tk = pos0 + n
         for i, b in enumerate(self.blocks):
             h = ops.layernorm(x, *b["ln"], eps=self.eps)
-            qkv = b["qkv"](h)
+            # W8A8: the LN output is quantised once for qkv and fc1 (SHARE_QUANT, md2fast.py:52, 174)
+            pre = b["qkv"].quant(h) if self.w8a8 else None
+            qkv = b["qkv"](h, pre=pre)
             q = torch.empty(1, H, n, hd, device=self.dev, dtype=BF)
             call("mx_rope_kv", stream(), qkv.data_ptr(), qkv.stride(0), self.cs.data_ptr(), q.data_ptr(),
                  self.kc[i].data_ptr(), self.vc[i].data_ptr(), 1, n, H, self.ctx, pos0, 1, 0)
             a = ops.sdpa(q, self.kc[i][:, :, :Tk], self.vc[i][:, :, :Tk], qpos0=pos0, causal_from=causal_from)
             r = b["proj"](a.view(n, self.D), res=x)
-            x = b["fc2"](b["fc1"](h, gelu=True), res=r)
+            x = b["fc2"](b["fc1"](h, gelu=True, pre=pre), res=r)
         return x
 
     def prefill(self, img_emb, prompt_ids):
@@ -126,17 +142,31 @@ class TextDecoder:
         xi = 0
         for i, b in enumerate(self.blocks):
             x, xn = self.xd[xi], self.xd[xi ^ 1]
-            _lib.check(lib.mx_ln_gemv2(st, x.data_ptr(), b["ln"][0].data_ptr(), b["ln"][1].data_ptr(), float(self.eps),
-                                       b["wqf"].data_ptr(), b["wqf"].stride(0), b["bqf"].data_ptr(), b["wqf"].shape[0],
-                                       self.D, b["nq"], self.qkv_d.data_ptr(), self.g_d.data_ptr(), 1), "mx_ln_gemv2")
+            if self.w8a8:
+                _lib.check(lib.mx_ln_gemv2_i8(st, x.data_ptr(), b["ln"][0].data_ptr(), b["ln"][1].data_ptr(),
+                                              float(self.eps), b["wqf"].data_ptr(), b["wqf"].stride(0),
+                                              b["sqf"].data_ptr(), b["bqf"].data_ptr(), b["wqf"].shape[0], self.D,
+                                              b["nq"], self.qkv_d.data_ptr(), self.g_d.data_ptr(), 1), "mx_ln_gemv2_i8")
+            else:
+                _lib.check(lib.mx_ln_gemv2(st, x.data_ptr(), b["ln"][0].data_ptr(), b["ln"][1].data_ptr(),
+                                           float(self.eps), b["wqf"].data_ptr(), b["wqf"].stride(0), b["bqf"].data_ptr(),
+                                           b["wqf"].shape[0], self.D, b["nq"], self.qkv_d.data_ptr(),
+                                           self.g_d.data_ptr(), 1), "mx_ln_gemv2")
             _lib.check(lib.mx_decode_attn(st, self.qkv_d.data_ptr(), self.cs.data_ptr(), self.kc[i].data_ptr(),
                                           self.vc[i].data_ptr(), self.H, self.ctx, self.state.data_ptr(), self.S,
                                           float(self.hd ** -0.5), self.attn_ws.data_ptr(), self.attn_cnt.data_ptr(),
                                           self.a_d.data_ptr()), "mx_decode_attn")
-            _lib.check(lib.mx_gemv_dual_res(st, self.g_d.data_ptr(), b["w2"].data_ptr(), b["b2"].data_ptr(),
-                                            b["w2"].shape[1], self.a_d.data_ptr(), b["wp"].data_ptr(),
-                                            b["bp"].data_ptr(), b["wp"].shape[1], x.data_ptr(), xn.data_ptr(), self.D),
-                       "mx_gemv_dual_res")
+            if self.w8a8:
+                _lib.check(lib.mx_gemv_dual_res_i8(st, self.g_d.data_ptr(), b["w2"].data_ptr(), b["sw2"].data_ptr(),
+                                                   b["b2"].data_ptr(), b["w2"].shape[1], self.a_d.data_ptr(),
+                                                   b["wp"].data_ptr(), b["swp"].data_ptr(), b["bp"].data_ptr(),
+                                                   b["wp"].shape[1], x.data_ptr(), xn.data_ptr(), self.D),
+                           "mx_gemv_dual_res_i8")
+            else:
+                _lib.check(lib.mx_gemv_dual_res(st, self.g_d.data_ptr(), b["w2"].data_ptr(), b["b2"].data_ptr(),
+                                                b["w2"].shape[1], self.a_d.data_ptr(), b["wp"].data_ptr(),
+                                                b["bp"].data_ptr(), b["wp"].shape[1], x.data_ptr(), xn.data_ptr(),
+                                                self.D), "mx_gemv_dual_res")
             xi ^= 1
         if xi:
             self.xd[0].copy_(self.xd[1])

@@ -276,6 +276,130 @@ def tune_gemm(lin, M, x2, y2, a, r2, ldr, r_rows, ws, reps=10):
 tune_gemm.split_k = False
 
 
+class MxI8Lin:
+    """W8A8 Linear (the reference's HI8Lin, moondream/gpu/hgemm.py:95-137): int8 weights with a per-output-channel scale
+    (amax / 127, round half to even, hgemm.py:101-106), int8 activations with a per-token dynamic scale (quant(),
+    tgemm.py:81-91), int32 MFMA accumulation, fp32 dequant ((acc * s_x) * s_w) + bias, GELU-tanh on that fp32 value
+    when asked (fused_gelu), one bf16 rounding (i8gemm.hip:181-197). `pre` takes an already quantised input (q, s),
+    so layers that read the same activation share one quantisation (md2fast.py:52, 174). A residual is added to the
+    rounded output and rounded again, exactly the reference's separate bf16 add (lin_res / mlp, md2fast.py:55-67),
+    so the class also offers fused_res.
+    Weights are zero-padded along K to a multiple of 128 (the int8 k-step); K must be a multiple of 16.
+    """
+    fused_gelu = True
+    fused_res = True
+
+    def __init__(self, weight, bias, dtype=BF, device="cuda"):
+        assert dtype == BF, "bf16 activations only"
+        w = weight.detach().to(device=device, dtype=BF)
+        self.N, self.K = w.shape
+        if self.K % 16 or self.N % 4:
+            raise ValueError(f"W8A8 Linear needs K % 16 == 0 and N % 4 == 0, got {tuple(w.shape)}")
+        self.Kw = (self.K + 127) // 128 * 128
+        self.wq, self.sw = self.quantize_weight(w, self.Kw)
+        self.b = None if bias is None else bias.detach().to(device=w.device, dtype=torch.float32).contiguous()
+        self.cfgs = {}
+        self.dev = w.device
+
+    @classmethod
+    def from_quantized(cls, wq, sw, bias):
+        """A Linear over already quantised weights (int8 (N, Kw) with Kw % 128 == 0 and zeros past K = Kw, fp32 (N,)
+        scales): row slices of a fused quantised weight share its storage."""
+        self = cls.__new__(cls)
+        self.N, self.Kw = wq.shape
+        self.K = self.Kw
+        if self.Kw % 128 or wq.stride(1) != 1 or wq.stride(0) % 16:
+            raise ValueError("quantised weight rows must be contiguous, 16-byte aligned, a multiple of 128 wide")
+        self.wq, self.sw = wq, sw
+        self.b = None if bias is None else bias.detach().to(device=wq.device, dtype=torch.float32).contiguous()
+        self.cfgs = {}
+        self.dev = wq.device
+        return self
+
+    @staticmethod
+    def quantize_weight(weight, Kw=None):
+        """(N, K) bf16 weight (on the device) -> int8 (N, Kw) zero-padded past K, fp32 (N,) per-row scale
+        (hgemm.py:101-106), by the library's quantisation kernel."""
+        w = weight.detach().to(dtype=BF).contiguous()
+        N, K = w.shape
+        Kw = K if Kw is None else Kw
+        q = torch.zeros(N, Kw, device=w.device, dtype=torch.int8)
+        s = torch.empty(N, device=w.device, dtype=torch.float32)
+        call("mx_quant_weight_i8", stream(), w.data_ptr(), w.stride(0), q.data_ptr(), q.stride(0), s.data_ptr(), N, K)
+        return q, s
+
+    def quant(self, x):
+        """Per-token int8 quantisation of x (..., K) -> (q (M, K) int8, s (M,) fp32)."""
+        x2 = _rows(x, self.K)
+        M = x2.shape[0]
+        q = torch.empty(M, self.K, device=x2.device, dtype=torch.int8)
+        sc = torch.empty(M, device=x2.device, dtype=torch.float32)
+        call("mx_quant_rows_i8", stream(), x2.data_ptr(), x2.stride(0), q.data_ptr(), q.stride(0), sc.data_ptr(), M,
+             self.K)
+        return q, sc
+
+    def _launch(self, cfg, q, sc, y2, M, a, r2, ldr, r_rows, P=None):
+        return _lib.load().mx_gemm_i8(stream(), cfg, q.data_ptr(), q.stride(0), self.wq.data_ptr(), self.wq.stride(0),
+                                      ptr(sc), self.sw.data_ptr(), ptr(self.b), ptr(r2), ldr, r_rows, ptr(y2),
+                                      y2.stride(0) if y2 is not None else 0, M, self.N, self.K, self.Kw, a, ptr(P),
+                                      P.stride(0) if P is not None else 0)
+
+    def _pick(self, M, q, sc, y2):
+        key = ("i8", M, self.N, self.Kw)
+        if key in _TUNED:
+            return _TUNED[key]
+        best = 0
+        if MxLin.autotune and not torch.cuda.is_current_stream_capturing():
+            bt = float("inf")
+            for cfg in range(_lib.load().mx_gemm_ncfg()):
+                if _lib.load().mx_gemm_cfg_kind(cfg) != 0:
+                    continue
+                run = lambda: self._launch(cfg, q, sc, y2, M, 0, None, 0, 0)
+                if run() != 0:
+                    continue
+                run()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(5):
+                    run()
+                e1.record()
+                e1.synchronize()
+                t = e0.elapsed_time(e1)
+                if t < bt:
+                    best, bt = cfg, t
+        _TUNED[key] = best
+        return best
+
+    def __call__(self, x, gelu=False, res=None, pre=None, act=None, out=None):
+        a = ACT[act if act is not None else gelu]
+        if a == 3:
+            raise ValueError("no gated GELU in the W8A8 path")
+        q, sc = pre if pre is not None else self.quant(x)
+        M = q.shape[0]
+        y = out if out is not None else torch.empty(M, self.N, device=q.device, dtype=BF)
+        y2 = y.view(-1, self.N) if y.dim() != 2 else y
+        r2, r_rows, ldr = None, 0, 0
+        if res is not None:
+            r2 = res.reshape(-1, self.N)
+            if r2.stride(1) != 1:
+                r2 = r2.contiguous()
+            ldr = r2.stride(0)
+            if r2.shape[0] != M:
+                raise ValueError("residual rows must equal the output rows")
+        cfg = self.cfgs.get(M)
+        if cfg is None:
+            cfg = self.cfgs[M] = self._pick(M, q, sc, y2)
+        _lib.check(self._launch(cfg, q, sc, y2, M, a, r2, ldr, r_rows), "mx_gemm_i8")
+        return y2.view(*x.shape[:-1], self.N) if out is None else y
+
+    def acc_i32(self, q, cfg=0):
+        """Raw int32 accumulators q Wq^T (M, N) (parity checks)."""
+        M = q.shape[0]
+        P = torch.empty(M, self.N, device=q.device, dtype=torch.int32)
+        _lib.check(self._launch(cfg, q, None, None, M, 0, None, 0, 0, P=P), "mx_gemm_i8")
+        return P
+
+
 def sdpa(q, k, v, out=None, scale=None, qpos0=0, causal_from=None):
     """Fused attention. q (B, H, Tq, D), k/v (B, H, Tk, D) strided views (unit stride on D); out (B, Tq, H*D).
 

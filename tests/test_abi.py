@@ -123,3 +123,15 @@ def test_other_entry_points_refuse_bad_shapes():
                            A16, 768, 1280, 700) == -2                                 # C not a multiple of 64
     assert lib.mx_rglru_scan(None, A16, A16, A16, 4, 1280, 700, A16, 1536, 0, A16, 768, 0) == -2
     assert lib.mx_counter_add(None, None, 1) == -6
+    # W8A8
+    assert lib.mx_quant_rows_i8(None, A16, 2048, A16, 2048, A16, 4, 2044) == -2                 # K % 8
+    assert lib.mx_quant_rows_i8(None, A16 + 8, 2048, A16, 2048, A16, 4, 2048) == -4             # x not 16-byte aligned
+    assert lib.mx_quant_rows_i8(None, A16, 2048, None, 2048, A16, 4, 2048) == -6
+    assert lib.mx_quant_weight_i8(None, A16, 2048, A16, 2040, A16, 4, 2048) == -2            # ldq < K
+    i8 = lambda **kw: lib.mx_gemm_i8(*{**dict(st=None, cfg=0, A=A16, lda=2048, W=A16, ldw=2048, sa=A16, sw=A16,
+                                                bias=A16, R=None, ldr=0, r_rows=0, C=A16, ldc=2048, M=64, N=2048,
+                                                K=2048, Kw=2048, act=0, P=None, ldp=0), **kw}.values())
+    assert i8(K=2040, lda=2040) == -2 and i8(Kw=2000) == -2 and i8(lda=2056 - 4) == -2
+    assert i8(cfg=8) == -1                                                          # wave-split configs: bf16 only
+    assert i8(cfg=15, P=A16, ldp=2048) == -1                                        # raw int32 needs a partial-sum cfg
+    assert i8(act=3) == -1 and i8(A=A16 + 8) == -4 and i8(sw=None) == -6

@@ -406,3 +406,70 @@ def test_synth_is_seeded_per_tensor():
     for k, v in a.items():
         assert torch.equal(v, b[k]), k
     assert not torch.equal(S.vision_weights(1, layers=1)["blocks.0.attn.qkv.weight"], a["blocks.0.attn.qkv.weight"])
+
+
+# ---------------------------------------------------------------------------------------------- W8A8 text linears
+def test_quant_rows_rounds_half_away_from_zero_with_floor():
+    """tgemm.py:81-91: s = max(amax, 1e-5) / 127, q = trunc(v + 0.5 sign v). Exact ties (v = +-2.5, +-0.5) go away
+    from zero (half-to-even would give 2 / 0), the amax element maps to +-127, an all-zero row keeps the 1e-5 floor."""
+    x = torch.tensor([[1.0, 0.0, -1.0, 0.0],
+                      [0.0, 0.0, 0.0, 0.0]], dtype=torch.float32)
+    # amax = 127/64 makes s = 1/64 exactly, so v = 64 x lands exactly on the ties (all values bf16-exact)
+    ties = (torch.tensor([[127.0, 2.5, -2.5, 0.5, -0.5, 1.5, 0.0, -127.0]]) / 64).to(torch.bfloat16)
+    q, sc = ot.quant_rows(ties)
+    assert sc.item() == 1 / 64
+    assert q[0].tolist() == [127, 3, -3, 1, -1, 2, 0, -127]
+    v = ties.float() / sc[:, None]
+    assert torch.round(v)[0].tolist() == [127, 2, -2, 0, 0, 2, 0, -127]  # half-to-even would differ on the ties
+    qz, sz = ot.quant_rows(x[1:].to(torch.bfloat16))
+    assert sz.item() == np.float32(1e-5) / np.float32(127.0) and int(qz.abs().max()) == 0
+    # dequantisation error within half a step everywhere, on random rows
+    xr = torch.randn(16, 256, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    qr, sr = ot.quant_rows(xr)
+    err = (qr.float() * sr[:, None] - xr.float()).abs()
+    assert bool((err <= sr[:, None] * 0.5 * (1 + 1e-5)).all())
+    assert bool((qr.abs().amax(1) == 127).all())
+
+
+def test_quant_weight_round_half_even_and_scale():
+    """hgemm.py:101-106: s = amax / 127 per output row, q = round-half-to-even(w / s) clamped to +-127; a zero row
+    keeps the 1e-8 floor."""
+    w = torch.tensor([[254.0, 5.0, -5.0, 3.0, 1.0], [0.0, 0.0, 0.0, 0.0, 0.0]]).to(torch.bfloat16)
+    q, s = ot.quant_weight(w)
+    # row 0: s = 2 -> v = [127, 2.5, -2.5, 1.5, 0.5] -> half-to-even [127, 2, -2, 2, 0]
+    assert s[0].item() == 2.0 and q[0].tolist() == [127, 2, -2, 2, 0]
+    assert s[1].item() == np.float32(1e-8) / np.float32(127.0) and q[1].abs().max() == 0
+
+
+def test_i8_linear_matches_fp64_brute_force():
+    """i8gemm.hip:181-197: the int32 sum is exact (checked against python integers), then fp32
+    ((acc * s_x) * s_w) + b in that order, GELU-tanh on the fp32 value, one bf16 rounding."""
+    g = torch.Generator().manual_seed(11)
+    q = torch.randint(-127, 128, (3, 40), generator=g, dtype=torch.int8)
+    wq = torch.randint(-127, 128, (5, 40), generator=g, dtype=torch.int8)
+    sx = torch.rand(3, generator=g) * 0.01 + 1e-3
+    sw = torch.rand(5, generator=g) * 0.01 + 1e-3
+    b = (torch.randn(5, generator=g) * 0.1).to(torch.bfloat16)
+    out = ot.i8_linear(q, sx, wq, sw, b)
+    outg = ot.i8_linear(q, sx, wq, sw, b, gelu_tanh=True)
+    for m in range(3):
+        for n in range(5):
+            acc = sum(int(q[m, k]) * int(wq[n, k]) for k in range(40))
+            v = np.float32(np.float32(np.float32(acc) * np.float32(sx[m])) * np.float32(sw[n])) + np.float32(b[n].float())
+            assert out[m, n].float().item() == torch.tensor(float(v)).to(torch.bfloat16).float().item()
+            vd = float(v)
+            gd = 0.5 * vd * (1 + math.tanh(0.7978845608028654 * (vd + 0.044715 * vd ** 3)))
+            assert abs(outg[m, n].float().item() - gd) <= 2 ** -7 * abs(gd) + 1e-6
+
+
+def test_w8a8_layer_stays_close_to_bf16():
+    """The W8A8 decoder restatement shares everything but the four text Linears with the bf16 one: on a 2-layer model
+    its prompt logits sit within the int8 quantisation noise of the bf16 logits (and are not identical)."""
+    w = S.text_weights(0, layers=2)
+    fr = S.freqs_cis(32, 2048)
+    img = S.activations(3, (20, 2048), "img")
+    p = S.prompt_ids(4, 6)
+    lb = ot.Text(w, 64, fr).prefill(img, p).float()
+    lq = ot.Text(w, 64, fr, w8a8=True).prefill(img, p).float()
+    r = ((lb - lq).norm() / lb.norm()).item()
+    assert 1e-4 < r < 5e-2, r
