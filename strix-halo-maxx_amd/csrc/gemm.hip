@@ -185,15 +185,20 @@ __device__ __forceinline__ void interleave_reads_mfma() {
 // every K / stride argument counts 16-bit units (2 int8): an LDS row is still 128 bytes (128 int8 of one k-step), a
 // fragment is still 16 bytes (16 consecutive k for the 32x32x32 int8 MFMA instead of 8 for the 32x32x16 bf16 one), so
 // the DMA, swizzle and pipeline are unchanged; the accumulators hold int32 bits.
-template <int BM, int BN, int WGM, int WGN, int S, bool I8>
+// KS = 2: 8 waves, the spatial WGM x WGN split twice over, each wave group taking half of every k-step's substeps
+// (same LDS bytes per k-step as KS = 1, twice the waves to pull them: a CU holding one workgroup reads its LDS at the
+// 8-wave rate); the second group's accumulators are added to the first's through LDS after the k loop.
+template <int BM, int BN, int WGM, int WGN, int S, bool I8, int KS = 1>
 __device__ __forceinline__ void gemm_body(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
     const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
     uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols,
     int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt,
     float* __restrict__ P, long ldp, long p_split, const float* __restrict__ sa, const float* __restrict__ sw) {
-  constexpr int NW = WGM * WGN, NT = 64 * NW;
+  constexpr int NWS = WGM * WGN, NW = NWS * KS, NT = 64 * NW;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
+  static_assert(KS == 1 || KS == 2, "one or two k groups");
+  constexpr int SPW = (BK / 16) / KS;  // 16-wide substeps per wave per k-step
   static_assert(S >= 2, "at least a double buffer");
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -205,8 +210,8 @@ __device__ __forceinline__ void gemm_body(
   constexpr int SP = BN + 8;  // row pitch of the epilogue's staging tile (reuses the ring)
   constexpr int SPF = BN + 4;  // row pitch of the fp32 staging tile of the partial-sum mode (4-wave tiles)
   constexpr int SMEM0 = S * STAGE > BM * SP ? S * STAGE : BM * SP;
-  // partial-sum mode and in-kernel split-K: 4-wave tiles whose fp32 staging tile fits the LDS
-  constexpr bool PSUM = NW == 4 && BM * BN <= 128 * 256;
+  // partial-sum mode: 2 x 2 spatial tiles whose fp32 staging tile fits the LDS; in-kernel split-K only without KS
+  constexpr bool PSUM = NWS == 4 && BM * BN <= 128 * 256;
   constexpr int SMEM = PSUM && BM * SPF * 2 > SMEM0 ? BM * SPF * 2 : SMEM0;
   __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
 
@@ -219,7 +224,9 @@ __device__ __forceinline__ void gemm_body(
   const int nkl = min(nk_all, kt0 + kt_per_split) - kt0;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave % WGM, wn = wave / WGM;
+  const int wsp = wave % NWS, kh = wave / NWS;  // spatial wave, k group
+  const int wm = wsp % WGM, wn = wsp / WGM;
+  const bool owner = kh == 0;                   // holds the summed tile after the k loop
   const int lr = lane & 31, hk = lane >> 5;
   const uint32_t sbase = lds_off(smem);
 
@@ -304,13 +311,13 @@ __device__ __forceinline__ void gemm_body(
     if (s < nkl) issue(kt0 + s, s);
   wait_stages<LPS, S - 1>(nkl - 1);  // stage 0 has landed
   __syncthreads();
-  read_frags(0, smem, 0);
+  read_frags(0, smem, kh * SPW);
 
   for (int it = 0; it < nkl; it++) {
     const uint16_t* As = smem + (it % S) * STAGE;
 #pragma unroll
-    for (int s = 0; s < BK / 16 - 1; s++) {
-      read_frags((s + 1) & 1, As, s + 1);
+    for (int s = 0; s < SPW - 1; s++) {
+      read_frags((s + 1) & 1, As, kh * SPW + s + 1);
       mfmas(s & 1);
       interleave();
     }
@@ -322,10 +329,41 @@ __device__ __forceinline__ void gemm_body(
     wait_stages<LPS, S - 2>(nkl - 2 - it);
     __syncthreads();
     if (it + S < nkl) issue(kt0 + it + S, it % S);
-    read_frags(0, smem + ((it + 1) % S) * STAGE, 0);
-    mfmas(1);
+    read_frags(0, smem + ((it + 1) % S) * STAGE, kh * SPW);
+    mfmas((SPW - 1) & 1);
     interleave();
     __builtin_amdgcn_sched_barrier(0);
+  }
+  static_assert(SPW % 2 == 0, "the tail reads into buffer 0");
+
+  // ---- KS = 2: the second k group's partial tiles join the first's, in a fixed order
+  if constexpr (KS == 2) {
+    float* red = reinterpret_cast<float*>(smem);
+    static_assert(NWS * FN * FM * 16 * 64 * 4 <= S * STAGE * 2, "the exchange fits the ring");
+    __syncthreads();  // every wave is past its last ring read
+    if (!owner) {
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) red[(((wsp * FN + i) * FM + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+    }
+    __syncthreads();
+    if (owner) {
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const float o = red[(((wsp * FN + i) * FM + j) * 16 + e) * 64 + lane];
+            if constexpr (I8)
+              acc[i][j][e] = __int_as_float(__float_as_int(acc[i][j][e]) + __float_as_int(o));
+            else
+              acc[i][j][e] += o;
+          }
+    }
   }
 
   // ---- partial-sum mode (mx_gemm_bf16_partial): this split's raw fp32 sums to its slab of P, staged like the bf16
@@ -334,14 +372,16 @@ __device__ __forceinline__ void gemm_body(
     if (P) {
       float* stf = reinterpret_cast<float*>(smem);
       __syncthreads();
+      if (owner) {
 #pragma unroll
-      for (int i = 0; i < FN; i++)
+        for (int i = 0; i < FN; i++)
 #pragma unroll
-        for (int j = 0; j < FM; j++)
+          for (int j = 0; j < FM; j++)
 #pragma unroll
-          for (int g = 0; g < 4; g++)
-            *reinterpret_cast<f32x4*>(stf + (wm * WTM + j * 32 + lr) * SPF + wn * WTN + i * 32 + 8 * g + 4 * hk) =
-                f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+            for (int g = 0; g < 4; g++)
+              *reinterpret_cast<f32x4*>(stf + (wm * WTM + j * 32 + lr) * SPF + wn * WTN + i * 32 + 8 * g + 4 * hk) =
+                  f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+      }
       __syncthreads();
       store_staged<BM, BN, SPF, NT>(stf, P + split * p_split, ldp, m0, n0, M, N, tid);
       return;
@@ -350,7 +390,7 @@ __device__ __forceinline__ void gemm_body(
 
   // ---- split-K: partial tile to the workspace; the last split to arrive reduces in split order (4-wave tiles only:
   // the 8-wave tiles serve grids large enough without it)
-  if (PSUM && !I8 && splits > 1) {
+  if (PSUM && KS == 1 && !I8 && splits > 1) {
     constexpr int TE = BM * BN;
     float* mine = ws + (long)(tile * splits + split) * TE;
 #pragma unroll
@@ -418,7 +458,7 @@ __device__ __forceinline__ void gemm_body(
     }
   }
   __syncthreads();
-  with_act(act, [&](auto ac) {
+  if (owner) with_act(act, [&](auto ac) {
     constexpr int ACT = decltype(ac)::value;
 #pragma unroll
     for (int i = 0; i < FN; i++)
@@ -459,6 +499,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bf16_kernel(
   gemm_body<BM, BN, WGM, WGN, S, false>(A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols,
                                         tiles_m, tiles_n, splits, kt_per_split, ws, cnt, P, ldp, p_split, nullptr,
                                         nullptr);
+}
+
+// The 8-wave form of a 2 x 2 tile: two wave groups, each on half of every k-step (KS = 2)
+template <int BM, int BN, int S>
+__global__ __launch_bounds__(512) void gemm_bf16_kh2_kernel(
+    const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
+    const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
+    uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols,
+    int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt,
+    float* __restrict__ P, long ldp, long p_split) {
+  gemm_body<BM, BN, 2, 2, S, false, 2>(A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols,
+                                       tiles_m, tiles_n, splits, kt_per_split, ws, cnt, P, ldp, p_split, nullptr,
+                                       nullptr);
 }
 
 // W8A8: C = epi(((float)(Aq Wq^T) * sa[m]) * sw[n] + bias[n]) (K, Kw, lda, ldw in 16-bit units); P (raw int32
@@ -665,7 +718,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_ks_kernel(
     store_staged<BM, BN, SP>(smem, C, ldc, m0, n0, M, N, tid);
 }
 
-struct Cfg { int bm, bn, stages, per_cu, kind, waves; };
+struct Cfg { int bm, bn, stages, per_cu, kind, waves, kh = 1; };
 // kind 0: LDS-shared tile split over the waves; kind 1: wave-split K (each wave the whole tile, a quarter of K).
 // Both stage operands through a `stages`-deep LDS ring.
 // per_cu: workgroups that fit one CU at once (LDS- or register-limited)
@@ -676,7 +729,11 @@ constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0, 4}, {64, 128, 4, 1, 0, 4}, {128, 64
                          // 8-wave tiles for large grids: 2 waves per SIMD hide each other's LDS reads and barriers
                          {256, 256, 2, 1, 0, 8}, {256, 128, 3, 1, 0, 8}, {128, 256, 3, 1, 0, 8},
                          // 4 waves of 128 x 128: 8 LDS reads per 16 MFMAs (LDS traffic at 3/4 of the MFMA time)
-                         {256, 256, 2, 1, 0, 4}};
+                         {256, 256, 2, 1, 0, 4},
+                         // 8-wave forms of the 2 x 2 tiles, two k groups (kh = 2): batch-1 grids, one workgroup per
+                         // CU, whose k loop waits on LDS reads at the 4-wave rate
+                         {128, 128, 4, 1, 0, 8, 2}, {64, 128, 4, 1, 0, 8, 2}, {128, 64, 4, 1, 0, 8, 2},
+                         {64, 64, 4, 2, 0, 8, 2}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -689,6 +746,19 @@ hipError_t launch(hipStream_t st, int splits, const uint16_t* A, long lda, const
   const int kps = (nk + splits - 1) / splits;
   hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn * splits), dim3(64 * WGM * WGN), 0, st, A, lda, W,
                      ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, tm, tn, splits, kps, ws, cnt, P,
+                     ldp, p_split);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int S>
+hipError_t launch_kh2(hipStream_t st, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                      const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N,
+                      int K, int Kw, int act, int act_ncols, float* P = nullptr, long ldp = 0, long p_split = 0) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  const int nk = Kw / BK;
+  const int kps = (nk + splits - 1) / splits;
+  hipLaunchKernelGGL((gemm_bf16_kh2_kernel<BM, BN, S>), dim3(tm * tn * splits), dim3(512), 0, st, A, lda, W, ldw, bias,
+                     R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, tm, tn, splits, kps, nullptr, nullptr, P,
                      ldp, p_split);
   return hipGetLastError();
 }
@@ -708,7 +778,7 @@ hipError_t launch_ks(hipStream_t st, const uint16_t* A, long lda, const uint16_t
 // 4-wave kind-0 tiles whose fp32 staging tile fits the LDS (the kernel's PSUM)
 bool psum_ok(int cfg) {
   const Cfg& c = kCfgs[cfg];
-  return c.kind == 1 || (c.waves == 4 && c.bm * c.bn <= 128 * 256);
+  return c.kind == 1 || (c.waves / c.kh == 4 && c.bm * c.bn <= 128 * 256);
 }
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -755,13 +825,13 @@ extern "C" long mx_gemm_ws_counters(int cfg, int splits, int M, int N) {
 // 256 CUs x per-tile time, with per-tile time ~ BM*BN*(k-steps)/efficiency. Returns cfg * 16 + splits.
 extern "C" int mx_gemm_pick(int M, int N, int Kw) {
   static const float eff[kNCfg] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f,
-                                   1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f, 1.4f};
+                                   1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f, 1.4f, 1.1f, 0.9f, 0.9f, 0.7f};
   const int nk = Kw / BK;
   int best = 0, bsplit = 1;
   float bt = 1e30f;
   for (int c = 0; c < kNCfg; c++) {
     for (int sp = 1; sp <= 8; sp *= 2) {
-      if (sp > 1 && (kCfgs[c].kind || !psum_ok(c) || nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk))
+      if (sp > 1 && (kCfgs[c].kind || kCfgs[c].kh != 1 || !psum_ok(c) || nk / sp < 4 || (sp - 1) * ((nk + sp - 1) / sp) >= nk))
         break;
       const long tiles = tiles_of(c, M, N) * sp;
       const long slots = 256L * kCfgs[c].per_cu;
@@ -791,7 +861,7 @@ extern "C" int mx_gemm_check(int cfg, int splits, const void* A, long lda, const
   if (bias && ((uintptr_t)bias & 15)) return MX_ELAYOUT;
   if (R && (((uintptr_t)R & 7) || ldr % 4 || ldr < N)) return MX_ELAYOUT;
   if (cfg >= 0 && splits > 1) {
-    if (kCfgs[cfg].kind || !psum_ok(cfg)) return MX_ESPLIT;  // 4-wave kind-0 tiles up to 128 x 256 only
+    if (kCfgs[cfg].kind || kCfgs[cfg].kh != 1 || !psum_ok(cfg)) return MX_ESPLIT;  // 4-wave kind-0 tiles up to 128 x 256
     const int nk = Kw / BK, kps = (nk + splits - 1) / splits;
     if (splits > nk || (splits - 1) * kps >= nk) return MX_ESPLIT;  // every split must own >= 1 k-step
     if (!ws || !cnt) return MX_ENULL;
@@ -837,6 +907,11 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
     case 16: e = launch<256, 128, 4, 2, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 17: e = launch<128, 256, 2, 4, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 18: e = L_(256, 256, 2); break;
+#define H_(BM, BN, S) launch_kh2<BM, BN, S>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
+    case 19: e = H_(128, 128, 4); break;
+    case 20: e = H_(64, 128, 4); break;
+    case 21: e = H_(128, 64, 4); break;
+    case 22: e = H_(64, 64, 4); break;
 #define W_(BM, BN, S, OCC) launch_ks<BM, BN, S, OCC>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
     case 8: e = W_(64, 64, 4, 2); break;
     case 9: e = W_(64, 128, 4, 1); break;
@@ -849,6 +924,7 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
   }
 #undef L_
 #undef W_
+#undef H_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
@@ -880,6 +956,12 @@ extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const u
     case 5: e = L_(128, 256, 3); break;
     case 6: e = L_(64, 64, 3); break;
     case 7: e = L_(128, 128, 2); break;
+#define H_(BM, BN, S) launch_kh2<BM, BN, S>(st, splits, A, lda, W, ldw, nullptr, nullptr, 0, 0, nullptr, 0, M, N, K, Kw, 0, 0, P, ldp, p_split)
+    case 19: e = H_(128, 128, 4); break;
+    case 20: e = H_(64, 128, 4); break;
+    case 21: e = H_(128, 64, 4); break;
+    case 22: e = H_(64, 64, 4); break;
+#undef H_
     case 8: e = W_(64, 64, 4, 2); break;
     case 9: e = W_(64, 128, 4, 1); break;
     case 10: e = W_(128, 64, 4, 1); break;

@@ -39,6 +39,20 @@ def _time_graph(fn, reps):
     return e0.elapsed_time(e1) / reps
 
 
+def _refine(cands, reps, log, name, rounds=3, top=4):
+    """Re-time the `top` fastest (time, pick, fn) candidates `rounds` times, interleaved, with 4x the reps, and return
+    the pick with the lowest median: first-sweep margins of ~1 % between tile configs are within run-to-run noise."""
+    cands = sorted(cands, key=lambda c: c[0])[:top]
+    ts = {c[1]: [] for c in cands}
+    for _ in range(rounds):
+        for _, pick, fn in cands:
+            ts[pick].append(_time_graph(fn, 4 * reps))
+    med = {k: sorted(v)[len(v) // 2] for k, v in ts.items()}
+    best = min(med, key=med.get)
+    log(f"tower {name} refined: " + ", ".join(f"{k}: {v * 1e3:.1f} us" for k, v in med.items()) + f" -> {best}")
+    return best
+
+
 def tune_tower_b1(reps, log):
     """In-context table entries for the batch-1 tower: {(M, N, Kw): (cfg, splits)} fused and partial."""
     dev = torch.device("cuda:0")
@@ -69,18 +83,19 @@ def tune_tower_b1(reps, log):
         for name, act, inp in (("qkv", 0, 1), ("fc1", 1, 4)):
             lin0 = blocks[0][name]
             out = torch.empty(M, lin0.N, device=dev, dtype=torch.bfloat16)
-            best, bt = None, float("inf")
+            cands = []
             for cfg in range(ncfg):
-                for b in blocks:
-                    b[name].cfgs[M] = (cfg, 1)
+                def run(cfg=cfg, name=name, act=act, inp=inp):
+                    for i, b in enumerate(blocks):
+                        b[name].cfgs[M] = (cfg, 1)
+                        b[name](saved[i][inp], gelu=bool(act), out=out)
                 try:
-                    t = _time_graph(lambda: [b[name](saved[i][inp], gelu=bool(act), out=out)
-                                             for i, b in enumerate(blocks)], reps)
+                    t = _time_graph(run, reps)
                 except _lib.MxError:
                     continue
                 log(f"tower {name} cfg {cfg}: {t * 1e3 / len(blocks):.2f} us/launch")
-                if t < bt:
-                    best, bt = (cfg, 1), t
+                cands.append((t, (cfg, 1), run))
+            best = _refine(cands, reps, log, name)
             for b in blocks:
                 b[name].cfgs.pop(M, None)
             fused[(M, lin0.N, lin0.Kw)] = best
@@ -92,7 +107,7 @@ def tune_tower_b1(reps, log):
             nk = lin0.Kw // 64
             xo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
             yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
-            best, bt = None, float("inf")
+            cands = []
             for cfg in range(ncfg):
                 for sp in (1, 2, 3, 4):
                     if sp > 1 and (nk // sp < 2 or (sp - 1) * (-(-nk // sp)) >= nk):
@@ -100,17 +115,17 @@ def tune_tower_b1(reps, log):
                     P = torch.empty(sp, M, lin0.N, device=dev, dtype=torch.float32)
                     if ops._partial(lin0, cfg, sp, ops._rows(saved[0][inp], lin0.K), P, M) != 0:
                         continue  # no partial-sum mode for this config
-                    ops._TUNED_P[key] = (cfg, sp)
 
-                    def run():
+                    def run(cfg=cfg, sp=sp, P=P, name=name, inp=inp, resi=resi, ln=ln, key=key):
+                        ops._TUNED_P[key] = (cfg, sp)
                         for i, b in enumerate(blocks):
                             lnp = b[ln] if ln else saved[i][6]
                             ops.residual_layernorm(b[name].partial(saved[i][inp], out=P), b[name].b, saved[i][resi],
                                                    lnp, eps=vt.eps, x_out=xo, y_out=yo)
                     t = _time_graph(run, reps)
                     log(f"tower {name} cfg {cfg} x{sp}: {t * 1e3 / len(blocks):.2f} us/launch (with the reduction)")
-                    if t < bt:
-                        best, bt = (cfg, sp), t
+                    cands.append((t, (cfg, sp), run))
+            best = _refine(cands, reps, log, name)
             ops._TUNED_P.pop(key, None)
             part[key] = best
             log(f"tower {name}: pick {best}")
