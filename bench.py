@@ -303,7 +303,10 @@ def decode_bench(steps_tokens=128, w8a8=False):
     import strix_halo_maxx_amd.synth as S
     dev = torch.device("cuda:0")
     w = S.text_weights(0)
-    dec = mt.TextDecoder(w, device=dev, ctx=1024, w8a8=w8a8)
+    # yes / no ids: 4 + 4 fixed ids (no tokenizer here); nq = 1 question of up to L = 32 ids (the reference's
+    # FastMD2 defaults, md2fast.py:69)
+    dec = mt.TextDecoder(w, device=dev, ctx=1024, w8a8=w8a8, yes_ids=(11, 222, 3333, 44444),
+                         no_ids=(55, 666, 7777, 50000))
     del w
     img = S.activations(3, (729, 2048), "img").to(dev)
     prompt = S.prompt_ids(4, 64)
@@ -321,6 +324,19 @@ def decode_bench(steps_tokens=128, w8a8=False):
         dec.graph.replay()
     torch.cuda.synchronize()
     t_dec = (time.perf_counter() - t0) / (steps_tokens - 1)
+    # the reference's yes/no query (FastMD2.query, md2fast.py:208-212): a 32-id question over the 730-token prefix,
+    # yes / no rows of the LM head, one HIP graph
+    dec.encode(img)
+    dec.set_questions([prompt[:32].tolist()])
+    dec.capture_query()
+    for _ in range(3):
+        dec.query()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        dec.query()
+    torch.cuda.synchronize()
+    t_q = (time.perf_counter() - t0) / 20
     c = S.TXT
     D, F, L, V = c["dim"], c["ff"], c["layers"], c["vocab"]
     lin = L * (3 * D * D + D * D + 2 * D * F)  # text Linear weights: bf16, or int8 + fp32 per-row scales (W8A8)
@@ -328,13 +344,14 @@ def decode_bench(steps_tokens=128, w8a8=False):
     ctx_mid = dec.pos_base + steps_tokens // 2
     kvbytes = 2 * 2 * L * ctx_mid * D
     bpt = wbytes + kvbytes
-    return {"prefill_ms": round(t_pre * 1e3, 3), "decode_tok_s": round(1.0 / t_dec, 1),
+    return {"prefill_ms": round(t_pre * 1e3, 3), "query_ms": round(t_q * 1e3, 3), "decode_tok_s": round(1.0 / t_dec, 1),
             "decode_ms_per_token": round(t_dec * 1e3, 4),
             "decode_roofline": {"bound": "hbm", "achieved": round(bpt / t_dec / 1e9, 1), "peak": PEAK_HBM / 1e9,
                                 "unit": "GB/s", "frac": round(bpt / t_dec / PEAK_HBM, 4),
                                 "bytes_per_token": bpt},
             "workload": "moondream2 text decoder, 24 layers, prefill 730 + 64 tokens, greedy "
-                        f"{steps_tokens} tokens, batch 1, one HIP graph per decode step"
+                        f"{steps_tokens} tokens, batch 1, one HIP graph per decode step; query_ms: one 32-id "
+                        "yes/no query over the 730-token prefix (graph)"
                         + (", W8A8 text Linears (int8 weights / activations, bf16 LM head)" if w8a8 else "")}
 
 

@@ -10,6 +10,11 @@ Restates moondream/gpu/md2fast.py:
   * _encode: x = cat[wte[bos], img_emb]; prefix prefill            md2fast.py:201-206
   * prompt mask: row i sees all prefix keys and prompt keys <= i  md2fast.py:132-136
   * lm head on the post-LN last position                          md2fast.py:208-212
+  * the yes/no query: questions zero-padded to L ids, run under the prefix + causal mask, the post-LN row of each
+    question's last real token through the LM head restricted to the yes / no rows (lm_small); decide's margin
+    logsumexp(yes) - logsumexp(no) in fp32, pred = margin > 0       md2fast.py:128-143, 208-212, 233-238, 270-279
+    (the reference runs the nq questions as one batch with nq cache copies of the prefix; rows of a batch are
+    independent, so the restatement runs them one at a time over a single cache)
 Greedy decode (ours; not in the reference snapshot): each step feeds argmax(logits) (torch.argmax: first index among
 equal maxima) at the next position, attending to every cached key (no mask needed: a single query at the end).
 freqs_cis uses theta = 10000 (moondream's value; not present in the snapshot: parity unpinned for theta itself).
@@ -139,16 +144,52 @@ class Text:
         w = self.w
         return F.linear(ln(x_last, w["post_ln.weight"], w["post_ln.bias"]), w["lm_head.weight"], w["lm_head.bias"])
 
-    def prefill(self, img_emb, prompt_ids, return_hidden=False):
+    def encode(self, img_emb):
+        """md2fast.py:201-206: [BOS] + image tokens, mask-free. Returns the prefix hidden states."""
         w = self.w
         x = torch.cat([w["wte"][self.bos:self.bos + 1], img_emb.to(BF)], dim=0)[None]
-        hp = self.layers(x, 0, None)
-        P = x.shape[1]
-        L = prompt_ids.shape[0]
+        self.P = x.shape[1]
+        return self.layers(x, 0, None)
+
+    @staticmethod
+    def prompt_mask(P, L):
+        """md2fast.py:132-136: prompt row i sees every prefix key and prompt keys <= i."""
         m = torch.zeros(L, P + L, dtype=torch.bool)
         m[:, :P] = True
         m[:, P:] = torch.tril(torch.ones(L, L, dtype=torch.bool))
-        xp = self.layers(F.embedding(prompt_ids[None], w["wte"]), P, m[None, None])
+        return m[None, None]
+
+    def query(self, questions, L, yn_ids=None):
+        """md2fast.py:208-212 with set_questions (md2fast.py:233-238): each question zero-padded to L ids; returns
+        (nq, len(yn_ids)) logits of the yes / no rows, or (nq, V) when yn_ids is None. Needs encode() first."""
+        w, P = self.w, self.P
+        out = []
+        for q in questions:
+            ids = torch.zeros(L, dtype=torch.int64)
+            ids[:len(q)] = torch.as_tensor(q, dtype=torch.int64)
+            x = self.layers(F.embedding(ids[None], w["wte"]), P, self.prompt_mask(P, L))
+            h = ln(x[0, len(q) - 1], w["post_ln.weight"], w["post_ln.bias"])
+            if yn_ids is None:
+                out.append(F.linear(h, w["lm_head.weight"], w["lm_head.bias"]))
+            else:
+                idx = torch.as_tensor(yn_ids)
+                out.append(F.linear(h, w["lm_head.weight"][idx], w["lm_head.bias"][idx]))
+        return torch.stack(out)
+
+    @staticmethod
+    def decide(logits, n_yes):
+        """md2fast.py:270-279 on yes/no-row logits: (pred_yes, margin) with margin = logsumexp(yes) -
+        logsumexp(no) in fp32."""
+        lg = logits.float()
+        m = (torch.logsumexp(lg[:n_yes], 0) - torch.logsumexp(lg[n_yes:], 0)).item()
+        return m > 0, m
+
+    def prefill(self, img_emb, prompt_ids, return_hidden=False):
+        w = self.w
+        hp = self.encode(img_emb)
+        P = self.P
+        L = prompt_ids.shape[0]
+        xp = self.layers(F.embedding(prompt_ids[None], w["wte"]), P, self.prompt_mask(P, L))
         self.pos = P + L
         lg = self.logits(xp[0, -1])
         return (lg, hp, xp) if return_hidden else lg

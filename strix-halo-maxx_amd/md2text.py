@@ -1,5 +1,5 @@
 """moondream2 text decoder on the MI355X kernels: prefix prefill (BOS + image tokens, mask-free), masked prompt
-prefill, and batch-1 greedy decode with a contiguous bf16 KV cache.
+prefill, the batched yes/no query, and batch-1 greedy decode with a contiguous bf16 KV cache.
 
 Follows the reference's FastMD2 text path (moondream/gpu/md2fast.py:162-212): the same layer loop
 (LN -> qkv -> rope + KV write -> SDPA -> parallel residual `fc2(gelu(fc1(h))) + (proj(a) + x)`), the same prefix /
@@ -10,6 +10,10 @@ rebuilt for batch-1 HBM streaming:
     the fc2 / proj GEMVs fused with the two residual adds;
   * the LM head GEMV carries the argmax, and the next step's embedding lookup reduces it on the device, so one HIP
     graph replays a whole step with the token and position kept in device memory (no host round trip per token).
+The yes/no query is the reference's own fast path (FastMD2._encode / _query / decide, md2fast.py:201-212, 266-279):
+nq questions share the image prefix, whose K/V the prefix prefill writes into every question's cache slot; the
+questions, zero-padded to L tokens, run as one batch of nq * L rows under the prefix + causal mask; the last real
+token of each question goes through the final LN and the LM head restricted to the yes / no token rows.
 """
 import torch
 
@@ -22,13 +26,18 @@ BOS = 50256  # moondream2's tokenizer bos_id (the Phi / GPT-2 <|endoftext|> id)
 
 
 class TextDecoder:
-    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", ctx=1024, attn_splits=4, w8a8=False):
+    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", ctx=1024, attn_splits=4, w8a8=False, nq=1, L=32,
+                 yes_ids=(), no_ids=()):
         """w8a8: the four text Linears of every layer run the reference's W8A8 path (its default text linear class,
-        HI8Lin, moondream/gpu/bench.py:20) in prefill and decode; the LM head stays bf16 (md2fast.py:115)."""
+        HI8Lin, moondream/gpu/bench.py:20) in prefill and decode; the LM head stays bf16 (md2fast.py:115).
+        nq, L: questions per query and tokens per question (the reference's NQ, L, md2fast.py:71-86); the KV cache
+        holds nq slots (decode uses slot 0). yes_ids / no_ids: the token ids the yes/no head keeps (the reference
+        derives them from its tokenizer, md2fast.py:138-142; there is no tokenizer here, the caller passes them)."""
         c = TXT
         self.dev = torch.device(device)
         self.D, self.H, self.hd, self.eps = c["dim"], c["heads"], c["hd"], c["ln_eps"]
         self.ctx = ctx
+        self.nq, self.L = nq, L
         dev = self.dev
         g = lambda n: weights[n].to(dev, BF).contiguous()
         f32 = lambda n: weights[n].to(dev, torch.float32).contiguous()
@@ -46,19 +55,19 @@ class TextDecoder:
             # fused quantisation equals quantising qkv and fc1 separately)
             wqf = torch.cat([weights[p + "attn.qkv.weight"], weights[p + "mlp.fc1.weight"]]).to(dev, BF).contiguous()
             bqf = torch.cat([weights[p + "attn.qkv.bias"], weights[p + "mlp.fc1.bias"]]).to(dev, torch.float32).contiguous()
-            nq = weights[p + "attn.qkv.weight"].shape[0]
-            blk = dict(ln=(g(p + "ln.weight"), g(p + "ln.bias")), bqf=bqf, nq=nq)
+            nqkv = weights[p + "attn.qkv.weight"].shape[0]
+            blk = dict(ln=(g(p + "ln.weight"), g(p + "ln.bias")), bqf=bqf, nq=nqkv)
             if w8a8:
                 wq, sq = ops.MxI8Lin.quantize_weight(wqf)
                 del wqf
-                blk.update(wqf=wq, sqf=sq, qkv=ops.MxI8Lin.from_quantized(wq[:nq], sq[:nq], bqf[:nq]),
-                           fc1=ops.MxI8Lin.from_quantized(wq[nq:], sq[nq:], bqf[nq:]),
+                blk.update(wqf=wq, sqf=sq, qkv=ops.MxI8Lin.from_quantized(wq[:nqkv], sq[:nqkv], bqf[:nqkv]),
+                           fc1=ops.MxI8Lin.from_quantized(wq[nqkv:], sq[nqkv:], bqf[nqkv:]),
                            proj=ops.MxI8Lin(weights[p + "attn.proj.weight"], weights[p + "attn.proj.bias"], BF, dev),
                            fc2=ops.MxI8Lin(weights[p + "mlp.fc2.weight"], weights[p + "mlp.fc2.bias"], BF, dev))
                 blk["wp"], blk["swp"] = blk["proj"].wq, blk["proj"].sw
                 blk["w2"], blk["sw2"] = blk["fc2"].wq, blk["fc2"].sw
             else:
-                blk.update(wqf=wqf, qkv=lin_cls(wqf[:nq], bqf[:nq], BF), fc1=lin_cls(wqf[nq:], bqf[nq:], BF),
+                blk.update(wqf=wqf, qkv=lin_cls(wqf[:nqkv], bqf[:nqkv], BF), fc1=lin_cls(wqf[nqkv:], bqf[nqkv:], BF),
                            proj=lin_cls(weights[p + "attn.proj.weight"], weights[p + "attn.proj.bias"], BF),
                            fc2=lin_cls(weights[p + "mlp.fc2.weight"], weights[p + "mlp.fc2.bias"], BF))
                 blk["wp"], blk["w2"] = blk["proj"].w, blk["fc2"].w
@@ -67,8 +76,26 @@ class TextDecoder:
         self.post_ln = (g("post_ln.weight"), g("post_ln.bias"))
         self.w_lm, self.b_lm = g("lm_head.weight"), f32("lm_head.bias")
         self.cs = freqs_cis(c["rot"], max(ctx, 2048), c["theta"]).to(dev).contiguous()
-        self.kc = [torch.zeros(1, self.H, ctx, self.hd, device=dev, dtype=BF) for _ in self.blocks]
-        self.vc = [torch.zeros(1, self.H, ctx, self.hd, device=dev, dtype=BF) for _ in self.blocks]
+        self.kc = [torch.zeros(self.nq, self.H, ctx, self.hd, device=dev, dtype=BF) for _ in self.blocks]
+        self.vc = [torch.zeros(self.nq, self.H, ctx, self.hd, device=dev, dtype=BF) for _ in self.blocks]
+        # ---- yes/no query state (md2fast.py:128-143)
+        self.yes_ids, self.no_ids = list(yes_ids), list(no_ids)
+        self.yn_ids = self.yes_ids + self.no_ids
+        self.lm_small = None
+        if self.yn_ids:
+            npad = -(-len(self.yn_ids) // 4) * 4  # the GEMM wants N % 4 == 0: zero rows pad the head
+            wy = torch.zeros(npad, self.D, device=dev, dtype=BF)
+            by = torch.zeros(npad, device=dev, dtype=torch.float32)
+            idx = torch.tensor(self.yn_ids, device=dev)
+            wy[:len(self.yn_ids)] = self.w_lm[idx]
+            by[:len(self.yn_ids)] = self.b_lm[idx]
+            self.lm_small = ops.MxLin(wy, by, BF, dev)
+        self.lm_full = None
+        self.full_logits = False  # True: all V logits (the reference's diagnostics switch, md2fast.py:116)
+        self.tok_buf = torch.zeros(self.nq, self.L, device=dev, dtype=torch.int64)
+        self.last_idx = torch.zeros(self.nq, device=dev, dtype=torch.int64)
+        self.prefix = None
+        self.query_graph = None
         # ---- decode-step device state
         lib = _lib.load()
         self.S = attn_splits
@@ -87,10 +114,12 @@ class TextDecoder:
         self.graph = None
 
     # ------------------------------------------------------------------ prefill (md2fast.py:169-212)
-    def _text_layers(self, x, pos0, causal_from):
-        """x (n, D) bf16 tokens at positions pos0 .. pos0 + n - 1; attends to keys 0 .. pos0 + n - 1 (key j visible
-        to query i iff j < causal_from or j <= pos0 + i; causal_from=None: all)."""
-        n = x.shape[0]
+    def _text_layers(self, x, pos0, causal_from, B=1, bcast=False):
+        """x (B * n, D) bf16: B sequences (cache slots 0 .. B - 1) of n tokens at positions pos0 .. pos0 + n - 1;
+        attends to keys 0 .. pos0 + n - 1 of its own slot (key j visible to query i iff j < causal_from or
+        j <= pos0 + i; causal_from=None: all). bcast (B = 1): the K/V rows go to every cache slot (the shared image
+        prefix, md2fast.py:177 rope_cache(..., bcast=(pos0 == 0)))."""
+        n = x.shape[0] // B
         H, hd = self.H, self.hd
         Tk = pos0 + n
         for i, b in enumerate(self.blocks):
@@ -98,26 +127,109 @@ class TextDecoder:
             # W8A8: the LN output is quantised once for qkv and fc1 (SHARE_QUANT, md2fast.py:52, 174)
             pre = b["qkv"].quant(h) if self.w8a8 else None
             qkv = b["qkv"](h, pre=pre)
-            q = torch.empty(1, H, n, hd, device=self.dev, dtype=BF)
+            q = torch.empty(B, H, n, hd, device=self.dev, dtype=BF)
             call("mx_rope_kv", stream(), qkv.data_ptr(), qkv.stride(0), self.cs.data_ptr(), q.data_ptr(),
-                 self.kc[i].data_ptr(), self.vc[i].data_ptr(), 1, n, H, self.ctx, pos0, 1, 0)
-            a = ops.sdpa(q, self.kc[i][:, :, :Tk], self.vc[i][:, :, :Tk], qpos0=pos0, causal_from=causal_from)
-            r = b["proj"](a.view(n, self.D), res=x)
+                 self.kc[i].data_ptr(), self.vc[i].data_ptr(), B, n, H, self.ctx, pos0, self.nq, int(bcast))
+            a = ops.sdpa(q, self.kc[i][:B, :, :Tk], self.vc[i][:B, :, :Tk], qpos0=pos0, causal_from=causal_from)
+            r = b["proj"](a.view(B * n, self.D), res=x)
             x = b["fc2"](b["fc1"](h, gelu=True, pre=pre), res=r)
         return x
 
     def prefill(self, img_emb, prompt_ids):
         """[BOS] + image tokens (mask-free, md2fast.py:201-206), then the prompt (prefix + causal mask,
         md2fast.py:208-212). Leaves the first generated token's argmax in `part` and returns the prompt's hidden states."""
-        n_img = img_emb.shape[0]
-        x = torch.cat([self.wte[BOS:BOS + 1], img_emb.to(self.dev, BF)], dim=0)
-        self._text_layers(x, 0, None)
-        P = n_img + 1
+        P = self.encode(img_emb)
         xp = self.wte[prompt_ids.to(self.dev)]
         xp = self._text_layers(xp, P, P)
         self.pos_base = P + xp.shape[0]
         self.lm_argmax(xp[-1], logits=True)
         return xp
+
+    def encode(self, img_emb):
+        """Prefix prefill: [BOS] + image tokens, mask-free, K/V into every cache slot (md2fast.py:201-206).
+        Returns the prefix length."""
+        x = torch.cat([self.wte[BOS:BOS + 1], img_emb.to(self.dev, BF)], dim=0)
+        if x.shape[0] + self.L > self.ctx:
+            raise ValueError(f"prefix {x.shape[0]} + L {self.L} exceeds the cache ({self.ctx})")
+        self._text_layers(x, 0, None, bcast=True)
+        self.prefix = x.shape[0]
+        return self.prefix
+
+    # ------------------------------------------------------------------ yes/no query (md2fast.py:208-212, 266-279)
+    def set_questions(self, questions):
+        """questions: nq token-id sequences (each 1 .. L ids, already templated). Zero-pads them to L and records
+        each one's last row (md2fast.py:233-238)."""
+        if len(questions) != self.nq:
+            raise ValueError(f"{len(questions)} questions for nq = {self.nq}")
+        buf = torch.zeros(self.nq, self.L, dtype=torch.int64)
+        last = torch.zeros(self.nq, dtype=torch.int64)
+        for b, q in enumerate(questions):
+            ids = torch.as_tensor(q, dtype=torch.int64).flatten()
+            if not 1 <= ids.numel() <= self.L:
+                raise ValueError(f"question {b}: {ids.numel()} ids, need 1 .. {self.L}")
+            if int(ids.min()) < 0 or int(ids.max()) >= self.V:
+                raise ValueError(f"question {b}: token id outside [0, {self.V})")
+            buf[b, :ids.numel()] = ids
+            last[b] = b * self.L + ids.numel() - 1
+        self.tok_buf.copy_(buf)
+        self.last_idx.copy_(last)
+
+    def _query(self):
+        if self.prefix is None:
+            raise RuntimeError("encode() the image prefix before querying")
+        P = self.prefix
+        x = self.wte[self.tok_buf.view(-1)]                                   # (nq * L, D)
+        x = self._text_layers(x, P, P, B=self.nq)
+        h = ops.layernorm(x.index_select(0, self.last_idx), *self.post_ln, eps=self.eps)  # (nq, D)
+        if self.full_logits:
+            if self.lm_full is None:
+                self.lm_full = ops.MxLin(self.w_lm, self.b_lm, BF, self.dev)  # shares the LM-head storage
+            return self.lm_full(h)
+        if self.lm_small is None:
+            raise RuntimeError("no yes/no ids were given: set full_logits or pass yes_ids / no_ids")
+        return self.lm_small(h)[:, :len(self.yn_ids)]
+
+    def query(self):
+        """(nq, n_yes + n_no) logits of the yes / no rows, or (nq, V) with full_logits; the captured graph when
+        there is one (md2fast.py:262-265)."""
+        if self.query_graph is not None:
+            self.query_graph[0].replay()
+            return self.query_graph[1]
+        return self._query()
+
+    def capture_query(self):
+        """HIP graph of the query for the current prefix length (md2fast.py:238-256): replays read tok_buf /
+        last_idx, so set_questions() between replays changes the questions."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self._query()  # tunes every shape before capture
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = self._query()
+        torch.cuda.synchronize()
+        self.query_graph = (g, out)
+        return g
+
+    def decide(self, logits):
+        """Per question (pred_yes, argmax id or -1, margin), margin = logsumexp(yes) - logsumexp(no) in fp32
+        (md2fast.py:270-279): -1 when only the yes / no rows were computed."""
+        lg = logits.float()
+        if lg.dim() == 1:
+            lg = lg[None]
+        ny = len(self.yes_ids)
+        out = []
+        for r in lg:
+            if r.numel() == len(self.yn_ids):
+                m, am = (torch.logsumexp(r[:ny], 0) - torch.logsumexp(r[ny:], 0)).item(), -1
+            else:
+                m = (torch.logsumexp(r[self.yes_ids], 0) - torch.logsumexp(r[self.no_ids], 0)).item()
+                am = int(r.argmax().item())
+            out.append((m > 0, am, m))
+        return out
 
     def lm_argmax(self, x_row, logits=False):
         call("mx_ln_gemv_argmax", stream(), x_row.data_ptr(), self.post_ln[0].data_ptr(), self.post_ln[1].data_ptr(),

@@ -206,3 +206,65 @@ def test_decoder_full_config_greedy_128(dev):
         assert toks == ref
     else:
         assert n_same >= first_tie
+
+
+YES, NO = [11, 222, 3333, 44444], [55, 666, 7777, 50000]
+
+
+def test_yes_no_query_batched_vs_oracle(dev):
+    """The reference's query (md2fast.py:201-212, 233-238, 270-279): 3 questions of 12, 32 and 1 ids padded to
+    L = 32, one batch of 96 rows over 3 cache slots holding the shared prefix. Yes/no logits and full logits within
+    rel-L2 1e-2 of the oracle per question (2 layers); decide() agrees wherever the oracle's |margin| >= TIE; the
+    yes/no head equals the full head's rows within the GEMM tolerance; the captured query graph replays the eager
+    result exactly, and follows set_questions() between replays."""
+    w = S.text_weights(0, layers=2)
+    fr = S.freqs_cis(32, 2048)
+    ora = ot.Text(w, 1024, fr)
+    dec = mt.TextDecoder(w, ctx=1024, nq=3, L=32, yes_ids=YES, no_ids=NO)
+    img = S.activations(3, (729, 2048), "img")
+    qs = [S.prompt_ids(40 + n, n).tolist() for n in (12, 32, 1)]
+    ora.encode(img)
+    ref = ora.query(qs, 32, YES + NO)
+    reff = ora.query(qs, 32)
+    assert dec.encode(img.to(dev)) == 730
+    dec.set_questions(qs)
+    lg = dec.query().cpu()
+    assert lg.shape == (3, 8)
+    for b in range(3):
+        assert rel(lg[b], ref[b]) <= 1e-2, (b, rel(lg[b], ref[b]))
+    for (p, am, m), b in zip(dec.decide(lg), range(3)):
+        rp, rm = ot.Text.decide(ref[b], len(YES))
+        assert am == -1
+        if abs(rm) >= TIE:
+            assert p == rp, (b, m, rm)
+    dec.full_logits = True
+    lgf = dec.query().cpu()
+    assert lgf.shape == (3, 51200)
+    for b in range(3):
+        assert rel(lgf[b], reff[b]) <= 1e-2, (b, rel(lgf[b], reff[b]))
+        assert rel(lgf[b, YES + NO], lg[b]) <= 5e-3
+    assert [d[1] for d in dec.decide(lgf)] == [int(torch.argmax(r.float())) for r in lgf]
+    dec.full_logits = False
+    dec.capture_query()
+    assert torch.equal(dec.query().cpu(), lg)
+    qs2 = [qs[2], qs[0], S.prompt_ids(77, 20).tolist()]
+    dec.set_questions(qs2)
+    lg2 = dec.query().cpu()
+    dec.query_graph = None
+    assert torch.equal(dec._query().cpu(), lg2)
+    assert torch.equal(lg2[1], lg[0]) or rel(lg2[1], lg[0]) <= 1e-3  # slot-independent up to the tile order
+
+
+def test_query_rejects_bad_questions(dev):
+    w = S.text_weights(0, layers=1)
+    dec = mt.TextDecoder(w, ctx=1024, nq=2, L=8, yes_ids=YES, no_ids=NO)
+    with pytest.raises(ValueError):
+        dec.set_questions([[1, 2]])                 # wrong count
+    with pytest.raises(ValueError):
+        dec.set_questions([[1] * 9, [2]])           # longer than L
+    with pytest.raises(ValueError):
+        dec.set_questions([[], [2]])                # empty
+    with pytest.raises(ValueError):
+        dec.set_questions([[51200], [2]])           # id outside the vocabulary
+    with pytest.raises(RuntimeError):
+        dec.query()                                 # no prefix yet

@@ -224,6 +224,36 @@ def test_text_decode_step_equals_longer_prefill():
     assert toks[0] == int(torch.argmax(lgs[0]))
 
 
+def test_query_padded_rows_equal_unpadded_prefill_fp64():
+    """The yes/no query (md2fast.py:208-212, 233-238): each question zero-padded to L, its last real row through the
+    post-LN and the yes / no rows of the LM head == the fp64 prefill of the unpadded question, restricted to those
+    rows. Reading a padded row, a wrong row order or a dropped prefix key would fail it."""
+    D, H, V, L = 64, 2, 97, 9
+    w = _tiny_text(D, 96, V)
+    fr = S.freqs_cis(32, 256)
+    img = (torch.randn(13, D, generator=gen(21)) * 0.5).to(BF)
+    qs = [torch.randint(0, V, (n,), generator=gen(22 + n)).tolist() for n in (4, 9, 1)]
+    yn = [5, 17, 40, 2]
+    m = ot.Text(w, 64, fr, bos=3, H=H)
+    m.encode(img)
+    lg = m.query(qs, L, yn).double()
+    full = m.query(qs, L).double()
+    for b, q in enumerate(qs):
+        ref = _fp64_text_prefill(w, img, torch.tensor(q), H, fr, 3)
+        assert ((lg[b] - ref[yn]).norm() / ref[yn].norm()) < 2e-2, b
+        assert ((full[b] - ref).norm() / ref.norm()) < 2e-2, b
+        assert torch.equal(full[b][yn], lg[b])  # the small head is the full head's rows
+
+
+def test_decide_margin_closed_form():
+    """decide (md2fast.py:270-279): margin = logsumexp(yes) - logsumexp(no)."""
+    lg = torch.tensor([0.0, math.log(3.0), math.log(2.0)])  # yes: e^0 + e^ln3 = 4; no: 2
+    pred, m = ot.Text.decide(lg, 2)
+    assert pred and abs(m - math.log(2.0)) < 1e-6
+    pred, m = ot.Text.decide(torch.tensor([math.log(2.0), 0.0, math.log(3.0)]), 1)  # 2 vs 1 + 3
+    assert not pred and abs(m - math.log(0.5)) < 1e-6
+
+
 def test_argmax_first_index_on_ties():
     """torch.argmax (the greedy rule) returns the first index among equal maxima; the GPU argmax key does too."""
     v = torch.tensor([0.5, 2.0, -1.0, 2.0, 2.0]).to(BF)
