@@ -13,7 +13,13 @@ reference's own restatements:
   * patch embedding + image_pos_emb, queries appended as rows   step8.py:251-267; preprocess /127.5 - 1 step8.py:379-383
 The query embedding (external embed_queries) is replaced by a linear map of (y, x) / 256: the same stand-in the GPU
 path uses; it is outside the block and not part of the parity claim.
+
+Tracking heads (track_heads): the reference's numpy fp32 restatement of model.heads, step8.py:327-362 (heads_np):
+each head Linear -> LayerNorm -> GELU erf -> Linear -> LayerNorm -> GELU erf -> Linear in fp32; the coordinate
+head's 2n logits read out per half as the expectation of the bin index under softmax(0.5 * logits) * mask, mask =
+|argmax - i| <= 20, renormalised, plus 0.5; the visibility head's output is the visibility logit.
 """
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -131,3 +137,52 @@ class Model:
         self.t += 1
         fin = layernorm(x, self.w["encoder_norm.weight"], self.w["encoder_norm.bias"])
         return (fin, hs) if return_blocks else fin
+
+
+def _head_mlp(x, p):
+    """step8.py:347-355: two (Linear, LayerNorm, erf GELU) stages then a Linear, numpy fp32. p: torch-layout
+    (out, in) weights w0 / w3 / w6, biases, LayerNorm g1 / b1 / g4 / b4 and eps e1 / e4 (nn.Sequential indices)."""
+    erf = lambda a: torch.erf(torch.from_numpy(np.ascontiguousarray(a))).numpy()
+    for lin, ln in ((0, 1), (3, 4)):
+        h = x @ p[f"w{lin}"].T + p[f"b{lin}"]
+        mu = h.mean(-1, keepdims=True)
+        var = ((h - mu) ** 2).mean(-1, keepdims=True)
+        h = (h - mu) / np.sqrt(var + np.float32(p[f"e{ln}"])) * p[f"g{ln}"] + p[f"b{ln}"]
+        x = 0.5 * h * (1.0 + erf(h * np.float32(0.7071067811865476)))
+    return x @ p["w6"].T + p["b6"]
+
+
+def soft_argmax(logits, radius=20):
+    """step8.py:356-361 on (Q, n) fp32 logits: E[i] under softmax(0.5 * logits) masked to |argmax - i| <= radius and
+    renormalised (argmax: first index among equal maxima)."""
+    n = logits.shape[-1]
+    idx = np.arange(n, dtype=np.float32)
+    am = logits.argmax(-1)[:, None]
+    mask = np.abs(am - idx) <= radius
+    z = logits * np.float32(0.5)
+    e = np.exp(z - z.max(-1, keepdims=True))
+    pr = e / e.sum(-1, keepdims=True) * mask
+    pr = pr / pr.sum(-1, keepdims=True)
+    return (pr * idx).sum(-1)
+
+
+def head_params(w, name, eps=1e-5):
+    """numpy fp32 parameters of one head from the weight dict (nn.Sequential indices 0 / 1 / 3 / 4 / 6)."""
+    g = lambda k: w[k].float().numpy()
+    p = {}
+    for i in (0, 3, 6):
+        p[f"w{i}"], p[f"b{i}"] = g(f"{name}.{i}.weight"), g(f"{name}.{i}.bias")
+    for i in (1, 4):
+        p[f"g{i}"], p[f"b{i}"], p[f"e{i}"] = g(f"{name}.{i}.weight"), g(f"{name}.{i}.bias"), eps
+    return p
+
+
+def track_heads(xq, w, eps=1e-5, radius=20):
+    """step8.py:333-362 (heads_np): encoder-normed query rows xq (Q, D) -> tracks (Q, 2) = (half 0, half 1)
+    readouts + 0.5, coordinate logits (Q, 2n), visibility logits (Q,). All numpy fp32."""
+    x = np.asarray(xq.float().numpy() if torch.is_tensor(xq) else xq, np.float32)
+    logits = _head_mlp(x, head_params(w, "coordinate_head", eps))
+    n = logits.shape[-1] // 2
+    tracks = np.stack([soft_argmax(logits[:, :n], radius), soft_argmax(logits[:, n:], radius)], -1) + np.float32(0.5)
+    vis = _head_mlp(x, head_params(w, "visible_head", eps))[:, 0]
+    return tracks, logits, vis

@@ -21,6 +21,8 @@ SIGNATURES = {
     "mx_gemm_check": [I, I, P, L, P, L, P, P, L, P, L, I, I, I, I, I, P, L, P, L],
     "mx_gemm_pick": [I, I, I],
     "mx_gemm_ws_elems": [I, I, I, I],
+    "mx_track_head_blob_elems": [I, I, I],
+    "mx_track_heads": [P, P, L, I, I, I, P, I, F, F, P, F, F, I, P, P, L, P],
     "mx_gemm_ws_counters": [I, I, I, I],
     "mx_gemm_ncfg": [],
     "mx_gemm_cfg_tile": [I, ctypes.POINTER(I), ctypes.POINTER(I)],
@@ -53,7 +55,7 @@ SIGNATURES = {
 STATUS = {0: "ok", -1: "bad config", -2: "unsupported shape/stride", -3: "split-K workspace too small",
           -4: "operand layout/alignment", -5: "HIP launch failed", -6: "null pointer"}
 
-RESTYPE = {"mx_gemm_ws_elems": L, "mx_gemm_ws_counters": L}
+RESTYPE = {"mx_gemm_ws_elems": L, "mx_gemm_ws_counters": L, "mx_track_head_blob_elems": L}
 
 _lib = None
 

@@ -21,7 +21,7 @@ VIS = dict(img=378, patch=14, grid=27, ntok=729, dim=1152, heads=16, hd=72, ff=4
 TXT = dict(dim=2048, heads=32, hd=64, rot=32, ff=8192, layers=24, vocab=51200, ln_eps=1e-5, theta=10000.0, ctx=2048)
 # ---- TAPNext-style TRecViT (tapnext/npu/step8.py:470-488; pack8.py:10)
 TRV = dict(dim=768, heads=12, hd=64, ff_gated=3072, ff_vit=3072, layers=12, img=256, patch=8, n_img=1024, n_q=256,
-           conv_taps=4, rms_eps=1e-6, ln_eps=1e-6)
+           conv_taps=4, rms_eps=1e-6, ln_eps=1e-6, head_hidden=256, head_ln_eps=1e-5, head_radius=20)
 
 
 def _gen(seed, name):
@@ -143,6 +143,16 @@ def trecvit_weights(seed=0, layers=None):
     w["image_pos_emb"] = normal(seed, "image_pos_emb", (1, g * g, D))
     w["query_proj.weight"] = normal(seed, "query_proj.weight", (D, 2))
     w["query_proj.bias"] = normal(seed, "query_proj.bias", (D,))
+    # tracking heads, fp32 (nn.Sequential: 0 Linear, 1 LayerNorm, 2 GELU, 3 Linear, 4 LayerNorm, 5 GELU, 6 Linear);
+    # the coordinate head reads 2 x 256 bins (one per pixel row / column of the 256 x 256 frame)
+    Hh, f32 = c["head_hidden"], torch.float32
+    for hn, no in (("coordinate_head", 2 * c["img"]), ("visible_head", 1)):
+        for i, shape in ((0, (Hh, D)), (3, (Hh, Hh)), (6, (no, Hh))):
+            w[f"{hn}.{i}.weight"] = normal(seed, f"{hn}.{i}.weight", shape, std=0.05, dtype=f32)
+            w[f"{hn}.{i}.bias"] = normal(seed, f"{hn}.{i}.bias", (shape[0],), dtype=f32)
+        for i in (1, 4):
+            w[f"{hn}.{i}.weight"] = 1 + normal(seed, f"{hn}.{i}.weight", (Hh,), std=0.1, dtype=f32)
+            w[f"{hn}.{i}.bias"] = normal(seed, f"{hn}.{i}.bias", (Hh,), std=0.1, dtype=f32)
     return w
 
 

@@ -19,6 +19,9 @@ Kernel mapping (per block, one frame = 1280 tokens):
 Inputs per frame: patch conv 8x8/8 of the /127.5 - 1 normalised frame (patchify kernel + GEMM, position embedding
 added in the epilogue) and 256 query tokens from a linear embedding of the (y, x) coordinates / 256 (a stand-in:
 the real embed_queries lives in the external model and is not part of the block).
+Outputs per frame (model.step's tracks, logits, vis; tapnext/npu/step8.py:327-362): the coordinate and visibility
+heads on the encoder-normed query tokens plus the windowed soft-argmax readout, one fp32 kernel (mx_track_heads)
+at the end of the frame's graph.
 """
 import math
 
@@ -29,6 +32,15 @@ from ._lib import call, ptr, stream
 from .synth import TRV
 
 BF = torch.bfloat16
+
+
+def _head_blob(weights, name, dev):
+    """One head's fp32 weight blob in the kernel's layout: W0^T | b0 | g1 | beta1 | W3^T | b3 | g4 | beta4 | W6^T | b6
+    (nn.Sequential indices: 0 / 3 / 6 Linear, 1 / 4 LayerNorm)."""
+    W = lambda i: weights[f"{name}.{i}.weight"].float()
+    B = lambda i: weights[f"{name}.{i}.bias"].float()
+    parts = [W(0).t(), B(0), W(1), B(1), W(3).t(), B(3), W(4), B(4), W(6).t(), B(6)]
+    return torch.cat([t.contiguous().reshape(-1) for t in parts]).to(dev)
 
 
 def _interleave_rows(w, b):
@@ -84,6 +96,21 @@ class TRecViT:
         self.patch = lin_cls(weights["lin_proj.weight"].reshape(self.D, -1), weights["lin_proj.bias"], BF)
         self.pos = g("image_pos_emb").view(self.n_img, self.D)
         self.qproj = lin_cls(weights["query_proj.weight"], weights["query_proj.bias"], BF)
+        # ---- tracking heads (optional: a weight dict without them yields tokens only)
+        self.has_heads = "coordinate_head.0.weight" in weights
+        if self.has_heads:
+            lib = _lib.load()
+            Hh = weights["coordinate_head.0.weight"].shape[0]
+            self.NOC = weights["coordinate_head.6.weight"].shape[0]
+            self.cblob = _head_blob(weights, "coordinate_head", dev)
+            self.vblob = _head_blob(weights, "visible_head", dev)
+            if (self.cblob.numel() != lib.mx_track_head_blob_elems(self.D, Hh, self.NOC)
+                    or self.vblob.numel() != lib.mx_track_head_blob_elems(self.D, Hh, 1)):
+                raise ValueError("head weights do not match Linear(D, H) / LayerNorm(H) / Linear(H, H) / Linear(H, NO)")
+            self.Hh, self.head_eps, self.radius = Hh, c["head_ln_eps"], c["head_radius"]
+            self.tracks = torch.zeros(self.n_q, 2, device=dev, dtype=torch.float32)
+            self.logits = torch.zeros(self.n_q, self.NOC, device=dev, dtype=torch.float32)
+            self.vis = torch.zeros(self.n_q, device=dev, dtype=torch.float32)
         # ---- streaming state: per block a 4-frame ring of [yg | xx] rows and the fp32 RG-LRU state
         T, D = self.T, self.D
         self.ring = [[torch.zeros(T, 2 * D, device=dev, dtype=BF) for _ in range(4)] for _ in self.blocks]
@@ -142,11 +169,26 @@ class TRecViT:
         x2 = b["oproj"](a.view(B * T, D), res=x1)
         return b["mlp3"](b["mlp0"](ops.layernorm(x2, *b["ln2"], eps=self.ln_eps), act="erf"), res=x2)
 
+    def heads(self, xq, tracks=None, logits=None, vis=None):
+        """model.heads on the encoder-normed query rows xq (Q, D) bf16: tracks (Q, 2) fp32 (first-half / second-half
+        readouts), coordinate logits (Q, NOC) fp32, visibility logits (Q,) fp32 (step8.py:327-362)."""
+        Q = xq.shape[0]
+        tracks = torch.empty(Q, 2, device=self.dev) if tracks is None else tracks
+        logits = torch.empty(Q, self.NOC, device=self.dev) if logits is None else logits
+        vis = torch.empty(Q, device=self.dev) if vis is None else vis
+        e = float(self.head_eps)
+        call("mx_track_heads", stream(), xq.data_ptr(), xq.stride(0), Q, self.D, self.Hh, self.cblob.data_ptr(),
+             self.NOC, e, e, self.vblob.data_ptr(), e, e, self.radius, tracks.data_ptr(), logits.data_ptr(),
+             logits.stride(0), vis.data_ptr())
+        return tracks, logits, vis
+
     def _frame(self, phase):
         x = self.embed(self.img, self.qfeat, self.x0)
         for i in range(len(self.blocks)):
             x = self.block_step(i, x, phase)
         fin = ops.layernorm(x, *self.enc_norm, eps=self.ln_eps)
+        if self.has_heads:
+            self.heads(fin[self.n_img:self.n_img + self.n_q], self.tracks, self.logits, self.vis)
         call("mx_counter_add", stream(), self.frame.data_ptr(), 1)
         return fin
 
@@ -165,6 +207,14 @@ class TRecViT:
             out = self._frame(phase)
         self.t += 1
         return out
+
+    def track(self, frame_u8, qfeat, use_graph=False):
+        """model.step's outputs for one streamed frame (davis_cpu.py:78): (tracks, logits, vis), views of device
+        buffers that the next frame overwrites."""
+        if not self.has_heads:
+            raise RuntimeError("the weights carry no tracking heads")
+        self.step(frame_u8, qfeat, use_graph)
+        return self.tracks, self.logits, self.vis
 
     def capture(self):
         """One HIP graph per ring phase (kernel arguments differ only in which ring slots they read/write)."""

@@ -123,6 +123,18 @@ def test_other_entry_points_refuse_bad_shapes():
                            A16, 768, 1280, 700) == -2                                 # C not a multiple of 64
     assert lib.mx_rglru_scan(None, A16, A16, A16, 4, 1280, 700, A16, 1536, 0, A16, 768, 0) == -2
     assert lib.mx_counter_add(None, None, 1) == -6
+    # tracking heads
+    assert lib.mx_track_head_blob_elems(768, 256, 512) == 768 * 256 + 6 * 256 + 256 * 256 + 256 * 512 + 512
+    hd = lambda **kw: lib.mx_track_heads(*(lambda a: (a.update(kw), list(a.values()))[1])(dict(
+        st=None, x=A16, ldx=768, Q=256, D=768, H=256, cb=A16, NOC=512, ce0=1e-5, ce1=1e-5, vb=A16, ve0=1e-5,
+        ve1=1e-5, radius=20, tr=A16, lg=A16, ldl=512, vis=A16)))
+    assert hd(H=257) == -2             # more hidden units than threads
+    assert hd(NOC=511) == -2           # odd coordinate logits
+    assert hd(NOC=1026, ldl=1026) == -2  # 513 bins per half
+    assert hd(ldl=500) == -2
+    assert hd(radius=-1) == -2
+    assert hd(vb=None) == -6
+    assert hd(Q=0, x=None) == 0        # nothing to do
     # W8A8
     assert lib.mx_quant_rows_i8(None, A16, 2048, A16, 2048, A16, 4, 2044) == -2                 # K % 8
     assert lib.mx_quant_rows_i8(None, A16 + 8, 2048, A16, 2048, A16, 4, 2048) == -4             # x not 16-byte aligned

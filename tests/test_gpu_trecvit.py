@@ -6,6 +6,7 @@ restatement); block hidden states rel-L2 <= 1e-2 per block and frame; 12-block s
 The SSM kernel inputs follow the reference's own directed SSM test (tapnext/npu/run8.py:316-327): y, x and the three
 history frames ~ N(0, 1) bf16, h0 ~ N(0, 1) fp32, conv_w N(0, 0.3), conv_b N(0, 0.1), a_param U(-3, 0.5),
 Wx / Wa N(0, 0.15) (12, 64, 64), bx / ba N(0, 0.3)."""
+import numpy as np
 import pytest
 import torch
 
@@ -156,6 +157,39 @@ def _qfeat(n=256):
     return (q[:, 1:] / 256.0).to(BF)
 
 
+def _check_heads(tr, lg, vis, ref, tol_logit=2e-4, tol_track=2e-3):
+    """GPU heads vs the oracle's on the same input rows: logits / vis within tol_logit (fp32, different summation
+    order); tracks within tol_track wherever the oracle's argmax is unambiguous (top-2 gap >= 1e-3)."""
+    rtr, rlg, rvis = ref
+    tr, lg, vis = tr.cpu().numpy(), lg.cpu().numpy(), vis.cpu().numpy()
+    assert np.abs(lg - rlg).max() <= tol_logit, np.abs(lg - rlg).max()
+    assert np.abs(vis - rvis).max() <= tol_logit
+    n = rlg.shape[1] // 2
+    checked = 0
+    for half in range(2):
+        top2 = -np.sort(-rlg[:, half * n:(half + 1) * n], axis=1)[:, :2]
+        ok = (top2[:, 0] - top2[:, 1]) >= 1e-3
+        checked += ok.sum()
+        assert np.abs(tr[ok, half] - rtr[ok, half]).max() <= tol_track
+    assert checked >= len(tr)  # most rows are unambiguous
+
+
+def test_track_heads_kernel_vs_oracle(dev):
+    """mx_track_heads on 257 rows (an odd count: the last workgroup holds one row) of encoder-normed-like bf16
+    tokens vs oracle.track_heads (step8.py:327-362)."""
+    w = S.trecvit_weights(0, layers=1)
+    m = tv.TRecViT(w, device=dev)
+    x = torch.randn(257, 768, generator=torch.Generator().manual_seed(7)).to(BF)
+    xd = x.to(dev)
+    tr, lg, vis = m.heads(xd)
+    _check_heads(tr, lg, vis, otr.track_heads(x, w))
+    # a strided view (every other row of a wider buffer) reads the same rows
+    wide = torch.zeros(257, 2 * 768, device=dev, dtype=BF)
+    wide[:, 768:] = xd
+    tr2, lg2, vis2 = m.heads(wide[:, 768:])
+    assert torch.equal(lg2, lg) and torch.equal(tr2, tr) and torch.equal(vis2, vis)
+
+
 def test_one_block_two_frames(dev):
     w = S.trecvit_weights(0, layers=1)
     frames = S.frames_u8(1, 2)
@@ -170,6 +204,8 @@ def test_one_block_two_frames(dev):
         print(f"frame {t}: block rel {rel(fin, fin_ref):.2e}", flush=True)
         assert rel(fin, fin_ref) <= 1e-2
         assert (m.h[0].cpu() - ora.h[0]).abs().max().item() <= 1e-2
+        # the heads launched at the end of the frame, on the frame's own query rows
+        _check_heads(m.tracks, m.logits, m.vis, otr.track_heads(fin[1024:].cpu(), w))
 
 
 def test_twelve_blocks_streamed_graph_and_clip(dev):

@@ -429,6 +429,49 @@ def test_trecvit_block_first_frame_vs_fp64():
 
 
 # ---------------------------------------------------------------------------------------------- synthetic inputs
+def test_soft_argmax_closed_forms():
+    """step8.py:356-361: a lone peak reads out its own bin; two bins a, b inside the window weigh as
+    sigmoid(0.5 (a - b)) (temperature 0.5); bins beyond +-20 of the argmax are ignored; equal maxima take the first
+    index's window; a window clipped at the border averages what is left."""
+    n = 256
+    lg = np.zeros((1, n), np.float32)
+    lg[0, 37] = 80.0
+    assert abs(otr.soft_argmax(lg)[0] - 37.0) < 1e-4
+    lg = np.full((1, n), -1e4, np.float32)
+    lg[0, 100], lg[0, 110] = 3.0, 1.0
+    p = 1.0 / (1.0 + math.exp(-0.5 * 2.0))
+    assert abs(otr.soft_argmax(lg)[0] - (100 * p + 110 * (1 - p))) < 1e-3
+    lg[0, 130] = 2.9   # 30 bins from the argmax: masked out
+    assert abs(otr.soft_argmax(lg)[0] - (100 * p + 110 * (1 - p))) < 1e-3
+    lg = np.zeros((1, n), np.float32)  # all equal: argmax 0, window [0, 20], uniform
+    assert abs(otr.soft_argmax(lg)[0] - 10.0) < 1e-4
+    lg[0, 200] = lg[0, 250] = 5.0      # equal maxima: the first one's window [180, 220]
+    e = np.exp(np.float32(0.5) * lg[0, 180:221].astype(np.float64))
+    assert abs(otr.soft_argmax(lg)[0] - (np.arange(180, 221) * e).sum() / e.sum()) < 1e-3
+
+
+def test_track_heads_mlp_vs_fp64():
+    """The head MLP (Linear -> LayerNorm -> erf GELU, twice, -> Linear) against torch fp64 with F.layer_norm and the
+    exact erf GELU; the tanh GELU or a LayerNorm without its affine differ by far more than the bound."""
+    w = S.trecvit_weights(0, layers=1)
+    x = torch.randn(5, 768, generator=gen(31)).to(BF)
+    tr, lg, vis = otr.track_heads(x, w)
+    wd = {k: v.double() for k, v in w.items() if "head" in k}
+
+    def mlp(h, name, approx="none"):
+        for lin, ln in ((0, 1), (3, 4)):
+            h = F.linear(h, wd[f"{name}.{lin}.weight"], wd[f"{name}.{lin}.bias"])
+            h = F.layer_norm(h, (h.shape[-1],), wd[f"{name}.{ln}.weight"], wd[f"{name}.{ln}.bias"], 1e-5)
+            h = F.gelu(h, approximate=approx)
+        return F.linear(h, wd[f"{name}.6.weight"], wd[f"{name}.6.bias"])
+    ref = mlp(x.double(), "coordinate_head")
+    assert np.abs(lg - ref.numpy()).max() < 2e-5  # fp32 vs fp64: measured 1.4e-6
+    assert np.abs(vis - mlp(x.double(), "visible_head")[:, 0].numpy()).max() < 2e-5
+    assert np.abs(mlp(x.double(), "coordinate_head", "tanh").numpy() - ref.numpy()).max() > 2e-4  # 6e-4
+    n = lg.shape[1] // 2
+    assert np.allclose(tr[:, 0], otr.soft_argmax(lg[:, :n]) + 0.5) and np.allclose(tr[:, 1], otr.soft_argmax(lg[:, n:]) + 0.5)
+
+
 def test_synth_is_seeded_per_tensor():
     """A subset of a model gets exactly the tensors the full model would get (per-name seeds)."""
     a = S.vision_weights(0, layers=1)
