@@ -111,6 +111,11 @@ int mx_rmsnorm(hipStream_t st, const uint16_t* X, long ldx, const uint16_t* sc1,
  * mode 0: moondream2 normalisation (md2fast.py:148-149); mode 1: TRecViT /127.5 - 1 (tapnext/npu/step8.py:379-383).
  * Replaces the torch permute/div/sub/reshape at md2fast.py:148-149 and the CPU conv input of step8.py:256. */
 int mx_patchify_u8(hipStream_t st, const uint8_t* img, uint16_t* out, long ldo, int B, int S, int P, int mode);
+/* TRecViT preprocess fused with the patch rows: (B, Hs, Ws, 3) u8 frames -> bilinear resize to S x S
+ * (align_corners = False, fp32 pixel values) -> x / 127.5 - 1 -> bf16 rows as mx_patchify_u8 mode 1. Replaces
+ * preprocess (F.interpolate + normalisation, tapnext/npu/step8.py:379-383) and the conv input of step8.py:256. */
+int mx_resize_patchify_u8(hipStream_t st, const uint8_t* img, int Hs, int Ws, uint16_t* out, long ldo, int B, int S,
+                          int P);
 
 /* ============================================================================================ text decoder
  * Partial rotary (dims 0..31) of q and k from fused qkv rows at positions pos0.., q -> q_out [B][H][n][64], rotated k

@@ -10,7 +10,9 @@ reference's own restatements:
                                     zero conv history and h = gated x (step8.py:232-233, cpuemu.py:41-42)
   * gated MLP gate/up split         r6/capture.py:66-69 (`gate, up = ffw_up(x).chunk(2)`)
   * attention: in_proj -> q, k, v heads -> softmax(q k^T / 8) v -> out_proj   r6/capture.py:78-84, pack8.py:10
-  * patch embedding + image_pos_emb, queries appended as rows   step8.py:251-267; preprocess /127.5 - 1 step8.py:379-383
+  * patch embedding + image_pos_emb, queries appended as rows   step8.py:251-267
+  * preprocess: bilinear resize to 256 (F.interpolate, align_corners=False, on fp32 pixel values), / 127.5 - 1,
+    fp32 until the bf16 conv input                                step8.py:379-383, :256
 The query embedding (external embed_queries) is replaced by a linear map of (y, x) / 256: the same stand-in the GPU
 path uses; it is outside the block and not part of the parity claim.
 
@@ -29,6 +31,14 @@ BF = torch.bfloat16
 def f(v):
     """round to bf16 and back to fp32"""
     return v.to(BF).float()
+
+
+def preprocess(frames_u8, res=256):
+    """step8.py:379-383: (F, H, W, 3) uint8 -> (F, res, res, 3) fp32 in [-1, 1]: channels-last float pixels,
+    bilinear resize (align_corners=False), then / 127.5 - 1."""
+    t = frames_u8.permute(0, 3, 1, 2).float()
+    t = F.interpolate(t, size=(res, res), mode="bilinear", align_corners=False)
+    return (t / 127.5 - 1.0).permute(0, 2, 3, 1).contiguous()
 
 
 def rmsnorm(x, scale, eps=1e-6):
@@ -92,7 +102,7 @@ class Model:
 
     def embed(self, frame_u8, qfeat):
         w = self.w
-        x = frame_u8.permute(2, 0, 1)[None].float() / 127.5 - 1.0
+        x = preprocess(frame_u8[None])[0].permute(2, 0, 1)[None]
         x = F.conv2d(x.to(BF), w["lin_proj.weight"], w["lin_proj.bias"], stride=w["lin_proj.weight"].shape[-1])
         x = x[0].flatten(1).transpose(0, 1) + w["image_pos_emb"][0]
         q = F.linear(qfeat.to(BF), w["query_proj.weight"], w["query_proj.bias"])

@@ -474,6 +474,18 @@ def patchify(img_u8, patch, mode, ldo=None, out=None):
     return y
 
 
+def resize_patchify(img_u8, size, patch, ldo=None, out=None):
+    """(B, Hs, Ws, 3) u8 -> bilinear resize to size x size, / 127.5 - 1, as (B * (size/P)^2, ldo) bf16 patch rows
+    (the TRecViT preprocess, tapnext/npu/step8.py:379-383, fused with the patch-conv input)."""
+    B, Hs, Ws, _ = img_u8.shape
+    K = 3 * patch * patch
+    ldo = (K + 7) // 8 * 8 if ldo is None else ldo
+    G = size // patch
+    y = out if out is not None else torch.empty(B * G * G, ldo, device=img_u8.device, dtype=BF)
+    call("mx_resize_patchify_u8", stream(), img_u8.data_ptr(), Hs, Ws, y.data_ptr(), ldo, B, size, patch)
+    return y
+
+
 def gemm_tile(cfg):
     import ctypes
     bm, bn = ctypes.c_int(), ctypes.c_int()

@@ -16,8 +16,9 @@ Kernel mapping (per block, one frame = 1280 tokens):
     -> GEMM out (+x) -> RMSNorm -> GEMM up with the gated-GELU epilogue (weight rows interleaved gate/up at load
     time) -> GEMM down (+res) -> LN -> GEMM qkv -> fused SDPA -> GEMM out_proj (+x1) -> LN -> GEMM mlp0 (GELU erf)
     -> GEMM mlp3 (+x2). A frame is one HIP graph per ring phase (4 graphs), with the frame counter in device memory.
-Inputs per frame: patch conv 8x8/8 of the /127.5 - 1 normalised frame (patchify kernel + GEMM, position embedding
-added in the epilogue) and 256 query tokens from a linear embedding of the (y, x) coordinates / 256 (a stand-in:
+Inputs per frame: patch conv 8x8/8 of the frame resized to 256 x 256 (bilinear) and normalised by /127.5 - 1
+(one resize + patchify kernel, or the plain patchify kernel for a frame already at 256, then a GEMM with the
+position embedding added in the epilogue) and 256 query tokens from a linear embedding of the (y, x) coordinates / 256 (a stand-in:
 the real embed_queries lives in the external model and is not part of the block).
 Outputs per frame (model.step's tracks, logits, vis; tapnext/npu/step8.py:327-362): the coordinate and visibility
 heads on the encoder-normed query tokens plus the windowed soft-argmax readout, one fp32 kernel (mx_track_heads)
@@ -136,7 +137,11 @@ class TRecViT:
 
     # ------------------------------------------------------------------ per-frame input (X0)
     def embed(self, img_u8, qfeat, out):
-        a = ops.patchify(img_u8[None], self.P, mode=1, ldo=self.patch.K)
+        S = self.G * self.P
+        if img_u8.shape[0] == S and img_u8.shape[1] == S:  # already at the model's size: the resize is the identity
+            a = ops.patchify(img_u8[None], self.P, mode=1, ldo=self.patch.K)
+        else:
+            a = ops.resize_patchify(img_u8[None], S, self.P, ldo=self.patch.K)
         self.patch(a, res=self.pos, out=out[:self.n_img])
         self.qproj(qfeat, out=out[self.n_img:self.n_img + qfeat.shape[0]])
         return out
@@ -193,8 +198,13 @@ class TRecViT:
         return fin
 
     def step(self, frame_u8, qfeat, use_graph=False):
-        """One streamed frame: frame_u8 (256, 256, 3) uint8, qfeat (n_q, 2) -> encoder-normed tokens (T, D).
-        The RG-LRU state and conv history advance (model.step)."""
+        """One streamed frame: frame_u8 (H, W, 3) uint8 (resized to 256 x 256 on the device), qfeat (n_q, 2) ->
+        encoder-normed tokens (T, D). The RG-LRU state and conv history advance (model.step)."""
+        if self.img.shape != frame_u8.shape:  # a new frame size: new input buffer, and the graphs read the old one
+            if frame_u8.dim() != 3 or frame_u8.shape[2] != 3:
+                raise ValueError("frames are (H, W, 3) uint8")
+            self.img = torch.zeros(frame_u8.shape, device=self.dev, dtype=torch.uint8)
+            self.graphs = {}
         self.img.copy_(frame_u8, non_blocking=True)
         self.qfeat.copy_(qfeat, non_blocking=True)
         phase = self.t % 4
@@ -235,7 +245,8 @@ class TRecViT:
 
     def forward_clip(self, frames_u8, qfeat):
         """F frames at once through every block (GEMMs with M = F x T rows, attention batched over frames, the RG-LRU
-        as a time scan). frames_u8 (F, 256, 256, 3); returns (F, T, D). Continues from the stacked history / state."""
+        as a time scan). frames_u8 (F, H, W, 3) (resized to 256 x 256 on the device); returns (F, T, D). Continues
+        from the stacked history / state."""
         F, T, D = frames_u8.shape[0], self.T, self.D
         x = torch.empty(F, T, D, device=self.dev, dtype=BF)
         for f in range(F):

@@ -110,6 +110,10 @@ def test_other_entry_points_refuse_bad_shapes():
     assert lib.mx_layernorm(None, A16, 1152, A16, A16, A16, 1152, 729, 1150, 1e-5) == -2
     assert lib.mx_rmsnorm(None, A16 + 4, 768, A16, A16, 768, 10, 768, 1e-6) == -4
     assert lib.mx_patchify_u8(None, A16, A16, 500, 1, 378, 14, 0) == -2          # ldo < 588
+    assert lib.mx_resize_patchify_u8(None, A16, 480, 854, A16, 190, 1, 256, 8) == -2  # ldo < 192
+    assert lib.mx_resize_patchify_u8(None, A16, 0, 854, A16, 192, 1, 256, 8) == -2    # empty source
+    assert lib.mx_resize_patchify_u8(None, A16, 480, 854, A16, 192, 1, 250, 8) == -2  # S % P
+    assert lib.mx_resize_patchify_u8(None, None, 480, 854, A16, 192, 1, 256, 8) == -6
     assert lib.mx_rope_kv(None, A16, 6144, A16, A16, A16, A16, 1, 100, 32, 1024, 1000, 1, 0) == -2  # pos past ctx
     assert lib.mx_ln_gemv2(None, A16, A16, A16, 1e-5, A16, 2048, A16, 100, 3000, 50, A16, A16, 1) == -2  # K
     assert lib.mx_ln_gemv_argmax(None, A16, A16, A16, 1e-5, A16, 2048, A16, 51200, 2048, None, A16, 10) == -3

@@ -190,6 +190,25 @@ def test_track_heads_kernel_vs_oracle(dev):
     assert torch.equal(lg2, lg) and torch.equal(tr2, tr) and torch.equal(vis2, vis)
 
 
+@pytest.mark.parametrize("hw", [(480, 854), (300, 200), (256, 256), (128, 96), (1, 1), (257, 255)])
+def test_resize_patchify_vs_oracle(dev, hw):
+    """mx_resize_patchify_u8 vs the oracle's preprocess (F.interpolate bilinear + / 127.5 - 1, step8.py:379-383)
+    rounded to bf16 and laid out as (c, ky, kx) patch rows: identical except where the two fp32 tap sums differ in
+    their last bit and that flips the bf16 rounding (at most 1 bf16 ulp, on at most 0.1 % of the elements)."""
+    H, W = hw
+    img = torch.randint(0, 256, (2, H, W, 3), generator=torch.Generator().manual_seed(H * 1000 + W), dtype=torch.uint8)
+    ref = otr.preprocess(img).to(BF)                                   # (2, 256, 256, 3)
+    ref = ref.view(2, 32, 8, 32, 8, 3).permute(0, 1, 3, 5, 2, 4).reshape(2 * 1024, 192)
+    out = ops.resize_patchify(img.to(dev), 256, 8, ldo=200).cpu()
+    assert torch.count_nonzero(out[:, 192:]) == 0
+    out = out[:, :192]
+    diff = (out.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert diff.max().item() <= 1
+    assert (diff > 0).float().mean().item() <= 1e-3
+    if H == W == 256:  # the identity resize equals the plain patchify kernel bit for bit
+        assert torch.equal(out, ops.patchify(img.to(dev), 8, mode=1, ldo=192).cpu())
+
+
 def test_one_block_two_frames(dev):
     w = S.trecvit_weights(0, layers=1)
     frames = S.frames_u8(1, 2)
@@ -206,6 +225,25 @@ def test_one_block_two_frames(dev):
         assert (m.h[0].cpu() - ora.h[0]).abs().max().item() <= 1e-2
         # the heads launched at the end of the frame, on the frame's own query rows
         _check_heads(m.tracks, m.logits, m.vis, otr.track_heads(fin[1024:].cpu(), w))
+
+
+def test_one_block_480p_frames_resized_on_device(dev):
+    """DAVIS-sized (480 x 854) frames resized on the device inside the step (and inside its graph) vs the oracle's
+    preprocess + block; then a switch back to 256 x 256 frames re-captures."""
+    w = S.trecvit_weights(0, layers=1)
+    frames = torch.randint(0, 256, (3, 480, 854, 3), generator=torch.Generator().manual_seed(9), dtype=torch.uint8)
+    qf = _qfeat()
+    ora = otr.Model(w)
+    m = tv.TRecViT(w, device=dev)
+    m.reset()
+    for t in range(3):
+        fin_ref = ora.step(frames[t], qf)
+        fin = m.step(frames[t].to(dev), qf.to(dev), use_graph=t > 0)
+        assert rel(fin, fin_ref) <= 1e-2, (t, rel(fin, fin_ref))
+    small = S.frames_u8(1, 1)[0]
+    fin_ref = ora.step(small, qf)
+    fin = m.step(small.to(dev), qf.to(dev), use_graph=True)
+    assert rel(fin, fin_ref) <= 1e-2
 
 
 def test_twelve_blocks_streamed_graph_and_clip(dev):

@@ -429,6 +429,33 @@ def test_trecvit_block_first_frame_vs_fp64():
 
 
 # ---------------------------------------------------------------------------------------------- synthetic inputs
+def test_preprocess_bilinear_closed_forms():
+    """step8.py:379-383 (F.interpolate bilinear, align_corners=False, then / 127.5 - 1): a 2x downscale averages
+    each 2 x 2 block exactly; the same size is the identity; a linear ramp stays linear inside the frame (source
+    coordinate scale (d + 0.5) - 0.5); an upscale clamps the first source coordinate at 0."""
+    img = torch.randint(0, 256, (1, 512, 512, 3), generator=gen(41), dtype=torch.uint8)
+    out = otr.preprocess(img)
+    blk = img.double().view(1, 256, 2, 256, 2, 3).mean(dim=(2, 4))
+    assert torch.equal(out.double(), (blk.float() / 127.5 - 1.0).double())
+    img = torch.randint(0, 256, (1, 256, 256, 3), generator=gen(42), dtype=torch.uint8)
+    assert torch.equal(otr.preprocess(img), img.float() / 127.5 - 1.0)
+    W = 480
+    ramp = (torch.arange(W) // 2).to(torch.uint8)        # 0, 0, 1, 1, ... : linear within pairs
+    img = ramp[None, None, :, None].expand(1, 8, W, 3).contiguous()
+    raw = (otr.preprocess(img).double() + 1.0) * 127.5
+    for d in (10, 100, 200):
+        s = 1.875 * (d + 0.5) - 0.5                      # W / 256 = 1.875
+        i0 = int(math.floor(s))
+        ref = (1 - (s - i0)) * (i0 // 2) + (s - i0) * ((i0 + 1) // 2)
+        assert abs(raw[0, 3, d, 0].item() - ref) < 1e-4
+    img = torch.randint(0, 256, (1, 128, 128, 3), generator=gen(43), dtype=torch.uint8)
+    up = (otr.preprocess(img).double() + 1.0) * 127.5
+    assert abs(up[0, 0, 0, 0].item() - img[0, 0, 0, 0].item()) < 1e-4    # d = 0: s = -0.25 -> 0
+    s = 0.5 * 1.5 - 0.5                                                     # d = 1: s = 0.25
+    ref = (1 - s) * img[0, 0, 0, 1].item() + s * img[0, 0, 1, 1].item()
+    assert abs(up[0, 0, 1, 1].item() - ref) < 1e-3
+
+
 def test_soft_argmax_closed_forms():
     """step8.py:356-361: a lone peak reads out its own bin; two bins a, b inside the window weigh as
     sigmoid(0.5 (a - b)) (temperature 0.5); bins beyond +-20 of the argmax are ignored; equal maxima take the first
