@@ -171,6 +171,17 @@ int mx_ssm_step(hipStream_t st, const uint16_t* x0, const uint16_t* x1, const ui
                 long ld_x, const uint16_t* yg, long ld_y, const uint16_t* conv_w, const uint16_t* conv_b,
                 const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT, const uint16_t* ba, const uint16_t* sp,
                 const int* frame, float* h, uint16_t* z, long ld_z, int T, int C);
+/* The same step for a moving crop of patch tokens with the state indexed by absolute patch (the shifted crop of
+ * tapnext/crop-study/crop_study.py:147-185, CropTracker(shift=True)): x0 / yg / z hold the launch's T tokens; h, the
+ * history taps x1..x3 (stride ld_x) and xsave (this frame's history slot, stride ld_save, receives x0) are addressed
+ * at state row rows[t] (distinct rows < srows). stamps [2][srows] {frame entered, last frame present} (set to
+ * {-8, -8} at a video start) replace the reference's zero-then-write of the state buffers: a row absent on the
+ * previous frame starts from zero state, history tap k is used only if the row was present since frame t - k. */
+int mx_ssm_step_rows(hipStream_t st, const uint16_t* x0, const uint16_t* x1, const uint16_t* x2, const uint16_t* x3,
+                     long ld_x, const uint16_t* yg, long ld_y, const uint16_t* conv_w, const uint16_t* conv_b,
+                     const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT, const uint16_t* ba,
+                     const uint16_t* sp, const int* frame, float* h, uint16_t* z, long ld_z, int T, int C,
+                     const int* rows, int* stamps, int srows, uint16_t* xsave, long ld_save);
 /* Clip form of the same recurrence: per-frame affine maps h -> A h + B for F frames (x_stack = 3 history frames then
  * the F frames, frame stride fs_x), then the time scan. No reference counterpart (the reference only streams):
  * a frame-parallel restatement of the same recurrence. */

@@ -149,6 +149,53 @@ class Model:
         return (fin, hs) if return_blocks else fin
 
 
+class CropModel(Model):
+    """crop_study.py:147-185 (CropTracker, shift=True) on the restated block: per block, the RG-LRU state and the
+    3-frame conv history of the image tokens live in buffers indexed by absolute patch (grid x grid rows); a frame
+    runs the block on the n x n crop's tokens (their patch embedding + their slice of the position embedding) and the
+    queries, with the state rows of those patches (crop_study.py:162-176), then zeroes every patch row and writes
+    back the crop's new state (crop_study.py:178-182). The first frame of the video runs without state."""
+
+    def __init__(self, w, H=12, grid=32):
+        self.grid = grid
+        super().__init__(w, H)
+
+    def reset(self):
+        super().reset()
+        G2 = self.grid * self.grid
+        D = self.w["encoder_norm.weight"].shape[0]
+        self.lru = [torch.zeros(G2, D) for _ in range(self.n)]
+        self.conv = [[torch.zeros(G2, D, dtype=BF) for _ in range(3)] for _ in range(self.n)]  # x_{t-1..t-3}
+        self.qs = [None] * self.n  # the query tokens' (h, history), kept by query slot
+
+    def crop_rows(self, r0, c0, n):
+        ar = torch.arange(n)
+        return ((r0 + ar)[:, None] * self.grid + (c0 + ar)[None]).flatten()
+
+    def step_crop(self, frame_u8, qfeat, r0, c0, n):
+        idx = self.crop_rows(r0, c0, n)
+        G2, hw = self.grid * self.grid, n * n
+        xf = self.embed(frame_u8, qfeat)       # a patch's embedding depends on its own pixels only
+        x = torch.cat([xf[idx], xf[G2:]])
+        first = self.t == 0
+        for i in range(self.n):
+            if first:
+                self.hist[i], self.h[i] = None, None
+            else:
+                qh, qhist = self.qs[i]
+                self.h[i] = torch.cat([self.lru[i][idx], qh])
+                self.hist[i] = [torch.cat([self.conv[i][k][idx], qhist[k]]) for k in range(3)]
+            x = self.block(i, x)
+            self.lru[i].zero_()                 # tokens outside the crop lose their state
+            for k in range(3):
+                self.conv[i][k].zero_()
+                self.conv[i][k][idx] = self.hist[i][k][:hw]
+            self.lru[i][idx] = self.h[i][:hw]
+            self.qs[i] = (self.h[i][hw:], [hk[hw:] for hk in self.hist[i]])
+        self.t += 1
+        return layernorm(x, self.w["encoder_norm.weight"], self.w["encoder_norm.bias"])
+
+
 def _head_mlp(x, p):
     """step8.py:347-355: two (Linear, LayerNorm, erf GELU) stages then a Linear, numpy fp32. p: torch-layout
     (out, in) weights w0 / w3 / w6, biases, LayerNorm g1 / b1 / g4 / b4 and eps e1 / e4 (nn.Sequential indices)."""

@@ -17,6 +17,13 @@
 //                then the scan composes the maps along time with a 64-lane wave scan (one lane per frame, shuffle
 //                steps 1, 2, 4, .., 32) and writes z for every frame. Same h as the streamed loop up to fp32
 //                reassociation.
+// Crop form (mx_ssm_step_rows, one streamed frame of a moving crop of patch tokens): token t's state lives in row
+// rows[t] of the absolute state buffers (h, the history taps, the 32 x 32 patch grid + query rows), so the state
+// moves with the image content and nothing is copied. Tokens that leave the crop drop their state and tokens that
+// enter start from zero: per state row, a stamp (frame it entered the crop, last frame it was in the crop), double
+// buffered by frame parity (read the previous frame's buffer, write this frame's), decides which state the row
+// still has: h0 only if it was in the crop on the previous frame, history tap k only if it has been in the crop
+// without a gap since frame t - k. The current frame's conv input is saved to its absolute row for later frames.
 // Tile: a workgroup owns 64 tokens x one 64-channel head of one frame; the conv output tile is staged in LDS as the
 // MFMA row operand; the gate weights are pre-transposed [head][out][in] so both operands are 16-byte lane reads; the
 // MFMA result layout (lane = output channel, registers = tokens) makes the elementwise tail coalesced along channels.
@@ -43,7 +50,18 @@ struct SsmArgs {
   uint16_t* z; long ld_z; long fs_z;
   float* A; float* B; long fs_ab;  // prep form outputs [F][T][C]
   int T, C, mode;          // mode 0 = step, 1 = prep
+  // crop form (rows != nullptr): token -> state row; stamps [2][srows] {entered, last present}; xsave: this frame's
+  // ring slot (absolute rows, stride ld_save) that receives the current conv input
+  const int* rows; int2* stamps; int srows; uint16_t* xsave; long ld_save;
 };
+
+// The crop form's view of one state row at frame tnow: fresh = not in the crop on frame tnow - 1; enter = frame it
+// entered the crop (tnow when fresh).
+__device__ __forceinline__ void row_stamp(const SsmArgs& p, int row, int tnow, bool& fresh, int& enter) {
+  const int2 s = p.stamps[((tnow - 1) & 1) * p.srows + row];
+  fresh = s.y != tnow - 1;
+  enter = fresh ? tnow : s.x;
+}
 
 __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[64 * XS];
@@ -51,7 +69,8 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   const int lr = lane & 31, hk = lane >> 5;
   const int t0 = blockIdx.x * 64, q = blockIdx.y, f = blockIdx.z;
   const int c0 = q * 64;
-  const bool first = (*p.frame + f) == 0;
+  const int tnow = *p.frame + f;
+  const bool first = tnow == 0;
 
   // ---- temporal conv of this 64 x 64 tile into LDS (8 channels per item, 2 items per thread)
 #pragma unroll
@@ -59,12 +78,25 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
     const int ch = tid + 256 * it;
     const int tok = ch >> 3, cc = (ch & 7) * 8;
     const int token = min(t0 + tok, p.T - 1);
+    const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;  // clamped: never out of bounds
+    int ntap = first ? 1 : 4;  // taps 0 .. ntap - 1 carry data; the older ones are zero
+    int enter = tnow;
+    if (p.rows && !first) {
+      bool fresh;
+      row_stamp(p, row, tnow, fresh, enter);
+      ntap = fresh ? 1 : min(4, tnow - enter + 1);  // tap k (frame tnow - k) needs enter <= tnow - k
+    }
     u32x4 xv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (i == 0 || !first) v = *reinterpret_cast<const u32x4*>(p.tap[i] + f * p.fs_x + (long)token * p.ld_x + c0 + cc);
+      const long r = i == 0 ? token : row;  // the current frame's rows are the launch's tokens
+      if (i < ntap) v = *reinterpret_cast<const u32x4*>(p.tap[i] + f * p.fs_x + r * p.ld_x + c0 + cc);
       xv[i] = v;
+    }
+    if (p.rows && t0 + tok < p.T) {
+      *reinterpret_cast<u32x4*>(p.xsave + (long)row * p.ld_save + c0 + cc) = xv[0];
+      if (q == 0 && cc == 0) p.stamps[(tnow & 1) * p.srows + row] = make_int2(enter, tnow);
     }
     const u32x4 bb = *reinterpret_cast<const u32x4*>(p.conv_b + c0 + cc);
     u32x4 w[4];
@@ -131,8 +163,14 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
     }
     const long idx = (long)token * p.C + c;
     if (p.mode == 0) {
-      float* hp = p.h + idx;
-      const float h = first ? g : __fadd_rn(__fmul_rn(Am, *hp), Bm);
+      const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;
+      float* hp = p.h + (long)row * p.C + c;
+      bool fresh = false;
+      if (p.rows && !first) {
+        int enter;
+        row_stamp(p, row, tnow, fresh, enter);
+      }
+      const float h = first ? g : __fadd_rn(__fmul_rn(Am, fresh ? 0.f : *hp), Bm);
       *hp = h;
       const float yv = bf2f(p.yg[f * p.fs_y + (long)token * p.ld_y + c]);
       p.z[f * p.fs_z + (long)token * p.ld_z + c] = f2bf(rbf(h) * yv);
@@ -228,10 +266,29 @@ extern "C" int mx_ssm_step(hipStream_t st, const uint16_t* x0, const uint16_t* x
                            const uint16_t* ba, const uint16_t* sp, const int* frame, float* h, uint16_t* z, long ld_z,
                            int T, int C) {
   SsmArgs p{{x0, x1, x2, x3}, ld_x, 0, yg, ld_y, 0, conv_w, conv_b, wxT, bx, waT, ba, sp, frame, h, 0, z, ld_z, 0,
-            nullptr, nullptr, 0, T, C, 0};
+            nullptr, nullptr, 0, T, C, 0, nullptr, nullptr, 0, nullptr, 0};
   int rc = check_common(p, 1);
   if (rc) return rc;
   if (!yg || !h || !z) return MX_ENULL;
+  hipLaunchKernelGGL(ssm_kernel, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// One streamed frame of a moving crop: T tokens (crop patches, then queries); x0 / yg / z: the launch's token rows;
+// x1..x3 (history, stride ld_x), h (fp32 [srows][C]) and xsave (this frame's history slot, stride ld_save):
+// absolute state rows, token t at rows[t] (distinct, < srows); stamps: [2][srows] int pairs, {-8, -8} after a reset.
+extern "C" int mx_ssm_step_rows(hipStream_t st, const uint16_t* x0, const uint16_t* x1, const uint16_t* x2,
+                                const uint16_t* x3, long ld_x, const uint16_t* yg, long ld_y, const uint16_t* conv_w,
+                                const uint16_t* conv_b, const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT,
+                                const uint16_t* ba, const uint16_t* sp, const int* frame, float* h, uint16_t* z,
+                                long ld_z, int T, int C, const int* rows, int* stamps, int srows, uint16_t* xsave,
+                                long ld_save) {
+  SsmArgs p{{x0, x1, x2, x3}, ld_x, 0, yg, ld_y, 0, conv_w, conv_b, wxT, bx, waT, ba, sp, frame, h, 0, z, ld_z, 0,
+            nullptr, nullptr, 0, T, C, 0, rows, reinterpret_cast<int2*>(stamps), srows, xsave, ld_save};
+  int rc = check_common(p, 1);
+  if (rc) return rc;
+  if (!yg || !h || !z || !rows || !stamps || !xsave) return MX_ENULL;
+  if (srows < T || ld_save % 8 || ((uintptr_t)xsave & 15) || ((uintptr_t)stamps & 7)) return MX_ESHAPE;
   hipLaunchKernelGGL(ssm_kernel, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
@@ -243,7 +300,8 @@ extern "C" int mx_ssm_prep(hipStream_t st, const uint16_t* x_stack, long ld_x, l
                            const uint16_t* ba, const uint16_t* sp, const int* frame, float* A, float* B, int F, int T,
                            int C) {
   SsmArgs p{{x_stack + 3 * fs_x, x_stack + 2 * fs_x, x_stack + fs_x, x_stack}, ld_x, fs_x, nullptr, 0, 0, conv_w,
-            conv_b, wxT, bx, waT, ba, sp, frame, nullptr, 0, nullptr, 0, 0, A, B, (long)T * C, T, C, 1};
+            conv_b, wxT, bx, waT, ba, sp, frame, nullptr, 0, nullptr, 0, 0, A, B, (long)T * C, T, C, 1,
+            nullptr, nullptr, 0, nullptr, 0};
   int rc = check_common(p, F);
   if (rc) return rc;
   if (!A || !B) return MX_ENULL;

@@ -162,8 +162,9 @@ class TRecViT:
              z.data_ptr(), D, T, D)
         return self._block_tail(b, z, x, 1)
 
-    def _block_tail(self, b, z, x, B):
-        T, D, H = self.T, self.D, self.H
+    def _block_tail(self, b, z, x, B, T=None):
+        T = self.T if T is None else T
+        D, H = self.D, self.H
         res = b["out"](z, res=x)
         g = b["up"](ops.rmsnorm(res, b["sc1"], eps=self.rms_eps), act="glu")
         x1 = b["down"](g, res=res)
@@ -269,3 +270,104 @@ class TRecViT:
         call("mx_counter_add", stream(), self.frame.data_ptr(), F)
         self.t += F
         return fin.view(F, T, D)
+
+
+class CropTracker:
+    """The TRecViT step over a moving n x n crop of the 32 x 32 patch grid with the recurrent state indexed by
+    absolute patch (tapnext/crop-study/crop_study.py:147-185, CropTracker with shift=True): each crop token keeps its
+    own slice of the position embedding, its RG-LRU state and conv history travel with the image content, tokens
+    that leave the crop drop their state and tokens that enter start from zero. (The un-shifted form, state by
+    crop-local slot, loses the tracks: common/book/negative-results.md F13.)
+
+    Nothing is gathered or scattered per block: the SSM kernel addresses the model's absolute state rows through a
+    row map (mx_ssm_step_rows), and per-row stamps in device memory say which state a row still has. The crop's
+    tokens run every other op of the block as a T = n^2 + n_q token frame. Owns the model's state: do not interleave
+    with TRecViT.step on the same model without a reset.
+    """
+
+    def __init__(self, model):
+        m = self.m = model
+        if m.T != m.n_img + m.n_q:
+            raise ValueError("the crop form needs the full token layout (patch grid + queries)")
+        dev, T, D = m.dev, m.T, m.D
+        self.rows = torch.zeros(T, device=dev, dtype=torch.int32)
+        self.stamps = torch.empty(2, T, 2, device=dev, dtype=torch.int32)
+        self.xc = torch.zeros(T, D, device=dev, dtype=BF)
+        self.cur = torch.zeros(T, 2 * D, device=dev, dtype=BF)
+        self.graphs = {}
+        self.reset()
+
+    def reset(self):
+        """A new video: zero the model's state and mark every state row as never in the crop."""
+        self.m.reset()
+        self.stamps.fill_(-8)
+
+    def _row_map(self, r0, c0, n):
+        G = self.m.G
+        if not (1 <= n <= G and 0 <= r0 <= G - n and 0 <= c0 <= G - n):
+            raise ValueError(f"crop ({r0}, {c0}, {n}) outside the {G} x {G} patch grid")
+        ar = torch.arange(n)
+        idx = ((r0 + ar)[:, None] * G + (c0 + ar)[None]).flatten()
+        return torch.cat([idx, self.m.n_img + torch.arange(self.m.n_q)]).to(torch.int32)
+
+    def _block(self, i, x, phase, T):
+        m = self.m
+        b, D, ring = m.blocks[i], m.D, m.ring[i]
+        cur = self.cur[:T]
+        b["yx"](ops.rmsnorm(x, b["sc0"], eps=m.rms_eps), gelu=True, act_cols=D, out=cur)
+        z = torch.empty(T, D, device=m.dev, dtype=BF)
+        taps = [cur[:, D:]] + [ring[(phase - k) % 4][:, D:] for k in (1, 2, 3)]
+        call("mx_ssm_step_rows", stream(), *(t.data_ptr() for t in taps), 2 * D, cur.data_ptr(), 2 * D,
+             b["conv_w"].data_ptr(), b["conv_b"].data_ptr(), b["wxT"].data_ptr(), b["bx"].data_ptr(),
+             b["waT"].data_ptr(), b["ba"].data_ptr(), b["sp"].data_ptr(), m.frame.data_ptr(), m.h[i].data_ptr(),
+             z.data_ptr(), D, T, D, self.rows.data_ptr(), self.stamps.data_ptr(), m.T,
+             ring[phase][:, D:].data_ptr(), 2 * D)
+        return m._block_tail(b, z, x, 1, T)
+
+    def _frame(self, phase, n):
+        m = self.m
+        T = n * n + m.n_q
+        x = m.embed(m.img, m.qfeat, m.x0)  # the whole grid: a patch's embedding only depends on its own pixels
+        xc = torch.index_select(x, 0, self.rows[:T], out=self.xc[:T])
+        for i in range(len(m.blocks)):
+            xc = self._block(i, xc, phase, T)
+        fin = ops.layernorm(xc, *m.enc_norm, eps=m.ln_eps)
+        if m.has_heads:
+            m.heads(fin[n * n:], m.tracks, m.logits, m.vis)
+        call("mx_counter_add", stream(), m.frame.data_ptr(), 1)
+        return fin
+
+    def step(self, frame_u8, qfeat, r0, c0, n, use_graph=False):
+        """One frame over the crop of patch rows r0 .. r0 + n - 1, columns c0 .. c0 + n - 1 (patch units):
+        returns the encoder-normed tokens (n^2 crop tokens, then the n_q query tokens)."""
+        m = self.m
+        if m.img.shape != frame_u8.shape:
+            if frame_u8.dim() != 3 or frame_u8.shape[2] != 3:
+                raise ValueError("frames are (H, W, 3) uint8")
+            m.img = torch.zeros(frame_u8.shape, device=m.dev, dtype=torch.uint8)
+            m.graphs, self.graphs = {}, {}
+        m.img.copy_(frame_u8, non_blocking=True)
+        m.qfeat.copy_(qfeat, non_blocking=True)
+        rows = self._row_map(r0, c0, n)
+        self.rows[:rows.numel()].copy_(rows)
+        phase = m.t % 4
+        if use_graph:
+            if (phase, n) not in self.graphs:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    out = self._frame(phase, n)
+                self.graphs[(phase, n)] = (g, out)
+            g, out = self.graphs[(phase, n)]
+            g.replay()
+        else:
+            out = self._frame(phase, n)
+        m.t += 1
+        return out
+
+    def track(self, frame_u8, qfeat, r0, c0, n, use_graph=False):
+        """(tracks, logits, vis) of the queries for one crop frame (full-frame coordinates, as the coordinate head
+        always reads out full-frame bins)."""
+        if not self.m.has_heads:
+            raise RuntimeError("the weights carry no tracking heads")
+        self.step(frame_u8, qfeat, r0, c0, n, use_graph)
+        return self.m.tracks, self.m.logits, self.m.vis

@@ -126,6 +126,11 @@ def test_other_entry_points_refuse_bad_shapes():
     assert lib.mx_ssm_step(None, A16, A16, A16, A16, 1536, A16, 1536, A16, A16, A16, A16, A16, A16, A16, A16, A16,
                            A16, 768, 1280, 700) == -2                                 # C not a multiple of 64
     assert lib.mx_rglru_scan(None, A16, A16, A16, 4, 1280, 700, A16, 1536, 0, A16, 768, 0) == -2
+    ssr = lambda T=512, srows=1280, rows=A16, stamps=A16, xsave=A16: lib.mx_ssm_step_rows(
+        None, A16, A16, A16, A16, 1536, A16, 1536, A16, A16, A16, A16, A16, A16, A16, A16, A16, A16, 768, T, 768,
+        rows, stamps, srows, xsave, 1536)
+    assert ssr(T=1300) == -2           # more tokens than state rows
+    assert ssr(rows=None) == -6 and ssr(stamps=None) == -6 and ssr(xsave=None) == -6
     assert lib.mx_counter_add(None, None, 1) == -6
     # tracking heads
     assert lib.mx_track_head_blob_elems(768, 256, 512) == 768 * 256 + 6 * 256 + 256 * 256 + 256 * 512 + 512

@@ -274,3 +274,54 @@ def test_twelve_blocks_streamed_graph_and_clip(dev):
         assert rel(clip[t], refs[t]) <= 2e-2
     for i in range(12):
         assert (m.h[i] - h_stream[i]).abs().max().item() <= 5e-2
+
+
+CROPS = [(4, 4, 16), (6, 3, 16), (6, 3, 20), (0, 0, 32), (10, 12, 16), (11, 12, 16)]
+
+
+def test_crop_full_grid_equals_streamed_step(dev):
+    """The crop form over the whole 32 x 32 grid (identity row map) is the plain streamed step bit for bit, frame
+    after frame (the reference's c256 == base check, crop_study.py:14)."""
+    w = S.trecvit_weights(0, layers=2)
+    frames = S.frames_u8(3, 5)
+    qf = _qfeat().to(dev)
+    a = tv.TRecViT(w, device=dev)
+    b = tv.TRecViT(w, device=dev)
+    ct = tv.CropTracker(b)
+    a.reset()
+    for t in range(5):
+        fa = a.step(frames[t].to(dev), qf).clone()
+        fb = ct.step(frames[t].to(dev), qf, 0, 0, 32, use_graph=t >= 2).clone()
+        assert torch.equal(fa, fb), t
+        assert torch.equal(a.tracks, b.tracks)
+
+
+def test_crop_moving_vs_oracle(dev):
+    """A crop that moves, grows, covers the grid and shrinks again (1 block) vs the oracle's CropTracker
+    restatement: encoder-normed tokens within the one-block tolerance, the state of the patches in the crop within
+    1e-2 at their absolute rows, the heads on the frame's own query rows as in the streamed test."""
+    w = S.trecvit_weights(0, layers=1)
+    frames = S.frames_u8(4, len(CROPS))
+    qf = _qfeat()
+    ora = otr.CropModel(w)
+    m = tv.TRecViT(w, device=dev)
+    ct = tv.CropTracker(m)
+    for t, (r0, c0, n) in enumerate(CROPS):
+        ref = ora.step_crop(frames[t], qf, r0, c0, n)
+        fin = ct.step(frames[t].to(dev), qf.to(dev), r0, c0, n, use_graph=t % 2 == 1)
+        assert fin.shape == (n * n + 256, 768)
+        print(f"crop {t} {(r0, c0, n)}: rel {rel(fin, ref):.2e}", flush=True)
+        assert rel(fin, ref) <= 1e-2, (t, rel(fin, ref))
+        idx = ora.crop_rows(r0, c0, n)
+        assert (m.h[0][idx.to(dev)].cpu() - ora.lru[0][idx]).abs().max().item() <= 1e-2
+        assert (m.h[0][1024:].cpu() - ora.qs[0][0]).abs().max().item() <= 1e-2
+        _check_heads(m.tracks, m.logits, m.vis, otr.track_heads(fin[n * n:].cpu(), w))
+
+
+def test_crop_rejects_windows_outside_the_grid(dev):
+    w = S.trecvit_weights(0, layers=1)
+    ct = tv.CropTracker(tv.TRecViT(w, device=dev))
+    fr, qf = S.frames_u8(1, 1)[0].to(dev), _qfeat().to(dev)
+    for bad in ((0, 0, 33), (20, 0, 16), (0, -1, 8), (0, 0, 0)):
+        with pytest.raises(ValueError):
+            ct.step(fr, qf, *bad)

@@ -456,6 +456,29 @@ def test_preprocess_bilinear_closed_forms():
     assert abs(up[0, 0, 1, 1].item() - ref) < 1e-3
 
 
+def test_crop_full_grid_equals_plain_step_and_state_moves():
+    """CropModel (crop_study.py:147-185): the full-grid crop equals the plain model step bit for bit (the reference's
+    own c256 == base check); after a move, the state of patches that left the crop is zero (h and the 3-frame
+    history) and the patches in the crop hold state under their absolute index."""
+    w = S.trecvit_weights(0, layers=1)
+    frames = torch.randint(0, 256, (3, 64, 64, 3), generator=gen(51), dtype=torch.uint8)
+    qf = (torch.rand(4, 2, generator=gen(52))).to(BF)
+    base, crop = otr.Model(w), otr.CropModel(w)
+    for t in range(2):
+        assert torch.equal(crop.step_crop(frames[t], qf, 0, 0, 32), base.step(frames[t], qf))
+    crop.reset()
+    crop.step_crop(frames[0], qf, 4, 4, 8)
+    kept = crop.crop_rows(4, 4, 8)
+    h_before = crop.lru[0].clone()
+    crop.step_crop(frames[1], qf, 6, 4, 8)     # move down by 2 patch rows
+    now = set(crop.crop_rows(6, 4, 8).tolist())
+    gone = [r for r in kept.tolist() if r not in now]
+    assert len(gone) == 16 and crop.lru[0][gone].abs().max() == 0
+    assert crop.lru[0][sorted(now)].abs().max() > 0 and h_before[kept].abs().max() > 0
+    for k in range(3):
+        assert crop.conv[0][k][gone].abs().max() == 0
+
+
 def test_soft_argmax_closed_forms():
     """step8.py:356-361: a lone peak reads out its own bin; two bins a, b inside the window weigh as
     sigmoid(0.5 (a - b)) (temperature 0.5); bins beyond +-20 of the argmax are ignored; equal maxima take the first
