@@ -52,6 +52,14 @@ int mx_gemm_cfg_kind(int cfg);
  * residual Linears x + proj(a) and x + fc2(f) (moondream/gpu/md2fast.py:152-157). */
 int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
                          float* P, long ldp, long p_split, int M, int N, int K, int Kw);
+/* C = epi(sum over s < nsplit of P[s] + bias), mx_gemm_bf16's epilogue (act 0-3, act_ncols, + R with r_rows) on raw
+ * partials of mx_gemm_bf16_partial, splits added in order; one split equals mx_gemm_bf16 bit for bit. With the
+ * partial GEMM it is the fence-free split-K of the small-M GEMMs (prompt and query rows): it stands for the
+ * reference's small-M split-K path (i8gemm_small_launch, moondream/gpu/hip/i8gemm.hip:555-592, chosen at
+ * moondream/gpu/hgemm.py:120-122). N % 4 == 0, ldp % 4 == 0, P 16-byte and C 8-byte aligned (4-byte for act 3). */
+int mx_gemm_reduce(hipStream_t st, const float* P, int nsplit, long p_split, long ldp, const float* bias,
+                   const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int act,
+                   int act_ncols);
 
 /* ============================================================================================ W8A8 (int8 MFMA)
  * Per-token int8 quantisation of bf16 activations: s[m] = max(max_k |x[m,k]|, 1e-5) / 127 and

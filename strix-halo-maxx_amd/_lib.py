@@ -23,6 +23,7 @@ SIGNATURES = {
     "mx_gemm_ws_elems": [I, I, I, I],
     "mx_track_head_blob_elems": [I, I, I],
     "mx_resize_patchify_u8": [P, P, I, I, P, L, I, I, I],
+    "mx_gemm_reduce": [P, P, I, L, L, P, P, L, I, P, L, I, I, I, I],
     "mx_ssm_step_rows": [P, P, P, P, P, L, P, L, P, P, P, P, P, P, P, P, P, P, L, I, I, P, P, I, P, L],
     "mx_track_heads": [P, P, L, I, I, I, P, I, F, F, P, F, F, I, P, P, L, P],
     "mx_gemm_ws_counters": [I, I, I, I],

@@ -795,6 +795,40 @@ long tiles_of(int cfg, int M, int N) {
   return (long)((M + kCfgs[cfg].bm - 1) / kCfgs[cfg].bm) * ((N + kCfgs[cfg].bn - 1) / kCfgs[cfg].bn);
 }
 
+// ---- split-K reduction + epilogue: C = epi(sum_s P[s] + bias) with the fused kernel's epilogue (epi_val), so one
+// split of raw partials reduced here equals the fused GEMM bit for bit. One thread per 4 output columns; the splits
+// are added in order (deterministic).
+template <int ACT>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restrict__ P, int ns, long p_split, long ldp,
+                                                          const float* __restrict__ bias, const uint16_t* __restrict__ R,
+                                                          long ldr, int r_rows, uint16_t* __restrict__ C, long ldc,
+                                                          int M, int N, int act_ncols) {
+  const int n4 = N >> 2;
+  const long total = (long)M * n4;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < total; i += (long)gridDim.x * 256L) {
+    const int m = (int)(i / n4), n = (int)(i % n4) * 4;
+    const float* pp = P + (long)m * ldp + n;
+    f32x4 acc = *reinterpret_cast<const f32x4*>(pp);
+    for (int sp = 1; sp < ns; sp++) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(pp + sp * p_split);
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[e] = acc[e] + t[e];
+    }
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (bias) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) bv[e] = bias[n + e];
+    }
+    u32x2 rv = {0u, 0u};
+    if (R) rv = *reinterpret_cast<const u32x2*>(R + (long)(r_rows > 0 ? m % r_rows : m) * ldr + n);
+    const u32x2 o = epi_val<ACT>(acc, bv, rv, R != nullptr, n, act_ncols);
+    if constexpr (ACT == 3)
+      *reinterpret_cast<uint32_t*>(C + (long)m * ldc + (n >> 1)) = o.x;
+    else
+      *reinterpret_cast<u32x2*>(C + (long)m * ldc + n) = o;
+  }
+}
+
 }  // namespace
 
 extern "C" int mx_gemm_ncfg(void) { return kNCfg; }
@@ -926,6 +960,35 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
 #undef W_
 #undef H_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// C = epi(sum over s < nsplit of P[s] + bias): the epilogue of mx_gemm_bf16 (act 0 / 1 / 2 on columns < act_ncols when
+// act_ncols > 0, 3 = gated GELU on interleaved (gate, up) column pairs with output width N / 2; then + R) on raw
+// partials from mx_gemm_bf16_partial, splits added in order. Partial GEMM + this reduction is the fence-free
+// split-K: no counters, no cross-workgroup visibility inside a launch (stream order is the only synchronisation).
+// No counterpart in the reference; it stands for the small-M split-K path of i8gemm_small_launch
+// (moondream/gpu/hip/i8gemm.hip:555-592) on the bf16 side.
+extern "C" int mx_gemm_reduce(hipStream_t st, const float* P, int nsplit, long p_split, long ldp, const float* bias,
+                              const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int act,
+                              int act_ncols) {
+  if (!P || !C) return MX_ENULL;
+  if (nsplit < 1 || nsplit > 64 || M < 1 || N < 4 || N % 4 || ldp % 4 || ldp < N || act < 0 || act > 3 ||
+      r_rows < 0 || (nsplit > 1 && p_split < (long)M * ldp) || p_split % 4)
+    return MX_ESHAPE;
+  if (act == 3 ? (ldc < N / 2 || ldc % 2) : (ldc < N || ldc % 4)) return MX_ESHAPE;
+  if (R && (ldr < N || ldr % 4 || act == 3)) return MX_ESHAPE;
+  if (((uintptr_t)P & 15) || ((uintptr_t)C & (act == 3 ? 3 : 7)) || ((uintptr_t)R & 7)) return MX_ELAYOUT;
+  const long total = (long)M * (N / 4);
+  const int blocks = (int)((total + 255) / 256 < 2048 ? (total + 255) / 256 : 2048);
+#define RL_(A) hipLaunchKernelGGL((gemm_reduce_kernel<A>), dim3(blocks), dim3(256), 0, st, P, nsplit, p_split, ldp, bias, R, ldr, r_rows, C, ldc, M, N, act_ncols)
+  switch (act) {
+    case 0: RL_(0); break;
+    case 1: RL_(1); break;
+    case 2: RL_(2); break;
+    default: RL_(3); break;
+  }
+#undef RL_
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
 // Raw split-K partial sums of A W^T for wave-split configs (kind 1): P[s][m][n] (fp32, row stride ldp, split stride

@@ -124,7 +124,20 @@ class MxLin:
         self.dev = self.w.device
 
     def _launch(self, cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws, act_cols=0):
-        return _lib.load().mx_gemm_bf16(
+        """splits > 0: mx_gemm_bf16 (in-kernel split-K when > 1); splits = -S: the fence-free split-K, raw partials of
+        S splits into the workspace (mx_gemm_bf16_partial) then the epilogue over their sum (mx_gemm_reduce)."""
+        lib = _lib.load()
+        if splits < 0:
+            S, N = -splits, self.N
+            if S * M * N > ws.ws.numel():
+                return -3
+            P = ws.ws[:S * M * N].view(S, M, N)
+            rc = _partial(self, cfg, S, x2, P, M)
+            if rc != 0:
+                return rc
+            return lib.mx_gemm_reduce(stream(), P.data_ptr(), S, M * N, N, ptr(self.b), ptr(r2), ldr, r_rows,
+                                      y2.data_ptr(), y2.stride(0), M, N, a, act_cols)
+        return lib.mx_gemm_bf16(
             stream(), cfg, splits, x2.data_ptr(), x2.stride(0), self.w.data_ptr(), self.w.stride(0), ptr(self.b),
             ptr(r2), ldr, r_rows, y2.data_ptr(), y2.stride(0), M, self.N, self.K, self.Kw, a, act_cols,
             ptr(ws.ws), ws.ws.numel(), ptr(ws.cnt), ws.cnt.numel())
@@ -176,6 +189,8 @@ class MxLin:
         cfg, splits = self.cfgs.get(M) or self._pick(M, x2, y2, a, r2, ldr, r_rows, ws)
         if splits > 1:
             ws.reserve(*_ws_need(cfg, splits, M, self.N))
+        elif splits < 0:
+            ws.reserve(-splits * M * self.N, 0)
         _lib.check(self._launch(cfg, splits, x2, y2, M, a, r2, ldr, r_rows, ws, act_cols), "mx_gemm_bf16")
         return y2.view(*x.shape[:-1], Nout) if out is None else y
 
@@ -251,10 +266,17 @@ def tune_gemm(lin, M, x2, y2, a, r2, ldr, r_rows, ws, reps=10):
             if sp > 1 and (nk // sp < 3 or (sp - 1) * (-(-nk // sp)) >= nk):
                 continue
             cands.append((cfg, sp))
+        if tune_gemm.partial and a != 3:
+            for sp in (2, 4, 8, 16):
+                if nk // sp < 2 or (sp - 1) * (-(-nk // sp)) >= nk:
+                    continue
+                cands.append((cfg, -sp))
     best, bt = None, float("inf")
     for cfg, sp in cands:
         if sp > 1:
             ws.reserve(*_ws_need(cfg, sp, M, lin.N))
+        elif sp < 0:
+            ws.reserve(-sp * M * lin.N, 0)
         run = lambda: lin._launch(cfg, sp, x2, y2, M, a, r2, ldr, r_rows, ws)
         if run() != 0:
             continue
@@ -274,6 +296,9 @@ def tune_gemm(lin, M, x2, y2, a, r2, ldr, r_rows, ws, reps=10):
 # Split-K candidates in the tuner: off by default (the cross-XCD release fence of the last-arriver reduction costs
 # more than the extra parallelism buys at these shapes; the path stays available and tested).
 tune_gemm.split_k = False
+# Fence-free split-K candidates (partial GEMM + mx_gemm_reduce, pick (cfg, -S)): on by default; they win where the
+# grid of output tiles is far below the 256 CUs (the 32 / 64-row prompt and query GEMMs).
+tune_gemm.partial = True
 
 
 class MxI8Lin:

@@ -7,7 +7,7 @@ partials reduced by the residual-LayerNorm kernel), each candidate (tile config,
 launches of that op across the tower's blocks, each on its own block's weights, replayed from a HIP graph. That is the
 cost the op has inside the tower, where a block's weights arrive from HBM rather than from a cache warmed by the
 previous launch; the split-K candidates are timed together with the reduction kernel that reads their partials. The
-other shapes (tower batch 13 / 256, text-decoder prefill, TRecViT stream and clip passes) come from the generic
+other shapes (tower batch 13 / 256, text-decoder prefill and yes/no query, TRecViT stream and clip passes) come from the generic
 per-shape autotuner (ops.tune_gemm, ops._partial_cfg) run on their own forwards. The result is written as JSON;
 ops.MxLin then uses it before autotuning (the reference's pick_cfg FIXED table, moondream/gpu/hgemm.py:47-76).
 """
@@ -146,10 +146,12 @@ def tune_generic(log):
             log(f"tower batch {B} tuned")
         del vt
         torch.cuda.empty_cache()
-        dec = md2text.TextDecoder(S.text_weights(0), device=dev, ctx=1024)
+        dec = md2text.TextDecoder(S.text_weights(0), device=dev, ctx=1024, yes_ids=(11, 222), no_ids=(55, 666))
         dec.prefill(S.activations(3, (729, 2048), "img").to(dev), S.prompt_ids(4, 64))
+        dec.set_questions([S.prompt_ids(4, 32).tolist()])   # the yes/no query: 32 rows
+        dec.query()
         torch.cuda.synchronize()
-        log("text prefill tuned")
+        log("text prefill and query tuned")
         del dec
         torch.cuda.empty_cache()
         m = trecvit.TRecViT(S.trecvit_weights(0), device=dev)
@@ -180,8 +182,8 @@ def main():
     fused.update(f1)                                     # ... with the in-context picks for the batch-1 tower
     part.update(p1)
     key = lambda k: ",".join(str(v) for v in k)
-    lines = ["{", ' "note": "MI355X (gfx950) GEMM tile table: (M, N, Kw) -> (tile config, split count); written by '
-                  'python -m strix_halo_maxx_amd.tune",']
+    lines = ["{", ' "note": "MI355X (gfx950) GEMM tile table: (M, N, Kw) -> (tile config, splits: > 0 in-kernel, -S = S '
+                  'raw partials + mx_gemm_reduce); written by python -m strix_halo_maxx_amd.tune",']
     for name, d, last in (("fused", fused, False), ("partial", part, True)):
         items = [f'  "{key(k)}": [{v[0]}, {v[1]}]' for k, v in sorted(d.items())]
         lines += [f' "{name}": {{', ",\n".join(items), " }" + ("" if last else ",")]

@@ -132,6 +132,15 @@ def test_other_entry_points_refuse_bad_shapes():
     assert ssr(T=1300) == -2           # more tokens than state rows
     assert ssr(rows=None) == -6 and ssr(stamps=None) == -6 and ssr(xsave=None) == -6
     assert lib.mx_counter_add(None, None, 1) == -6
+    rd = lambda **kw: lib.mx_gemm_reduce(*(lambda a: (a.update(kw), list(a.values()))[1])(dict(
+        st=None, P=A16, ns=4, ps=64 * 2048, ldp=2048, bias=None, R=None, ldr=0, rr=0, C=A16, ldc=2048, M=64,
+        N=2048, act=0, an=0)))
+    assert rd(N=2046, ldp=2046, ldc=2046) == -2   # N % 4
+    assert rd(ps=100) == -2                       # split stride under M * ldp
+    assert rd(act=4) == -2
+    assert rd(act=3, R=A16, ldr=2048) == -2       # no residual with the gated GELU
+    assert rd(P=A16 + 4) == -4                    # P not 16-byte aligned
+    assert rd(C=None) == -6
     # tracking heads
     assert lib.mx_track_head_blob_elems(768, 256, 512) == 768 * 256 + 6 * 256 + 256 * 256 + 256 * 512 + 512
     hd = lambda **kw: lib.mx_track_heads(*(lambda a: (a.update(kw), list(a.values()))[1])(dict(

@@ -109,6 +109,59 @@ def test_gemm_partial_splits(dev, M, K, N):
             assert err <= 1e-5 * ref.abs().max().item(), (cfg, sp, err)
 
 
+@pytest.mark.parametrize("cfg", [0, 3, 6, 8, 12, 19, 22])
+def test_gemm_reduce_one_split_equals_fused(dev, cfg):
+    """mx_gemm_reduce over one split of raw partials applies the fused kernel's epilogue to the same fp32
+    accumulator: bit for bit mx_gemm_bf16 for act 0 / 1 / 2, the column-limited GELU, the residual (also
+    row-broadcast) and the gated GELU; M = 63 and N = 4300 leave partial tiles."""
+    M, K, N = 63, 1000, 4300
+    g = gen(21)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    r = torch.randn(M, N, generator=g).to(BF).to(dev)
+    r7 = torch.randn(7, N, generator=g).to(BF).to(dev)
+    lin = ops.MxLin(w, b)
+    x2 = ops._rows(x, lin.K)
+    print(f"reduce cfg={cfg}", flush=True)
+    for kw in (dict(), dict(gelu=True), dict(act="erf"), dict(gelu=True, act_cols=1000), dict(res=r),
+               dict(gelu=True, res=r), dict(res=r7), dict(act="glu")):
+        lin.cfgs[M] = (cfg, 1)
+        y1 = lin(x, **kw).cpu()
+        lin.cfgs[M] = (cfg, -1)
+        y2 = lin(x, **kw).cpu()
+        assert torch.equal(y1, y2), (cfg, kw)
+
+
+@pytest.mark.parametrize("M,K,N", [(32, 8192, 2048), (64, 2048, 6144), (37, 2048, 2048), (730, 8192, 2048)])
+def test_gemm_partial_reduce_splits_vs_fp32(dev, M, K, N):
+    """The fence-free split-K (partial GEMM + mx_gemm_reduce, picks (cfg, -S)) at the prompt / query shapes: within
+    the GEMM tolerance of fp32 for S = 2, 4, 8, 16 (with and without the residual), and without the residual within
+    what a different fp32 summation order allows of the one-split result: one bf16 rounding of each plus
+    K 2^-24 sum_k |x_k w_k| per element (the two differ only in that order; the rounding flips it causes are a few
+    percent of the elements)."""
+    g = gen(M + N)
+    x = torch.randn(M, K, generator=g).to(BF)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    r = torch.randn(M, N, generator=g).to(BF)
+    ref = x.float() @ w.float().t() + b.float()
+    lin = ops.MxLin(w, b)
+    xd, rd = x.to(dev), r.to(dev)
+    lin.cfgs[M] = (6, 1)
+    y1 = lin(xd).cpu().float()
+    absum = x.float().abs() @ w.float().abs().t()
+    slack = K * 2.0 ** -24 * absum + 2.0 ** -8 * y1.abs() * 2
+    for S in (2, 4, 8, 16):
+        for cfg in (6, 22, 0):
+            lin.cfgs[M] = (cfg, -S)
+            y = lin(xd).cpu()
+            assert rel(y, ref) < 5e-3, (cfg, S)
+            assert bool(((y.float() - y1).abs() <= slack).all()), (cfg, S)
+            yr = lin(xd, res=rd).cpu()
+            assert rel(yr, ref + r.float()) < 5e-3, (cfg, S)
+
+
 def test_residual_layernorm_matches_unfused(dev):
     """x = bf16(bf16(sum P + bias) + res) bit for bit from the partials (CPU restatement, same fp32 order); the same
     within 1 ulp of the single-pass GEMM epilogue (different summation order); y equals layernorm(x) exactly."""
