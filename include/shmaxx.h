@@ -81,6 +81,16 @@ int mx_quant_weight_i8(hipStream_t st, const uint16_t* w, long ldw, int8_t* q, l
 int mx_gemm_i8(hipStream_t st, int cfg, const int8_t* A, long lda, const int8_t* W, long ldw, const float* sa,
                const float* sw, const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M,
                int N, int K, int Kw, int act, int32_t* P, long ldp);
+/* W8A8 split-K for the small-M GEMMs: raw int32 partials of `splits` contiguous k ranges (P[s][m][n], row stride ldp,
+ * split stride p_split; kind-0 configs with a partial-sum mode), then mx_gemm_i8_reduce: the exact int32 sum of
+ * the partials through mx_gemm_i8's epilogue, so the pair equals mx_gemm_i8 bit for bit for any split count. Stands
+ * for the reference's small-M int8 split-K (i8gemm_small_launch + its reduce, moondream/gpu/hip/i8gemm.hip:389-443,
+ * :555-592). */
+int mx_gemm_i8_partial(hipStream_t st, int cfg, int splits, const int8_t* A, long lda, const int8_t* W, long ldw,
+                       int32_t* P, long ldp, long p_split, int M, int N, int K, int Kw);
+int mx_gemm_i8_reduce(hipStream_t st, const int32_t* P, int nsplit, long p_split, long ldp, const float* sa,
+                      const float* sw, const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C,
+                      long ldc, int M, int N, int act);
 /* Split-K workspace a (cfg, splits) call needs: fp32 elements / tile counters. Replaces the fixed-size
  * workspace() of moondream/gpu/hgemm.py:78-83. */
 long mx_gemm_ws_elems(int cfg, int splits, int M, int N);

@@ -24,6 +24,8 @@ SIGNATURES = {
     "mx_track_head_blob_elems": [I, I, I],
     "mx_resize_patchify_u8": [P, P, I, I, P, L, I, I, I],
     "mx_gemm_reduce": [P, P, I, L, L, P, P, L, I, P, L, I, I, I, I],
+    "mx_gemm_i8_partial": [P, I, I, P, L, P, L, P, L, L, I, I, I, I],
+    "mx_gemm_i8_reduce": [P, P, I, L, L, P, P, P, P, L, I, P, L, I, I, I],
     "mx_ssm_step_rows": [P, P, P, P, P, L, P, L, P, P, P, P, P, P, P, P, P, P, L, I, I, P, P, I, P, L],
     "mx_track_heads": [P, P, L, I, I, I, P, I, F, F, P, F, F, I, P, P, L, P],
     "mx_gemm_ws_counters": [I, I, I, I],

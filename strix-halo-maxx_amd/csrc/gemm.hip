@@ -521,9 +521,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_i8_kernel(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw, const float* __restrict__ sa,
     const float* __restrict__ sw, const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr,
     int r_rows, uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols, int tiles_m,
-    int tiles_n, float* __restrict__ P, long ldp) {
+    int tiles_n, float* __restrict__ P, long ldp, int splits, int kt_per_split, long p_split) {
   gemm_body<BM, BN, WGM, WGN, S, true>(A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols,
-                                       tiles_m, tiles_n, 1, Kw / BK, nullptr, nullptr, P, ldp, 0, sa, sw);
+                                       tiles_m, tiles_n, splits, kt_per_split, nullptr, nullptr, P, ldp, p_split, sa,
+                                       sw);
 }
 
 // Wave-split-K kernel (see the header): 4 waves share the LDS ring of a BM x BN tile; wave w multiplies the k
@@ -784,10 +785,13 @@ bool psum_ok(int cfg) {
 template <int BM, int BN, int WGM, int WGN, int S>
 hipError_t launch_i8(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* sa,
                      const float* sw, const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C,
-                     long ldc, int M, int N, int K, int Kw, int act, float* P, long ldp) {
+                     long ldc, int M, int N, int K, int Kw, int act, float* P, long ldp, int splits = 1,
+                     long p_split = 0) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn), dim3(64 * WGM * WGN), 0, st, A, lda, W,
-                     ldw, sa, sw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, 0, tm, tn, P, ldp);
+  const int nk = Kw / BK, kps = (nk + splits - 1) / splits;
+  hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WGM, WGN, S>), dim3(tm * tn * splits), dim3(64 * WGM * WGN), 0, st, A, lda,
+                     W, ldw, sa, sw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, 0, tm, tn, P, ldp, splits, kps,
+                     p_split);
   return hipGetLastError();
 }
 
@@ -826,6 +830,40 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
       *reinterpret_cast<uint32_t*>(C + (long)m * ldc + (n >> 1)) = o.x;
     else
       *reinterpret_cast<u32x2*>(C + (long)m * ldc + n) = o;
+  }
+}
+
+// The W8A8 form: int32 partials summed exactly, then epi_val's int8 epilogue (it takes the int32 sum as the bit
+// pattern of an fp32 register, as the tile kernel hands it its accumulator).
+template <int ACT>
+__global__ __launch_bounds__(256) void gemm_reduce_i8_kernel(const int32_t* __restrict__ P, int ns, long p_split,
+                                                             long ldp, const float* __restrict__ sa,
+                                                             const float* __restrict__ sw,
+                                                             const float* __restrict__ bias,
+                                                             const uint16_t* __restrict__ R, long ldr, int r_rows,
+                                                             uint16_t* __restrict__ C, long ldc, int M, int N) {
+  const int n4 = N >> 2;
+  const long total = (long)M * n4;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < total; i += (long)gridDim.x * 256L) {
+    const int m = (int)(i / n4), n = (int)(i % n4) * 4;
+    const int32_t* pp = P + (long)m * ldp + n;
+    int32_t acc[4] = {pp[0], pp[1], pp[2], pp[3]};
+    for (int sp = 1; sp < ns; sp++) {
+      const u32x4 t = *reinterpret_cast<const u32x4*>(pp + sp * p_split);
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[e] += (int32_t)t[e];
+    }
+    f32x4 s, bv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; e++) s[e] = __int_as_float(acc[e]);
+    if (bias) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) bv[e] = bias[n + e];
+    }
+    const f32x4 sw4 = *reinterpret_cast<const f32x4*>(sw + n);
+    u32x2 rv = {0u, 0u};
+    if (R) rv = *reinterpret_cast<const u32x2*>(R + (long)(r_rows > 0 ? m % r_rows : m) * ldr + n);
+    *reinterpret_cast<u32x2*>(C + (long)m * ldc + n) = epi_val<ACT, true>(s, bv, rv, R != nullptr, n, 0, sa[m], sw4);
   }
 }
 
@@ -986,6 +1024,65 @@ extern "C" int mx_gemm_reduce(hipStream_t st, const float* P, int nsplit, long p
     case 1: RL_(1); break;
     case 2: RL_(2); break;
     default: RL_(3); break;
+  }
+#undef RL_
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// W8A8 split-K: raw int32 partials of S splits of the int8 GEMM (the same tile kernel in its raw mode, each split a
+// contiguous range of k-steps). Integer sums are exact in any order, so partials + mx_gemm_i8_reduce equal
+// mx_gemm_i8 bit for bit whatever the split count.
+extern "C" int mx_gemm_i8_partial(hipStream_t st, int cfg, int splits, const int8_t* A, long lda, const int8_t* W,
+                                  long ldw, int32_t* P, long ldp, long p_split, int M, int N, int K, int Kw) {
+  if (!A || !W || !P) return MX_ENULL;
+  if (cfg < 0 || cfg >= kNCfg || kCfgs[cfg].kind != 0 || !psum_ok(cfg)) return MX_EBADCFG;
+  if (M < 1 || N < 1 || N % 4 || K < 16 || K % 16 || Kw % 128 || Kw < K) return MX_ESHAPE;
+  if (lda % 16 || lda < K || ldw % 16 || ldw < Kw) return MX_ESHAPE;
+  const int nk = Kw / 128;
+  if (splits < 1 || splits > nk) return MX_ESPLIT;
+  const int kps = (nk + splits - 1) / splits;
+  if ((splits - 1) * kps >= nk) return MX_ESPLIT;  // every split owns >= 1 k-step
+  if (ldp % 4 || ldp < N || ((uintptr_t)P & 15) || p_split % 4 || (splits > 1 && p_split < (long)M * ldp))
+    return MX_ELAYOUT;
+  if (((uintptr_t)A | (uintptr_t)W) & 15) return MX_ELAYOUT;
+  const uint16_t* A16 = reinterpret_cast<const uint16_t*>(A);
+  const uint16_t* W16 = reinterpret_cast<const uint16_t*>(W);
+  float* Pf = reinterpret_cast<float*>(P);
+  hipError_t e;
+#define I_(BM, BN, WGM, WGN, S) launch_i8<BM, BN, WGM, WGN, S>(st, A16, lda / 2, W16, ldw / 2, nullptr, nullptr, nullptr, nullptr, 0, 0, nullptr, 0, M, N, K / 2, Kw / 2, 0, Pf, ldp, splits, p_split)
+  switch (cfg) {
+    case 0: e = I_(128, 128, 2, 2, 4); break;
+    case 1: e = I_(64, 128, 2, 2, 4); break;
+    case 2: e = I_(128, 64, 2, 2, 4); break;
+    case 3: e = I_(64, 64, 2, 2, 4); break;
+    case 4: e = I_(256, 128, 2, 2, 3); break;
+    case 5: e = I_(128, 256, 2, 2, 3); break;
+    case 6: e = I_(64, 64, 2, 2, 3); break;
+    case 7: e = I_(128, 128, 2, 2, 2); break;
+    default: return MX_EBADCFG;
+  }
+#undef I_
+  return e == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// C = the W8A8 epilogue of mx_gemm_i8 (((float)acc * sa[m]) * sw[n] + bias[n], act 0 / 1 / 2 on that fp32 value, one
+// bf16 rounding, then + R) on acc = the int32 sum of nsplit raw partials. sw 16-byte aligned.
+extern "C" int mx_gemm_i8_reduce(hipStream_t st, const int32_t* P, int nsplit, long p_split, long ldp, const float* sa,
+                                 const float* sw, const float* bias, const uint16_t* R, long ldr, int r_rows,
+                                 uint16_t* C, long ldc, int M, int N, int act) {
+  if (!P || !C || !sa || !sw) return MX_ENULL;
+  if (nsplit < 1 || nsplit > 64 || M < 1 || N < 4 || N % 4 || ldp % 4 || ldp < N || act < 0 || act > 2 ||
+      r_rows < 0 || (nsplit > 1 && p_split < (long)M * ldp) || p_split % 4 || ldc < N || ldc % 4)
+    return MX_ESHAPE;
+  if (R && (ldr < N || ldr % 4)) return MX_ESHAPE;
+  if (((uintptr_t)P & 15) || ((uintptr_t)C & 7) || ((uintptr_t)R & 7) || ((uintptr_t)sw & 15)) return MX_ELAYOUT;
+  const long total = (long)M * (N / 4);
+  const int blocks = (int)((total + 255) / 256 < 2048 ? (total + 255) / 256 : 2048);
+#define RL_(A) hipLaunchKernelGGL((gemm_reduce_i8_kernel<A>), dim3(blocks), dim3(256), 0, st, P, nsplit, p_split, ldp, sa, sw, bias, R, ldr, r_rows, C, ldc, M, N)
+  switch (act) {
+    case 0: RL_(0); break;
+    case 1: RL_(1); break;
+    default: RL_(2); break;
   }
 #undef RL_
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;

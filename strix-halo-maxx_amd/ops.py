@@ -363,23 +363,46 @@ class MxI8Lin:
              self.K)
         return q, sc
 
-    def _launch(self, cfg, q, sc, y2, M, a, r2, ldr, r_rows, P=None):
-        return _lib.load().mx_gemm_i8(stream(), cfg, q.data_ptr(), q.stride(0), self.wq.data_ptr(), self.wq.stride(0),
-                                      ptr(sc), self.sw.data_ptr(), ptr(self.b), ptr(r2), ldr, r_rows, ptr(y2),
-                                      y2.stride(0) if y2 is not None else 0, M, self.N, self.K, self.Kw, a, ptr(P),
-                                      P.stride(0) if P is not None else 0)
+    def _launch(self, cfg, q, sc, y2, M, a, r2, ldr, r_rows, P=None, splits=1):
+        """splits = -S: raw int32 partials of S splits into the workspace (mx_gemm_i8_partial), then the W8A8
+        epilogue over their exact sum (mx_gemm_i8_reduce): equal to the one-launch GEMM bit for bit."""
+        lib = _lib.load()
+        if splits < 0:
+            S, N = -splits, self.N
+            ws = Workspace.get(q.device)
+            if S * M * N > ws.ws.numel():
+                return -3
+            Pw = ws.ws[:S * M * N].view(torch.int32).view(S, M, N)
+            rc = lib.mx_gemm_i8_partial(stream(), cfg, S, q.data_ptr(), q.stride(0), self.wq.data_ptr(),
+                                        self.wq.stride(0), Pw.data_ptr(), N, M * N, M, N, self.K, self.Kw)
+            if rc != 0:
+                return rc
+            return lib.mx_gemm_i8_reduce(stream(), Pw.data_ptr(), S, M * N, N, ptr(sc), self.sw.data_ptr(),
+                                         ptr(self.b), ptr(r2), ldr, r_rows, y2.data_ptr(), y2.stride(0), M, N, a)
+        return lib.mx_gemm_i8(stream(), cfg, q.data_ptr(), q.stride(0), self.wq.data_ptr(), self.wq.stride(0),
+                              ptr(sc), self.sw.data_ptr(), ptr(self.b), ptr(r2), ldr, r_rows, ptr(y2),
+                              y2.stride(0) if y2 is not None else 0, M, self.N, self.K, self.Kw, a, ptr(P),
+                              P.stride(0) if P is not None else 0)
 
     def _pick(self, M, q, sc, y2):
+        """(cfg, splits) for this M: every kind-0 tile config in one launch, and with raw partials over 2 / 4 / 8 / 16
+        k-splits plus the reduction, each timed on the real operands (outside graph capture)."""
         key = ("i8", M, self.N, self.Kw)
         if key in _TUNED:
             return _TUNED[key]
-        best = 0
+        best = (0, 1)
         if MxLin.autotune and not torch.cuda.is_current_stream_capturing():
             bt = float("inf")
-            for cfg in range(_lib.load().mx_gemm_ncfg()):
-                if _lib.load().mx_gemm_cfg_kind(cfg) != 0:
-                    continue
-                run = lambda: self._launch(cfg, q, sc, y2, M, 0, None, 0, 0)
+            nk = self.Kw // 128
+            ws = Workspace.get(q.device)
+            cands = [(c, 1) for c in range(_lib.load().mx_gemm_ncfg()) if _lib.load().mx_gemm_cfg_kind(c) == 0]
+            if tune_gemm.partial:
+                cands += [(c, -sp) for c, _ in list(cands) for sp in (2, 4, 8, 16)
+                          if nk // sp >= 2 and (sp - 1) * (-(-nk // sp)) < nk]
+            for cfg, sp in cands:
+                if sp < 0:
+                    ws.reserve(-sp * M * self.N, 0)
+                run = lambda: self._launch(cfg, q, sc, y2, M, 0, None, 0, 0, splits=sp)
                 if run() != 0:
                     continue
                 run()
@@ -391,7 +414,7 @@ class MxI8Lin:
                 e1.synchronize()
                 t = e0.elapsed_time(e1)
                 if t < bt:
-                    best, bt = cfg, t
+                    best, bt = (cfg, sp), t
         _TUNED[key] = best
         return best
 
@@ -414,7 +437,10 @@ class MxI8Lin:
         cfg = self.cfgs.get(M)
         if cfg is None:
             cfg = self.cfgs[M] = self._pick(M, q, sc, y2)
-        _lib.check(self._launch(cfg, q, sc, y2, M, a, r2, ldr, r_rows), "mx_gemm_i8")
+        cfg, splits = cfg if isinstance(cfg, tuple) else (cfg, 1)
+        if splits < 0:
+            Workspace.get(q.device).reserve(-splits * M * self.N, 0)
+        _lib.check(self._launch(cfg, q, sc, y2, M, a, r2, ldr, r_rows, splits=splits), "mx_gemm_i8")
         return y2.view(*x.shape[:-1], self.N) if out is None else y
 
     def acc_i32(self, q, cfg=0):

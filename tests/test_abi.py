@@ -141,6 +141,15 @@ def test_other_entry_points_refuse_bad_shapes():
     assert rd(act=3, R=A16, ldr=2048) == -2       # no residual with the gated GELU
     assert rd(P=A16 + 4) == -4                    # P not 16-byte aligned
     assert rd(C=None) == -6
+    assert lib.mx_gemm_i8_partial(None, 8, 2, A16, 2048, A16, 2048, A16, 2048, 64 * 2048, 64, 2048, 2048,
+                                  2048) == -1     # kind-1 config
+    assert lib.mx_gemm_i8_partial(None, 0, 17, A16, 2048, A16, 2048, A16, 2048, 64 * 2048, 64, 2048, 2048,
+                                  2048) == -3     # more splits than 128-wide k-steps
+    assert lib.mx_gemm_i8_partial(None, 0, 2, A16, 2048, A16, 2048, A16, 2048, 100, 64, 2048, 2048, 2048) == -4
+    assert lib.mx_gemm_i8_reduce(None, A16, 2, 64 * 2048, 2048, A16, A16, None, None, 0, 0, A16, 2048, 64, 2048,
+                                 3) == -2         # no gated GELU in W8A8
+    assert lib.mx_gemm_i8_reduce(None, A16, 2, 64 * 2048, 2048, None, A16, None, None, 0, 0, A16, 2048, 64, 2048,
+                                 0) == -6
     # tracking heads
     assert lib.mx_track_head_blob_elems(768, 256, 512) == 768 * 256 + 6 * 256 + 256 * 256 + 256 * 512 + 512
     hd = lambda **kw: lib.mx_track_heads(*(lambda a: (a.update(kw), list(a.values()))[1])(dict(

@@ -100,6 +100,32 @@ def test_gemm_i8_epilogues_match_oracle(dev, M, K, N):
         lin.cfgs.pop(M, None)
 
 
+@pytest.mark.parametrize("M,K,N", [(32, 8192, 2048), (64, 2048, 6144), (57, 2048, 2048)])
+def test_gemm_i8_split_partials_equal_one_launch(dev, M, K, N):
+    """W8A8 split-K (mx_gemm_i8_partial + mx_gemm_i8_reduce, MxI8Lin picks (cfg, -S)): the int32 sum of the split
+    partials is exact, so every output equals the one-launch GEMM bit for bit for S = 2, 3, 8, 16, with GELU and
+    with the residual."""
+    g = gen(M + K)
+    x = torch.randn(M, K, generator=g).to(BF).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    r = torch.randn(M, N, generator=g).to(BF).to(dev)
+    lin = ops.MxI8Lin(w, b, BF, dev)
+    pre = lin.quant(x)
+    for cfg in (0, 3, 6):
+        ref = {}
+        lin.cfgs[M] = (cfg, 1)
+        for kw in (dict(), dict(gelu=True), dict(res=r)):
+            ref[str(kw.keys())] = lin(x, pre=pre, **kw).cpu()
+        for S in (2, 3, 8, 16):
+            if K // 128 < S:
+                continue
+            lin.cfgs[M] = (cfg, -S)
+            print(f"i8 split cfg={cfg} S={S}", flush=True)
+            for kw in (dict(), dict(gelu=True), dict(res=r)):
+                assert torch.equal(lin(x, pre=pre, **kw).cpu(), ref[str(kw.keys())]), (cfg, S, kw)
+
+
 def test_decode_gemvs_i8_match_oracle(dev):
     """The batch-1 W8A8 GEMVs: without the LayerNorm both are bit-exact against the oracle chain (same per-token scale,
     same quantised values, exact int32 sums, the same fp32 dequant order), GELU rows within one bf16 ulp; with the
