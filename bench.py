@@ -392,6 +392,7 @@ def trecvit_bench(frames=64, clip=16):
         m.forward_clip(fr[c0:c0 + clip], qf)
     torch.cuda.synchronize()
     ms_clip = (time.perf_counter() - t0) / frames * 1e3
+    scan = scan_roofline(m, clip)
     c = S.TRV
     T, D = 1280, c["dim"]
     gemm = 2 * T * (D * 2 * D + D * D + D * 2 * c["ff_gated"] + c["ff_gated"] * D + D * 3 * D + D * D + 2 * D * c["ff_vit"])
@@ -401,8 +402,43 @@ def trecvit_bench(frames=64, clip=16):
     return {"stream_ms_per_frame": round(ms_stream, 3), "clip_ms_per_frame": round(ms_clip, 3), "clip_frames": clip,
             "frames": frames, "gflop_per_frame": round(fl / 1e9, 1),
             "stream_mfma_frac": round(fl / (ms_stream / 1e3) / PEAK_BF16, 4),
-            "clip_mfma_frac": round(fl / (ms_clip / 1e3) / PEAK_BF16, 4),
+            "clip_mfma_frac": round(fl / (ms_clip / 1e3) / PEAK_BF16, 4), "scan_roofline": scan,
             "workload": "TAPNext-style TRecViT, 12 blocks, hidden 768, 1024 patch + 256 query tokens, 64 frames"}
+
+
+def scan_roofline(m, F, launches=24):
+    """HBM roofline of the RG-LRU time scan (mx_rglru_scan) at the clip shape: F frames x 1280 tokens x 768
+    channels. Algorithmic bytes per launch: A, B (fp32) and yg (bf16) read and z (bf16) written per (frame, token,
+    channel), the fp32 state read and written once: 12 F T C + 8 T C. Timed with HIP events on the launching stream
+    over `launches` launches, each on its own buffers (cold: 24 x 160 MB is far past the 256 MB MALL)."""
+    import torch
+    from strix_halo_maxx_amd import _lib
+    dev, T, C = m.dev, m.T, m.D
+    g = torch.Generator(device=dev).manual_seed(3)
+    bufs = []
+    for _ in range(launches):
+        A = torch.rand(F, T, C, device=dev, generator=g)
+        B = torch.randn(F, T, C, device=dev, generator=g)
+        yg = torch.randn(F, T, 2 * C, device=dev, generator=g).to(torch.bfloat16)
+        bufs.append((A, B, torch.zeros(T, C, device=dev), yg, torch.empty(F, T, C, device=dev, dtype=torch.bfloat16)))
+    run = lambda b: _lib.call("mx_rglru_scan", _lib.stream(), b[0].data_ptr(), b[1].data_ptr(), b[2].data_ptr(), F,
+                              T, C, b[3].data_ptr(), 2 * C, T * 2 * C, b[4].data_ptr(), C, T * C)
+    for b in bufs[:2]:
+        run(b)
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for b in bufs:
+        run(b)
+    e1.record(st)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / launches
+    nbytes = 12 * F * T * C + 8 * T * C
+    del bufs
+    torch.cuda.empty_cache()
+    return {"bound": "hbm", "kernel": "rglru_chain_kernel", "achieved": round(nbytes / us / 1e3, 1),
+            "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(nbytes / us / 1e3 / (PEAK_HBM / 1e9), 4),
+            "avg_launch_us": round(us, 2), "bytes_per_launch": nbytes}
 
 
 def tower_time(vt, img, steps, warmup):

@@ -685,8 +685,9 @@ extern "C" int mx_embed_step(hipStream_t st, const unsigned long long* part, int
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
-// ws: >= H * S * 66 floats (split partials); cnt: unused (kept for ABI stability, may be null). Two launches:
-// the split-KV pass and the per-head merge (a kernel boundary instead of a device-scope fence + counter).
+// One launch, one 1024-thread workgroup per head: every key of the context is covered by the 16 waves' loads of one
+// pass (contexts up to 16 x 8 x 8 = 1024 keys per pass, more in further passes), merged in LDS. S, ws and cnt are
+// unused (a split-KV form across workgroups measured no faster) and kept for ABI stability; ws / cnt may be null.
 extern "C" int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H,
                               int ctx, const int* state, int S, float scale, float* ws, int* cnt, uint16_t* out) {
   (void)S;

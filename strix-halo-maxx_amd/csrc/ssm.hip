@@ -14,9 +14,14 @@
 //   mx_ssm_step  one streamed frame: h (fp32 state) updated in place, z written (the model.step contract)
 //   mx_ssm_prep + mx_rglru_scan  a clip of F frames at once: prep writes the per-frame affine map h -> A h + B
 //                (A = a, B = bf(g * mult); first frame A = 0, B = g) for every (frame, token, channel) in one launch,
-//                then the scan composes the maps along time with a 64-lane wave scan (one lane per frame, shuffle
-//                steps 1, 2, 4, .., 32) and writes z for every frame. Same h as the streamed loop up to fp32
-//                reassociation.
+//                then the scan runs the maps along time and writes z for every frame. Two scan kernels:
+//                * chains (the clip shapes): one thread per (token, 4 channels) applies h = A h + B frame by frame,
+//                  with the loads of 2 frames issued together; T C / 4 independent chains fill the GPU, every
+//                  access is a coalesced stream, and h / z equal the streamed loop bit for bit (same operations in
+//                  the same order);
+//                * wave-parallel (too few chains to fill the GPU): one lane per frame, the maps composed with a
+//                  64-lane shuffle scan (steps 1, 2, 4, .., 32); same h as the streamed loop up to fp32
+//                  reassociation.
 // Crop form (mx_ssm_step_rows, one streamed frame of a moving crop of patch tokens): token t's state lives in row
 // rows[t] of the absolute state buffers (h, the history taps, the 32 x 32 patch grid + query rows), so the state
 // moves with the image content and nothing is copied. Tokens that leave the crop drop their state and tokens that
@@ -245,6 +250,46 @@ __global__ __launch_bounds__(256) void rglru_scan_kernel(const float* __restrict
   if (lane < 16 && c0 + wave * 16 + lane < C) h[(long)token * C + c0 + wave * 16 + lane] = carry;
 }
 
+// ---- chain scan: thread = (token, 4 consecutive channels), frames in order
+constexpr int CHF = 2;  // frames whose loads are issued before their arithmetic (2-4 measured best: occupancy)
+
+__global__ __launch_bounds__(256) void rglru_chain_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                          long fs_ab, float* __restrict__ h, int F, int T, int C,
+                                                          const uint16_t* __restrict__ yg, long ld_y, long fs_y,
+                                                          uint16_t* __restrict__ z, long ld_z, long fs_z) {
+  const int c4n = C >> 2;
+  const long i = blockIdx.x * 256L + threadIdx.x;
+  if (i >= (long)T * c4n) return;
+  const int t = (int)(i / c4n), c = (int)(i % c4n) * 4;
+  const long o = (long)t * C + c;
+  f32x4 hv = *reinterpret_cast<const f32x4*>(h + o);
+  for (int f0 = 0; f0 < F; f0 += CHF) {
+    const int nf = min(CHF, F - f0);
+    f32x4 av[CHF], bv[CHF];
+    u32x2 yv[CHF];
+#pragma unroll
+    for (int k = 0; k < CHF; k++) {
+      if (k < nf) {
+        const long f = f0 + k;
+        av[k] = *reinterpret_cast<const f32x4*>(A + f * fs_ab + o);
+        bv[k] = *reinterpret_cast<const f32x4*>(B + f * fs_ab + o);
+        yv[k] = *reinterpret_cast<const u32x2*>(yg + f * fs_y + (long)t * ld_y + c);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < CHF; k++) {
+      if (k < nf) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) hv[e] = __fadd_rn(__fmul_rn(av[k][e], hv[e]), bv[k][e]);
+        const u32x2 zo = {pack2(rbf(hv[0]) * lo_bf(yv[k].x), rbf(hv[1]) * hi_bf(yv[k].x)),
+                          pack2(rbf(hv[2]) * lo_bf(yv[k].y), rbf(hv[3]) * hi_bf(yv[k].y))};
+        *reinterpret_cast<u32x2*>(z + (long)(f0 + k) * fs_z + (long)t * ld_z + c) = zo;
+      }
+    }
+  }
+  *reinterpret_cast<f32x4*>(h + o) = hv;
+}
+
 int check_common(const SsmArgs& p, int F) {
   for (int i = 0; i < 4; i++)
     if (!p.tap[i]) return MX_ENULL;
@@ -315,7 +360,15 @@ extern "C" int mx_rglru_scan(hipStream_t st, const float* A, const float* B, flo
                              const uint16_t* yg, long ld_y, long fs_y, uint16_t* z, long ld_z, long fs_z) {
   if (!A || !B || !h || !yg || !z) return MX_ENULL;
   if (F < 1 || T < 1 || T > 65535 || C % 64) return MX_ESHAPE;
-  hipLaunchKernelGGL(rglru_scan_kernel, dim3(C / SC, T), dim3(256), 0, st, A, B, (long)T * C, h, F, C, yg, ld_y,
-                     fs_y, z, ld_z, fs_z);
+  // chains when they fill the GPU (>= 64 K of them: 256 CUs x 256 threads) and the rows allow 16 / 8-byte accesses
+  const long chains = (long)T * C / 4;
+  const bool aligned = !(((uintptr_t)A | (uintptr_t)B | (uintptr_t)h) & 15) && !(((uintptr_t)yg | (uintptr_t)z) & 7) &&
+                       ld_y % 4 == 0 && fs_y % 4 == 0 && ld_z % 4 == 0 && fs_z % 4 == 0;
+  if (chains >= 65536 && aligned)
+    hipLaunchKernelGGL(rglru_chain_kernel, dim3((unsigned)((chains + 255) / 256)), dim3(256), 0, st, A, B,
+                       (long)T * C, h, F, T, C, yg, ld_y, fs_y, z, ld_z, fs_z);
+  else
+    hipLaunchKernelGGL(rglru_scan_kernel, dim3(C / SC, T), dim3(256), 0, st, A, B, (long)T * C, h, F, C, yg, ld_y,
+                       fs_y, z, ld_z, fs_z);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
