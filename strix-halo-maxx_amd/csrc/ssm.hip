@@ -76,6 +76,34 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   const int c0 = q * 64;
   const int tnow = *p.frame + f;
   const bool first = tnow == 0;
+  // this thread's slots in the gate products' result layout (lane = channel, registers = 16 tokens)
+  const int tm = wave >> 1, tn = wave & 1;
+  const int cl = tn * 32 + lr, c = c0 + cl;
+
+  // ---- step form: the fp32 state and yg of this thread's 16 (token, channel) slots are loaded first, so their
+  // latency runs under the conv and the gate products (each slot belongs to this thread alone)
+  float hpre[16], ypre[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    hpre[r] = 0.f;
+    ypre[r] = 0.f;
+  }
+  if (p.mode == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int token = t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
+      if (token < p.T) {
+        const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;
+        bool fresh = false;
+        if (p.rows && !first) {
+          int enter;
+          row_stamp(p, row, tnow, fresh, enter);
+        }
+        if (!first && !fresh) hpre[r] = p.h[(long)row * p.C + c];
+        ypre[r] = bf2f(p.yg[f * p.fs_y + (long)token * p.ld_y + c]);
+      }
+    }
+  }
 
   // ---- temporal conv of this 64 x 64 tile into LDS (8 channels per item, 2 items per thread)
 #pragma unroll
@@ -128,7 +156,6 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   __syncthreads();
 
   // ---- gates: wave -> 32 tokens (tm) x 32 output channels (tn) of both gates
-  const int tm = wave >> 1, tn = wave & 1;
   f32x16 gx, ga;
 #pragma unroll
   for (int e = 0; e < 16; e++) { gx[e] = 0.f; ga[e] = 0.f; }
@@ -143,7 +170,6 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   }
 
   // ---- elementwise RG-LRU: lane = channel, registers = 16 tokens
-  const int cl = tn * 32 + lr, c = c0 + cl;
   const float spc = bf2f(p.sp[c]), bxc = bf2f(p.bx[c]), bac = bf2f(p.ba[c]);
 #pragma unroll
   for (int r = 0; r < 16; r++) {
@@ -169,16 +195,9 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
     const long idx = (long)token * p.C + c;
     if (p.mode == 0) {
       const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;
-      float* hp = p.h + (long)row * p.C + c;
-      bool fresh = false;
-      if (p.rows && !first) {
-        int enter;
-        row_stamp(p, row, tnow, fresh, enter);
-      }
-      const float h = first ? g : __fadd_rn(__fmul_rn(Am, fresh ? 0.f : *hp), Bm);
-      *hp = h;
-      const float yv = bf2f(p.yg[f * p.fs_y + (long)token * p.ld_y + c]);
-      p.z[f * p.fs_z + (long)token * p.ld_z + c] = f2bf(rbf(h) * yv);
+      const float h = first ? g : __fadd_rn(__fmul_rn(Am, hpre[r]), Bm);  // hpre = 0 for a fresh crop row
+      p.h[(long)row * p.C + c] = h;
+      p.z[f * p.fs_z + (long)token * p.ld_z + c] = f2bf(rbf(h) * ypre[r]);
     } else {
       p.A[f * p.fs_ab + idx] = Am;
       p.B[f * p.fs_ab + idx] = Bm;
