@@ -231,6 +231,65 @@ def summarize_traffic(fetch_csv, write_csv, reps=3):
             "kernel):\n\n```json\n" + json.dumps(blob, indent=1) + "\n```\n")
 
 
+def summarize_counters(paths, reps=3):
+    """Markdown table of per-op rocprofv3 --pmc counters over `bench.py --traffic-probe` (the probe dispatches sit
+    between the run's last two marker fills, `reps` x 27 per op class, in op_classes order): MfmaUtil (percent of the
+    active cycles the MFMA units were busy), fractions of the wave time (SQ_WAVE_CYCLES) spent waiting (s_waitcnt /
+    barriers), stalled at issue, and issuing VALU / LDS / VMEM instructions, LDS bank-conflict cycles per launch, and
+    the L2 hit rate, for whichever of these counters the CSVs hold (several passes: one CSV each). When a CSV holds a
+    counter another one also holds, the later CSV's value is used."""
+    import csv
+    import torch
+    import strix_halo_maxx_amd.md2 as md2
+    import strix_halo_maxx_amd.synth as S
+    vt = md2.VisionTower(S.vision_weights(0), device=torch.device("cuda:0"))
+    img = S.images_u8(1, 1).to("cuda:0")
+    with torch.inference_mode():
+        vt(img)
+        classes = op_classes(vt, img)
+    per = reps * len(vt.blocks)
+    vals = {}
+    for path in paths:
+        with open(path) as f:
+            names = {r["Counter_Name"] for r in csv.DictReader(f)}
+        for counter in sorted(names):
+            seq = _pmc_sequence(path, counter)
+            if counter == "MfmaUtil":  # a percentage: the mean over the dimension rows, not their sum
+                rows = {}
+                with open(path) as f:
+                    for r in csv.DictReader(f):
+                        if r["Counter_Name"] == counter:
+                            rows.setdefault(int(r["Dispatch_Id"]), []).append(float(r["Counter_Value"]))
+                seq = [(k, sum(rows[d]) / len(rows[d])) for (k, _), d in zip(seq, sorted(rows))]
+            fills = [i for i, (k, _) in enumerate(seq) if "FillFunctor" in k]
+            probe = seq[fills[-2] + 1:fills[-1]]
+            if len(probe) != per * len(classes):
+                raise RuntimeError(f"{counter}: {len(probe)} probe dispatches")
+            vals[counter] = [sum(v for _, v in probe[j * per:(j + 1) * per]) / per for j in range(len(classes))]
+    cols = []
+    g = lambda c, j: vals[c][j] if c in vals else None
+    if "MfmaUtil" in vals:
+        cols.append(("MfmaUtil %", lambda j: f"{g('MfmaUtil', j):.1f}"))
+    if "SQ_WAVE_CYCLES" in vals:
+        for c, lab in (("SQ_WAIT_ANY", "waiting (waitcnt, barrier) / wave time"),
+                       ("SQ_WAIT_INST_ANY", "issue-stalled / wave time"),
+                       ("SQ_WAIT_INST_LDS", "LDS-issue-stalled / wave time"),
+                       ("SQ_ACTIVE_INST_VALU", "VALU + MFMA issue / wave time"),
+                       ("SQ_ACTIVE_INST_LDS", "LDS issue / wave time"),
+                       ("SQ_INST_CYCLES_VMEM_RD", "VMEM-read issue / wave time")):
+            if c in vals:
+                cols.append((lab, lambda j, c=c: f"{g(c, j) / g('SQ_WAVE_CYCLES', j):.2f}"))
+    if "SQ_LDS_BANK_CONFLICT" in vals:
+        cols.append(("LDS bank-conflict cycles", lambda j: f"{g('SQ_LDS_BANK_CONFLICT', j):,.0f}"))
+    if "TCC_HIT_sum" in vals and "TCC_MISS_sum" in vals:
+        cols.append(("L2 hit rate", lambda j: f"{g('TCC_HIT_sum', j) / (g('TCC_HIT_sum', j) + g('TCC_MISS_sum', j)):.2f}"))
+    head = "| op | kernel | " + " | ".join(c for c, _ in cols) + " |"
+    rows = [head, "|" + "---|" * (len(cols) + 2)]
+    for j, (label, (ksym, _, _, _)) in enumerate(classes.items()):
+        rows.append(f"| {label} | `{ksym}` | " + " | ".join(fn(j) for _, fn in cols) + " |")
+    return "\n".join(rows) + "\n"
+
+
 def summarize_trace(trace_csv, top=30):
     """Kernel-trace rows grouped by (kernel, workgroups x threads): calls, mean / median / total duration."""
     import csv
@@ -468,7 +527,12 @@ def main():
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic summary of two --pmc passes over --traffic-probe (see summarize_traffic)")
     ap.add_argument("--summarize-trace", metavar="TRACE_CSV", help="print a rocprofv3 kernel trace grouped by kernel")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="PMC_CSV",
+                    help="print per-op MFMA / wait / LDS / L2 counters of --pmc passes over --traffic-probe")
     a = ap.parse_args()
+    if a.summarize_counters:
+        print(summarize_counters(a.summarize_counters))
+        return
     if a.summarize_trace:
         print(summarize_trace(a.summarize_trace))
         return
