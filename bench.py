@@ -291,15 +291,19 @@ def summarize_counters(paths, reps=3):
 
 
 def summarize_trace(trace_csv, top=30):
-    """Kernel-trace rows grouped by (kernel, workgroups x threads): calls, mean / median / total duration."""
+    """Kernel-trace rows grouped by (kernel, workgroups x threads per workgroup): calls, mean / median / total
+    duration. Workgroups count the whole (X, Y, Z) grid."""
     import csv
     groups = {}
     with open(trace_csv) as f:
         for r in csv.DictReader(f):
             k = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "")
             k = k[:k.index("(")] if "(" in k and "<" not in k[:k.index("(")] else k[:k.rfind(">") + 1] if ">" in k else k
-            wg = int(r["Workgroup_Size_X"])
-            key = (k[:58], int(r["Grid_Size_X"]) // wg, wg)
+            wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+            nwg = 1
+            for ax in "XYZ":
+                nwg *= int(r[f"Grid_Size_{ax}"]) // int(r[f"Workgroup_Size_{ax}"])
+            key = (k[:58], nwg, wg)
             groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     lines = [f"{'kernel':58s} {'workgroups':>12s} {'calls':>6s} {'mean_us':>9s} {'median_us':>9s} {'total_ms':>9s}"]
     for (k, g, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:

@@ -215,8 +215,8 @@ int mx_rglru_scan(hipStream_t st, const float* A, const float* B, float* h, int 
  * LayerNorm -> GELU erf -> Linear(H,NO) in fp32, and the coordinate head's two n-bin halves read out as
  * E[i] under softmax(0.5 logits) masked to |argmax - i| <= radius, renormalised, + 0.5.
  * Weight blob per head (fp32): W0^T [D][H] | b0 | g0 | beta0 | W1^T [H][H] | b1 | g1 | beta1 | W2^T [H][NO] | b2.
- * x: bf16 rows (stride ldx); outputs fp32 tracks (Q, 2), logits (Q, NOC) stride ldl, vis (Q). H <= 256, NOC even
- * with NOC / 2 <= 512. */
+ * x: bf16 rows (stride ldx); outputs fp32 tracks (Q, 2), logits (Q, NOC) stride ldl, vis (Q). D and H multiples
+ * of 32, H <= 256, NOC even and <= 512. */
 long mx_track_head_blob_elems(int D, int H, int NO);
 int mx_track_heads(hipStream_t st, const uint16_t* x, long ldx, int Q, int D, int H, const float* cblob, int NOC,
                    float ce0, float ce1, const float* vblob, float ve0, float ve1, int radius, float* tracks,

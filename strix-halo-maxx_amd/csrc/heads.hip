@@ -6,10 +6,13 @@
 // the expectation of the bin index under softmax(0.5 * logits) restricted to bins within `radius` of the argmax
 // (first index among equal maxima), plus 0.5. The visibility head's single output is the visibility logit.
 //
-// Layout: one workgroup of 256 threads per (pair of query rows, head). The query rows are staged in LDS as fp32;
-// thread j owns hidden unit j (H <= 256) and walks the transposed weights W^T[k][j], so every weight load is a
-// coalesced row of W^T shared by the workgroup's QB query rows. Sums run in a fixed order (k ascending for the dot
-// products, lanes then waves for the reductions), so the result does not depend on the launch.
+// Layout: one workgroup of 512 threads (8 waves) per (pair of query rows, head). The query rows are staged in LDS as
+// fp32. In a hidden layer, thread t owns hidden unit j = t % 256 (H <= 256) for the k half t / 256 and walks the
+// transposed weights W^T[k][j] of that half with 16 loads in flight, so every weight load is a coalesced row of W^T
+// shared by the workgroup's QB query rows; the halves' sums meet in LDS (half 0 + half 1). The output Linear gives
+// each thread one output column over the whole K (the single visibility output: a block reduction). Two waves per
+// SIMD keep the load latency of one under the other's work. Sums run in a fixed order (k ascending within a half,
+// then the halves; lanes then waves for the reductions), so the result does not depend on the launch.
 //
 // Weight blob of one head (fp32, contiguous):
 //   W0T [D][H] | b0 [H] | g0 [H] | beta0 [H] | W1T [H][H] | b1 [H] | g1 [H] | beta1 [H] | W2T [H][NO] | b2 [NO]
@@ -17,10 +20,14 @@
 
 namespace {
 
-constexpr int NT = 256;  // threads per workgroup
-constexpr int QB = 2;    // query rows per workgroup
+constexpr int NT = 512;       // threads per workgroup (8 waves: measured 54 us per frame's heads, 4 waves 75, 16 waves 80)
+constexpr int NWV = NT / 64;  // waves per workgroup
+constexpr int HU = 256;       // hidden units per k part (the hidden width is at most HU)
+constexpr int NP = NT / HU;   // k parts of a hidden layer
+constexpr int QB = 2;         // query rows per workgroup
+constexpr int KU = 16;        // weight loads a thread issues before their products
 
-// Block-wide sums of QB values per thread (every thread gets the totals). red: 4 waves x QB floats of LDS.
+// Block-wide sums of QB values per thread (every thread gets the totals). red: NWV waves x QB floats of LDS.
 __device__ __forceinline__ void block_sum(float (&v)[QB], float* red) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
@@ -31,37 +38,62 @@ __device__ __forceinline__ void block_sum(float (&v)[QB], float* red) {
     for (int r = 0; r < QB; r++) red[w * QB + r] = v[r];
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < QB; r++) v[r] = ((red[r] + red[QB + r]) + red[2 * QB + r]) + red[3 * QB + r];
+  for (int r = 0; r < QB; r++) {
+    float t = red[r];
+#pragma unroll
+    for (int ww = 1; ww < NWV; ww++) t = t + red[ww * QB + r];
+    v[r] = t;
+  }
 }
 
-// y[r][j] = GELU(LN(sum_k x[r][k] W^T[k][j] + b[j])) for j < H (thread j), r < nr; x and y in LDS.
+// acc[r] += sum over k in [k0, k1) of x[r][k] W^T[k][col], k ascending, KU loads issued ahead of their products.
+__device__ __forceinline__ void dot_col(const float* x, int ldxs, int k0, int k1, const float* __restrict__ WT, long ldw,
+                                        int col, float (&acc)[QB]) {
+  for (int k = k0; k < k1; k += KU) {
+    float w[KU];
+#pragma unroll
+    for (int u = 0; u < KU; u++) w[u] = WT[(long)(k + u) * ldw + col];
+#pragma unroll
+    for (int u = 0; u < KU; u++)
+#pragma unroll
+      for (int r = 0; r < QB; r++) acc[r] = acc[r] + x[r * ldxs + k + u] * w[u];
+  }
+}
+
+// y[r][j] = GELU(LN(sum_k x[r][k] W^T[k][j] + b[j])) for j < H, r < QB; x and y in LDS. part: LDS for the k parts
+// 1 .. NP - 1's partial sums ([NP - 1][QB][HU]), added to part 0's in part order.
 __device__ void dense_ln_gelu(const float* x, int ldxs, int K, const float* __restrict__ WT, const float* b,
-                              const float* g, const float* be, float eps, int H, float* y, int ldys, float* red) {
-  const int j = threadIdx.x;
+                              const float* g, const float* be, float eps, int H, float* y, int ldys, float* red,
+                              float* part) {
+  const int j = threadIdx.x % HU, kp = threadIdx.x / HU;
   float acc[QB];
 #pragma unroll
   for (int r = 0; r < QB; r++) acc[r] = 0.f;
-  if (j < H) {
-    for (int k = 0; k < K; k++) {
-      const float w = WT[(long)k * H + j];
+  if (j < H) dot_col(x, ldxs, kp * (K / NP), (kp + 1) * (K / NP), WT, H, j, acc);
+  if (kp > 0 && j < H)
 #pragma unroll
-      for (int r = 0; r < QB; r++) acc[r] = acc[r] + x[r * ldxs + k] * w;
+    for (int r = 0; r < QB; r++) part[((kp - 1) * QB + r) * HU + j] = acc[r];
+  __syncthreads();
+  const bool mine = kp == 0 && j < H;
+  if (mine)
+#pragma unroll
+    for (int r = 0; r < QB; r++) {
+#pragma unroll
+      for (int q = 1; q < NP; q++) acc[r] = acc[r] + part[((q - 1) * QB + r) * HU + j];
+      acc[r] = acc[r] + b[j];
     }
-#pragma unroll
-    for (int r = 0; r < QB; r++) acc[r] = acc[r] + b[j];
-  }
   float s[QB];
 #pragma unroll
-  for (int r = 0; r < QB; r++) s[r] = j < H ? acc[r] : 0.f;
+  for (int r = 0; r < QB; r++) s[r] = mine ? acc[r] : 0.f;
   block_sum(s, red);
   float mu[QB], d[QB];
 #pragma unroll
   for (int r = 0; r < QB; r++) {
     mu[r] = s[r] / (float)H;
-    d[r] = j < H ? (acc[r] - mu[r]) * (acc[r] - mu[r]) : 0.f;
+    d[r] = mine ? (acc[r] - mu[r]) * (acc[r] - mu[r]) : 0.f;
   }
   block_sum(d, red);
-  if (j < H) {
+  if (mine) {
 #pragma unroll
     for (int r = 0; r < QB; r++) {
       const float var = d[r] / (float)H;
@@ -91,7 +123,8 @@ __global__ void __launch_bounds__(NT) track_heads_kernel(
   float* h0 = xs + QB * D;          // [QB][H]
   float* h1 = h0 + QB * H;          // [QB][H]
   float* os = h1 + QB * H;          // [QB][NOC]
-  float* red = os + QB * NOC;       // [4][QB] (sums), [4][2] (argmax)
+  float* part = os + QB * NOC;      // [NP - 1][QB][HU] k-part partial sums
+  float* red = part + (NP - 1) * QB * HU;  // [NWV][QB] (sums), then [NWV] argmax indices
   for (int e = tid; e < QB * D; e += NT) {
     const int r = e / D, k = e - r * D;
     xs[e] = r < nr ? bf2f(x[(long)(q0 + r) * ldx + k]) : 0.f;
@@ -103,32 +136,35 @@ __global__ void __launch_bounds__(NT) track_heads_kernel(
   const float *b1 = W1 + (long)H * H, *g1 = b1 + H, *be1 = g1 + H;
   const float* W2 = be1 + H;
   const float* b2 = W2 + (long)H * NO;
-  dense_ln_gelu(xs, D, D, W0, b0, g0, be0, e0, H, h0, H, red);
-  dense_ln_gelu(h0, H, H, W1, b1, g1, be1, e1, H, h1, H, red);
+  dense_ln_gelu(xs, D, D, W0, b0, g0, be0, e0, H, h0, H, red, part);
+  dense_ln_gelu(h0, H, H, W1, b1, g1, be1, e1, H, h1, H, red, part);
+  if (head) {
+    // the one visibility output: thread k < H holds the product of hidden unit k, summed over the block
+    float pv[QB];
+#pragma unroll
+    for (int r = 0; r < QB; r++) pv[r] = tid < H ? h1[r * H + tid] * W2[tid] : 0.f;
+    block_sum(pv, red);
+#pragma unroll
+    for (int r = 0; r < QB; r++)
+      if (tid == r && r < nr) vis[q0 + r] = pv[r] + b2[0];
+    return;
+  }
   for (int o = tid; o < NO; o += NT) {
     float acc[QB];
 #pragma unroll
     for (int r = 0; r < QB; r++) acc[r] = 0.f;
-    for (int k = 0; k < H; k++) {
-      const float w = W2[(long)k * NO + o];
-#pragma unroll
-      for (int r = 0; r < QB; r++) acc[r] = acc[r] + h1[r * H + k] * w;
-    }
+    dot_col(h1, H, 0, H, W2, NO, o, acc);
 #pragma unroll
     for (int r = 0; r < QB; r++) os[r * NOC + o] = acc[r] + b2[o];
   }
   __syncthreads();
-  if (head) {
-    if (tid < nr) vis[q0 + tid] = os[tid * NOC];
-    return;
-  }
   for (int e = tid; e < nr * NOC; e += NT) {
     const int r = e / NOC, o = e - r * NOC;
     logits[(long)(q0 + r) * ldl + o] = os[r * NOC + o];
   }
   // ---- windowed soft-argmax of each n-bin half, one (row, half) at a time
   const int n = NOC / 2, lane = tid & 63, w = tid >> 6;
-  float* redi = red + 4 * QB;
+  float* redi = red + NWV * QB;
   for (int r = 0; r < nr; r++) {
     for (int half = 0; half < 2; half++) {
       const float* z = os + r * NOC + half * n;
@@ -146,7 +182,7 @@ __global__ void __launch_bounds__(NT) track_heads_kernel(
       __syncthreads();
       float mv = red[0];
       int am = __float_as_int(redi[0]);
-      for (int ww = 1; ww < 4; ww++) arg_better(mv, am, red[ww], __float_as_int(redi[ww]));
+      for (int ww = 1; ww < NWV; ww++) arg_better(mv, am, red[ww], __float_as_int(redi[ww]));
       const float zmax = 0.5f * mv;
       // softmax over all n bins, then the window mask, then renormalised (the order of the readout's definition)
       float es[2], s1[QB] = {}, s2[QB] = {}, s3[QB] = {};
@@ -188,13 +224,15 @@ extern "C" long mx_track_head_blob_elems(int D, int H, int NO) {
 extern "C" int mx_track_heads(hipStream_t st, const uint16_t* x, long ldx, int Q, int D, int H, const float* cblob,
                               int NOC, float ce0, float ce1, const float* vblob, float ve0, float ve1, int radius,
                               float* tracks, float* logits, long ldl, float* vis) {
-  // H <= 256: one hidden unit per thread; NOC / 2 <= 512: the readout covers at most 2 bins per thread
-  if (Q < 0 || D < 1 || D > 4096 || H < 1 || H > NT || NOC < 2 || NOC % 2 || NOC / 2 > 2 * NT || radius < 0 ||
-      ldx < D || ldl < NOC)
+  // H <= 256: one hidden unit per thread of a k part; D, H multiples of 32: whole KU groups in each of the 2 k parts;
+  // NOC <= 512: one output column per thread, at most 2 bins per thread in the readout
+  if (Q < 0 || D < 64 || D > 4096 || D % (KU * NP) || H < 64 || H > HU || H % (KU * NP) || NOC < 2 || NOC % 2 ||
+      NOC > 512 || radius < 0 || ldx < D || ldl < NOC)
     return MX_ESHAPE;
   if (Q == 0) return MX_OK;
   if (!x || !cblob || !vblob || !tracks || !logits || !vis) return MX_ENULL;
-  const size_t smem = sizeof(float) * ((size_t)QB * D + 2 * QB * H + (size_t)QB * NOC + 8 * QB + 8);
+  const size_t smem =
+      sizeof(float) * ((size_t)QB * D + 2 * QB * H + (size_t)QB * NOC + (NP - 1) * QB * HU + 2 * NWV * QB);
   if (smem > 160 * 1024) return MX_ESHAPE;
   hipLaunchKernelGGL(track_heads_kernel, dim3((Q + QB - 1) / QB, 2), dim3(NT), smem, st, x, ldx, Q, D, H, cblob, NOC,
                      ce0, ce1, vblob, ve0, ve1, radius, tracks, logits, ldl, vis);
