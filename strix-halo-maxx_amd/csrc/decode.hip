@@ -185,8 +185,8 @@ __global__ __launch_bounds__(256) void gemv_dual_res_kernel(const uint16_t* __re
 
 // ---------------------------------------------------------------------------------------------- W8A8 GEMVs
 // The reference's W8A8 text linears (moondream/gpu/hgemm.py:95-137) at batch 1: int8 weight rows (per-row scale sw),
-// the activation row quantised per token (s = max(amax, 1e-5) / 127, q = trunc(v + 0.5 sign), tgemm.py:81-91) by every
-// wave from the whole row it holds, int8 dot products (v_dot4) summed exactly in int32, then the fp32 dequant
+// the activation row quantised per token (s = max(amax, 1e-5) / 127, q = trunc(v + 0.5 sign), tgemm.py:81-91) once
+// per workgroup into LDS, int8 dot products (v_dot4) summed exactly in int32, then the fp32 dequant
 // ((acc * s) * sw) + b and any GELU on that fp32 value before the one bf16 rounding (i8gemm.hip:181-197).
 // Layout: a row of K int8 is K / 16 chunks of 16 bytes; lane l holds chunks l + 64 j (j < KI), i.e. elements
 // 16 (l + 64 j) .. +15, and loads the activation values at the same positions (two 8-wide bf16 chunks per int8 chunk).
@@ -215,83 +215,77 @@ __device__ __forceinline__ int reduce_rows_i(int (&v)[R], int lane) {
   return t;
 }
 
-// The activation row in int8-chunk order: xc[2 j], xc[2 j + 1] = bf16 elements 16 (lane + 64 j) .. +7, +8 .. +15.
-template <int KI>
-__device__ __forceinline__ void load_vec_i8order(u32x4 (&xc)[2 * KI], const uint16_t* x, int lane) {
-#pragma unroll
-  for (int j = 0; j < KI; j++) {
-    xc[2 * j] = *reinterpret_cast<const u32x4*>(x + (lane + 64 * j) * 16);
-    xc[2 * j + 1] = *reinterpret_cast<const u32x4*>(x + (lane + 64 * j) * 16 + 8);
-  }
-}
-
-// Per-token quantisation of the row held as in load_vec_i8order (every lane ends with the same scale); returns s.
-template <int KI>
-__device__ __forceinline__ float quant_row_i8(const u32x4 (&xc)[2 * KI], i32x4v (&q)[KI]) {
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 2 * KI; i++)
-#pragma unroll
-    for (int e = 0; e < 4; e++) amax = fmaxf(amax, fmaxf(fabsf(lo_bf(xc[i][e])), fabsf(hi_bf(xc[i][e]))));
-  amax = wave_max(amax);
-  const float s = fmaxf(amax, 1e-5f) / 127.0f;
-#pragma unroll
-  for (int j = 0; j < KI; j++)
-#pragma unroll
-    for (int w = 0; w < 4; w++) {  // int32 word w of chunk j: elements 4 w .. 4 w + 3
-      uint32_t word = 0u;
-#pragma unroll
-      for (int b = 0; b < 4; b++) {
-        const int e = 4 * w + b;  // element within the 16-wide chunk
-        const uint32_t u = xc[2 * j + (e >> 3)][(e & 7) >> 1];
-        const float f = (e & 1) ? hi_bf(u) : lo_bf(u);
-        const float t = f / s;
-        const int qi = (int)(t + (t >= 0.f ? 0.5f : -0.5f));
-        word |= ((uint32_t)qi & 0xffu) << (8 * b);
-      }
-      q[j][w] = (int)word;
-    }
-  return s;
-}
-
+// 16 int8 x int8 products of one activation chunk and one weight chunk (4 packed words each), added to acc.
 __device__ __forceinline__ int dot16_i8(const i32x4v& a, const u32x4& b, int acc) {
 #pragma unroll
   for (int w = 0; w < 4; w++) acc = __builtin_amdgcn_sdot4(a[w], (int)b[w], acc, false);
   return acc;
 }
 
-// LN (fp32 statistics, one rounding) of a row held in int8-chunk order, gamma / beta read at the same positions.
-template <int KI>
-__device__ __forceinline__ void ln_i8order(u32x4 (&xc)[2 * KI], const uint16_t* gamma, const uint16_t* beta, float eps,
-                                           int K, int lane) {
-  float s = 0.f;
+// Workgroup-wide max / sum of one value per thread through red (4 floats); every thread gets the result.
+__device__ __forceinline__ float block_max4(float v, float* red) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+__device__ __forceinline__ float block_sum4(float v, float* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// Per-token int8 quantisation (tgemm.py:81-91 _quant_rows: s = max(max |x|, 1e-5) / 127, q = trunc(x / s + 0.5 sign),
+// IEEE division) of a vector of 256 E values (thread t holds values t E .. t E + E - 1, already rounded to bf16)
+// shared by the 256 threads of a workgroup, done once per workgroup: qs receives the int8 values in k order (4 per
+// word, the order of a weight row's 16-byte chunks); the scale is the workgroup's (through smax, 4 floats). The caller
+// synchronises before reading qs.
+template <int E>
+__device__ __forceinline__ float quant_vals_block_i8(const float (&f)[E], uint32_t* qs, float* smax) {
+  static_assert(E % 4 == 0, "whole words per thread");
+  float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 2 * KI; i++)
+  for (int i = 0; i < E; i++) amax = fmaxf(amax, fabsf(f[i]));
+  amax = block_max4(amax, smax);
+  const float s = fmaxf(amax, 1e-5f) / 127.0f;
 #pragma unroll
-    for (int e = 0; e < 4; e++) s += lo_bf(xc[i][e]) + hi_bf(xc[i][e]);
-  const float mean = wave_sum(s) / (float)K;
-  float ss = 0.f;
+  for (int i = 0; i < E / 4; i++) {
+    uint32_t word = 0u;
 #pragma unroll
-  for (int i = 0; i < 2 * KI; i++)
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const float d0 = lo_bf(xc[i][e]) - mean, d1 = hi_bf(xc[i][e]) - mean;
-      ss += d0 * d0 + d1 * d1;
+    for (int b = 0; b < 4; b++) {
+      const float t = f[4 * i + b] / s;
+      const int qi = (int)(t + (t >= 0.f ? 0.5f : -0.5f));
+      word |= ((uint32_t)qi & 0xffu) << (8 * b);
     }
-  const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)K + eps);
+    qs[threadIdx.x * (E / 4) + i] = word;
+  }
+  return s;
+}
+
+// This thread's E consecutive bf16 elements of x (t E .. t E + E - 1) as fp32.
+template <int E>
+__device__ __forceinline__ void load_slice(const uint16_t* __restrict__ x, float (&f)[E]) {
 #pragma unroll
-  for (int i = 0; i < 2 * KI; i++) {
-    const int off = (lane + 64 * (i >> 1)) * 16 + 8 * (i & 1);
-    const u32x4 g = *reinterpret_cast<const u32x4*>(gamma + off);
-    const u32x4 b = *reinterpret_cast<const u32x4*>(beta + off);
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-      xc[i][e] = pack2((lo_bf(xc[i][e]) - mean) * rstd * lo_bf(g[e]) + lo_bf(b[e]),
-                       (hi_bf(xc[i][e]) - mean) * rstd * hi_bf(g[e]) + hi_bf(b[e]));
+  for (int i = 0; i < E / 4; i++) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(x + threadIdx.x * E + 4 * i);
+    f[4 * i] = lo_bf(v.x);
+    f[4 * i + 1] = hi_bf(v.x);
+    f[4 * i + 2] = lo_bf(v.y);
+    f[4 * i + 3] = hi_bf(v.y);
   }
 }
 
-// [qkv | fc1] = dequant(quant(LN(x)) . Wq^T); out1 = rows < n1 (bf16), out2 = GELU rows >= n1 (act2 1 tanh, 2 erf)
+template <int E>
+__device__ __forceinline__ float quant_block_i8(const uint16_t* __restrict__ x, uint32_t* qs, float* smax) {
+  float f[E];
+  load_slice<E>(x, f);
+  return quant_vals_block_i8<E>(f, qs, smax);
+}
+
+// [qkv | fc1] = dequant(quant(LN(x)) . Wq^T); out1 = rows < n1 (bf16), out2 = GELU rows >= n1 (act2 1 tanh, 2 erf).
+// The LayerNorm and the quantisation of x run once per workgroup (thread t on elements 4 KI t ..), into LDS, while
+// the weight loads are in flight.
 template <int KI, int R>
 __global__ __launch_bounds__(256) void ln_gemv2_i8_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ gamma,
@@ -301,13 +295,16 @@ __global__ __launch_bounds__(256) void ln_gemv2_i8_kernel(const uint16_t* __rest
                                                           int N, int n1, uint16_t* __restrict__ out1,
                                                           uint16_t* __restrict__ out2, int act2) {
   constexpr int SH = 6 - (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);
+  constexpr int E = 4 * KI;  // elements of x per thread
+  __shared__ __attribute__((aligned(16))) uint32_t qs[KI * 256];
+  __shared__ float red[3][4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * R;
-  if (row0 >= N) return;
+  const bool active = row0 < N;  // every wave takes part in the workgroup's LayerNorm and quantisation (barriers)
   const int nme = row0 + (lane >> SH);
-  u32x4 xc[2 * KI];
-  load_vec_i8order<KI>(xc, x, lane);
-  const float bme = (bias && nme < N) ? bias[nme] : 0.f, swme = nme < N ? sw[nme] : 0.f;
+  float f[E];
+  load_slice<E>(x, f);
+  const float bme = (bias && active && nme < N) ? bias[nme] : 0.f, swme = active && nme < N ? sw[nme] : 0.f;
   u32x4 wv[R][KI];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -315,9 +312,28 @@ __global__ __launch_bounds__(256) void ln_gemv2_i8_kernel(const uint16_t* __rest
 #pragma unroll
     for (int j = 0; j < KI; j++) wv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (lane + 64 * j) * 16));
   }
-  if (gamma) ln_i8order<KI>(xc, gamma, beta, eps, KI * 1024, lane);
+  if (gamma) {  // torch F.layer_norm numerics: fp32 statistics, biased variance, one rounding to bf16
+    constexpr float K = KI * 1024;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < E; i++) sum += f[i];
+    const float mean = block_sum4(sum, red[0]) / K;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < E; i++) ss += (f[i] - mean) * (f[i] - mean);
+    const float rstd = 1.0f / sqrtf(block_sum4(ss, red[1]) / K + eps);
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const int k = threadIdx.x * E + i;
+      f[i] = rbf((f[i] - mean) * rstd * bf2f(gamma[k]) + bf2f(beta[k]));
+    }
+  }
+  const float sx = quant_vals_block_i8<E>(f, qs, red[2]);
+  __syncthreads();
+  if (!active) return;
   i32x4v q[KI];
-  const float sx = quant_row_i8<KI>(xc, q);
+#pragma unroll
+  for (int j = 0; j < KI; j++) q[j] = *reinterpret_cast<const i32x4v*>(&qs[4 * (lane + 64 * j)]);
   int acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -340,7 +356,8 @@ __global__ __launch_bounds__(256) void ln_gemv2_i8_kernel(const uint16_t* __rest
 }
 
 // x' = bf16(bf16(fc2(g)) + bf16(bf16(proj(a)) + x)) with both Linears W8A8 (the parallel residual of
-// md2fast.py:198 through lin_res / mlp with fused_res off)
+// md2fast.py:198 through lin_res / mlp with fused_res off). g and a are quantised once per workgroup into LDS while
+// the weight loads are in flight.
 template <int KI1, int KI2, int R>
 __global__ __launch_bounds__(256) void gemv_dual_res_i8_kernel(
     const uint16_t* __restrict__ g, const int8_t* __restrict__ W2, const float* __restrict__ sw2,
@@ -348,11 +365,13 @@ __global__ __launch_bounds__(256) void gemv_dual_res_i8_kernel(
     const float* __restrict__ swp, const float* __restrict__ bp, const uint16_t* __restrict__ xres,
     uint16_t* __restrict__ out, int N) {
   constexpr int SH = 6 - (R == 1 ? 1 : R == 2 ? 2 : R == 4 ? 3 : 4);
+  __shared__ __attribute__((aligned(16))) uint32_t qgs[KI1 * 256], qas[KI2 * 256];
+  __shared__ float smax[2][4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * R;
-  if (row0 >= N) return;
+  const bool active = row0 < N;  // every wave takes part in the workgroup's quantisation (barriers)
   const int nme = row0 + ((lane >> SH) & (R - 1));
-  const bool in = nme < N;
+  const bool in = active && nme < N;
   u32x4 w2[R][KI1], wp[R][KI2];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -366,18 +385,15 @@ __global__ __launch_bounds__(256) void gemv_dual_res_i8_kernel(
   }
   const float b2me = in ? b2[nme] : 0.f, bpme = in ? bp[nme] : 0.f, xme = in ? bf2f(xres[nme]) : 0.f;
   const float sw2me = in ? sw2[nme] : 0.f, swpme = in ? swp[nme] : 0.f;
+  const float sg = quant_block_i8<KI1 * 4>(g, qgs, smax[0]);
+  const float sa = quant_block_i8<KI2 * 4>(a, qas, smax[1]);
+  __syncthreads();
+  if (!active) return;
   i32x4v qg[KI1], qa[KI2];
-  float sg, sa;
-  {
-    u32x4 gc[2 * KI1];
-    load_vec_i8order<KI1>(gc, g, lane);
-    sg = quant_row_i8<KI1>(gc, qg);
-  }
-  {
-    u32x4 ac[2 * KI2];
-    load_vec_i8order<KI2>(ac, a, lane);
-    sa = quant_row_i8<KI2>(ac, qa);
-  }
+#pragma unroll
+  for (int j = 0; j < KI1; j++) qg[j] = *reinterpret_cast<const i32x4v*>(&qgs[4 * (lane + 64 * j)]);
+#pragma unroll
+  for (int j = 0; j < KI2; j++) qa[j] = *reinterpret_cast<const i32x4v*>(&qas[4 * (lane + 64 * j)]);
   int acc[2 * R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
