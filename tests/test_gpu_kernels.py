@@ -164,7 +164,8 @@ def test_gemm_partial_reduce_splits_vs_fp32(dev, M, K, N):
 
 def test_residual_layernorm_matches_unfused(dev):
     """x = bf16(bf16(sum P + bias) + res) bit for bit from the partials (CPU restatement, same fp32 order); the same
-    within 1 ulp of the single-pass GEMM epilogue (different summation order); y equals layernorm(x) exactly."""
+    within one ulp of the pre-rounding sum plus one of x of the single-pass GEMM epilogue (different summation order);
+    y equals layernorm(x) exactly."""
     M, K, N = 729, 1152, 1152
     g = gen(11)
     x = torch.randn(M, K, generator=g).to(BF).to(dev)
@@ -182,9 +183,15 @@ def test_residual_layernorm_matches_unfused(dev):
     acc = Pc[0].clone()
     for i in range(1, Pc.shape[0]):
         acc += Pc[i]
-    exp = ((acc + lin.b.cpu()).to(BF).float() + r.cpu().float()).to(BF)
+    gsum = acc + lin.b.cpu().float()
+    exp = (gsum.to(BF).float() + r.cpu().float()).to(BF)
     assert torch.equal(xo.cpu(), exp)
-    assert within_ulps(xo, lin(x, res=r), n=1, frac=1e-2)
+    # Another summation order may round bf16(g) one ulp the other way; after + res that is one ulp of g plus one ulp
+    # of the sum, which exceeds one ulp of the sum where g and res cancel.
+    a, f = xo.float().cpu(), lin(x, res=r).float().cpu()
+    tol = 2.0 ** -7 * (gsum.abs() + torch.maximum(a.abs(), f.abs())) + 1e-30
+    over, frac = int(((a - f).abs() > tol).sum()), (a != f).float().mean().item()
+    assert over == 0 and frac <= 1e-2, (P.shape[0], over, frac)
     assert torch.equal(yo.cpu(), ops.layernorm(xo, gam, bet, eps=1e-6).cpu())
 
 
