@@ -4,10 +4,12 @@
 // 2 per token, all replayed from one HIP graph, with the step's position and the token living in device memory:
 //   ln_gemv2      h = LN(x) (recomputed per wave from the 4 KB row), [qkv | fc1] = h [Wqkv | Wfc1]^T + b, GELU on
 //                 the fc1 part (the reference's qkv and fc1 both read the same LN output, md2fast.py:173-198)
-//   decode_attn   rope on q / k of the new token, K/V append at `pos`, attention over keys 0..pos: one workgroup per
-//                 head, a one-pass online softmax per wave, the 16 waves merged in LDS
-//   gemv_dual_res x' = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)): the parallel residual of
-//                 md2fast.py:198 with the reference's rounding order, both GEMVs in one pass over [Wfc2 | Wproj]
+//   attn_fc2      rope on q / k of the new token, K/V append at `pos`, attention over keys 0..pos (one workgroup per
+//                 head, a one-pass online softmax per wave, the 16 waves merged in LDS) and, on workgroups of their
+//                 own in the same launch, y2 = bf16(fc2(g) + b2), which needs only the fc1 output
+//   gemv_res2     x' = bf16(y2 + bf16(bf16(proj(a) + bp) + x)): the parallel residual of md2fast.py:198 with the
+//                 reference's rounding order
+//   (decode_attn + gemv_dual_res: the same two steps as attention alone, then both GEMVs in one pass)
 //   ln_gemv_argmax  logits = LN(x) Wlm^T + b (bf16, as the reference's bf16 lm_head) and a per-workgroup argmax
 //   embed_step    reduce the per-workgroup argmaxes (first index wins ties, like torch.argmax), append the token to
 //                 the output, x = wte[token], advance the position counter
@@ -222,12 +224,17 @@ __device__ __forceinline__ int dot16_i8(const i32x4v& a, const u32x4& b, int acc
   return acc;
 }
 
-// Workgroup-wide max / sum of one value per thread through red (4 floats); every thread gets the result.
-__device__ __forceinline__ float block_max4(float v, float* red) {
+// Workgroup-wide max / sum of one value per thread through red (NW floats, NW = waves per workgroup); every thread
+// gets the result.
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* red) {
   v = wave_max(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; w++) m = fmaxf(m, red[w]);
+  return m;
 }
 __device__ __forceinline__ float block_sum4(float v, float* red) {
   v = wave_sum(v);
@@ -237,17 +244,17 @@ __device__ __forceinline__ float block_sum4(float v, float* red) {
 }
 
 // Per-token int8 quantisation (tgemm.py:81-91 _quant_rows: s = max(max |x|, 1e-5) / 127, q = trunc(x / s + 0.5 sign),
-// IEEE division) of a vector of 256 E values (thread t holds values t E .. t E + E - 1, already rounded to bf16)
-// shared by the 256 threads of a workgroup, done once per workgroup: qs receives the int8 values in k order (4 per
-// word, the order of a weight row's 16-byte chunks); the scale is the workgroup's (through smax, 4 floats). The caller
-// synchronises before reading qs.
-template <int E>
+// IEEE division) of a vector of 64 NW E values (thread t holds values t E .. t E + E - 1, already rounded to bf16)
+// shared by the 64 NW threads of a workgroup, done once per workgroup: qs receives the int8 values in k order (4 per
+// word, the order of a weight row's 16-byte chunks); the scale is the workgroup's (through smax, NW floats). The
+// caller synchronises before reading qs.
+template <int E, int NW = 4>
 __device__ __forceinline__ float quant_vals_block_i8(const float (&f)[E], uint32_t* qs, float* smax) {
   static_assert(E % 4 == 0, "whole words per thread");
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < E; i++) amax = fmaxf(amax, fabsf(f[i]));
-  amax = block_max4(amax, smax);
+  amax = block_max<NW>(amax, smax);
   const float s = fmaxf(amax, 1e-5f) / 127.0f;
 #pragma unroll
   for (int i = 0; i < E / 4; i++) {
@@ -276,11 +283,11 @@ __device__ __forceinline__ void load_slice(const uint16_t* __restrict__ x, float
   }
 }
 
-template <int E>
+template <int E, int NW = 4>
 __device__ __forceinline__ float quant_block_i8(const uint16_t* __restrict__ x, uint32_t* qs, float* smax) {
   float f[E];
   load_slice<E>(x, f);
-  return quant_vals_block_i8<E>(f, qs, smax);
+  return quant_vals_block_i8<E, NW>(f, qs, smax);
 }
 
 // [qkv | fc1] = dequant(quant(LN(x)) . Wq^T); out1 = rows < n1 (bf16), out2 = GELU rows >= n1 (act2 1 tanh, 2 erf).
@@ -518,65 +525,85 @@ constexpr int DA_UNROLL = 8;   // key rounds (8 keys per wave each) whose K and 
 // 8 (lane & 7) .. +7), and runs an online softmax over them in one pass: the K and V rows of DA_UNROLL rounds are
 // loaded together, scores reduced within each 8-lane group, the wave's running max raised (and its O, l rescaled)
 // per batch. The 16 waves' (m, l, O) are merged in LDS. P is rounded to bf16 and l sums the rounded values.
-__global__ __launch_bounds__(1024) void decode_attn_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
-                                                           uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-                                                           int H, int ctx, const int* __restrict__ state,
-                                                           float scale_log2, uint16_t* __restrict__ out) {
-  __shared__ float qs[64];
-  __shared__ uint16_t knew[64], vnew[64];
+// The body for head h, run by a 1024-thread workgroup (every thread reaches its barriers).
+__device__ __forceinline__ void attn_head(int h, const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
+                                          uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int H, int ctx,
+                                          const int* __restrict__ state, float scale_log2,
+                                          uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint16_t qs[64], knew[64], vnew[64];  // bf16 q, k, v of the new token
   __shared__ float rec[DA_W][66];  // (m, l, o[64]) of each wave
-  const int h = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = state[1];
   const int L = pos + 1;
-  const float* cp = cs + (long)pos * 32;
-  const uint16_t* src = qkv + h * 64;
-  const uint16_t* ksrc = qkv + H * 64 + h * 64;
-  const uint16_t* vsrc = qkv + 2 * H * 64 + h * 64;
+  // the rope's inputs through pointers the compiler cannot see through: loads from the read-only arguments could
+  // otherwise be moved freely, behind the cache rows' loads below
+  typedef __attribute__((address_space(1))) const float gfloat;
+  typedef __attribute__((address_space(1))) const uint16_t gu16;
+  const float* cpg = cs + (long)pos * 32;
+  const uint16_t* srcg = qkv + h * 64;
+  asm volatile("" : "+s"(cpg), "+s"(srcg));
+  gfloat* cp = (gfloat*)cpg;
+  gu16* src = (gu16*)srcg;
+  gu16* ksrc = src + H * 64;
+  gu16* vsrc = src + 2 * H * 64;
   const uint16_t* kh = kc + (long)h * ctx * 64;
   const uint16_t* vh = vc + (long)h * ctx * 64;
-  // rope of q and k for the new token (fp32, as the prefill rope kernel)
-  if (tid < 64) {
-    const int d = tid;
-    float qv, kv;
-    if (d < 32) {
-      const int j = d >> 1;
-      const float c = cp[2 * j], s = cp[2 * j + 1];
-      const float qa = bf2f(src[j]), qb = bf2f(src[16 + j]), ka = bf2f(ksrc[j]), kb = bf2f(ksrc[16 + j]);
-      qv = (d & 1) ? __fadd_rn(__fmul_rn(qa, s), __fmul_rn(qb, c)) : __fsub_rn(__fmul_rn(qa, c), __fmul_rn(qb, s));
-      kv = (d & 1) ? __fadd_rn(__fmul_rn(ka, s), __fmul_rn(kb, c)) : __fsub_rn(__fmul_rn(ka, c), __fmul_rn(kb, s));
-    } else {
-      qv = bf2f(src[d]);
-      kv = bf2f(ksrc[d]);
+  // Every wave computes the rope of q and k for the new token (lane d on dim d; fp32, as the prefill rope kernel) from
+  // loads issued before the first pass's K / V rows, so that the waits for them do not wait for the cache rows
+  // (loads complete in issue order); wave 0 publishes the results.
+  const int d = lane, jr = (d & 31) >> 1;
+  const float cr = cp[2 * jr], sr = cp[2 * jr + 1];
+  const int d0 = d < 32 ? jr : d;
+  const uint16_t q0 = src[d0], q1 = src[16 + jr], k0 = ksrc[d0], k1 = ksrc[16 + jr], vn = vsrc[d];
+  const int sub = lane & 7, kg = lane >> 3;
+  u32x4 kk[DA_UNROLL], vv[DA_UNROLL];
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  // K / V rows of one pass, loaded unconditionally (keys past L read row L - 1, so the wait counts stay exact); in the
+  // loop, keys past L become zeros (their scores are masked, and 0 * V stays finite) and the row at pos the new
+  // token's
+  auto load_pass = [&](int b0) {
+#pragma unroll
+    for (int u = 0; u < DA_UNROLL; u++) {
+      const int key = min(b0 + kg + 8 * DA_W * u, L - 1);
+      const unsigned off = (unsigned)key * 64u + (unsigned)sub * 8u;  // 32-bit offset from the head's base
+      kk[u] = *reinterpret_cast<const u32x4*>(kh + off);
+      vv[u] = *reinterpret_cast<const u32x4*>(vh + off);
     }
-    qs[d] = rbf(qv);
-    knew[d] = f2bf(kv);
-    vnew[d] = vsrc[d];
+  };
+  asm volatile("" ::: "memory");  // the rope's loads are issued first (no load moves across)
+  __builtin_amdgcn_sched_barrier(0);
+  load_pass(wave * 8);
+  {
+    // branch-free (a branch would let the compiler sink these loads behind the cache rows')
+    const float qa = bf2f(q0), qb = bf2f(q1), ka = bf2f(k0), kb = bf2f(k1);
+    const float qo = __fadd_rn(__fmul_rn(qa, sr), __fmul_rn(qb, cr)), qe = __fsub_rn(__fmul_rn(qa, cr), __fmul_rn(qb, sr));
+    const float ko = __fadd_rn(__fmul_rn(ka, sr), __fmul_rn(kb, cr)), ke = __fsub_rn(__fmul_rn(ka, cr), __fmul_rn(kb, sr));
+    const float qv = d < 32 ? ((d & 1) ? qo : qe) : qa;
+    const float kv = d < 32 ? ((d & 1) ? ko : ke) : ka;
+    if (wave == 0) {
+      qs[d] = f2bf(qv);
+      knew[d] = f2bf(kv);
+      vnew[d] = vn;
+      // append the new token's K / V to the cache (this step takes them from LDS)
+      kc[((long)h * ctx + pos) * 64 + d] = f2bf(kv);
+      vc[((long)h * ctx + pos) * 64 + d] = vn;
+    }
   }
   __syncthreads();
-  if (tid < 64) {  // append the new token's K / V to the cache (this step reads them from LDS)
-    kc[((long)h * ctx + pos) * 64 + tid] = knew[tid];
-    vc[((long)h * ctx + pos) * 64 + tid] = vnew[tid];
-  }
-  const int sub = lane & 7, kg = lane >> 3;
-  float qv[8];
-#pragma unroll
-  for (int e = 0; e < 8; e++) qv[e] = qs[sub * 8 + e];
+  const u32x4 qp = *reinterpret_cast<const u32x4*>(&qs[sub * 8]);  // q dims 8 sub .. +7, bf16 pairs
   float m_run = -1e30f, l_run = 0.f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   // the loop bound is wave-uniform (every lane takes part in the wave-wide max); keys past L are masked
   for (int b0 = wave * 8; b0 < L; b0 += 8 * DA_W * DA_UNROLL) {
+    if (b0 != wave * 8) load_pass(b0);
     const int base = b0 + kg;
-    u32x4 kk[DA_UNROLL], vv[DA_UNROLL];
 #pragma unroll
-    for (int u = 0; u < DA_UNROLL; u++) {
-      const int key = base + 8 * DA_W * u;
-      const bool cached = key < L && key != pos;
-      kk[u] = cached ? *reinterpret_cast<const u32x4*>(kh + (long)key * 64 + sub * 8)
-                     : *reinterpret_cast<const u32x4*>(&knew[sub * 8]);
-      vv[u] = cached ? *reinterpret_cast<const u32x4*>(vh + (long)key * 64 + sub * 8)
-                     : *reinterpret_cast<const u32x4*>(&vnew[sub * 8]);
-    }
+    for (int u = 0; u < DA_UNROLL; u++)
+      if (base + 8 * DA_W * u >= pos) {
+        const bool me = base + 8 * DA_W * u == pos;
+        kk[u] = me ? *reinterpret_cast<const u32x4*>(&knew[sub * 8]) : zero4;
+        vv[u] = me ? *reinterpret_cast<const u32x4*>(&vnew[sub * 8]) : zero4;
+      }
     float sv[DA_UNROLL];
     float mb = -1e30f;
 #pragma unroll
@@ -584,8 +611,8 @@ __global__ __launch_bounds__(1024) void decode_attn_kernel(const uint16_t* __res
       float s = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        s = __builtin_fmaf(lo_bf(kk[u][e]), qv[2 * e], s);
-        s = __builtin_fmaf(hi_bf(kk[u][e]), qv[2 * e + 1], s);
+        s = __builtin_fmaf(lo_bf(kk[u][e]), lo_bf(qp[e]), s);
+        s = __builtin_fmaf(hi_bf(kk[u][e]), hi_bf(qp[e]), s);
       }
       s += __shfl_xor(s, 1, 64);
       s += __shfl_xor(s, 2, 64);
@@ -640,6 +667,172 @@ __global__ __launch_bounds__(1024) void decode_attn_kernel(const uint16_t* __res
       acc += rec[w][2 + tid] * f;
     }
     out[h * 64 + tid] = f2bf(acc / Lt);
+  }
+}
+
+__global__ __launch_bounds__(1024) void decode_attn_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
+                                                           uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                           int H, int ctx, const int* __restrict__ state,
+                                                           float scale_log2, uint16_t* __restrict__ out) {
+  attn_head(blockIdx.x, qkv, cs, kc, vc, H, ctx, state, scale_log2, out);
+}
+
+// ---------------------------------------------------------------------------------------------- attention + fc2
+// The parallel residual's fc2 GEMV needs only the fc1 output, not the attention's, so it shares the attention's
+// launch: workgroups 0 .. H-1 run the attention (one head each, latency-bound on H CUs), workgroups H .. stream the
+// fc2 rows on the other CUs, one row per wave, the activation g staged in LDS while the weight row is in flight.
+// y2 = bf16(g W2^T + b2), the first rounded term of the residual sum; proj + residual follow in gemv_res2.
+template <int KC1>
+__global__ __launch_bounds__(1024) void attn_fc2_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
+                                                        uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int H,
+                                                        int ctx, const int* __restrict__ state, float scale_log2,
+                                                        uint16_t* __restrict__ attn_out, const uint16_t* __restrict__ g,
+                                                        const uint16_t* __restrict__ W2, const float* __restrict__ b2,
+                                                        uint16_t* __restrict__ y2, int N) {
+  if ((int)blockIdx.x < H) {
+    attn_head(blockIdx.x, qkv, cs, kc, vc, H, ctx, state, scale_log2, attn_out);
+    return;
+  }
+  __shared__ __attribute__((aligned(16))) uint16_t gs[KC1 * 512];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = ((int)blockIdx.x - H) * DA_W + wave;
+  const int nr = min(n, N - 1);
+  u32x4 w[KC1];
+#pragma unroll
+  for (int i = 0; i < KC1; i++)
+    w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W2 + (long)nr * KC1 * 512 + (lane + 64 * i) * 8));
+  const float bn = b2[nr];
+  for (int c = threadIdx.x; c < KC1 * 64; c += 64 * DA_W)
+    *reinterpret_cast<u32x4*>(&gs[c * 8]) = *reinterpret_cast<const u32x4*>(g + c * 8);
+  __syncthreads();
+  if (n >= N) return;
+  float acc[1] = {0.f};
+#pragma unroll
+  for (int i = 0; i < KC1; i++) acc[0] = dot8(w[i], *reinterpret_cast<const u32x4*>(&gs[(lane + 64 * i) * 8]), acc[0]);
+  const float tot = reduce_rows<1>(acc, lane);
+  if (lane == 0) y2[n] = f2bf(tot + bn);
+}
+
+// The W8A8 form: g quantised per token once per fc2 workgroup (16 waves) into LDS, int8 dots summed exactly,
+// y2 = bf16(((acc s_g) s_w) + b2) (the epilogue of the W8A8 dual GEMV).
+template <int KI1>
+__global__ __launch_bounds__(1024) void attn_fc2_i8_kernel(const uint16_t* __restrict__ qkv,
+                                                           const float* __restrict__ cs, uint16_t* __restrict__ kc,
+                                                           uint16_t* __restrict__ vc, int H, int ctx,
+                                                           const int* __restrict__ state, float scale_log2,
+                                                           uint16_t* __restrict__ attn_out,
+                                                           const uint16_t* __restrict__ g,
+                                                           const int8_t* __restrict__ W2, const float* __restrict__ sw2,
+                                                           const float* __restrict__ b2, uint16_t* __restrict__ y2,
+                                                           int N) {
+  if ((int)blockIdx.x < H) {
+    attn_head(blockIdx.x, qkv, cs, kc, vc, H, ctx, state, scale_log2, attn_out);
+    return;
+  }
+  __shared__ __attribute__((aligned(16))) uint32_t qgs[KI1 * 256];
+  __shared__ float smax[DA_W];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = ((int)blockIdx.x - H) * DA_W + wave;
+  const int nr = min(n, N - 1);
+  u32x4 w[KI1];
+#pragma unroll
+  for (int j = 0; j < KI1; j++)
+    w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W2 + (long)nr * KI1 * 1024 + (lane + 64 * j) * 16));
+  const float swn = sw2[nr], bn = b2[nr];
+  // K2 = 1024 KI1 values over 1024 threads: KI1 per thread
+  const float sg = quant_block_i8<KI1, DA_W>(g, qgs, smax);
+  __syncthreads();
+  if (n >= N) return;
+  int acc[1] = {0};
+#pragma unroll
+  for (int j = 0; j < KI1; j++)
+    acc[0] = dot16_i8(*reinterpret_cast<const i32x4v*>(&qgs[4 * (lane + 64 * j)]), w[j], acc[0]);
+  const int tot = reduce_rows_i<1>(acc, lane);
+  if (lane == 0) {
+    const float tf = (float)tot * sg;
+    const float vf = tf * swn + bn;
+    y2[n] = f2bf(vf);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- gemv_res2
+// x' = bf16(y2 + bf16(bf16(proj(a) + bp) + x)): the rest of the parallel residual after attn_fc2 (the same
+// roundings, in the same order, as gemv_dual_res). R rows per wave, 4 waves per workgroup.
+template <int KC2, int R>
+__global__ __launch_bounds__(256) void gemv_res2_kernel(const uint16_t* __restrict__ y2, const uint16_t* __restrict__ a,
+                                                        const uint16_t* __restrict__ Wp, const float* __restrict__ bp,
+                                                        const uint16_t* __restrict__ xres, uint16_t* __restrict__ out,
+                                                        int N) {
+  constexpr int SH = 6 - (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  if (row0 >= N) return;
+  const int nme = row0 + (lane >> SH);
+  const bool in = nme < N;
+  u32x4 ac[KC2];
+  load_vec<KC2>(ac, a, lane);
+  u32x4 wp[R][KC2];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int n = min(row0 + r, N - 1);
+#pragma unroll
+    for (int i = 0; i < KC2; i++)
+      wp[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Wp + (long)n * KC2 * 512 + (lane + 64 * i) * 8));
+  }
+  const float bpme = in ? bp[nme] : 0.f, xme = in ? bf2f(xres[nme]) : 0.f, yme = in ? bf2f(y2[nme]) : 0.f;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    acc[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < KC2; i++) acc[r] = dot8(wp[r][i], ac[i], acc[r]);
+  }
+  const float tot = reduce_rows<R>(acc, lane);
+  if ((lane & ((1 << SH) - 1)) == 0 && in) out[nme] = f2bf(yme + rbf(rbf(tot + bpme) + xme));
+}
+
+// The W8A8 form: a quantised once per workgroup into LDS (the W8A8 dual GEMV's proj half).
+template <int KI2, int R>
+__global__ __launch_bounds__(256) void gemv_res2_i8_kernel(const uint16_t* __restrict__ y2,
+                                                           const uint16_t* __restrict__ a,
+                                                           const int8_t* __restrict__ Wp, const float* __restrict__ swp,
+                                                           const float* __restrict__ bp,
+                                                           const uint16_t* __restrict__ xres,
+                                                           uint16_t* __restrict__ out, int N) {
+  constexpr int SH = 6 - (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);
+  __shared__ __attribute__((aligned(16))) uint32_t qas[KI2 * 256];
+  __shared__ float smax[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  const bool active = row0 < N;  // every wave takes part in the workgroup's quantisation (barriers)
+  const int nme = row0 + (lane >> SH);
+  const bool in = active && nme < N;
+  u32x4 wp[R][KI2];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int n = min(row0 + r, N - 1);
+#pragma unroll
+    for (int j = 0; j < KI2; j++)
+      wp[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Wp + (long)n * KI2 * 1024 + (lane + 64 * j) * 16));
+  }
+  const float bpme = in ? bp[nme] : 0.f, swpme = in ? swp[nme] : 0.f;
+  const float xme = in ? bf2f(xres[nme]) : 0.f, yme = in ? bf2f(y2[nme]) : 0.f;
+  const float sa = quant_block_i8<KI2 * 4>(a, qas, smax);
+  __syncthreads();
+  if (!active) return;
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    acc[r] = 0;
+#pragma unroll
+    for (int j = 0; j < KI2; j++)
+      acc[r] = dot16_i8(*reinterpret_cast<const i32x4v*>(&qas[4 * (lane + 64 * j)]), wp[r][j], acc[r]);
+  }
+  const int tot = reduce_rows_i<R>(acc, lane);
+  if ((lane & ((1 << SH) - 1)) == 0 && in) {
+    const float tp = (float)tot * sa;
+    const float vp = tp * swpme + bpme;
+    out[nme] = f2bf(yme + rbf(rbf(vp) + xme));
   }
 }
 
@@ -716,6 +909,38 @@ extern "C" int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* 
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
+// Attention (as mx_decode_attn) and y2 = bf16(g W2^T + b2) in one launch: H attention workgroups plus one
+// workgroup per 16 fc2 rows. W2 is (N, K2) row-major; K2 = 8192 or 4096. Followed by mx_gemv_res2.
+extern "C" int mx_decode_attn_fc2(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc,
+                                  int H, int ctx, const int* state, float scale, uint16_t* attn_out,
+                                  const uint16_t* g, const uint16_t* W2, const float* b2, int K2, uint16_t* y2, int N) {
+  if (!qkv || !cs || !kc || !vc || !state || !attn_out || !g || !W2 || !b2 || !y2) return MX_ENULL;
+  if (H < 1 || ctx < 1 || N < 1) return MX_ESHAPE;
+  if (((uintptr_t)g | (uintptr_t)W2) & 15) return MX_ELAYOUT;
+  const dim3 gr(H + (N + DA_W - 1) / DA_W);
+  const float sl2 = scale * 1.4426950408889634f;
+  if (K2 == 8192)
+    hipLaunchKernelGGL((attn_fc2_kernel<16>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, attn_out, g, W2, b2, y2, N);
+  else if (K2 == 4096)
+    hipLaunchKernelGGL((attn_fc2_kernel<8>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, attn_out, g, W2, b2, y2, N);
+  else return MX_ESHAPE;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// out = bf16(y2 + bf16(bf16(a Wp^T + bp) + xres)); Wp (N, Kp) row-major, Kp = 2048 or 1024. out may alias xres.
+extern "C" int mx_gemv_res2(hipStream_t st, const uint16_t* y2, const uint16_t* a, const uint16_t* Wp, const float* bp,
+                            int Kp, const uint16_t* xres, uint16_t* out, int N) {
+  if (!y2 || !a || !Wp || !bp || !xres || !out) return MX_ENULL;
+  if (N < 1) return MX_ESHAPE;
+  if (((uintptr_t)a | (uintptr_t)Wp) & 15) return MX_ELAYOUT;
+  constexpr int R = 2;
+  const dim3 gr((N + 4 * R - 1) / (4 * R));
+  if (Kp == 2048) hipLaunchKernelGGL((gemv_res2_kernel<4, R>), gr, dim3(256), 0, st, y2, a, Wp, bp, xres, out, N);
+  else if (Kp == 1024) hipLaunchKernelGGL((gemv_res2_kernel<2, R>), gr, dim3(256), 0, st, y2, a, Wp, bp, xres, out, N);
+  else return MX_ESHAPE;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
 // W8A8 [qkv | fc1] GEMV with the LayerNorm fused (gamma = beta = null: none): the LN output is quantised per token,
 // Wq int8 (N, ldw bytes), sw / bias fp32 per row. K = 2048 or 1024. Replaces HI8Lin on the shared quantised LN output
 // (md2fast.py:174-198) for one token.
@@ -748,6 +973,38 @@ extern "C" int mx_gemv_dual_res_i8(hipStream_t st, const uint16_t* g, const int8
     hipLaunchKernelGGL((gemv_dual_res_i8_kernel<8, 2, R>), gr, dim3(256), 0, st, g, W2, sw2, b2, a, Wp, swp, bp, xres, out, N);
   else if (K2 == 4096 && Kp == 1024)
     hipLaunchKernelGGL((gemv_dual_res_i8_kernel<4, 1, R>), gr, dim3(256), 0, st, g, W2, sw2, b2, a, Wp, swp, bp, xres, out, N);
+  else return MX_ESHAPE;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// The W8A8 forms: W2 int8 (N, K2) with per-row scale sw2 (K2 = 8192 or 4096), Wp int8 (N, Kp) with swp (Kp = 2048 or
+// 1024); g and a are quantised per token inside.
+extern "C" int mx_decode_attn_fc2_i8(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc,
+                                     int H, int ctx, const int* state, float scale, uint16_t* attn_out,
+                                     const uint16_t* g, const int8_t* W2, const float* sw2, const float* b2, int K2,
+                                     uint16_t* y2, int N) {
+  if (!qkv || !cs || !kc || !vc || !state || !attn_out || !g || !W2 || !sw2 || !b2 || !y2) return MX_ENULL;
+  if (H < 1 || ctx < 1 || N < 1) return MX_ESHAPE;
+  if (((uintptr_t)g | (uintptr_t)W2) & 15) return MX_ELAYOUT;
+  const dim3 gr(H + (N + DA_W - 1) / DA_W);
+  const float sl2 = scale * 1.4426950408889634f;
+  if (K2 == 8192)
+    hipLaunchKernelGGL((attn_fc2_i8_kernel<8>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, attn_out, g, W2, sw2, b2, y2, N);
+  else if (K2 == 4096)
+    hipLaunchKernelGGL((attn_fc2_i8_kernel<4>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, attn_out, g, W2, sw2, b2, y2, N);
+  else return MX_ESHAPE;
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+extern "C" int mx_gemv_res2_i8(hipStream_t st, const uint16_t* y2, const uint16_t* a, const int8_t* Wp,
+                               const float* swp, const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N) {
+  if (!y2 || !a || !Wp || !swp || !bp || !xres || !out) return MX_ENULL;
+  if (N < 1) return MX_ESHAPE;
+  if (((uintptr_t)a | (uintptr_t)Wp) & 15) return MX_ELAYOUT;
+  constexpr int R = 2;
+  const dim3 gr((N + 4 * R - 1) / (4 * R));
+  if (Kp == 2048) hipLaunchKernelGGL((gemv_res2_i8_kernel<2, R>), gr, dim3(256), 0, st, y2, a, Wp, swp, bp, xres, out, N);
+  else if (Kp == 1024) hipLaunchKernelGGL((gemv_res2_i8_kernel<1, R>), gr, dim3(256), 0, st, y2, a, Wp, swp, bp, xres, out, N);
   else return MX_ESHAPE;
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

@@ -107,6 +107,10 @@ class TextDecoder:
         self.qkv_d = torch.zeros(3 * self.D, device=dev, dtype=BF)
         self.g_d = torch.zeros(c["ff"], device=dev, dtype=BF)
         self.a_d = torch.zeros(self.D, device=dev, dtype=BF)
+        self.y2_d = torch.zeros(self.D, device=dev, dtype=BF)  # bf16(fc2(g) + b2) of the decode step
+        # decode: fc2 shares the attention's launch (mx_decode_attn_fc2) and proj + residual follow (mx_gemv_res2);
+        # False: attention, then both GEMVs in one pass (mx_gemv_dual_res). Same roundings either way.
+        self.fc2_with_attn = True
         self.attn_ws = torch.zeros(self.H * self.S * 66, device=dev, dtype=torch.float32)
         self.attn_cnt = torch.zeros(self.H, device=dev, dtype=torch.int32)
         self.logits = torch.zeros(self.V, device=dev, dtype=BF)
@@ -264,6 +268,10 @@ class TextDecoder:
                                            float(self.eps), b["wqf"].data_ptr(), b["wqf"].stride(0), b["bqf"].data_ptr(),
                                            b["wqf"].shape[0], self.D, b["nq"], self.qkv_d.data_ptr(),
                                            self.g_d.data_ptr(), 1), "mx_ln_gemv2")
+            if self.fc2_with_attn:
+                self._attn_fc2_res(b, i, x, xn)
+                xi ^= 1
+                continue
             _lib.check(lib.mx_decode_attn(st, self.qkv_d.data_ptr(), self.cs.data_ptr(), self.kc[i].data_ptr(),
                                           self.vc[i].data_ptr(), self.H, self.ctx, self.state.data_ptr(), self.S,
                                           float(self.hd ** -0.5), self.attn_ws.data_ptr(), self.attn_cnt.data_ptr(),
@@ -284,6 +292,26 @@ class TextDecoder:
             self.xd[0].copy_(self.xd[1])
         self.lm_argmax(self.xd[0], logits=logits)
         self._embed()
+
+    def _attn_fc2_res(self, b, i, x, xn):
+        """Layer i's attention with the fc2 GEMV in the same launch (it reads only the fc1 output), then proj +
+        the parallel residual: xn = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)) (md2fast.py:198)."""
+        st, lib = stream(), _lib.load()
+        attn = (st, self.qkv_d.data_ptr(), self.cs.data_ptr(), self.kc[i].data_ptr(), self.vc[i].data_ptr(), self.H,
+                self.ctx, self.state.data_ptr(), float(self.hd ** -0.5), self.a_d.data_ptr(), self.g_d.data_ptr())
+        if self.w8a8:
+            _lib.check(lib.mx_decode_attn_fc2_i8(*attn, b["w2"].data_ptr(), b["sw2"].data_ptr(), b["b2"].data_ptr(),
+                                                 b["w2"].shape[1], self.y2_d.data_ptr(), self.D),
+                       "mx_decode_attn_fc2_i8")
+            _lib.check(lib.mx_gemv_res2_i8(st, self.y2_d.data_ptr(), self.a_d.data_ptr(), b["wp"].data_ptr(),
+                                           b["swp"].data_ptr(), b["bp"].data_ptr(), b["wp"].shape[1], x.data_ptr(),
+                                           xn.data_ptr(), self.D), "mx_gemv_res2_i8")
+        else:
+            _lib.check(lib.mx_decode_attn_fc2(*attn, b["w2"].data_ptr(), b["b2"].data_ptr(), b["w2"].shape[1],
+                                              self.y2_d.data_ptr(), self.D), "mx_decode_attn_fc2")
+            _lib.check(lib.mx_gemv_res2(st, self.y2_d.data_ptr(), self.a_d.data_ptr(), b["wp"].data_ptr(),
+                                        b["bp"].data_ptr(), b["wp"].shape[1], x.data_ptr(), xn.data_ptr(), self.D),
+                       "mx_gemv_res2")
 
     def capture_step(self):
         """HIP graph of one decode step (the state counter makes each replay the next token)."""

@@ -146,6 +146,59 @@ def test_decode_attn_vs_fp32(dev, L):
     assert torch.count_nonzero(cnt) == 0
 
 
+@pytest.mark.parametrize("w8a8", [False, True])
+@pytest.mark.parametrize("D,F_,L,N", [(2048, 8192, 1, 2048), (2048, 8192, 922, 2048), (1024, 4096, 300, 1000)])
+def test_attn_fc2_res2_equals_dual(dev, w8a8, D, F_, L, N):
+    """mx_decode_attn_fc2 + mx_gemv_res2 (fc2 in the attention's launch, then proj + residual) against
+    mx_decode_attn + mx_gemv_dual_res (and the _i8 forms), bit for bit: the attention output, the K/V append and
+    x' = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)). Each row's fp32 total has the same pairwise tree
+    in both (the dual kernel's halving exchange and the plain butterfly add the same pairs), the W8A8 sums are exact
+    int32 and the per-token scale is a max; N = 1000 leaves a partial last fc2 workgroup."""
+    H, ctx, pos = D // 64, 1024, L - 1
+    g = gen(L + N)
+    kc = torch.randn(H, ctx, 64, generator=g).to(BF)
+    vc = torch.randn(H, ctx, 64, generator=g).to(BF)
+    qkv = torch.randn(3 * H * 64, generator=g).to(BF)
+    gi = torch.randn(F_, generator=g).to(BF)
+    x = torch.randn(N, generator=g).to(BF)
+    W2 = (torch.randn(N, F_, generator=g) * 0.02).to(BF)
+    Wp = (torch.randn(N, D, generator=g) * 0.02).to(BF)
+    b2 = torch.randn(N, generator=g) * 0.02
+    bp = torch.randn(N, generator=g) * 0.02
+    fr = S.freqs_cis(32, 2048).to(dev)
+    qkvd, gd, xd = qkv.to(dev), gi.to(dev), x.to(dev)
+    state = torch.tensor([0, pos], device=dev, dtype=torch.int32)
+    if w8a8:
+        l2, lp = ops.MxI8Lin(W2, b2, device=dev), ops.MxI8Lin(Wp, bp, device=dev)
+        w2 = (l2.wq.data_ptr(), l2.sw.data_ptr(), l2.b.data_ptr())
+        wp = (lp.wq.data_ptr(), lp.sw.data_ptr(), lp.b.data_ptr())
+    else:
+        W2d, Wpd, b2d, bpd = W2.to(dev), Wp.to(dev), b2.to(dev), bp.to(dev)
+        w2, wp = (W2d.data_ptr(), b2d.data_ptr()), (Wpd.data_ptr(), bpd.data_ptr())
+    res = []
+    for fused in (False, True):
+        kd, vd = kc.to(dev), vc.to(dev)
+        a = torch.full((H * 64,), float("nan"), device=dev).to(BF)
+        out = torch.empty(N, device=dev, dtype=BF)
+        attn = (_lib.stream(), qkvd.data_ptr(), fr.data_ptr(), kd.data_ptr(), vd.data_ptr(), H, ctx, state.data_ptr())
+        print(f"attn_fc2 w8a8={w8a8} D={D} L={L} N={N} fused={fused}", flush=True)
+        sfx = "_i8" if w8a8 else ""
+        if fused:
+            y2 = torch.empty(N, device=dev, dtype=BF)
+            _lib.call("mx_decode_attn_fc2" + sfx, *attn, 0.125, a.data_ptr(), gd.data_ptr(), *w2, F_, y2.data_ptr(), N)
+            _lib.call("mx_gemv_res2" + sfx, _lib.stream(), y2.data_ptr(), a.data_ptr(), *wp, D, xd.data_ptr(),
+                      out.data_ptr(), N)
+        else:
+            _lib.call("mx_decode_attn", *attn, 8, 0.125, None, None, a.data_ptr())
+            _lib.call("mx_gemv_dual_res" + sfx, _lib.stream(), gd.data_ptr(), *w2, F_, a.data_ptr(), *wp, D,
+                      xd.data_ptr(), out.data_ptr(), N)
+        res.append([t.cpu() for t in (a, out, kd[:, pos], vd[:, pos])])
+    for u, v in zip(*res):
+        assert torch.equal(u, v)
+    ref = (W2.float() @ gi.float() + b2) + (Wp.float() @ res[0][0].float() + bp) + x.float()
+    assert rel(res[1][1], ref) < (2e-2 if w8a8 else 5e-3)
+
+
 def _models(layers, seed=0):
     w = S.text_weights(seed, layers=layers)
     fr = S.freqs_cis(32, 2048)
