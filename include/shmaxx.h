@@ -179,23 +179,28 @@ int mx_embed_step(hipStream_t st, const unsigned long long* part, int nparts, co
  * query. */
 int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H, int ctx,
                    const int* state, int S, float scale, float* ws, int* cnt, uint16_t* out);
-/* The decode step's attention and the parallel residual's fc2 GEMV in one launch (fc2 reads only the fc1 output g):
- * attention as mx_decode_attn into attn_out, and y2 = bf16(g W2^T + b2) (W2 (N, K2) contiguous, K2 8192 / 4096) on
- * workgroups of their own beside the H attention workgroups. mx_gemv_res2 then forms
- * out = bf16(y2 + bf16(bf16(attn_out Wp^T + bp) + xres)) (Wp (N, Kp) contiguous, Kp 2048 / 1024; out may alias xres):
- * together the same value, with the same roundings, as mx_decode_attn + mx_gemv_dual_res, i.e. the attention and
- * parallel residual of md2fast.py:185-198 for one token. The _i8 forms take the W8A8 weights and quantise g / a per
- * token inside (the epilogue of mx_gemv_dual_res_i8). */
+/* The decode step's attention and the parallel residual's fc2 GEMV in one launch (fc2 reads only the fc1 output g),
+ * i.e. the attention and parallel residual of md2fast.py:185-198 for one token:
+ *  - mx_decode_attn_fc2: the attention of mx_decode_attn on H S workgroups (S splits of each head's keys,
+ *    1 <= S <= 8) and y2 = bf16(g W2^T + b2) (W2 (N, K2) contiguous, K2 8192 / 4096) on workgroups of their own.
+ *    S = 1 writes attn_out (H 64 bf16); S > 1 writes each split's unnormalised softmax record (M, Lsum, acc[64]) to
+ *    part (H S 66 floats) instead.
+ *  - mx_gemv_res2: out = bf16(y2 + bf16(bf16(a Wp^T + bp) + xres)) (Wp (N, Kp) contiguous, Kp = 64 H = 2048 / 1024;
+ *    out may alias xres), with a = attn_out (S = 1) or merged from part (S > 1).
+ * With S = 1 the pair gives mx_decode_attn + mx_gemv_dual_res bit for bit; S > 1 rounds the merged attention output
+ * once more in a different order. The _i8 forms take the W8A8 weights and quantise g / a per token inside (the
+ * epilogue of mx_gemv_dual_res_i8). */
 int mx_decode_attn_fc2(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H, int ctx,
-                       const int* state, float scale, uint16_t* attn_out, const uint16_t* g, const uint16_t* W2,
-                       const float* b2, int K2, uint16_t* y2, int N);
-int mx_gemv_res2(hipStream_t st, const uint16_t* y2, const uint16_t* a, const uint16_t* Wp, const float* bp, int Kp,
-                 const uint16_t* xres, uint16_t* out, int N);
+                       const int* state, float scale, int S, float* part, uint16_t* attn_out, const uint16_t* g,
+                       const uint16_t* W2, const float* b2, int K2, uint16_t* y2, int N);
+int mx_gemv_res2(hipStream_t st, const uint16_t* y2, const uint16_t* a, int S, const float* part, const uint16_t* Wp,
+                 const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N);
 int mx_decode_attn_fc2_i8(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc, int H,
-                          int ctx, const int* state, float scale, uint16_t* attn_out, const uint16_t* g,
-                          const int8_t* W2, const float* sw2, const float* b2, int K2, uint16_t* y2, int N);
-int mx_gemv_res2_i8(hipStream_t st, const uint16_t* y2, const uint16_t* a, const int8_t* Wp, const float* swp,
-                    const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N);
+                          int ctx, const int* state, float scale, int S, float* part, uint16_t* attn_out,
+                          const uint16_t* g, const int8_t* W2, const float* sw2, const float* b2, int K2, uint16_t* y2,
+                          int N);
+int mx_gemv_res2_i8(hipStream_t st, const uint16_t* y2, const uint16_t* a, int S, const float* part, const int8_t* Wp,
+                    const float* swp, const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N);
 
 /* ============================================================================================ TRecViT recurrence
  * One streamed frame of conv_1d + block-diagonal gates + RG-LRU + y-gate (numerics of tapnext/npu/pack8.py:253-279

@@ -525,16 +525,21 @@ constexpr int DA_UNROLL = 8;   // key rounds (8 keys per wave each) whose K and 
 // 8 (lane & 7) .. +7), and runs an online softmax over them in one pass: the K and V rows of DA_UNROLL rounds are
 // loaded together, scores reduced within each 8-lane group, the wave's running max raised (and its O, l rescaled)
 // per batch. The 16 waves' (m, l, O) are merged in LDS. P is rounded to bf16 and l sums the rounded values.
-// The body for head h, run by a 1024-thread workgroup (every thread reaches its barriers).
-__device__ __forceinline__ void attn_head(int h, const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
-                                          uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int H, int ctx,
-                                          const int* __restrict__ state, float scale_log2,
-                                          uint16_t* __restrict__ out) {
+// The body for head h, run by a 1024-thread workgroup (every thread reaches its barriers). With S > 1 the head's
+// keys are split over S workgroups: split sp takes keys [sp c, sp c + c) (c = ceil(L / S) rounded up to 8) and writes
+// the unnormalised record (M, Lsum, acc[64]) of its 16 waves to part + (h S + sp) 66 for merge_attn; with S = 1 the
+// workgroup writes the head's output.
+__device__ __forceinline__ void attn_head(int h, int sp, int S, const uint16_t* __restrict__ qkv,
+                                          const float* __restrict__ cs, uint16_t* __restrict__ kc,
+                                          uint16_t* __restrict__ vc, int H, int ctx, const int* __restrict__ state,
+                                          float scale_log2, uint16_t* __restrict__ out, float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) uint16_t qs[64], knew[64], vnew[64];  // bf16 q, k, v of the new token
   __shared__ float rec[DA_W][66];  // (m, l, o[64]) of each wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = state[1];
   const int L = pos + 1;
+  const int chunk = S == 1 ? L : (((L + S - 1) / S + 7) & ~7);
+  const int kb = sp * chunk, ke = min(L, kb + chunk);  // this workgroup's keys (empty when kb >= L)
   // the rope's inputs through pointers the compiler cannot see through: loads from the read-only arguments could
   // otherwise be moved freely, behind the cache rows' loads below
   typedef __attribute__((address_space(1))) const float gfloat;
@@ -572,7 +577,7 @@ __device__ __forceinline__ void attn_head(int h, const uint16_t* __restrict__ qk
   };
   asm volatile("" ::: "memory");  // the rope's loads are issued first (no load moves across)
   __builtin_amdgcn_sched_barrier(0);
-  load_pass(wave * 8);
+  load_pass(kb + wave * 8);
   {
     // branch-free (a branch would let the compiler sink these loads behind the cache rows')
     const float qa = bf2f(q0), qb = bf2f(q1), ka = bf2f(k0), kb = bf2f(k1);
@@ -584,23 +589,24 @@ __device__ __forceinline__ void attn_head(int h, const uint16_t* __restrict__ qk
       qs[d] = f2bf(qv);
       knew[d] = f2bf(kv);
       vnew[d] = vn;
-      // append the new token's K / V to the cache (this step takes them from LDS)
-      kc[((long)h * ctx + pos) * 64 + d] = f2bf(kv);
-      vc[((long)h * ctx + pos) * 64 + d] = vn;
+      if (sp == 0) {  // append the new token's K / V to the cache (this step takes them from LDS)
+        kc[((long)h * ctx + pos) * 64 + d] = f2bf(kv);
+        vc[((long)h * ctx + pos) * 64 + d] = vn;
+      }
     }
   }
   __syncthreads();
   const u32x4 qp = *reinterpret_cast<const u32x4*>(&qs[sub * 8]);  // q dims 8 sub .. +7, bf16 pairs
   float m_run = -1e30f, l_run = 0.f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  // the loop bound is wave-uniform (every lane takes part in the wave-wide max); keys past L are masked
-  for (int b0 = wave * 8; b0 < L; b0 += 8 * DA_W * DA_UNROLL) {
-    if (b0 != wave * 8) load_pass(b0);
+  // the loop bound is wave-uniform (every lane takes part in the wave-wide max); keys past ke are masked
+  for (int b0 = kb + wave * 8; b0 < ke; b0 += 8 * DA_W * DA_UNROLL) {
+    if (b0 != kb + wave * 8) load_pass(b0);
     const int base = b0 + kg;
 #pragma unroll
     for (int u = 0; u < DA_UNROLL; u++)
-      if (base + 8 * DA_W * u >= pos) {
-        const bool me = base + 8 * DA_W * u == pos;
+      if (base + 8 * DA_W * u >= min(pos, ke)) {
+        const bool me = base + 8 * DA_W * u == pos && pos < ke;
         kk[u] = me ? *reinterpret_cast<const u32x4*>(&knew[sub * 8]) : zero4;
         vv[u] = me ? *reinterpret_cast<const u32x4*>(&vnew[sub * 8]) : zero4;
       }
@@ -617,7 +623,7 @@ __device__ __forceinline__ void attn_head(int h, const uint16_t* __restrict__ qk
       s += __shfl_xor(s, 1, 64);
       s += __shfl_xor(s, 2, 64);
       s += __shfl_xor(s, 4, 64);
-      s = (base + 8 * DA_W * u < L) ? s * scale_log2 : -INFINITY;
+      s = (base + 8 * DA_W * u < ke) ? s * scale_log2 : -INFINITY;
       sv[u] = s;
       mb = fmaxf(mb, s);
     }
@@ -666,15 +672,42 @@ __device__ __forceinline__ void attn_head(int h, const uint16_t* __restrict__ qk
       Lt += rec[w][1] * f;
       acc += rec[w][2 + tid] * f;
     }
-    out[h * 64 + tid] = f2bf(acc / Lt);
+    if (S == 1) {
+      out[h * 64 + tid] = f2bf(acc / Lt);
+    } else {
+      float* r = part + ((long)h * S + sp) * 66;
+      r[2 + tid] = acc;
+      if (tid == 0) { r[0] = M; r[1] = Lt; }
+    }
   }
+}
+
+// The attention output a[c .. c + E - 1] (within one head) from the S split records of its head:
+// bf16(sum_s acc_s 2^(M_s - M) / sum_s Lsum_s 2^(M_s - M)), M = max_s M_s (an empty split has Lsum = acc = 0).
+template <int E>
+__device__ __forceinline__ void merge_attn(const float* __restrict__ part, int S, int c, float (&f)[E]) {
+  const float* r = part + (long)(c >> 6) * S * 66;
+  const int d0 = c & 63;
+  float M = -1e30f;
+  for (int s = 0; s < S; s++) M = fmaxf(M, r[s * 66]);
+  float Lt = 0.f, acc[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) acc[e] = 0.f;
+  for (int s = 0; s < S; s++) {
+    const float w = __builtin_amdgcn_exp2f(r[s * 66] - M);
+    Lt += r[s * 66 + 1] * w;
+#pragma unroll
+    for (int e = 0; e < E; e++) acc[e] += r[s * 66 + 2 + d0 + e] * w;
+  }
+#pragma unroll
+  for (int e = 0; e < E; e++) f[e] = rbf(acc[e] / Lt);
 }
 
 __global__ __launch_bounds__(1024) void decode_attn_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
                                                            uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                                                            int H, int ctx, const int* __restrict__ state,
                                                            float scale_log2, uint16_t* __restrict__ out) {
-  attn_head(blockIdx.x, qkv, cs, kc, vc, H, ctx, state, scale_log2, out);
+  attn_head(blockIdx.x, 0, 1, qkv, cs, kc, vc, H, ctx, state, scale_log2, out, nullptr);
 }
 
 // ---------------------------------------------------------------------------------------------- attention + fc2
@@ -686,16 +719,17 @@ template <int KC1>
 __global__ __launch_bounds__(1024) void attn_fc2_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
                                                         uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int H,
                                                         int ctx, const int* __restrict__ state, float scale_log2,
+                                                        int S, float* __restrict__ part,
                                                         uint16_t* __restrict__ attn_out, const uint16_t* __restrict__ g,
                                                         const uint16_t* __restrict__ W2, const float* __restrict__ b2,
                                                         uint16_t* __restrict__ y2, int N) {
-  if ((int)blockIdx.x < H) {
-    attn_head(blockIdx.x, qkv, cs, kc, vc, H, ctx, state, scale_log2, attn_out);
+  if ((int)blockIdx.x < H * S) {
+    attn_head(blockIdx.x / S, blockIdx.x % S, S, qkv, cs, kc, vc, H, ctx, state, scale_log2, attn_out, part);
     return;
   }
   __shared__ __attribute__((aligned(16))) uint16_t gs[KC1 * 512];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n = ((int)blockIdx.x - H) * DA_W + wave;
+  const int n = ((int)blockIdx.x - H * S) * DA_W + wave;
   const int nr = min(n, N - 1);
   u32x4 w[KC1];
 #pragma unroll
@@ -719,20 +753,20 @@ template <int KI1>
 __global__ __launch_bounds__(1024) void attn_fc2_i8_kernel(const uint16_t* __restrict__ qkv,
                                                            const float* __restrict__ cs, uint16_t* __restrict__ kc,
                                                            uint16_t* __restrict__ vc, int H, int ctx,
-                                                           const int* __restrict__ state, float scale_log2,
-                                                           uint16_t* __restrict__ attn_out,
+                                                           const int* __restrict__ state, float scale_log2, int S,
+                                                           float* __restrict__ part, uint16_t* __restrict__ attn_out,
                                                            const uint16_t* __restrict__ g,
                                                            const int8_t* __restrict__ W2, const float* __restrict__ sw2,
                                                            const float* __restrict__ b2, uint16_t* __restrict__ y2,
                                                            int N) {
-  if ((int)blockIdx.x < H) {
-    attn_head(blockIdx.x, qkv, cs, kc, vc, H, ctx, state, scale_log2, attn_out);
+  if ((int)blockIdx.x < H * S) {
+    attn_head(blockIdx.x / S, blockIdx.x % S, S, qkv, cs, kc, vc, H, ctx, state, scale_log2, attn_out, part);
     return;
   }
   __shared__ __attribute__((aligned(16))) uint32_t qgs[KI1 * 256];
   __shared__ float smax[DA_W];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n = ((int)blockIdx.x - H) * DA_W + wave;
+  const int n = ((int)blockIdx.x - H * S) * DA_W + wave;
   const int nr = min(n, N - 1);
   u32x4 w[KI1];
 #pragma unroll
@@ -757,20 +791,20 @@ __global__ __launch_bounds__(1024) void attn_fc2_i8_kernel(const uint16_t* __res
 
 // ---------------------------------------------------------------------------------------------- gemv_res2
 // x' = bf16(y2 + bf16(bf16(proj(a) + bp) + x)): the rest of the parallel residual after attn_fc2 (the same
-// roundings, in the same order, as gemv_dual_res). R rows per wave, 4 waves per workgroup.
+// roundings, in the same order, as gemv_dual_res). R rows per wave, 4 waves per workgroup. S > 1: a is merged from
+// the attention's split records into LDS first (while the weight rows are in flight).
 template <int KC2, int R>
 __global__ __launch_bounds__(256) void gemv_res2_kernel(const uint16_t* __restrict__ y2, const uint16_t* __restrict__ a,
+                                                        int S, const float* __restrict__ part,
                                                         const uint16_t* __restrict__ Wp, const float* __restrict__ bp,
                                                         const uint16_t* __restrict__ xres, uint16_t* __restrict__ out,
                                                         int N) {
   constexpr int SH = 6 - (R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4);
+  __shared__ __attribute__((aligned(16))) uint16_t as[KC2 * 512];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * R;
-  if (row0 >= N) return;
   const int nme = row0 + (lane >> SH);
-  const bool in = nme < N;
-  u32x4 ac[KC2];
-  load_vec<KC2>(ac, a, lane);
+  const bool in = row0 < N && nme < N;
   u32x4 wp[R][KC2];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -780,6 +814,23 @@ __global__ __launch_bounds__(256) void gemv_res2_kernel(const uint16_t* __restri
       wp[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Wp + (long)n * KC2 * 512 + (lane + 64 * i) * 8));
   }
   const float bpme = in ? bp[nme] : 0.f, xme = in ? bf2f(xres[nme]) : 0.f, yme = in ? bf2f(y2[nme]) : 0.f;
+  u32x4 ac[KC2];
+  if (S > 1) {  // workgroup-uniform
+    for (int c = threadIdx.x; c < KC2 * 64; c += 256) {
+      float f[8];
+      merge_attn<8>(part, S, c * 8, f);
+      u32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[e] = pack2(f[2 * e], f[2 * e + 1]);
+      *reinterpret_cast<u32x4*>(&as[c * 8]) = v;
+    }
+    __syncthreads();
+    if (row0 >= N) return;
+    load_vec<KC2>(ac, as, lane);
+  } else {
+    if (row0 >= N) return;
+    load_vec<KC2>(ac, a, lane);
+  }
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -794,7 +845,8 @@ __global__ __launch_bounds__(256) void gemv_res2_kernel(const uint16_t* __restri
 // The W8A8 form: a quantised once per workgroup into LDS (the W8A8 dual GEMV's proj half).
 template <int KI2, int R>
 __global__ __launch_bounds__(256) void gemv_res2_i8_kernel(const uint16_t* __restrict__ y2,
-                                                           const uint16_t* __restrict__ a,
+                                                           const uint16_t* __restrict__ a, int S,
+                                                           const float* __restrict__ part,
                                                            const int8_t* __restrict__ Wp, const float* __restrict__ swp,
                                                            const float* __restrict__ bp,
                                                            const uint16_t* __restrict__ xres,
@@ -817,7 +869,14 @@ __global__ __launch_bounds__(256) void gemv_res2_i8_kernel(const uint16_t* __res
   }
   const float bpme = in ? bp[nme] : 0.f, swpme = in ? swp[nme] : 0.f;
   const float xme = in ? bf2f(xres[nme]) : 0.f, yme = in ? bf2f(y2[nme]) : 0.f;
-  const float sa = quant_block_i8<KI2 * 4>(a, qas, smax);
+  float sa;
+  if (S > 1) {  // workgroup-uniform: this thread's KI2 * 4 values of a merged from the split records
+    float f[KI2 * 4];
+    merge_attn<KI2 * 4>(part, S, threadIdx.x * KI2 * 4, f);
+    sa = quant_vals_block_i8<KI2 * 4>(f, qas, smax);
+  } else {
+    sa = quant_block_i8<KI2 * 4>(a, qas, smax);
+  }
   __syncthreads();
   if (!active) return;
   int acc[R];
@@ -909,34 +968,54 @@ extern "C" int mx_decode_attn(hipStream_t st, const uint16_t* qkv, const float* 
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
-// Attention (as mx_decode_attn) and y2 = bf16(g W2^T + b2) in one launch: H attention workgroups plus one
-// workgroup per 16 fc2 rows. W2 is (N, K2) row-major; K2 = 8192 or 4096. Followed by mx_gemv_res2.
-extern "C" int mx_decode_attn_fc2(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc,
-                                  int H, int ctx, const int* state, float scale, uint16_t* attn_out,
-                                  const uint16_t* g, const uint16_t* W2, const float* b2, int K2, uint16_t* y2, int N) {
-  if (!qkv || !cs || !kc || !vc || !state || !attn_out || !g || !W2 || !b2 || !y2) return MX_ENULL;
-  if (H < 1 || ctx < 1 || N < 1) return MX_ESHAPE;
+// Attention (as mx_decode_attn) and y2 = bf16(g W2^T + b2) in one launch: H S attention workgroups (S splits of
+// each head's keys, 1 <= S <= 8) plus one workgroup per 16 fc2 rows. S = 1 writes attn_out; S > 1 writes the split
+// records to part (H S 66 floats) instead, for mx_gemv_res2 to merge. W2 is (N, K2) row-major; K2 = 8192 or 4096.
+static int attn_fc2_check(const void* qkv, const void* cs, const void* kc, const void* vc, const void* state, int H,
+                          int ctx, int S, const void* part, const void* attn_out, const void* g, const void* W2,
+                          const void* b2, const void* y2, int N) {
+  if (!qkv || !cs || !kc || !vc || !state || !g || !W2 || !b2 || !y2) return MX_ENULL;
+  if (H < 1 || ctx < 1 || N < 1 || S < 1 || S > 8) return MX_ESHAPE;
+  if (S == 1 ? !attn_out : !part) return MX_ENULL;
   if (((uintptr_t)g | (uintptr_t)W2) & 15) return MX_ELAYOUT;
-  const dim3 gr(H + (N + DA_W - 1) / DA_W);
+  return MX_OK;
+}
+
+extern "C" int mx_decode_attn_fc2(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc,
+                                  int H, int ctx, const int* state, float scale, int S, float* part,
+                                  uint16_t* attn_out, const uint16_t* g, const uint16_t* W2, const float* b2, int K2,
+                                  uint16_t* y2, int N) {
+  const int rc = attn_fc2_check(qkv, cs, kc, vc, state, H, ctx, S, part, attn_out, g, W2, b2, y2, N);
+  if (rc != MX_OK) return rc;
+  const dim3 gr(H * S + (N + DA_W - 1) / DA_W);
   const float sl2 = scale * 1.4426950408889634f;
   if (K2 == 8192)
-    hipLaunchKernelGGL((attn_fc2_kernel<16>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, attn_out, g, W2, b2, y2, N);
+    hipLaunchKernelGGL((attn_fc2_kernel<16>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, S, part, attn_out, g, W2, b2, y2, N);
   else if (K2 == 4096)
-    hipLaunchKernelGGL((attn_fc2_kernel<8>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, attn_out, g, W2, b2, y2, N);
+    hipLaunchKernelGGL((attn_fc2_kernel<8>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, S, part, attn_out, g, W2, b2, y2, N);
   else return MX_ESHAPE;
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
-// out = bf16(y2 + bf16(bf16(a Wp^T + bp) + xres)); Wp (N, Kp) row-major, Kp = 2048 or 1024. out may alias xres.
-extern "C" int mx_gemv_res2(hipStream_t st, const uint16_t* y2, const uint16_t* a, const uint16_t* Wp, const float* bp,
-                            int Kp, const uint16_t* xres, uint16_t* out, int N) {
-  if (!y2 || !a || !Wp || !bp || !xres || !out) return MX_ENULL;
-  if (N < 1) return MX_ESHAPE;
+// out = bf16(y2 + bf16(bf16(a Wp^T + bp) + xres)); a is the attention output (S = 1) or merged from the S split
+// records in part; Wp (N, Kp) row-major, Kp = 2048 or 1024 (= 64 H). out may alias xres.
+static int res2_check(const void* y2, const void* a, int S, const void* part, const void* Wp, const void* bp,
+                      const void* xres, const void* out, int N) {
+  if (!y2 || !Wp || !bp || !xres || !out) return MX_ENULL;
+  if (N < 1 || S < 1 || S > 8) return MX_ESHAPE;
+  if (S == 1 ? !a : !part) return MX_ENULL;
   if (((uintptr_t)a | (uintptr_t)Wp) & 15) return MX_ELAYOUT;
+  return MX_OK;
+}
+
+extern "C" int mx_gemv_res2(hipStream_t st, const uint16_t* y2, const uint16_t* a, int S, const float* part,
+                            const uint16_t* Wp, const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N) {
+  const int rc = res2_check(y2, a, S, part, Wp, bp, xres, out, N);
+  if (rc != MX_OK) return rc;
   constexpr int R = 2;
   const dim3 gr((N + 4 * R - 1) / (4 * R));
-  if (Kp == 2048) hipLaunchKernelGGL((gemv_res2_kernel<4, R>), gr, dim3(256), 0, st, y2, a, Wp, bp, xres, out, N);
-  else if (Kp == 1024) hipLaunchKernelGGL((gemv_res2_kernel<2, R>), gr, dim3(256), 0, st, y2, a, Wp, bp, xres, out, N);
+  if (Kp == 2048) hipLaunchKernelGGL((gemv_res2_kernel<4, R>), gr, dim3(256), 0, st, y2, a, S, part, Wp, bp, xres, out, N);
+  else if (Kp == 1024) hipLaunchKernelGGL((gemv_res2_kernel<2, R>), gr, dim3(256), 0, st, y2, a, S, part, Wp, bp, xres, out, N);
   else return MX_ESHAPE;
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
@@ -980,31 +1059,32 @@ extern "C" int mx_gemv_dual_res_i8(hipStream_t st, const uint16_t* g, const int8
 // The W8A8 forms: W2 int8 (N, K2) with per-row scale sw2 (K2 = 8192 or 4096), Wp int8 (N, Kp) with swp (Kp = 2048 or
 // 1024); g and a are quantised per token inside.
 extern "C" int mx_decode_attn_fc2_i8(hipStream_t st, const uint16_t* qkv, const float* cs, uint16_t* kc, uint16_t* vc,
-                                     int H, int ctx, const int* state, float scale, uint16_t* attn_out,
-                                     const uint16_t* g, const int8_t* W2, const float* sw2, const float* b2, int K2,
-                                     uint16_t* y2, int N) {
-  if (!qkv || !cs || !kc || !vc || !state || !attn_out || !g || !W2 || !sw2 || !b2 || !y2) return MX_ENULL;
-  if (H < 1 || ctx < 1 || N < 1) return MX_ESHAPE;
-  if (((uintptr_t)g | (uintptr_t)W2) & 15) return MX_ELAYOUT;
-  const dim3 gr(H + (N + DA_W - 1) / DA_W);
+                                     int H, int ctx, const int* state, float scale, int S, float* part,
+                                     uint16_t* attn_out, const uint16_t* g, const int8_t* W2, const float* sw2,
+                                     const float* b2, int K2, uint16_t* y2, int N) {
+  const int rc = attn_fc2_check(qkv, cs, kc, vc, state, H, ctx, S, part, attn_out, g, W2, b2, y2, N);
+  if (rc != MX_OK) return rc;
+  if (!sw2) return MX_ENULL;
+  const dim3 gr(H * S + (N + DA_W - 1) / DA_W);
   const float sl2 = scale * 1.4426950408889634f;
   if (K2 == 8192)
-    hipLaunchKernelGGL((attn_fc2_i8_kernel<8>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, attn_out, g, W2, sw2, b2, y2, N);
+    hipLaunchKernelGGL((attn_fc2_i8_kernel<8>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, S, part, attn_out, g, W2, sw2, b2, y2, N);
   else if (K2 == 4096)
-    hipLaunchKernelGGL((attn_fc2_i8_kernel<4>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, attn_out, g, W2, sw2, b2, y2, N);
+    hipLaunchKernelGGL((attn_fc2_i8_kernel<4>), gr, dim3(64 * DA_W), 0, st, qkv, cs, kc, vc, H, ctx, state, sl2, S, part, attn_out, g, W2, sw2, b2, y2, N);
   else return MX_ESHAPE;
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
-extern "C" int mx_gemv_res2_i8(hipStream_t st, const uint16_t* y2, const uint16_t* a, const int8_t* Wp,
-                               const float* swp, const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N) {
-  if (!y2 || !a || !Wp || !swp || !bp || !xres || !out) return MX_ENULL;
-  if (N < 1) return MX_ESHAPE;
-  if (((uintptr_t)a | (uintptr_t)Wp) & 15) return MX_ELAYOUT;
+extern "C" int mx_gemv_res2_i8(hipStream_t st, const uint16_t* y2, const uint16_t* a, int S, const float* part,
+                               const int8_t* Wp, const float* swp, const float* bp, int Kp, const uint16_t* xres,
+                               uint16_t* out, int N) {
+  const int rc = res2_check(y2, a, S, part, Wp, bp, xres, out, N);
+  if (rc != MX_OK) return rc;
+  if (!swp) return MX_ENULL;
   constexpr int R = 2;
   const dim3 gr((N + 4 * R - 1) / (4 * R));
-  if (Kp == 2048) hipLaunchKernelGGL((gemv_res2_i8_kernel<2, R>), gr, dim3(256), 0, st, y2, a, Wp, swp, bp, xres, out, N);
-  else if (Kp == 1024) hipLaunchKernelGGL((gemv_res2_i8_kernel<1, R>), gr, dim3(256), 0, st, y2, a, Wp, swp, bp, xres, out, N);
+  if (Kp == 2048) hipLaunchKernelGGL((gemv_res2_i8_kernel<2, R>), gr, dim3(256), 0, st, y2, a, S, part, Wp, swp, bp, xres, out, N);
+  else if (Kp == 1024) hipLaunchKernelGGL((gemv_res2_i8_kernel<1, R>), gr, dim3(256), 0, st, y2, a, S, part, Wp, swp, bp, xres, out, N);
   else return MX_ESHAPE;
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

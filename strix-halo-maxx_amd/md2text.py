@@ -26,7 +26,7 @@ BOS = 50256  # moondream2's tokenizer bos_id (the Phi / GPT-2 <|endoftext|> id)
 
 
 class TextDecoder:
-    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", ctx=1024, attn_splits=4, w8a8=False, nq=1, L=32,
+    def __init__(self, weights, lin_cls=ops.MxLin, device="cuda", ctx=1024, attn_splits=1, w8a8=False, nq=1, L=32,
                  yes_ids=(), no_ids=()):
         """w8a8: the four text Linears of every layer run the reference's W8A8 path (its default text linear class,
         HI8Lin, moondream/gpu/bench.py:20) in prefill and decode; the LM head stays bf16 (md2fast.py:115).
@@ -98,6 +98,10 @@ class TextDecoder:
         self.query_graph = None
         # ---- decode-step device state
         lib = _lib.load()
+        if not 1 <= attn_splits <= 8:
+            raise ValueError(f"attn_splits {attn_splits} outside 1..8")
+        # decode attention: workgroups per head (S > 1: their records merged by mx_gemv_res2). One is fastest at
+        # contexts up to 1024 (1453 / 1364 / 1249 tok/s for 1 / 2 / 4): the merge costs more than it saves.
         self.S = attn_splits
         self.nparts = lib.mx_lm_argmax_nparts(self.V)
         self.part = torch.zeros(self.nparts, device=dev, dtype=torch.int64)
@@ -111,7 +115,7 @@ class TextDecoder:
         # decode: fc2 shares the attention's launch (mx_decode_attn_fc2) and proj + residual follow (mx_gemv_res2);
         # False: attention, then both GEMVs in one pass (mx_gemv_dual_res). Same roundings either way.
         self.fc2_with_attn = True
-        self.attn_ws = torch.zeros(self.H * self.S * 66, device=dev, dtype=torch.float32)
+        self.attn_ws = torch.zeros(self.H * 8 * 66, device=dev, dtype=torch.float32)  # split records, S <= 8
         self.attn_cnt = torch.zeros(self.H, device=dev, dtype=torch.int32)
         self.logits = torch.zeros(self.V, device=dev, dtype=BF)
         self.pos_base = 0
@@ -297,21 +301,22 @@ class TextDecoder:
         """Layer i's attention with the fc2 GEMV in the same launch (it reads only the fc1 output), then proj +
         the parallel residual: xn = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)) (md2fast.py:198)."""
         st, lib = stream(), _lib.load()
+        S, part = self.S, self.attn_ws.data_ptr()
         attn = (st, self.qkv_d.data_ptr(), self.cs.data_ptr(), self.kc[i].data_ptr(), self.vc[i].data_ptr(), self.H,
-                self.ctx, self.state.data_ptr(), float(self.hd ** -0.5), self.a_d.data_ptr(), self.g_d.data_ptr())
+                self.ctx, self.state.data_ptr(), float(self.hd ** -0.5), S, part, self.a_d.data_ptr(),
+                self.g_d.data_ptr())
+        att = (self.y2_d.data_ptr(), self.a_d.data_ptr(), S, part)
         if self.w8a8:
             _lib.check(lib.mx_decode_attn_fc2_i8(*attn, b["w2"].data_ptr(), b["sw2"].data_ptr(), b["b2"].data_ptr(),
                                                  b["w2"].shape[1], self.y2_d.data_ptr(), self.D),
                        "mx_decode_attn_fc2_i8")
-            _lib.check(lib.mx_gemv_res2_i8(st, self.y2_d.data_ptr(), self.a_d.data_ptr(), b["wp"].data_ptr(),
-                                           b["swp"].data_ptr(), b["bp"].data_ptr(), b["wp"].shape[1], x.data_ptr(),
-                                           xn.data_ptr(), self.D), "mx_gemv_res2_i8")
+            _lib.check(lib.mx_gemv_res2_i8(st, *att, b["wp"].data_ptr(), b["swp"].data_ptr(), b["bp"].data_ptr(),
+                                           b["wp"].shape[1], x.data_ptr(), xn.data_ptr(), self.D), "mx_gemv_res2_i8")
         else:
             _lib.check(lib.mx_decode_attn_fc2(*attn, b["w2"].data_ptr(), b["b2"].data_ptr(), b["w2"].shape[1],
                                               self.y2_d.data_ptr(), self.D), "mx_decode_attn_fc2")
-            _lib.check(lib.mx_gemv_res2(st, self.y2_d.data_ptr(), self.a_d.data_ptr(), b["wp"].data_ptr(),
-                                        b["bp"].data_ptr(), b["wp"].shape[1], x.data_ptr(), xn.data_ptr(), self.D),
-                       "mx_gemv_res2")
+            _lib.check(lib.mx_gemv_res2(st, *att, b["wp"].data_ptr(), b["bp"].data_ptr(), b["wp"].shape[1],
+                                        x.data_ptr(), xn.data_ptr(), self.D), "mx_gemv_res2")
 
     def capture_step(self):
         """HIP graph of one decode step (the state counter makes each replay the next token)."""

@@ -119,16 +119,18 @@ def test_other_entry_points_refuse_bad_shapes():
     assert lib.mx_ln_gemv_argmax(None, A16, A16, A16, 1e-5, A16, 2048, A16, 51200, 2048, None, A16, 10) == -3
     assert lib.mx_decode_attn(None, A16, A16, A16, A16, 0, 1024, A16, 8, 0.125, A16, A16, A16) == -2   # H < 1
     assert lib.mx_decode_attn(None, A16, A16, A16, A16, 32, 1024, A16, 8, 0.125, None, None, None) == -6
-    af = lambda H=32, K2=8192, g=A16, y2=A16: lib.mx_decode_attn_fc2(None, A16, A16, A16, A16, H, 1024, A16, 0.125, A16,
-                                                                    g, A16, A16, K2, y2, 2048)
+    af = lambda H=32, K2=8192, g=A16, y2=A16, S=1, part=None, a=A16: lib.mx_decode_attn_fc2(
+        None, A16, A16, A16, A16, H, 1024, A16, 0.125, S, part, a, g, A16, A16, K2, y2, 2048)
     assert af(H=0) == -2 and af(K2=4000) == -2 and af(g=A16 + 2) == -4 and af(y2=None) == -6
-    af8 = lambda K2=8192, sw=A16: lib.mx_decode_attn_fc2_i8(None, A16, A16, A16, A16, 32, 1024, A16, 0.125, A16, A16,
-                                                            A16, sw, A16, K2, A16, 2048)
+    assert af(S=9, part=A16) == -2 and af(S=0) == -2 and af(S=2) == -6 and af(a=None) == -6  # S, part / attn_out
+    af8 = lambda K2=8192, sw=A16: lib.mx_decode_attn_fc2_i8(None, A16, A16, A16, A16, 32, 1024, A16, 0.125, 1, None,
+                                                            A16, A16, A16, sw, A16, K2, A16, 2048)
     assert af8(K2=2048) == -2 and af8(sw=None) == -6
-    assert lib.mx_gemv_res2(None, A16, A16, A16, A16, 3000, A16, A16, 2048) == -2            # Kp
-    assert lib.mx_gemv_res2(None, A16, A16 + 8, A16, A16, 2048, A16, A16, 2048) == -4
-    assert lib.mx_gemv_res2_i8(None, A16, A16, A16, None, A16, 2048, A16, A16, 2048) == -6
-    assert lib.mx_gemv_res2_i8(None, A16, A16, A16, A16, A16, 2048, A16, A16, 0) == -2
+    assert lib.mx_gemv_res2(None, A16, A16, 1, None, A16, A16, 3000, A16, A16, 2048) == -2           # Kp
+    assert lib.mx_gemv_res2(None, A16, A16 + 8, 1, None, A16, A16, 2048, A16, A16, 2048) == -4
+    assert lib.mx_gemv_res2(None, A16, None, 4, None, A16, A16, 2048, A16, A16, 2048) == -6          # no records
+    assert lib.mx_gemv_res2_i8(None, A16, A16, 1, None, A16, None, A16, 2048, A16, A16, 2048) == -6
+    assert lib.mx_gemv_res2_i8(None, A16, A16, 1, None, A16, A16, A16, 2048, A16, A16, 0) == -2
     assert lib.mx_residual_layernorm(None, A16, 5, 0, 1152, None, A16, 1152, A16, 1152, None, None, None, 0,
                                      729, 1152, 1e-6) == -2                       # more than 4 splits
     assert lib.mx_gemm_bf16_partial(None, 15, 2, A16, 1152, A16, 1152, A16, 1152, 729 * 1152, 729, 1152,

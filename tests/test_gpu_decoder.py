@@ -150,10 +150,12 @@ def test_decode_attn_vs_fp32(dev, L):
 @pytest.mark.parametrize("D,F_,L,N", [(2048, 8192, 1, 2048), (2048, 8192, 922, 2048), (1024, 4096, 300, 1000)])
 def test_attn_fc2_res2_equals_dual(dev, w8a8, D, F_, L, N):
     """mx_decode_attn_fc2 + mx_gemv_res2 (fc2 in the attention's launch, then proj + residual) against
-    mx_decode_attn + mx_gemv_dual_res (and the _i8 forms), bit for bit: the attention output, the K/V append and
-    x' = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)). Each row's fp32 total has the same pairwise tree
-    in both (the dual kernel's halving exchange and the plain butterfly add the same pairs), the W8A8 sums are exact
-    int32 and the per-token scale is a max; N = 1000 leaves a partial last fc2 workgroup."""
+    mx_decode_attn + mx_gemv_dual_res (and the _i8 forms). One split per head: bit for bit, the attention output, the
+    K/V append and x' = bf16(bf16(fc2(g) + b2) + bf16(bf16(proj(a) + bp) + x)) (each row's fp32 total has the same
+    pairwise tree in both, the W8A8 sums are exact int32 and the per-token scale is a max). 2 and 4 splits merged
+    from their records: the same K/V append, x' within the GEMV tolerance of the fp32 product and within one bf16
+    rounding of the attention output of the one-split result (L = 1: splits with no keys). N = 1000 leaves a partial
+    last fc2 workgroup."""
     H, ctx, pos = D // 64, 1024, L - 1
     g = gen(L + N)
     kc = torch.randn(H, ctx, 64, generator=g).to(BF)
@@ -175,28 +177,43 @@ def test_attn_fc2_res2_equals_dual(dev, w8a8, D, F_, L, N):
     else:
         W2d, Wpd, b2d, bpd = W2.to(dev), Wp.to(dev), b2.to(dev), bp.to(dev)
         w2, wp = (W2d.data_ptr(), b2d.data_ptr()), (Wpd.data_ptr(), bpd.data_ptr())
-    res = []
-    for fused in (False, True):
+    part = torch.full((H * 4 * 66,), float("nan"), device=dev)
+    res = {}
+    for mode in ("dual", 1, 2, 4):
         kd, vd = kc.to(dev), vc.to(dev)
         a = torch.full((H * 64,), float("nan"), device=dev).to(BF)
         out = torch.empty(N, device=dev, dtype=BF)
         attn = (_lib.stream(), qkvd.data_ptr(), fr.data_ptr(), kd.data_ptr(), vd.data_ptr(), H, ctx, state.data_ptr())
-        print(f"attn_fc2 w8a8={w8a8} D={D} L={L} N={N} fused={fused}", flush=True)
+        print(f"attn_fc2 w8a8={w8a8} D={D} L={L} N={N} mode={mode}", flush=True)
         sfx = "_i8" if w8a8 else ""
-        if fused:
-            y2 = torch.empty(N, device=dev, dtype=BF)
-            _lib.call("mx_decode_attn_fc2" + sfx, *attn, 0.125, a.data_ptr(), gd.data_ptr(), *w2, F_, y2.data_ptr(), N)
-            _lib.call("mx_gemv_res2" + sfx, _lib.stream(), y2.data_ptr(), a.data_ptr(), *wp, D, xd.data_ptr(),
-                      out.data_ptr(), N)
-        else:
+        if mode == "dual":
             _lib.call("mx_decode_attn", *attn, 8, 0.125, None, None, a.data_ptr())
             _lib.call("mx_gemv_dual_res" + sfx, _lib.stream(), gd.data_ptr(), *w2, F_, a.data_ptr(), *wp, D,
                       xd.data_ptr(), out.data_ptr(), N)
-        res.append([t.cpu() for t in (a, out, kd[:, pos], vd[:, pos])])
-    for u, v in zip(*res):
+        else:
+            y2 = torch.empty(N, device=dev, dtype=BF)
+            _lib.call("mx_decode_attn_fc2" + sfx, *attn, 0.125, mode, part.data_ptr(), a.data_ptr(), gd.data_ptr(),
+                      *w2, F_, y2.data_ptr(), N)
+            _lib.call("mx_gemv_res2" + sfx, _lib.stream(), y2.data_ptr(), a.data_ptr(), mode, part.data_ptr(), *wp,
+                      D, xd.data_ptr(), out.data_ptr(), N)
+        res[mode] = [t.cpu() for t in (a, out, kd[:, pos], vd[:, pos])]
+    for u, v in zip(res["dual"], res[1]):
         assert torch.equal(u, v)
-    ref = (W2.float() @ gi.float() + b2) + (Wp.float() @ res[0][0].float() + bp) + x.float()
+    a1 = res[1][0].float()
+    ref = (W2.float() @ gi.float() + b2) + (Wp.float() @ a1 + bp) + x.float()
     assert rel(res[1][1], ref) < (2e-2 if w8a8 else 5e-3)
+    # one bf16 rounding of each a element, carried through proj: |Wp| 2^-8 |a| per row; the W8A8 form may also move
+    # every int8 value of a by a step (the per-token scale follows max |a|): |Wp| s_a more. Then one rounding each of
+    # proj(a) + bp and of the output.
+    sa = a1.abs().max().item() / 127.0
+    da = 2.0 ** -8 * a1.abs() + (sa if w8a8 else 0.0)
+    pr = Wp.float() @ a1 + bp
+    slack = Wp.float().abs() @ da + 2.0 ** -7 * (res[1][1].float().abs() + ref.abs() + pr.abs()) + 1e-6
+    for sp in (2, 4):
+        assert torch.equal(res[sp][2], res[1][2]) and torch.equal(res[sp][3], res[1][3]), sp
+        o = res[sp][1].float()
+        assert rel(o, ref) < (2e-2 if w8a8 else 5e-3), sp
+        assert bool(((o - res[1][1].float()).abs() <= slack).all()), sp
 
 
 def _models(layers, seed=0):
