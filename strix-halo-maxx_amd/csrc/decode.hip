@@ -748,7 +748,11 @@ __global__ __launch_bounds__(1024) void attn_fc2_kernel(const uint16_t* __restri
 }
 
 // The W8A8 form: g quantised per token once per fc2 workgroup (16 waves) into LDS, int8 dots summed exactly,
-// y2 = bf16(((acc s_g) s_w) + b2) (the epilogue of the W8A8 dual GEMV).
+// y2 = bf16(((acc s_g) s_w) + b2) (the epilogue of the W8A8 dual GEMV). Its 16.8 MB of int8 rows stream in less time
+// than the attention takes, so the fc2 workgroups start FC2_I8_NAP x 1024 cycles late: the attention's cache loads
+// then do not queue behind them (decode 1762 -> 1815 tok/s at 4; the bf16 form, whose 33.5 MB take as long as the
+// attention, only loses from a delay).
+constexpr int FC2_I8_NAP = 4;
 template <int KI1>
 __global__ __launch_bounds__(1024) void attn_fc2_i8_kernel(const uint16_t* __restrict__ qkv,
                                                            const float* __restrict__ cs, uint16_t* __restrict__ kc,
@@ -765,6 +769,8 @@ __global__ __launch_bounds__(1024) void attn_fc2_i8_kernel(const uint16_t* __res
   }
   __shared__ __attribute__((aligned(16))) uint32_t qgs[KI1 * 256];
   __shared__ float smax[DA_W];
+#pragma unroll
+  for (int i = 0; i < FC2_I8_NAP; i++) __builtin_amdgcn_s_sleep(16);  // 16 x 64 cycles each
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = ((int)blockIdx.x - H * S) * DA_W + wave;
   const int nr = min(n, N - 1);
