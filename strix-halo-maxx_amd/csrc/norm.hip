@@ -8,6 +8,10 @@
 
 namespace {
 
+// Both kernels issue every load of the row (and gamma / beta / sc1) in one straight run before any arithmetic, and
+// run the arithmetic on every chunk: a row is latency-bound, and conditional loads or loads after the statistics
+// would cost further memory round trips. Chunks past the row's end reload its last chunk, add zeros to the sums and
+// store nothing.
 template <int MAXC>
 __global__ __launch_bounds__(256) void layernorm_kernel(const uint16_t* __restrict__ X, long ldx,
                                                         const uint16_t* __restrict__ gamma,
@@ -18,27 +22,34 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const uint16_t* __restri
   if (row >= rows) return;
   const int nch = D >> 3;
   const uint16_t* x = X + (long)row * ldx;
+  u32x4 q[MAXC], gv[MAXC], ev[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = min(lane + 64 * i, nch - 1);
+    q[i] = *reinterpret_cast<const u32x4*>(x + c * 8);
+    gv[i] = *reinterpret_cast<const u32x4*>(gamma + c * 8);
+    ev[i] = *reinterpret_cast<const u32x4*>(beta + c * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float v[MAXC][8];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      const u32x4 q = *reinterpret_cast<const u32x4*>(x + c * 8);
+    const bool ok = lane + 64 * i < nch;
 #pragma unroll
-      for (int e = 0; e < 4; e++) { v[i][2 * e] = lo_bf(q[e]); v[i][2 * e + 1] = hi_bf(q[e]); }
+    for (int e = 0; e < 4; e++) { v[i][2 * e] = lo_bf(q[i][e]); v[i][2 * e + 1] = hi_bf(q[i][e]); }
 #pragma unroll
-      for (int e = 0; e < 8; e++) s += v[i][e];
-    }
+    for (int e = 0; e < 8; e++) s += ok ? v[i][e] : 0.f;
   }
   const float mean = wave_sum(s) / (float)D;
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
+    const bool ok = lane + 64 * i < nch;
 #pragma unroll
-      for (int e = 0; e < 8; e++) { const float d = v[i][e] - mean; ss += d * d; }
+    for (int e = 0; e < 8; e++) {
+      const float d = v[i][e] - mean;
+      ss += ok ? d * d : 0.f;
     }
   }
   const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
@@ -46,18 +57,14 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const uint16_t* __restri
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
     const int c = lane + 64 * i;
-    if (c < nch) {
-      const u32x4 g = *reinterpret_cast<const u32x4*>(gamma + c * 8);
-      const u32x4 bb = *reinterpret_cast<const u32x4*>(beta + c * 8);
-      u32x4 o;
+    u32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float y0 = (v[i][2 * e] - mean) * rstd * lo_bf(g[e]) + lo_bf(bb[e]);
-        const float y1 = (v[i][2 * e + 1] - mean) * rstd * hi_bf(g[e]) + hi_bf(bb[e]);
-        o[e] = pack2(y0, y1);
-      }
-      *reinterpret_cast<u32x4*>(y + c * 8) = o;
+    for (int e = 0; e < 4; e++) {
+      const float y0 = (v[i][2 * e] - mean) * rstd * lo_bf(gv[i][e]) + lo_bf(ev[i][e]);
+      const float y1 = (v[i][2 * e + 1] - mean) * rstd * hi_bf(gv[i][e]) + hi_bf(ev[i][e]);
+      o[e] = pack2(y0, y1);
     }
+    if (c < nch) *reinterpret_cast<u32x4*>(y + c * 8) = o;
   }
 }
 
@@ -70,18 +77,23 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   if (row >= rows) return;
   const int nch = D >> 3;
   const uint16_t* x = X + (long)row * ldx;
+  u32x4 q[MAXC], gv[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = min(lane + 64 * i, nch - 1);
+    q[i] = *reinterpret_cast<const u32x4*>(x + c * 8);
+    gv[i] = *reinterpret_cast<const u32x4*>(sc1 + c * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float v[MAXC][8];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      const u32x4 q = *reinterpret_cast<const u32x4*>(x + c * 8);
+    const bool ok = lane + 64 * i < nch;
 #pragma unroll
-      for (int e = 0; e < 4; e++) { v[i][2 * e] = lo_bf(q[e]); v[i][2 * e + 1] = hi_bf(q[e]); }
+    for (int e = 0; e < 4; e++) { v[i][2 * e] = lo_bf(q[i][e]); v[i][2 * e + 1] = hi_bf(q[i][e]); }
 #pragma unroll
-      for (int e = 0; e < 8; e++) s += rbf(v[i][e] * v[i][e]);
-    }
+    for (int e = 0; e < 8; e++) s += ok ? rbf(v[i][e] * v[i][e]) : 0.f;
   }
   const float ms = rbf(wave_sum(s) / (float)D);
   const float rstd = rbf(1.0f / sqrtf(rbf(ms + eps)));
@@ -89,17 +101,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
     const int c = lane + 64 * i;
-    if (c < nch) {
-      const u32x4 g = *reinterpret_cast<const u32x4*>(sc1 + c * 8);
-      u32x4 o;
+    u32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float y0 = rbf(v[i][2 * e] * rstd) * lo_bf(g[e]);
-        const float y1 = rbf(v[i][2 * e + 1] * rstd) * hi_bf(g[e]);
-        o[e] = pack2(y0, y1);
-      }
-      *reinterpret_cast<u32x4*>(y + c * 8) = o;
+    for (int e = 0; e < 4; e++) {
+      const float y0 = rbf(v[i][2 * e] * rstd) * lo_bf(gv[i][e]);
+      const float y1 = rbf(v[i][2 * e + 1] * rstd) * hi_bf(gv[i][e]);
+      o[e] = pack2(y0, y1);
     }
+    if (c < nch) *reinterpret_cast<u32x4*>(y + c * 8) = o;
   }
 }
 
@@ -117,77 +126,74 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nch = D >> 3;
-  // every load of the row is issued before any arithmetic (the row is latency-bound, not bandwidth-bound)
+  // Every load of the row, gamma and beta included, is issued before any arithmetic, in one straight run: the row is
+  // latency-bound, not bandwidth-bound, and conditional loads would let the compiler wait for some of them before
+  // issuing the rest. Chunks past the row's end load its last chunk and a missing bias / gamma / beta loads from
+  // another valid row; neither is used.
   f32x4 pv[MAXC][NS][2];
-  u32x4 rv[MAXC];
+  u32x4 rv[MAXC], gv[MAXC], ev[MAXC];
   f32x4 bv[MAXC][2];
+  const float* bsrc = bias ? bias : P;
+  const uint16_t* gsrc = gamma ? gamma : R;
+  const uint16_t* esrc = beta ? beta : R;
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      const float* p = P + (long)row * ldp + c * 8;
+    const int c = min(lane + 64 * i, nch - 1);
+    const float* p = P + (long)row * ldp + c * 8;
 #pragma unroll
-      for (int sp = 0; sp < NS; sp++) {
-        pv[i][sp][0] = *reinterpret_cast<const f32x4*>(p + sp * p_split);
-        pv[i][sp][1] = *reinterpret_cast<const f32x4*>(p + sp * p_split + 4);
-      }
-      rv[i] = *reinterpret_cast<const u32x4*>(R + (long)row * ldr + c * 8);
-      if (bias) {
-        bv[i][0] = *reinterpret_cast<const f32x4*>(bias + c * 8);
-        bv[i][1] = *reinterpret_cast<const f32x4*>(bias + c * 8 + 4);
-      } else {
-        bv[i][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-        bv[i][1] = bv[i][0];
-      }
+    for (int sp = 0; sp < NS; sp++) {
+      pv[i][sp][0] = *reinterpret_cast<const f32x4*>(p + sp * p_split);
+      pv[i][sp][1] = *reinterpret_cast<const f32x4*>(p + sp * p_split + 4);
     }
+    rv[i] = *reinterpret_cast<const u32x4*>(R + (long)row * ldr + c * 8);
+    bv[i][0] = *reinterpret_cast<const f32x4*>(bsrc + c * 8);
+    bv[i][1] = *reinterpret_cast<const f32x4*>(bsrc + c * 8 + 4);
+    gv[i] = *reinterpret_cast<const u32x4*>(gsrc + c * 8);
+    ev[i] = *reinterpret_cast<const u32x4*>(esrc + c * 8);
   }
+  __builtin_amdgcn_sched_barrier(0);  // all of them before the first use
+  // The arithmetic runs on every chunk (a branch around it would let the loads sink into it); chunks past the row's
+  // end add zeros to the row sums and store nothing.
   float v[MAXC][8];
   float s = 0.f;
+  const bool hb = bias != nullptr;
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
     const int c = lane + 64 * i;
-    if (c < nch) {
-      float a[8];
+    const bool ok = c < nch;
+    float a[8];
 #pragma unroll
-      for (int e = 0; e < 4; e++) { a[e] = pv[i][0][0][e]; a[4 + e] = pv[i][0][1][e]; }
+    for (int e = 0; e < 4; e++) { a[e] = pv[i][0][0][e]; a[4 + e] = pv[i][0][1][e]; }
 #pragma unroll
-      for (int sp = 1; sp < NS; sp++)
+    for (int sp = 1; sp < NS; sp++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) { a[e] += pv[i][sp][0][e]; a[4 + e] += pv[i][sp][1][e]; }
-      if (bias) {
+      for (int e = 0; e < 4; e++) { a[e] += pv[i][sp][0][e]; a[4 + e] += pv[i][sp][1][e]; }
 #pragma unroll
-        for (int e = 0; e < 4; e++) { a[e] += bv[i][0][e]; a[4 + e] += bv[i][1][e]; }
-      }
-      u32x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        v[i][2 * e] = rbf(rbf(a[2 * e]) + lo_bf(rv[i][e]));
-        v[i][2 * e + 1] = rbf(rbf(a[2 * e + 1]) + hi_bf(rv[i][e]));
-        o[e] = pack2(v[i][2 * e], v[i][2 * e + 1]);
-      }
-      *reinterpret_cast<u32x4*>(Xo + (long)row * ldxo + c * 8) = o;
-#pragma unroll
-      for (int e = 0; e < 8; e++) s += v[i][e];
+    for (int e = 0; e < 4; e++) {
+      a[e] = hb ? a[e] + bv[i][0][e] : a[e];
+      a[4 + e] = hb ? a[4 + e] + bv[i][1][e] : a[4 + e];
     }
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[i][2 * e] = rbf(rbf(a[2 * e]) + lo_bf(rv[i][e]));
+      v[i][2 * e + 1] = rbf(rbf(a[2 * e + 1]) + hi_bf(rv[i][e]));
+      o[e] = pack2(v[i][2 * e], v[i][2 * e + 1]);
+    }
+    if (ok) *reinterpret_cast<u32x4*>(Xo + (long)row * ldxo + c * 8) = o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) s += ok ? v[i][e] : 0.f;
   }
   if (!gamma) return;
-  u32x4 gv[MAXC], ev[MAXC];
-#pragma unroll
-  for (int i = 0; i < MAXC; i++) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      gv[i] = *reinterpret_cast<const u32x4*>(gamma + c * 8);
-      ev[i] = *reinterpret_cast<const u32x4*>(beta + c * 8);
-    }
-  }
   const float mean = wave_sum(s) / (float)D;
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
+    const bool ok = lane + 64 * i < nch;
 #pragma unroll
-      for (int e = 0; e < 8; e++) { const float d = v[i][e] - mean; ss += d * d; }
+    for (int e = 0; e < 8; e++) {
+      const float d = v[i][e] - mean;
+      ss += ok ? d * d : 0.f;
     }
   }
   const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
@@ -195,16 +201,14 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
     const int c = lane + 64 * i;
-    if (c < nch) {
-      u32x4 o;
+    u32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float y0 = (v[i][2 * e] - mean) * rstd * lo_bf(gv[i][e]) + lo_bf(ev[i][e]);
-        const float y1 = (v[i][2 * e + 1] - mean) * rstd * hi_bf(gv[i][e]) + hi_bf(ev[i][e]);
-        o[e] = pack2(y0, y1);
-      }
-      *reinterpret_cast<u32x4*>(y + c * 8) = o;
+    for (int e = 0; e < 4; e++) {
+      const float y0 = (v[i][2 * e] - mean) * rstd * lo_bf(gv[i][e]) + lo_bf(ev[i][e]);
+      const float y1 = (v[i][2 * e + 1] - mean) * rstd * hi_bf(gv[i][e]) + hi_bf(ev[i][e]);
+      o[e] = pack2(y0, y1);
     }
+    if (c < nch) *reinterpret_cast<u32x4*>(y + c * 8) = o;
   }
 }
 
