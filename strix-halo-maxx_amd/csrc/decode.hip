@@ -28,10 +28,11 @@ __device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc) {
   return acc;
 }
 
-// LayerNorm of a row held as KC chunks per lane (chunk c = lane + 64 i): bf16 result in place (torch F.layer_norm
-// numerics: fp32 statistics, biased variance, one rounding).
+// LayerNorm of a row held as KC chunks per lane (chunk c = lane + 64 i), with gamma / beta chunks gc / bc loaded by
+// the caller (before its weight rows, so the normalisation need not wait for them): bf16 result in place (torch
+// F.layer_norm numerics: fp32 statistics, biased variance, one rounding).
 template <int KC>
-__device__ __forceinline__ void ln_chunks(u32x4 (&xc)[KC], const uint16_t* gamma, const uint16_t* beta, float eps,
+__device__ __forceinline__ void ln_chunks(u32x4 (&xc)[KC], const u32x4 (&gc)[KC], const u32x4 (&bc)[KC], float eps,
                                           int K, int lane) {
   float s = 0.f;
 #pragma unroll
@@ -50,9 +51,7 @@ __device__ __forceinline__ void ln_chunks(u32x4 (&xc)[KC], const uint16_t* gamma
   const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)K + eps);
 #pragma unroll
   for (int i = 0; i < KC; i++) {
-    const int c = lane + 64 * i;
-    const u32x4 g = *reinterpret_cast<const u32x4*>(gamma + c * 8);
-    const u32x4 b = *reinterpret_cast<const u32x4*>(beta + c * 8);
+    const u32x4 g = gc[i], b = bc[i];
 #pragma unroll
     for (int e = 0; e < 4; e++)
       xc[i][e] = pack2((lo_bf(xc[i][e]) - mean) * rstd * lo_bf(g[e]) + lo_bf(b[e]),
@@ -105,8 +104,10 @@ __global__ __launch_bounds__(256) void ln_gemv2_kernel(const uint16_t* __restric
   if (row0 >= N) return;
   const int nme = row0 + (lane >> SH);  // the output row this lane completes
   // the small operands first, so the LayerNorm runs while the weight rows stream in
-  u32x4 xc[KC];
+  u32x4 xc[KC], gc[KC], bc[KC];
   load_vec<KC>(xc, x, lane);
+  load_vec<KC>(gc, gamma ? gamma : x, lane);  // x: a stand-in when there is no LayerNorm (not used)
+  load_vec<KC>(bc, beta ? beta : x, lane);
   const float bme = (bias && nme < N) ? bias[nme] : 0.f;
   u32x4 wv[R][KC];
 #pragma unroll
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(256) void ln_gemv2_kernel(const uint16_t* __restric
 #pragma unroll
     for (int i = 0; i < KC; i++) wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (lane + 64 * i) * 8));
   }
-  if (gamma) ln_chunks<KC>(xc, gamma, beta, eps, KC * 512, lane);
+  if (gamma) ln_chunks<KC>(xc, gc, bc, eps, KC * 512, lane);
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -444,8 +445,10 @@ __global__ __launch_bounds__(256) void ln_gemv_argmax_kernel(const uint16_t* __r
   unsigned long long best = 0ull;
   if (row0 < N) {
     const int nme = row0 + (lane >> SH);
-    u32x4 xc[KC];
+    u32x4 xc[KC], gc[KC], bc[KC];
     load_vec<KC>(xc, x, lane);
+    load_vec<KC>(gc, gamma, lane);
+    load_vec<KC>(bc, beta, lane);
     const float bme = nme < N ? bias[nme] : 0.f;
     u32x4 wv[R][KC];
 #pragma unroll
@@ -454,7 +457,7 @@ __global__ __launch_bounds__(256) void ln_gemv_argmax_kernel(const uint16_t* __r
 #pragma unroll
       for (int i = 0; i < KC; i++) wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (lane + 64 * i) * 8));
     }
-    ln_chunks<KC>(xc, gamma, beta, eps, KC * 512, lane);
+    ln_chunks<KC>(xc, gc, bc, eps, KC * 512, lane);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
