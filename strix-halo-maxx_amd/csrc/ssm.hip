@@ -79,37 +79,66 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   // this thread's slots in the gate products' result layout (lane = channel, registers = 16 tokens)
   const int tm = wave >> 1, tn = wave & 1;
   const int cl = tn * 32 + lr, c = c0 + cl;
+  // the gate products' weight fragments and the per-channel RG-LRU parameters depend on nothing below: issued first
+  // (the 16-bit parameters held unpacked, so no wait is needed to pack them)
+  u32x4 wxf[4], waf[4];
+  {
+    const uint16_t* wxr = p.wxT + ((long)q * 64 + tn * 32 + lr) * 64;
+    const uint16_t* war = p.waT + ((long)q * 64 + tn * 32 + lr) * 64;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) {
+      wxf[s4] = *reinterpret_cast<const u32x4*>(wxr + 16 * s4 + 8 * hk);
+      waf[s4] = *reinterpret_cast<const u32x4*>(war + 16 * s4 + 8 * hk);
+    }
+  }
+  const uint32_t spw = p.sp[c], bxw = p.bx[c], baw = p.ba[c];
 
   // ---- step form: the fp32 state and yg of this thread's 16 (token, channel) slots are loaded first, so their
-  // latency runs under the conv and the gate products (each slot belongs to this thread alone)
-  float hpre[16], ypre[16];
-#pragma unroll
-  for (int r = 0; r < 16; r++) {
-    hpre[r] = 0.f;
-    ypre[r] = 0.f;
-  }
+  // latency runs under the conv and the gate products (each slot belongs to this thread alone). The loads take
+  // clamped indices and no branch separates them (a per-slot branch made the compiler wait for each slot's loads in
+  // turn); which slots count (token < T, first frame, fresh crop row) is applied where the values are used. The crop
+  // form's row map, stamps and state are three dependent rounds, each issued for all 16 slots.
+  float hraw[16];
+  uint32_t yraw[16];    // the yg bf16 word of each slot, held unpacked (packing two per register would wait for them)
+  int rw[16];           // state row of each slot
+  uint32_t freshm = 0u;  // bit r: slot r's crop row was not in the crop on the previous frame (its state reads as 0)
   if (p.mode == 0) {
+    if (p.rows) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int token = min(t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3), p.T - 1);
+        rw[r] = min(max(p.rows[token], 0), p.srows - 1);
+      }
+      if (!first) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          bool fresh;
+          int enter;
+          row_stamp(p, rw[r], tnow, fresh, enter);
+          freshm |= (fresh ? 1u : 0u) << r;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) rw[r] = min(t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3), p.T - 1);
+    }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int token = t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
-      if (token < p.T) {
-        const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;
-        bool fresh = false;
-        if (p.rows && !first) {
-          int enter;
-          row_stamp(p, row, tnow, fresh, enter);
-        }
-        if (!first && !fresh) hpre[r] = p.h[(long)row * p.C + c];
-        ypre[r] = bf2f(p.yg[f * p.fs_y + (long)token * p.ld_y + c]);
-      }
+      const int token = min(t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3), p.T - 1);
+      hraw[r] = p.h[(long)rw[r] * p.C + c];
+      yraw[r] = p.yg[f * p.fs_y + (long)token * p.ld_y + c];
     }
   }
 
-  // ---- temporal conv of this 64 x 64 tile into LDS (8 channels per item, 2 items per thread)
+  // ---- temporal conv of this 64 x 64 tile into LDS (8 channels per item, 2 items per thread). Both items' loads go
+  // out before either item's arithmetic (one memory round trip, not two); both items share the channel group cc
+  // (256 is a multiple of 8), so the conv weights and bias are loaded once.
+  const int cc = (tid & 7) * 8;
+  u32x4 xv[2][4];
+  int rowv[2], enterv[2];
 #pragma unroll
   for (int it = 0; it < 2; it++) {
-    const int ch = tid + 256 * it;
-    const int tok = ch >> 3, cc = (ch & 7) * 8;
+    const int tok = (tid + 256 * it) >> 3;
     const int token = min(t0 + tok, p.T - 1);
     const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;  // clamped: never out of bounds
     int ntap = first ? 1 : 4;  // taps 0 .. ntap - 1 carry data; the older ones are zero
@@ -119,22 +148,27 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
       row_stamp(p, row, tnow, fresh, enter);
       ntap = fresh ? 1 : min(4, tnow - enter + 1);  // tap k (frame tnow - k) needs enter <= tnow - k
     }
-    u32x4 xv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       u32x4 v = {0u, 0u, 0u, 0u};
       const long r = i == 0 ? token : row;  // the current frame's rows are the launch's tokens
       if (i < ntap) v = *reinterpret_cast<const u32x4*>(p.tap[i] + f * p.fs_x + r * p.ld_x + c0 + cc);
-      xv[i] = v;
+      xv[it][i] = v;
     }
-    if (p.rows && t0 + tok < p.T) {
-      *reinterpret_cast<u32x4*>(p.xsave + (long)row * p.ld_save + c0 + cc) = xv[0];
-      if (q == 0 && cc == 0) p.stamps[(tnow & 1) * p.srows + row] = make_int2(enter, tnow);
-    }
-    const u32x4 bb = *reinterpret_cast<const u32x4*>(p.conv_b + c0 + cc);
-    u32x4 w[4];
+    rowv[it] = row;
+    enterv[it] = enter;
+  }
+  const u32x4 bb = *reinterpret_cast<const u32x4*>(p.conv_b + c0 + cc);
+  u32x4 w[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) w[i] = *reinterpret_cast<const u32x4*>(p.conv_w + i * p.C + c0 + cc);
+  for (int i = 0; i < 4; i++) w[i] = *reinterpret_cast<const u32x4*>(p.conv_w + i * p.C + c0 + cc);
+#pragma unroll
+  for (int it = 0; it < 2; it++) {
+    const int tok = (tid + 256 * it) >> 3;
+    if (p.rows && t0 + tok < p.T) {
+      *reinterpret_cast<u32x4*>(p.xsave + (long)rowv[it] * p.ld_save + c0 + cc) = xv[it][0];
+      if (q == 0 && cc == 0) p.stamps[(tnow & 1) * p.srows + rowv[it]] = make_int2(enterv[it], tnow);
+    }
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -143,11 +177,11 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
       for (int hl = 0; hl < 2; hl++) {
         auto get = [&](u32x4 v) { return hl ? hi_bf(v[e]) : lo_bf(v[e]); };
         // w row i = tap (t-3+i): oldest first; xv index 3-i holds frame t-3+i
-        float s = rbf(get(xv[3]) * get(w[0]));
-        s = s + rbf(get(xv[2]) * get(w[1]));
-        s = s + rbf(get(xv[1]) * get(w[2]));
-        s = s + rbf(get(xv[0]) * get(w[3]));
-        r[hl] = rbf(s) + get(bb);
+        float sum = rbf(get(xv[it][3]) * get(w[0]));
+        sum = sum + rbf(get(xv[it][2]) * get(w[1]));
+        sum = sum + rbf(get(xv[it][1]) * get(w[2]));
+        sum = sum + rbf(get(xv[it][0]) * get(w[3]));
+        r[hl] = rbf(sum) + get(bb);
       }
       o[e] = pack2(r[0], r[1]);
     }
@@ -159,18 +193,16 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   f32x16 gx, ga;
 #pragma unroll
   for (int e = 0; e < 16; e++) { gx[e] = 0.f; ga[e] = 0.f; }
-  const uint16_t* wxr = p.wxT + ((long)q * 64 + tn * 32 + lr) * 64;
-  const uint16_t* war = p.waT + ((long)q * 64 + tn * 32 + lr) * 64;
 #pragma unroll
   for (int s = 0; s < 4; s++) {
     const int k = 16 * s + 8 * hk;
     const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(&xs[(tm * 32 + lr) * XS + k]));
-    gx = mfma32(a, as_bf16x8(*reinterpret_cast<const u32x4*>(wxr + k)), gx);
-    ga = mfma32(a, as_bf16x8(*reinterpret_cast<const u32x4*>(war + k)), ga);
+    gx = mfma32(a, as_bf16x8(wxf[s]), gx);
+    ga = mfma32(a, as_bf16x8(waf[s]), ga);
   }
 
   // ---- elementwise RG-LRU: lane = channel, registers = 16 tokens
-  const float spc = bf2f(p.sp[c]), bxc = bf2f(p.bx[c]), bac = bf2f(p.ba[c]);
+  const float spc = bf2f((uint16_t)spw), bxc = bf2f((uint16_t)bxw), bac = bf2f((uint16_t)baw);
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int tl = tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
@@ -194,10 +226,10 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
     }
     const long idx = (long)token * p.C + c;
     if (p.mode == 0) {
-      const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;
-      const float h = first ? g : __fadd_rn(__fmul_rn(Am, hpre[r]), Bm);  // hpre = 0 for a fresh crop row
-      p.h[(long)row * p.C + c] = h;
-      p.z[f * p.fs_z + (long)token * p.ld_z + c] = f2bf(rbf(h) * ypre[r]);
+      const float hp = ((freshm >> r) & 1u) ? 0.f : hraw[r];  // a fresh crop row starts from 0
+      const float h = first ? g : __fadd_rn(__fmul_rn(Am, hp), Bm);
+      p.h[(long)rw[r] * p.C + c] = h;
+      p.z[f * p.fs_z + (long)token * p.ld_z + c] = f2bf(rbf(h) * bf2f((uint16_t)yraw[r]));
     } else {
       p.A[f * p.fs_ab + idx] = Am;
       p.B[f * p.fs_ab + idx] = Bm;
