@@ -6,8 +6,10 @@ Prints ONE JSON line with the headline value plus:
                 algorithmic FLOPs per launch / average launch time vs the 2.5 PFLOP/s dense bf16 MFMA peak
   cpu_baseline  the oracle (the reference's PyTorch bf16 path restated, torch on the host cores) on the same
                 workload, a bounded number of frames
-  extra         secondary workloads when asked for (--extra): tower batch 13 / 256 throughput
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extra]
+  extra         secondary workloads (skipped with --no-extra): tower batch 13 / 256 throughput (batch 256 = the
+                throughput-bound tower), text decoder prefill / decode / yes-no query (bf16 and W8A8), TRecViT
+                streamed / clip; the decoder and TRecViT lines carry their own CPU baselines (the oracle on the host)
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 """
 import argparse
 import json
@@ -332,12 +334,17 @@ def measured_traffic(label, sym):
     return int(e["bytes_per_launch"]), os.path.relpath(TRAFFIC_FILE, os.path.dirname(TRAFFIC_FILE) + "/..")
 
 
+def _cpu_threads():
+    """Threads for the CPU baselines: the host's logical CPUs, at most 16 (the box's CPU share for one GPU)."""
+    return min(os.cpu_count() or 1, 16)
+
+
 def cpu_baseline(budget_s=20.0):
     """The oracle (torch bf16 on the host cores) on the same workload: whole 27-block tower, batch 1."""
     import torch
     import oracle.md2_vision as ov
     import strix_halo_maxx_amd.synth as S
-    threads = min(os.cpu_count() or 1, 16)
+    threads = _cpu_threads()
     torch.set_num_threads(threads)
     w = S.vision_weights(0)
     img = S.images_u8(1, 1)
@@ -352,8 +359,64 @@ def cpu_baseline(budget_s=20.0):
             ov.tower(w, img)
             ts.append(time.perf_counter() - t0)
     return {"value": round(statistics.median(ts) * 1e3, 2), "unit": "ms/frame", "cores": threads, "kind": "port",
+            "threads": threads, "host_logical_cpus": os.cpu_count(),
             "sample": f"oracle (reference's torch bf16 path restated) full 27-block tower + post-LN, batch 1, "
                       f"median of {n} frames after 1 warm-up, torch.set_num_threads({threads})"}
+
+
+def cpu_baseline_decoder(n_tokens=8):
+    """Config 2 on the host cores: the oracle decoder (the reference's torch bf16 text path restated), prefill of
+    1 + 729 image tokens + 64 prompt ids once, then n_tokens greedy steps; tok/s over the decode steps."""
+    import torch
+    import oracle.md2_text as ot
+    import strix_halo_maxx_amd.synth as S
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    w = S.text_weights(0)
+    img = S.activations(3, (729, 2048), "img")
+    prompt = S.prompt_ids(4, 64)
+    with torch.inference_mode():
+        m = ot.Text(w, 1024, S.freqs_cis(32, 2048))
+        t0 = time.perf_counter()
+        lg = m.prefill(img, prompt)
+        t_pre = time.perf_counter() - t0
+        ts = []
+        for _ in range(n_tokens):
+            tok = int(torch.argmax(lg))
+            t0 = time.perf_counter()
+            lg = m.step(tok)
+            ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    return {"value": round(1.0 / med, 2), "unit": "tok/s", "prefill_ms": round(t_pre * 1e3, 1), "cores": threads,
+            "kind": "port", "threads": threads, "host_logical_cpus": os.cpu_count(),
+            "sample": f"oracle text decoder, 24 layers: one prefill of 730 + 64 tokens, then {n_tokens} greedy steps "
+                      f"(tok/s = 1 / median step time), torch.set_num_threads({threads})"}
+
+
+def cpu_baseline_trecvit(frames=8):
+    """Config 3 on the host cores: the oracle TRecViT (the reference's torch bf16 block restated), 12 blocks, 1024
+    patch + 256 query tokens, `frames` streamed frames after one warm-up frame; ms/frame (median)."""
+    import torch
+    import oracle.trecvit as otr
+    import strix_halo_maxx_amd.synth as S
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    m = otr.Model(S.trecvit_weights(0))
+    fr = S.frames_u8(1, frames + 1)
+    q = S.query_points(5, 256)
+    qf = (q[:, 1:] / 256.0).to(torch.bfloat16)
+    ts = []
+    with torch.inference_mode():
+        for t in range(frames + 1):
+            t0 = time.perf_counter()
+            m.step(fr[t], qf)
+            if t:
+                ts.append(time.perf_counter() - t0)
+    return {"value": round(statistics.median(ts) * 1e3, 1), "unit": "ms/frame", "cores": threads, "kind": "port",
+            "threads": threads, "host_logical_cpus": os.cpu_count(),
+            "sample": f"oracle TRecViT, 12 blocks, 1280 tokens, median of {frames} streamed frames after 1 warm-up "
+                      f"frame, torch.set_num_threads({threads}); the reference published 710.5 ms/frame at 1,072 "
+                      f"tokens with 8 threads on its own CPU"}
 
 
 def decode_bench(steps_tokens=128, w8a8=False):
@@ -384,7 +447,7 @@ def decode_bench(steps_tokens=128, w8a8=False):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps_tokens - 1):
-        dec.graph.replay()
+        dec.replay_step()
     torch.cuda.synchronize()
     t_dec = (time.perf_counter() - t0) / (steps_tokens - 1)
     # the reference's yes/no query (FastMD2.query, md2fast.py:208-212): a 32-id question over the 730-token prefix,
@@ -504,6 +567,55 @@ def scan_roofline(m, F, launches=24):
             "avg_launch_us": round(us, 2), "bytes_per_launch": nbytes}
 
 
+def large_batch_ops(vt, imgs, reps=5):
+    """Per-op launch time of one tower block at a large batch (the throughput-bound config: its GEMMs run the
+    large-M tiles, not the batch-1 split-K path): qkv, attention, proj (+ residual), LN, fc1 (+ GELU), fc2
+    (+ residual), each on block 0's real operands, `reps` launches between HIP events on the launching stream.
+    Returns {op: {"us", "tflops", "mfma_frac"}} (LN: GB/s instead)."""
+    import torch
+    import strix_halo_maxx_amd.ops as ops
+    B = imgs.shape[0]
+    T, D, H, hd = vt.T, vt.D, vt.H, vt.hd
+    M = B * T
+    b = vt.blocks[0]
+    x = vt.embed(imgs)
+    h = ops.layernorm(x, *b["ln1"], eps=vt.eps)
+    qkv = b["qkv"](h)
+    q5 = qkv.view(B, T, 3, H, hd)
+    q, k, v = (q5[:, :, j].transpose(1, 2) for j in range(3))
+    a = vt.attn(q, k, v).view(M, D)
+    x1 = b["proj"](a, res=x)
+    h2 = ops.layernorm(x1, *b["ln2"], eps=vt.eps)
+    f = b["fc1"](h2, gelu=True)
+    F = f.shape[1]
+    y = torch.empty_like(x)
+    ops_ = {"qkv": (2 * M * D * 3 * D, lambda: b["qkv"](h, out=qkv)),
+            "attn": (4 * B * H * T * T * hd, lambda: ops.sdpa(q, k, v, out=a.view(B, T, D))),
+            "proj": (2 * M * D * D, lambda: b["proj"](a, res=x, out=y)),
+            "ln": (0, lambda: ops.layernorm(x1, *b["ln2"], eps=vt.eps, out=h2)),
+            "fc1": (2 * M * D * F, lambda: b["fc1"](h2, gelu=True, out=f)),
+            "fc2": (2 * M * F * D, lambda: b["fc2"](f, res=x1, out=y))}
+    st = torch.cuda.current_stream()
+    res = {}
+    for name, (fl, fn) in ops_.items():
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        if fl:
+            res[name] = {"us": round(us, 1), "tflops": round(fl / us / 1e6, 1), "mfma_frac": round(fl / us / 1e6 / (PEAK_BF16 / 1e12), 4)}
+        else:
+            res[name] = {"us": round(us, 1), "gb_s": round(4 * M * D / us / 1e3, 1)}
+    gemm_fl = sum(ops_[k][0] for k in ("qkv", "proj", "fc1", "fc2"))
+    gemm_us = sum(res[k]["us"] for k in ("qkv", "proj", "fc1", "fc2"))
+    res["gemms"] = {"tflops": round(gemm_fl / gemm_us / 1e6, 1), "mfma_frac": round(gemm_fl / gemm_us / 1e6 / (PEAK_BF16 / 1e12), 4)}
+    return res
+
+
 def tower_time(vt, img, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -525,7 +637,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--extra", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="headline tower only (no batch 13 / 256, decoder, TRecViT)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the eager launches that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count (see traffic_probe)")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -583,7 +695,8 @@ def main():
                       "batch": 1, "tokens": 729, "layers": 27},
            "tower_tflops": round(tower_flops / s / 1e12, 1), "tower_mfma_frac": round(tower_flops / s / PEAK_BF16, 4),
            "roofline": roof}
-    if a.extra:
+    if not a.no_extra:
+        print("[bench] tower batch 13 / 256", file=sys.stderr, flush=True)
         with torch.inference_mode():
             for B in (13, 256):
                 imgs = S.images_u8(2, B).to(dev)
@@ -591,25 +704,33 @@ def main():
                 out.setdefault("extra", {})[f"tower_b{B}"] = {"ms_per_batch": round(sb * 1e3, 3),
                                                               "images_per_s": round(B / sb, 1),
                                                               "mfma_frac": round(B * tower_flops / sb / PEAK_BF16, 4)}
+                if B == 256:
+                    vt.graphs.clear()
+                    out["extra"]["tower_b256"]["per_op_block0"] = large_batch_ops(vt, imgs)
                 del imgs
                 vt.graphs.clear()
                 torch.cuda.empty_cache()
     del vt
     torch.cuda.empty_cache()
-    print("[bench] decoder", file=sys.stderr, flush=True)
-    with torch.inference_mode():
-        out.setdefault("extra", {})["decoder"] = decode_bench()
-    torch.cuda.empty_cache()
-    print("[bench] decoder w8a8", file=sys.stderr, flush=True)
-    with torch.inference_mode():
-        out["extra"]["decoder_w8a8"] = decode_bench(w8a8=True)
-    torch.cuda.empty_cache()
-    print("[bench] trecvit", file=sys.stderr, flush=True)
-    with torch.inference_mode():
-        out["extra"]["trecvit"] = trecvit_bench()
+    if not a.no_extra:
+        print("[bench] decoder", file=sys.stderr, flush=True)
+        with torch.inference_mode():
+            out.setdefault("extra", {})["decoder"] = decode_bench()
+        torch.cuda.empty_cache()
+        print("[bench] decoder w8a8", file=sys.stderr, flush=True)
+        with torch.inference_mode():
+            out["extra"]["decoder_w8a8"] = decode_bench(w8a8=True)
+        torch.cuda.empty_cache()
+        print("[bench] trecvit", file=sys.stderr, flush=True)
+        with torch.inference_mode():
+            out["extra"]["trecvit"] = trecvit_bench()
     if not a.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline()
+        if not a.no_extra:
+            print("[bench] cpu baseline: decoder, trecvit", file=sys.stderr, flush=True)
+            out["extra"]["decoder"]["cpu_baseline"] = cpu_baseline_decoder()
+            out["extra"]["trecvit"]["cpu_baseline"] = cpu_baseline_trecvit()
     print(json.dumps(out), flush=True)
 
 

@@ -170,9 +170,12 @@ int mx_ln_gemv_argmax(hipStream_t st, const uint16_t* x, const uint16_t* gamma, 
                       unsigned long long* part, int nparts);
 int mx_lm_argmax_nparts(int N);
 /* Reduce the argmax keys -> token; tokens[state[0]] = token; state[1] = pos_base + state[0]; state[0]++;
- * x = wte[token]. Replaces the host-side argmax + F.embedding of a greedy step (md2fast.py:209). */
+ * x = wte[token]. cap = the steps the caller's buffers hold (tokens[] entries and cache rows past pos_base): at
+ * state[0] >= cap nothing is recorded and the state stops advancing, so a step the caller did not stop cannot write
+ * past them (the decode attention also clamps its position below ctx). Replaces the host-side argmax + F.embedding
+ * of a greedy step (md2fast.py:209). */
 int mx_embed_step(hipStream_t st, const unsigned long long* part, int nparts, const uint16_t* wte, int D, int* state,
-                  int pos_base, int* tokens, uint16_t* x);
+                  int pos_base, int* tokens, int cap, uint16_t* x);
 /* One decode token: rope of q and k at pos = state[1], K/V append at pos, attention over keys 0..pos into out
  * (H * 64): one workgroup per head, 16 waves with a one-pass online softmax each, merged in LDS. S, ws and cnt
  * are unused (ws / cnt may be null; kept for ABI stability). Replaces the SDPA over the KV cache of md2fast.py:185 for one

@@ -86,18 +86,21 @@ def i8_linear(q, sx, wq, sw, bias, gelu_tanh=False):
 
 
 class Text:
-    def __init__(self, w, ctx, freqs, bos=50256, H=32, w8a8=False):
+    def __init__(self, w, ctx, freqs, bos=50256, H=32, w8a8=False, dtype=BF):
+        """dtype: the activation / cache type. BF is the reference's bf16 path; torch.float32 (with fp32 weights)
+        is the same op sequence without bf16 roundings, used as the arbiter of near-tied greedy steps."""
         self.w = w
         self.H = H
         self.w8a8 = w8a8
+        self.dt = dtype
         self.D = w["wte"].shape[1]
         self.hd = self.D // H
         n = 0
         while f"blocks.{n}.ln.weight" in w:
             n += 1
         self.n = n
-        self.kc = [torch.zeros(1, H, ctx, self.hd, dtype=BF) for _ in range(n)]
-        self.vc = [torch.zeros(1, H, ctx, self.hd, dtype=BF) for _ in range(n)]
+        self.kc = [torch.zeros(1, H, ctx, self.hd, dtype=dtype) for _ in range(n)]
+        self.vc = [torch.zeros(1, H, ctx, self.hd, dtype=dtype) for _ in range(n)]
         self.cos, self.sin = freqs[..., 0].contiguous(), freqs[..., 1].contiguous()
         self.bos = bos
         if w8a8:
@@ -147,7 +150,7 @@ class Text:
     def encode(self, img_emb):
         """md2fast.py:201-206: [BOS] + image tokens, mask-free. Returns the prefix hidden states."""
         w = self.w
-        x = torch.cat([w["wte"][self.bos:self.bos + 1], img_emb.to(BF)], dim=0)[None]
+        x = torch.cat([w["wte"][self.bos:self.bos + 1], img_emb.to(self.dt)], dim=0)[None]
         self.P = x.shape[1]
         return self.layers(x, 0, None)
 

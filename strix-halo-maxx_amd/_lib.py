@@ -49,7 +49,7 @@ SIGNATURES = {
     "mx_gemv_dual_res_i8": [P, P, P, P, P, I, P, P, P, P, I, P, P, I],
     "mx_lm_argmax_nparts": [I],
     "mx_ln_gemv_argmax": [P, P, P, P, F, P, L, P, I, I, P, P, I],
-    "mx_embed_step": [P, P, I, P, I, P, I, P, P],
+    "mx_embed_step": [P, P, I, P, I, P, I, P, I, P],
     "mx_decode_attn": [P, P, P, P, P, I, I, P, I, F, P, P, P],
     "mx_decode_attn_fc2": [P, P, P, P, P, I, I, P, F, I, P, P, P, P, P, I, P, I],
     "mx_gemv_res2": [P, P, P, I, P, P, P, I, P, P, I],

@@ -489,10 +489,13 @@ __global__ __launch_bounds__(256) void ln_gemv_argmax_kernel(const uint16_t* __r
 
 // ---------------------------------------------------------------------------------------------- embed_step
 // state[0] = step s (tokens emitted so far), state[1] = position of the token fed this step (= pos_base + s).
+// cap: the number of steps the caches and tokens[] have room for; at s >= cap nothing is recorded and the state stops
+// advancing (the host refuses such steps; this keeps a step it did not refuse inside the buffers).
 __global__ __launch_bounds__(1024) void embed_step_kernel(const unsigned long long* __restrict__ part, int nparts,
                                                           const uint16_t* __restrict__ wte, int D,
                                                           int* __restrict__ state, int pos_base,
-                                                          int* __restrict__ tokens, uint16_t* __restrict__ x) {
+                                                          int* __restrict__ tokens, int cap,
+                                                          uint16_t* __restrict__ x) {
   __shared__ unsigned long long sb[16];
   __shared__ int stok;
   unsigned long long b = 0ull;
@@ -510,9 +513,11 @@ __global__ __launch_bounds__(1024) void embed_step_kernel(const unsigned long lo
     const int tok = (int)(0xffffffffu - (uint32_t)(m & 0xffffffffull));
     stok = tok;
     const int s = state[0];
-    tokens[s] = tok;
-    state[1] = pos_base + s;
-    state[0] = s + 1;
+    if (s < cap) {
+      tokens[s] = tok;
+      state[1] = pos_base + s;
+      state[0] = s + 1;
+    }
   }
   __syncthreads();
   const int tok = stok;
@@ -539,7 +544,8 @@ __device__ __forceinline__ void attn_head(int h, int sp, int S, const uint16_t* 
   __shared__ __attribute__((aligned(16))) uint16_t qs[64], knew[64], vnew[64];  // bf16 q, k, v of the new token
   __shared__ float rec[DA_W][66];  // (m, l, o[64]) of each wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pos = state[1];
+  // state[1] reaches ctx only for a step the host refuses (the embed step's cap); never address past the cache
+  const int pos = min(max(state[1], 0), ctx - 1);
   const int L = pos + 1;
   const int chunk = S == 1 ? L : (((L + S - 1) / S + 7) & ~7);
   const int kb = sp * chunk, ke = min(L, kb + chunk);  // this workgroup's keys (empty when kb >= L)
@@ -955,10 +961,11 @@ extern "C" int mx_ln_gemv_argmax(hipStream_t st, const uint16_t* x, const uint16
 }
 
 extern "C" int mx_embed_step(hipStream_t st, const unsigned long long* part, int nparts, const uint16_t* wte, int D,
-                             int* state, int pos_base, int* tokens, uint16_t* x) {
+                             int* state, int pos_base, int* tokens, int cap, uint16_t* x) {
   if (!part || !wte || !state || !tokens || !x) return MX_ENULL;
-  if (nparts < 1 || D % 8) return MX_ESHAPE;
-  hipLaunchKernelGGL(embed_step_kernel, dim3(1), dim3(1024), 0, st, part, nparts, wte, D, state, pos_base, tokens, x);
+  if (nparts < 1 || D % 8 || cap < 1 || pos_base < 0) return MX_ESHAPE;
+  hipLaunchKernelGGL(embed_step_kernel, dim3(1), dim3(1024), 0, st, part, nparts, wte, D, state, pos_base, tokens, cap,
+                     x);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 

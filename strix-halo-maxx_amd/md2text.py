@@ -119,6 +119,7 @@ class TextDecoder:
         self.attn_cnt = torch.zeros(self.H, device=dev, dtype=torch.int32)
         self.logits = torch.zeros(self.V, device=dev, dtype=BF)
         self.pos_base = 0
+        self.steps = 0
         self.graph = None
 
     # ------------------------------------------------------------------ prefill (md2fast.py:169-212)
@@ -245,18 +246,42 @@ class TextDecoder:
              ptr(self.logits) if logits else None, self.part.data_ptr(), self.nparts)
 
     # ------------------------------------------------------------------ decode
+    def _check_room(self, pos_base, n_tokens):
+        """n_tokens generated from a prefill that ends at pos_base - 1 need n_tokens - 1 decode steps at positions
+        pos_base .. pos_base + n_tokens - 2, all below ctx."""
+        if n_tokens < 1 or pos_base + n_tokens - 1 > self.ctx:
+            raise ValueError(f"{n_tokens} tokens after a {pos_base}-token prefill exceed the {self.ctx}-entry KV cache")
+
     def start_decode(self):
         """Reset the step counter and feed the prefill's argmax token (becomes tokens[0])."""
         self.state.zero_()
+        self.steps = 0
         self._embed()
 
     def _embed(self):
+        # cap: steps the cache holds beyond the prefill (+ 1 for the prefill's own token), so the device state can
+        # never index past the cache or tokens[] even if a step the host allowed ran once too often
+        cap = max(1, min(self.ctx - self.pos_base + 1, self.ctx))
         call("mx_embed_step", stream(), self.part.data_ptr(), self.nparts, self.wte.data_ptr(), self.D,
-             self.state.data_ptr(), self.pos_base, self.tokens.data_ptr(), self.xd[0].data_ptr())
+             self.state.data_ptr(), self.pos_base, self.tokens.data_ptr(), cap, self.xd[0].data_ptr())
+
+    def _count_step(self):
+        """Host count of the decode steps since start_decode (the device state is never read back): refuse a step
+        whose position would fall outside the cache."""
+        if self.pos_base + self.steps >= self.ctx:
+            raise ValueError(f"decode step at position {self.pos_base + self.steps} is past the {self.ctx}-entry cache")
+        self.steps += 1
+
+    def replay_step(self):
+        """One decode step by graph replay (captured with capture_step), with the same capacity check."""
+        self._count_step()
+        self.graph.replay()
 
     def decode_step(self, logits=False):
         """One greedy step for the token in xd[0] at position state[1]: appends its K/V, computes the next token's
         argmax and embeds it into xd[0]. Graph-capturable (no host reads)."""
+        if not torch.cuda.is_current_stream_capturing():
+            self._count_step()
         st = stream()
         lib = _lib.load()
         xi = 0
@@ -327,14 +352,16 @@ class TextDecoder:
         return g
 
     def generate(self, img_emb, prompt_ids, n_tokens, use_graph=True):
-        """Prefill + greedy decode; returns the n_tokens generated ids (the first comes from the prompt prefill)."""
+        """Prefill + greedy decode; returns the n_tokens generated ids (the first comes from the prompt prefill).
+        Raises ValueError, before any work, when the prefill plus n_tokens - 1 decode steps would not fit the cache."""
+        self._check_room(1 + img_emb.shape[0] + prompt_ids.shape[0], n_tokens)
         self.prefill(img_emb, prompt_ids)
         self.start_decode()
         if use_graph:
             if self.graph is None:
                 self.capture_step()  # recording does not execute the step
             for _ in range(n_tokens - 1):
-                self.graph.replay()
+                self.replay_step()
         else:
             for _ in range(n_tokens - 1):
                 self.decode_step()

@@ -2,8 +2,9 @@
 
 Every tensor is drawn from its own torch.Generator seeded by (base seed, crc32(name)), so any subset of a model
 (one block, two layers, ...) gets exactly the tensors the full model would get. Weights and biases ~ N(0, 0.02);
-LayerNorm gamma = 1, beta = 0; RMSNorm scale = 0 (so scale + 1 = 1). All tensors are returned on the CPU in bf16 unless
+LayerNorm gamma = 1, beta = 0. All tensors are returned on the CPU in bf16 unless
 stated; callers move them to the device.
+TRecViT RMSNorm scales ~ N(0, 0.1), so the (1 + scale) factor differs from 1 per channel.
 
 Parameter names follow the models the reference loads:
   * moondream2 vision / text (md2fast.py:90-94, :108-112 read model.vision.blocks[i].attn.qkv etc.)
@@ -116,8 +117,8 @@ def trecvit_weights(seed=0, layers=None):
         mb = f"blocks.{i}.ssm_block.mlp_block."
         vb = f"blocks.{i}.vit_block."
         sb = f"blocks.{i}.ssm_block."
-        w[sb + "temporal_pre_norm.scale"] = zeros((D,))
-        w[sb + "channel_pre_norm.scale"] = zeros((D,))
+        w[sb + "temporal_pre_norm.scale"] = normal(seed, sb + "temporal_pre_norm.scale", (D,), std=0.1)
+        w[sb + "channel_pre_norm.scale"] = normal(seed, sb + "channel_pre_norm.scale", (D,), std=0.1)
         for name, shape in ((rb + "linear_yx", (2 * D, D)), (rb + "linear_out", (D, D)),
                             (mb + "ffw_up", (2 * c["ff_gated"], D)), (mb + "ffw_down", (D, c["ff_gated"])),
                             (vb + "self_attention.in_proj", (3 * D, D)), (vb + "self_attention.out_proj", (D, D)),

@@ -7,6 +7,7 @@ import os
 import re
 
 import pytest
+import torch
 
 from strix_halo_maxx_amd import _lib
 
@@ -186,3 +187,20 @@ def test_other_entry_points_refuse_bad_shapes():
     assert i8(cfg=8) == -1                                                          # wave-split configs: bf16 only
     assert i8(cfg=15, P=A16, ldp=2048) == -1                                        # raw int32 needs a partial-sum cfg
     assert i8(act=3) == -1 and i8(A=A16 + 8) == -4 and i8(sw=None) == -6
+
+
+def test_generate_refuses_to_overrun_the_kv_cache():
+    """A prefill of 1 + 729 + 64 tokens leaves 1024 - 794 = 230 decode steps in a 1024-entry cache: generate() of
+    231 tokens fits, of 232 raises ValueError before any device work (the check needs no GPU)."""
+    import strix_halo_maxx_amd.md2text as mt
+    dec = mt.TextDecoder.__new__(mt.TextDecoder)
+    dec.ctx = 1024
+    img, prompt = torch.zeros(729, 2048), torch.zeros(64, dtype=torch.long)
+    dec._check_room(1 + 729 + 64, 231)
+    with pytest.raises(ValueError):
+        dec.generate(img, prompt, 232)
+    with pytest.raises(ValueError):
+        dec._check_room(1024, 2)
+    dec.pos_base, dec.steps = 1000, 24
+    with pytest.raises(ValueError):
+        dec._count_step()

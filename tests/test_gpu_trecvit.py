@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+import test_oracle as TO
 import oracle.trecvit as otr
 import strix_halo_maxx_amd.ops as ops
 import strix_halo_maxx_amd.synth as S
@@ -74,6 +75,42 @@ def test_ssm_step_vs_oracle(dev, first):
     assert ulp_ok(z, z_ref)
 
 
+@pytest.mark.parametrize("case", ["gateless", "generic"])
+def test_ssm_step_vs_fp64_closed_form(dev, case):
+    """The HIP step's later-frame update against the fp64 closed form h = a h0 + sqrt(1 - a^2) xc sigma(gx),
+    a = (1 + e^p)^(-8 sigma(ga)) (pack8.py:266-276, cpuemu.py:37-45), within the bound that the reference's bf16
+    rounding chain allows (the same bound that pins the oracle), element by element."""
+    d = (TO._rglru_gateless_case if case == "gateless" else TO._rglru_generic_case)(31)
+    _, h = gpu_ssm_step(d, dev, first=False)
+    ref, bound = TO.rglru_fp64(d)
+    err = (h.double() - ref).abs()
+    print(f"closed form {case}: max err {err.max().item():.2e}, max err / bound {(err / bound).max().item():.2f}",
+          flush=True)
+    assert bool((err <= bound).all())
+    wrong, _ = TO.rglru_fp64(d, "sqrt1ma")
+    assert ((h.double() - wrong).abs() > bound).double().mean().item() > 0.3
+
+
+def test_rmsnorm_random_scale_vs_oracle(dev):
+    """mx_rmsnorm with a random scale (sc1 = bf16(scale + 1)) against the oracle's rmsnorm (pack8.py:222-229): at
+    most one bf16 ulp anywhere (the fp32 sum of the rounded squares runs in another order), and a kernel that
+    ignored the scale would be far off."""
+    g = torch.Generator().manual_seed(12)
+    for rows, D in ((1280, 768), (37, 768), (5, 1536)):
+        x = (torch.randn(rows, D, generator=g) * 2).to(BF)
+        scale = (torch.randn(D, generator=g) * 0.3).to(BF)
+        ref = otr.rmsnorm(x, scale)
+        sc1 = (scale.float() + 1).to(BF)
+        y = ops.rmsnorm(x.to(dev), sc1.to(dev)).cpu()
+        d = (y.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+        print(f"rmsnorm {rows}x{D}: max ulp diff {d.max().item()}, differing {(d > 0).float().mean().item():.2e}",
+              flush=True)
+        assert d.max().item() <= 1
+        assert (d > 0).float().mean().item() <= 1e-2
+        unscaled = otr.rmsnorm(x, torch.zeros_like(scale))
+        assert rel(y, unscaled) > 0.1
+
+
 def test_ssm_invariants_on_gpu(dev):
     """a_param -> -inf makes softplus -> 0, so a -> 1 and mult -> 0: the state is carried unchanged."""
     d = ssm_inputs(8)
@@ -130,6 +167,27 @@ def test_rglru_scan_matches_streamed_steps(dev, T):
     _lib.call("mx_rglru_scan", _lib.stream(), A.data_ptr(), B.data_ptr(), h2.data_ptr(), F_, T, C,
               st[3:].data_ptr(), 2 * C, T * 2 * C, z2.data_ptr(), C, T * C)
     torch.cuda.synchronize()
+    # the oracle's streamed recurrence (cpuemu.py:33-47, pack8.py:253-279) over the same frames
+    h_o = torch.zeros(T, C)
+    hist = [torch.zeros(T, C, dtype=BF)] * 3
+    z_o = []
+    for t in range(F_):
+        zt, h_o = otr.ssm(ygs[t], frames[t], hist, h_o, d["conv_w"], d["conv_b"], d["a_param"], d["wx"], d["bx"],
+                          d["wa"], d["ba"], t == 0)
+        hist = [frames[t], hist[0], hist[1]]
+        z_o.append(zt)
+    e_h = (h2.cpu() - h_o).abs().max().item()
+    print(f"scan T={T}: final state vs oracle {e_h:.2e}", flush=True)
+    assert e_h <= 1e-3
+    # z = bf16(bf16(h) yg): within two bf16 roundings plus |yg| times the state tolerance (a gate pre-activation that
+    # rounds to the neighbouring bf16 value, fp32 MFMA sums against the oracle's fp64 ones, moves h by up to that
+    # much), and one bf16 rounding apart on all but 0.2 % of the elements
+    for t in range(F_):
+        zt, zr = z2[t].float().cpu(), z_o[t].float()
+        ulp = torch.ldexp(torch.ones_like(zr), torch.frexp(zr)[1] - 8)
+        d = (zt - zr).abs()
+        assert rel(zt, zr) <= 1e-3 and bool((d <= 2 * ulp + ygs[t].float().abs() * 1e-3 + 1e-6).all()), t
+        assert (d > ulp).float().mean().item() <= 2e-3, t
     if T == 1280:
         assert torch.equal(h2, h)
         for t in range(F_):
@@ -282,6 +340,39 @@ def test_twelve_blocks_streamed_graph_and_clip(dev):
         assert rel(clip[t], refs[t]) <= 2e-2
     for i in range(12):
         assert (m.h[i] - h_stream[i]).abs().max().item() <= 5e-2
+
+
+def test_twelve_blocks_state_per_block_vs_oracle(dev):
+    """Config 3 shape (12 blocks, 1280 tokens) streamed for 16 frames, each GPU block fed the oracle's block input
+    and the oracle's previous state (conv history and RG-LRU h): every block's new fp32 state within 1e-3 of the
+    oracle's (max abs), every block's output within rel-L2 1e-2, at every frame."""
+    w = S.trecvit_weights(0)
+    NF = 16
+    frames = S.frames_u8(11, NF)
+    qf = _qfeat()
+    ora = otr.Model(w)
+    m = tv.TRecViT(w, device=dev)
+    m.reset()
+    D = m.D
+    worst_h, worst_x = 0.0, 0.0
+    for t in range(NF):
+        phase = t % 4
+        x = ora.embed(frames[t], qf)
+        for i in range(len(m.blocks)):
+            if t > 0:  # the oracle's state before this frame: h and x_{t-1}, x_{t-2}, x_{t-3}
+                m.h[i].copy_(ora.h[i])
+                for k in (1, 2, 3):
+                    m.ring[i][(phase - k) % 4][:, D:].copy_(ora.hist[i][k - 1])
+            m.frame.fill_(t)
+            y = m.block_step(i, x.to(dev), phase)
+            x = ora.block(i, x)
+            eh = (m.h[i].cpu() - ora.h[i]).abs().max().item()
+            ex = rel(y, x)
+            worst_h, worst_x = max(worst_h, eh), max(worst_x, ex)
+            assert eh <= 1e-3, (t, i, eh)
+            assert ex <= 1e-2, (t, i, ex)
+        ora.t += 1
+        print(f"frame {t}: worst state err {worst_h:.2e}, worst block rel {worst_x:.2e}", flush=True)
 
 
 CROPS = [(4, 4, 16), (6, 3, 16), (6, 3, 20), (0, 0, 32), (10, 12, 16), (11, 12, 16)]

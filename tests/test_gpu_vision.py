@@ -121,6 +121,46 @@ def test_tower_batch13(dev, full):
         assert rel(out[i], ref[0]) <= 2e-2, i
 
 
+def test_tower_batch256_config4(dev, full):
+    """Config 4, the throughput-bound tower at batch 256 (186,624 token rows; the large-M GEMM tiles, not the
+    split-K batch-1 path): the first, a middle and the last crop each match their own batch-1 oracle output."""
+    w, _, _, _ = full
+    imgs = S.images_u8(8, 256)
+    vt = md2.VisionTower(w)
+    out = vt(imgs.to(dev))
+    assert out.shape == (256, 729, 1152)
+    for i in (0, 131, 255):
+        ref = ov.tower(w, imgs[i:i + 1])
+        r = rel(out[i], ref[0])
+        print(f"batch 256, crop {i}: rel-L2 vs oracle {r:.2e}", flush=True)
+        assert r <= 2e-2, i
+    del out
+    torch.cuda.empty_cache()
+
+
+def test_projection_mlp_vs_oracle(dev):
+    """The post-LN features through cat([x, x]) -> fc1 2304 -> 8192 + GELU-tanh -> fc2 8192 -> 2048
+    (md2fast.py:158-160; mlp md2fast.py:55-61): VisionTower.project on the oracle's post-LN features against the
+    oracle's projection of the same features (rel-L2 <= 1e-2), and the whole tower with project=True against
+    the oracle's tower(project=True) (the end-to-end bound, rel-L2 <= 2e-2)."""
+    w = S.vision_weights(0, proj=True)
+    img = S.images_u8(1, 1)
+    feats = ov.tower(w, img)
+    ref = ov.tower(w, img, project=True)
+    assert ref.shape == (1, 729, 2048)
+    vt = md2.VisionTower(w)
+    p = vt.project(feats[0].to(dev))
+    ref_p = ov.lin(ov.gelu(ov.lin(torch.cat([feats, feats], -1), w["proj_mlp.fc1.weight"], w["proj_mlp.fc1.bias"])),
+                   w["proj_mlp.fc2.weight"], w["proj_mlp.fc2.bias"])
+    assert torch.equal(ref_p, ref)
+    r1 = rel(p, ref[0])
+    out = vt(img.to(dev), project=True)
+    r2 = rel(out, ref)
+    print(f"projection on oracle features rel {r1:.2e}; tower + projection rel {r2:.2e}", flush=True)
+    assert out.shape == (1, 729, 2048)
+    assert r1 <= 1e-2 and r2 <= 2e-2
+
+
 def test_graph_replay_bit_exact(dev, full):
     """HIP-graph replay of the ctypes-launched kernels equals eager bit for bit (test_hgemm.py:51-67), over
     several replays with eager work in between."""

@@ -347,6 +347,110 @@ def test_rglru_fixed_point():
     assert (h.double() - B / (1 - A)).abs().max() < 1e-4
 
 
+U = 2.0 ** -8  # unit roundoff of bf16 (8 significand bits, round to nearest even)
+
+
+def rglru_fp64(d, variant=None):
+    """One non-first RG-LRU frame (pack8.py:253-279, cpuemu.py:37-45) from its mathematical definition in fp64, and a
+    first-order bound on the oracle's deviation from it caused by its bf16 roundings. Returns (h, bound).
+
+        xc   = sum_i x_{t-3+i} w_i + b                   (conv_1d, tap 0 = oldest)
+        gx   = xc_h Wx_h + bx,   ga = xc_h Wa_h + ba      (block-diagonal gates, W[h][in][out])
+        a    = (1 + e^p)^(-8 sigma(ga))                  (= exp(-8 sigma(ga) softplus(p)))
+        h    = a h0 + sqrt(1 - a^2) xc sigma(gx)
+
+    `variant` computes a plausible wrong restatement instead (for the negative checks): "sqrt1ma" uses sqrt(1 - a),
+    "xc" drops the input gate (xc instead of xc sigma(gx)), "coef4" uses -4 instead of -8, "decay_h0" uses (1 - a) h0,
+    "wT" multiplies by the transposed per-head gate matrices.
+    The bound follows each rounding site of the oracle's chain (every bf16 rounding contributes u |value| and is
+    carried to h through the derivatives), times 1.25 for the second-order terms."""
+    T, C = d["xx"].shape
+    H = d["wx"].shape[0]
+    dd = lambda t: t.double()
+    taps = [dd(d["hist"][2]), dd(d["hist"][1]), dd(d["hist"][0]), dd(d["xx"])]
+    w = dd(d["conv_w"])
+    prods = [t * w[i][None] for i, t in enumerate(taps)]
+    xc = sum(prods) + dd(d["conv_b"])[None]
+    e_xc = U * (2 * sum(p.abs() for p in prods) + dd(d["conv_b"]).abs()[None] + xc.abs())
+
+    def gate(W, b):
+        W = W.transpose(-1, -2) if variant == "wT" else W
+        pre = torch.einsum("thi,hij->thj", xc.view(T, H, 64), dd(W)).reshape(T, C)
+        e = torch.einsum("thi,hij->thj", e_xc.view(T, H, 64), dd(W).abs()).reshape(T, C)
+        g = pre + dd(b).reshape(-1)[None]
+        s = torch.sigmoid(g)
+        e_g = e + U * pre.abs() + U * g.abs()
+        return s, s * (1 - s) * e_g + U * s
+    sx, e_sx = gate(d["wx"], d["bx"])
+    sa, e_sa = gate(d["wa"], d["ba"])
+    p = dd(d["a_param"])[None]
+    sp = torch.log1p(torch.exp(p))
+    coef = 4.0 if variant == "coef4" else 8.0
+    a = (1 + torch.exp(p)) ** (-coef * sa)
+    L = -8.0 * sa * sp
+    e_L = 8.0 * (e_sa * sp + sa * U * sp) + U * L.abs()
+    e_a = a * e_L + U * a
+    g = xc * sx
+    e_g = e_xc * sx + xc.abs() * e_sx + U * g.abs()
+    om = 1 - a * a
+    e_om = a * a * (2 * e_L + U) + U * om
+    mult = torch.sqrt(om)
+    e_mult = e_om / (2 * mult.clamp_min(1e-300)) + U * mult
+    nx = g * mult
+    e_nx = e_g * mult + g.abs() * e_mult + U * nx.abs()
+    h0 = dd(d["h0"])
+    if variant == "sqrt1ma":
+        nx = g * torch.sqrt(1 - a)
+    elif variant == "xc":
+        nx = xc * mult
+    h = (1 - a) * h0 + nx if variant == "decay_h0" else a * h0 + nx
+    bound = 1.25 * (e_a * h0.abs() + e_nx) + 1e-6 * h.abs() + 1e-30
+    return h, bound
+
+
+def _rglru_generic_case(seed):
+    """Non-first frame with every tap and both gate matrices in play; a_param U(-3, 0.5) and gate biases so that
+    a spans (0, 1) away from both ends, sigma(gx) spans (0.1, 0.9)."""
+    d = _ssm_case(T=64, C=128, H=2, seed=seed)
+    g = gen(seed + 100)
+    d["ba"] = (torch.rand(2, 64, generator=g) * 3 - 2).to(BF)
+    d["bx"] = (torch.rand(2, 64, generator=g) * 4 - 2).to(BF)
+    d["h0"] = torch.randn(64, 128, generator=g) * 0.5
+    return d
+
+
+def _rglru_gateless_case(seed):
+    """The closed form with the gate matrices zero (sigma(gx) = sigma(bx), sigma(ga) = sigma(ba), known exactly) and
+    only the current conv tap: h = a h0 + sqrt(1 - a^2) (x w_3 + b) sigma(bx), a = (1 + e^p)^(-8 sigma(ba))."""
+    d = _rglru_generic_case(seed)
+    d["wx"] = torch.zeros_like(d["wx"])
+    d["wa"] = torch.zeros_like(d["wa"])
+    d["conv_w"] = d["conv_w"].clone()
+    d["conv_w"][:3] = 0
+    return d
+
+
+@pytest.mark.parametrize("case", ["gateless", "generic"])
+def test_rglru_update_vs_fp64_closed_form(case):
+    """The oracle's later-frame RG-LRU update against the fp64 closed form h = a h0 + sqrt(1 - a^2) xc sigma(gx),
+    a = (1 + e^p)^(-8 sigma(ga)), within the bound its own bf16 roundings allow, element by element; and each
+    plausible wrong restatement (sqrt(1 - a), the ungated xc, a -4 coefficient, (1 - a) h0) lies outside that bound
+    on a large share of the elements, so the check tells them apart."""
+    d = (_rglru_gateless_case if case == "gateless" else _rglru_generic_case)(31)
+    _, h = _run_ssm(d, False)
+    ref, bound = rglru_fp64(d)
+    err = (h.double() - ref).abs()
+    assert bool((err <= bound).all()), (err - bound).max().item()
+    # the bound is tight, not vacuous: a few bf16 ulps (the generic case carries the conv's rounding through the
+    # 64-term gate products as well)
+    assert bound.median().item() < (0.05 if case == "gateless" else 0.12) * ref.abs().median().item()
+    for variant in ("sqrt1ma", "xc", "coef4", "decay_h0") + (("wT",) if case == "generic" else ()):
+        wrong, _ = rglru_fp64(d, variant)
+        frac = ((h.double() - wrong).abs() > bound).double().mean().item()
+        print(case, variant, f"{frac:.2f} of the elements outside the bound")
+        assert frac > 0.3, (variant, frac)
+
+
 def scan_fp64(A, B, h0):
     """The time scan the GPU kernel runs: inclusive prefix over frames of (a, b) o (a', b') = (a' a, a' b + b')."""
     a, b = A.clone(), B.clone()
