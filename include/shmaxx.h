@@ -61,6 +61,18 @@ int mx_gemm_reduce(hipStream_t st, const float* P, int nsplit, long p_split, lon
                    const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int act,
                    int act_ncols);
 
+/* mx_gemm_bf16 without a caller workspace: in-kernel split-K (splits > 1, or a split pick when cfg < 0) uses a fixed
+ * device array of the library (mx_gemm_noalloc_max_ws() fp32 partial elements, 16 MiB, plus 65,536 tile counters)
+ * instead of ws / cnt; a call needing more returns -3 before launching. It allocates nothing (no hipMalloc, no torch
+ * allocation) and clears the counters it uses with a kernel, so it can be captured into a HIP graph. Each GPU holds
+ * its own copy of the array for the life of the process, and every such call on a GPU shares it: calls that overlap
+ * on one GPU (different streams) race. No counterpart in the reference: it is for callers that cannot allocate
+ * (code under graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int mx_gemm_bf16_noalloc(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                         const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M,
+                         int N, int K, int Kw, int act, int act_ncols);
+long mx_gemm_noalloc_max_ws(void);
+
 /* ============================================================================================ W8A8 (int8 MFMA)
  * Per-token int8 quantisation of bf16 activations: s[m] = max(max_k |x[m,k]|, 1e-5) / 127 and
  * q[m,k] = trunc(x / s + 0.5 sign) (round half away from zero), fp32 math with IEEE division. K % 8 == 0; strides in

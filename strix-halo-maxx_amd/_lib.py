@@ -59,12 +59,15 @@ SIGNATURES = {
     "mx_ssm_prep": [P, P, L, L, P, P, P, P, P, P, P, P, P, P, I, I, I],
     "mx_rglru_scan": [P, P, P, P, I, I, I, P, L, L, P, L, L],
     "mx_counter_add": [P, P, I],
+    "mx_gemm_bf16_noalloc": [P, I, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I, I, I],
+    "mx_gemm_noalloc_max_ws": [],
 }
 
 STATUS = {0: "ok", -1: "bad config", -2: "unsupported shape/stride", -3: "split-K workspace too small",
           -4: "operand layout/alignment", -5: "HIP launch failed", -6: "null pointer"}
 
-RESTYPE = {"mx_gemm_ws_elems": L, "mx_gemm_ws_counters": L, "mx_track_head_blob_elems": L}
+RESTYPE = {"mx_gemm_ws_elems": L, "mx_gemm_ws_counters": L, "mx_track_head_blob_elems": L,
+           "mx_gemm_noalloc_max_ws": L}
 
 _lib = None
 

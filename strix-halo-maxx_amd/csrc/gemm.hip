@@ -29,6 +29,8 @@
 //
 // Operand contract: A has K valid columns; the k loop runs to Kw (a multiple of 64, >= K) and W must hold zeros in
 // columns [K, Kw). A chunks beyond K are fetched from column 0 of the same row (finite data times W's zeros).
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -998,6 +1000,74 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
 #undef W_
 #undef H_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// ---------------------------------------------------------------------------------------------- allocation-free form
+// mx_gemm_bf16 for callers that cannot allocate (code under HIP-graph capture, tight serving loops, harnesses that
+// forbid hipMalloc): the split-K workspace is a fixed file-scope device array instead of a caller buffer. Each GPU
+// holds its own copy for the life of the process; its address is looked up once per device with the device current
+// (host code never passes the array's name itself to a kernel). Calls on one GPU share it: two such calls that
+// overlap on that GPU (on different streams) race.
+constexpr long kScratchWs = 4L << 20;   // fp32 partial-tile elements (16 MiB)
+constexpr long kScratchCnt = 1L << 16;  // per-tile arrival counters
+static __device__ __align__(256) float scratch[kScratchWs + kScratchCnt];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+float* scratch_ptr() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+__global__ void zero_ints_kernel(int* __restrict__ p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0;
+}
+}  // namespace
+
+extern "C" long mx_gemm_noalloc_max_ws(void) { return kScratchWs; }
+
+extern "C" int mx_gemm_bf16_noalloc(hipStream_t st, int cfg, int splits, const uint16_t* A, long lda, const uint16_t* W,
+                                    long ldw, const float* bias, const uint16_t* R, long ldr, int r_rows, uint16_t* C,
+                                    long ldc, int M, int N, int K, int Kw, int act, int act_ncols) {
+  if (cfg < 0) {
+    const int p = mx_gemm_pick(M, N, Kw);
+    cfg = p / 16;
+    splits = p % 16;
+    if (splits > 1 && (mx_gemm_ws_elems(cfg, splits, M, N) > kScratchWs ||
+                       mx_gemm_ws_counters(cfg, splits, M, N) > kScratchCnt))
+      splits = 1;
+  }
+  if (splits < 1) splits = 1;
+  float* ws = nullptr;
+  int* cnt = nullptr;
+  long ncnt = 0;
+  if (splits > 1) {
+    if (cfg >= kNCfg) return MX_EBADCFG;
+    const long need = mx_gemm_ws_elems(cfg, splits, M, N);
+    ncnt = mx_gemm_ws_counters(cfg, splits, M, N);
+    if (need > kScratchWs || ncnt > kScratchCnt) return MX_ESPLIT;  // beyond the fixed workspace
+    ws = scratch_ptr();
+    if (!ws) return MX_ELAUNCH;
+    cnt = reinterpret_cast<int*>(ws + kScratchWs);
+    const int rc = mx_gemm_check(cfg, splits, A, lda, W, ldw, bias, R, ldr, C, ldc, M, N, K, Kw, act, ws, kScratchWs,
+                                 cnt, kScratchCnt);
+    if (rc) return rc;
+    // the counters must start at zero: a kernel clears them (no memset node, so the call stays graph-capturable)
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)((ncnt + 255) / 256)), dim3(256), 0, st, cnt, ncnt);
+    if (hipGetLastError() != hipSuccess) return MX_ELAUNCH;
+  }
+  return mx_gemm_bf16(st, cfg, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws,
+                      splits > 1 ? kScratchWs : 0, cnt, splits > 1 ? kScratchCnt : 0);
 }
 
 // C = epi(sum over s < nsplit of P[s] + bias): the epilogue of mx_gemm_bf16 (act 0 / 1 / 2 on columns < act_ncols when
