@@ -481,6 +481,37 @@ def decode_bench(steps_tokens=128, w8a8=False):
                         + (", W8A8 text Linears (int8 weights / activations, bf16 LM head)" if w8a8 else "")}
 
 
+def frame_bench(reps=20):
+    """The whole moondream2 yes/no frame (FastMD2, md2fast.py:147-160, 201-212): vision tower at batch 1 +
+    projection MLP + 730-token prefix prefill (one HIP graph), then one 32-id question over it with the yes / no rows
+    of the LM head (a second graph). ms per frame = both replays; the reference publishes 88.7 ms for the same frame
+    on its own GPU (moondream/gpu/README.md:11-13)."""
+    import torch
+    import strix_halo_maxx_amd.md2frame as mf
+    import strix_halo_maxx_amd.synth as S
+    dev = torch.device("cuda:0")
+    f = mf.FastMD2(S.vision_weights(0, proj=True), S.text_weights(0), device=dev, nq=1, L=32,
+                   yes_ids=(11, 222, 3333, 44444), no_ids=(55, 666, 7777, 50000))
+    img = S.images_u8(1, 1)[0].to(dev)
+    f.set_questions([S.prompt_ids(4, 32).tolist()])
+    f.img.copy_(img)
+    f.capture()
+    for _ in range(3):
+        f.frame(img)
+    torch.cuda.synchronize()
+    t = {}
+    for name, fn in (("encode", lambda: f.encode(img)), ("query", f.query), ("frame", lambda: f.frame(img))):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        t[name] = (time.perf_counter() - t0) / reps * 1e3
+    return {"frame_ms": round(t["frame"], 3), "encode_ms": round(t["encode"], 3), "query_ms": round(t["query"], 3),
+            "workload": "moondream2 yes/no frame: vision tower (27 blocks, batch 1) + projection MLP + 730-token "
+                        "prefix prefill (24 text layers), then one 32-id question + yes/no head; two HIP graphs"}
+
+
 def trecvit_bench(frames=64, clip=16):
     """Config 3: TRecViT, 12 blocks, 1024 patch + 256 query tokens, streamed for `frames` frames (one HIP graph per
     frame), plus the clip-parallel form (`clip` frames per pass through every block)."""
@@ -720,6 +751,10 @@ def main():
         print("[bench] decoder w8a8", file=sys.stderr, flush=True)
         with torch.inference_mode():
             out["extra"]["decoder_w8a8"] = decode_bench(w8a8=True)
+        torch.cuda.empty_cache()
+        print("[bench] moondream2 yes/no frame", file=sys.stderr, flush=True)
+        with torch.inference_mode():
+            out["extra"]["md2_frame"] = frame_bench()
         torch.cuda.empty_cache()
         print("[bench] trecvit", file=sys.stderr, flush=True)
         with torch.inference_mode():
