@@ -91,7 +91,7 @@ def op_classes(vt, img):
     def psym(l):
         cfg, sp = ops._TUNED_P[(M, l.N, l.Kw)]
         return f"{gemm_symbol(cfg)} x{sp} splits"
-    attn_sym = "attn_fwd_kernel<{}, {}>".format(hd, "4, 1, 64, 3" if ((T + 127) // 128) * H * B >= 512 else "1, 4, 128, 2")
+    attn_sym = ops.sdpa_symbol(B, H, T, hd)
     F, Kw2 = blocks[0]["fc1"].N, blocks[0]["fc2"].Kw
     sp_proj, sp_fc2 = saved[0][4].shape[0], saved[0][8].shape[0]
     # algorithmic HBM bytes per launch: every operand once (bf16 activations / weights, fp32 split-K partials)

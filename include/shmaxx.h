@@ -119,6 +119,10 @@ int mx_sdpa(hipStream_t st, const uint16_t* Q, long sq_b, long sq_h, long sq_t, 
             long so_t, int B, int H, int Tq, int Tk, int D, float scale, int qpos0, int causal_from);
 int mx_sdpa_check(const void* Q, long sq_t, const void* K, long sk_t, const void* V, long sv_t, const void* O,
                   long so_t, int B, int H, int Tq, int Tk, int D);
+/* The tiling mx_sdpa picks for (B, H, Tq, D): t[0..3] = query waves, key waves, keys per staged block, ring stages
+ * (the kernel is attn_fwd_kernel<D, t0, t1, t2, t3>). The reference picks its tile from a fixed table by head dim
+ * (moondream/gpu/hattn.py:21); this one also looks at the grid size. */
+void mx_sdpa_tiling(int B, int H, int Tq, int D, int* t);
 
 /* ============================================================================================ norms
  * LayerNorm over rows of D (fp32 statistics, one rounding). Replaces F.layer_norm in _ln (md2fast.py:43-44) and the

@@ -38,6 +38,7 @@ SIGNATURES = {
     "mx_quant_weight_i8": [P, P, L, P, L, P, I, I],
     "mx_sdpa": [P, P, L, L, L, P, L, L, L, P, L, L, L, P, L, L, L, I, I, I, I, I, F, I, I],
     "mx_sdpa_check": [P, L, P, L, P, L, P, L, I, I, I, I, I],
+    "mx_sdpa_tiling": [I, I, I, I, P],
     "mx_layernorm": [P, P, L, P, P, P, L, I, I, F],
     "mx_residual_layernorm": [P, P, I, L, L, P, P, L, P, L, P, P, P, L, I, I, F],
     "mx_rmsnorm": [P, P, L, P, P, L, I, I, F],
@@ -67,7 +68,7 @@ STATUS = {0: "ok", -1: "bad config", -2: "unsupported shape/stride", -3: "split-
           -4: "operand layout/alignment", -5: "HIP launch failed", -6: "null pointer"}
 
 RESTYPE = {"mx_gemm_ws_elems": L, "mx_gemm_ws_counters": L, "mx_track_head_blob_elems": L,
-           "mx_gemm_noalloc_max_ws": L}
+           "mx_gemm_noalloc_max_ws": L, "mx_sdpa_tiling": None}
 
 _lib = None
 

@@ -18,7 +18,7 @@
 //    the 64 banks; D = 72 rows (144 bytes) need no swizzle.
 //  * Workgroup = NQW query waves x NKW key waves. Each KB-key block is split into NKW sub-blocks of KB / NKW keys;
 //    key wave w consumes sub-block w of every block, and the partial (max, sum, O) of each query are merged at the
-//    end in fp32. Batch-1 shapes (16 heads x 729 queries = 368 query waves) use NKW = 4 so that ~1500 waves run.
+//    end in fp32. Workgroups of 4, 8 or 16 waves; small grids (batch-1 shapes: 16 heads x 729 queries) use NKW = 4.
 //  * Head dim 72 pads to 80 along the QK contraction (5 k-steps; Q's padding is zero, so the neighbouring LDS bytes
 //    that K's padding reads are multiplied by 0) and to 96 output rows for PV (3 row tiles; rows >= 72 are dropped).
 // Numerics: fp32 scores and accumulators; P is rounded to bf16 before the PV product and the softmax denominator is
@@ -35,22 +35,28 @@ struct AttnCfg {
   static constexpr bool SWZ = (D == 64);
   static constexpr int KBW = KB / NKW;              // keys per key wave per block
   static constexpr int NST = KBW / 32;              // S^T tiles per key wave per block
+  static constexpr int NW = NQW * NKW;              // waves per workgroup
   static constexpr int NCH = 2 * KB * CPR;          // K + V chunks per block
   static constexpr int NI = (NCH + 63) / 64;        // DMA instructions per block
-  static constexpr int NIW = (NI + 3) / 4;          // ... per wave (instructions >= NI are padding)
-  // one ring stage: K block, V block, then the padding instructions' landing area, which also absorbs the last
-  // rows' over-reads (PV rows 72..95 of D = 72, QK chunk 9 of D = 72)
-  static constexpr int STAGE_B = NIW * 4 * 1024 + 1024;
+  static constexpr int NIW = (NI + NW - 1) / NW;    // ... per wave (instructions >= NI are padding)
+  // one ring stage: K block, V block (NI KB together), then a 1 KB landing slot that every padding instruction
+  // writes (the same bytes: the block's first chunk), which also absorbs the last rows' over-reads (PV rows 72..95
+  // of D = 72; the QK over-read of K's last row, chunk 9 of D = 72, lands in the V block)
+  static constexpr int STAGE_B = NI * 1024 + 1024;
   static constexpr int RING_B = S * STAGE_B;
-  static constexpr int COMB_B = NKW > 1 ? NKW * NQW * (2 * 64 + (DV / 32) * 16 * 64) * 4 : 0;
+  // O registers per lane that hold output rows < D (register u: tile u / 16, row 32 (u / 16) + 8 ((u % 16) / 4) +
+  // 4 (lane >> 5) + u % 4): all 32 for D = 64, tiles 0-1 and the first 4 registers of tile 2 for D = 72
+  static constexpr int NU = D == 72 ? 36 : 32;
+  static constexpr int COMB_B = NKW > 1 ? NW * (2 + NU) * 64 * 4 : 0;
   static constexpr int BYTES = RING_B > COMB_B ? RING_B : COMB_B;
   static_assert(KBW % 32 == 0 && NST >= 1, "key sub-block of whole 32-key tiles");
-  static_assert(NQW * NKW == 4, "4 waves");
+  static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
+  static_assert(BYTES <= 160 * 1024, "LDS");
   static_assert(D == 64 || D == 72, "head dim");
 };
 
 template <int D, int NQW, int NKW, int KB, int S>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(
+__global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
     const uint16_t* __restrict__ Q, long sq_b, long sq_h, long sq_t,
     const uint16_t* __restrict__ K, long sk_b, long sk_h, long sk_t,
     const uint16_t* __restrict__ V, long sv_b, long sv_h, long sv_t,
@@ -100,15 +106,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
   }
   const int nkb = (kend + KB - 1) / KB;
 
-  // ---- this lane's DMA chunks: instruction q = wave + 4 i of a block covers chunks 64 q .. 64 q + 63, which are all
+  // ---- this lane's DMA chunks: instruction q = wave + NW i of a block covers chunks 64 q .. 64 q + 63, which are all
   // K chunks (q < KB * CPR / 64) or all V chunks; instructions q >= NI are padding and refetch the block's first chunk
+  // into the stage's landing slot
   static_assert((KB * CPR) % 64 == 0, "an instruction never straddles the K and V parts");
   constexpr int NIK = KB * CPR / 64;  // K instructions per block
   uint32_t doff[NIW];                 // byte offset of this lane's chunk from the block's first row
   int dkey[NIW];                      // its key within the block
 #pragma unroll
   for (int i = 0; i < NIW; i++) {
-    const int q = wave + 4 * i;
+    const int q = wave + C::NW * i;
     const int ch = q < C::NI ? (q * 64 + lane) % (KB * CPR) : 0;
     const int key = ch / CPR, slot = ch % CPR;
     const int c = C::SWZ ? (slot ^ ((key >> 1) & 7)) : slot;
@@ -125,18 +132,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     if (lim >= KB - 1) {
 #pragma unroll
       for (int i = 0; i < NIW; i++) {
-        const int q = wave + 4 * i;
-        dma16s((q >= NIK && q < C::NI) ? vbase : kbase, doff[i], base + q * 1024);
+        const int q = wave + C::NW * i;
+        dma16s((q >= NIK && q < C::NI) ? vbase : kbase, doff[i], base + min(q, C::NI) * 1024);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < NIW; i++) {
-        const int q = wave + 4 * i;
+        const int q = wave + C::NW * i;
         const bool isv = q >= NIK && q < C::NI;
         const long st_el = isv ? sv_t : sk_t;
         const int key = dkey[i];
         const uint32_t off = doff[i] - (uint32_t)((key > lim ? key - lim : 0) * st_el * 2);
-        dma16s(isv ? vbase : kbase, off, base + q * 1024);
+        dma16s(isv ? vbase : kbase, off, base + min(q, C::NI) * 1024);
       }
     }
   };
@@ -261,23 +268,20 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
   }
 
   if constexpr (NKW > 1) {
-    // ---- merge the key waves' partial results (fp32) through LDS: every key wave finishes 1 / NKW of the output
-    // rows (d) of its query tile, summing the partials in key-wave order
-    constexpr int OW = (DV / 32) * 16 * 64;  // floats of O per wave
-    constexpr int NE = (DV / 32) * 16;       // O registers per lane
-    static_assert(NE % NKW == 0, "registers split evenly over the key waves");
+    // ---- merge the key waves' partial results (fp32) through LDS. Only the NU registers holding output rows < D
+    // are staged; every key wave finishes the groups of 4 registers (4 consecutive output rows) g with
+    // g % NKW == kw, summing the partials in key-wave order
+    constexpr int NU = C::NU, NW = C::NW;
     float* cm = reinterpret_cast<float*>(smem);
-    float* cl = cm + NKW * NQW * 64;
-    float* co = cl + NKW * NQW * 64;
+    float* cl = cm + NW * 64;
+    float* co = cl + NW * 64;  // [slot][u][lane]
     wait_vm<0>();
     __syncthreads();
     const int slot = kw * NQW + qg;
     cm[slot * 64 + lane] = m_run;
     cl[slot * 64 + lane] = l_run;
 #pragma unroll
-    for (int dt = 0; dt < DV / 32; dt++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) co[slot * OW + (dt * 16 + e) * 64 + lane] = oacc[dt][e];
+    for (int u = 0; u < NU; u++) co[(slot * NU + u) * 64 + lane] = oacc[u / 16][u % 16];
     __syncthreads();
     float M = -1e30f;
 #pragma unroll
@@ -291,25 +295,23 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     if (qi >= Tq) return;
     const float inv = 1.f / L;
     uint16_t* orow = O + b * so_b + (long)qi * so_t + h * so_h;
-    // this wave's share: registers r = 4 g' of 4 consecutive output rows, g' = kw, kw + NKW, ...
 #pragma unroll
-    for (int g2 = kw; g2 < NE / 4; g2 += NKW) {
+    for (int g2 = 0; g2 < NU / 4; g2++) {
+      if (g2 % NKW != kw) continue;  // wave-uniform
       float o4[4];
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         float acc = 0.f;
 #pragma unroll
-        for (int k = 0; k < NKW; k++) acc += co[(k * NQW + qg) * OW + (4 * g2 + u) * 64 + lane] * f[k];
+        for (int k = 0; k < NKW; k++) acc += co[((k * NQW + qg) * NU + 4 * g2 + u) * 64 + lane] * f[k];
         o4[u] = acc * inv;
       }
       const int dt = g2 / 4, g = g2 % 4;
-      const int d = dt * 32 + 8 * g + 4 * hk;
-      if (d < D) {
-        u32x2 o;
-        o.x = pack2(o4[0], o4[1]);
-        o.y = pack2(o4[2], o4[3]);
-        *reinterpret_cast<u32x2*>(orow + d) = o;
-      }
+      const int d = dt * 32 + 8 * g + 4 * hk;  // < D for every staged register
+      u32x2 o;
+      o.x = pack2(o4[0], o4[1]);
+      o.y = pack2(o4[2], o4[3]);
+      *reinterpret_cast<u32x2*>(orow + d) = o;
     }
     return;
   }
@@ -343,7 +345,7 @@ template <int D, int NQW, int NKW, int KB, int S>
 hipError_t launch(hipStream_t st, const Args& a) {
   const long nt = (long)((a.Tq + 32 * NQW - 1) / (32 * NQW)) * a.H * a.B;
   if (nt > 0x7fffffffL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, NQW, NKW, KB, S>), dim3((unsigned)nt), dim3(256), 0, st, a.Q, a.sq_b, a.sq_h,
+  hipLaunchKernelGGL((attn_fwd_kernel<D, NQW, NKW, KB, S>), dim3((unsigned)nt), dim3(64 * NQW * NKW), 0, st, a.Q, a.sq_b, a.sq_h,
                      a.sq_t, a.K, a.sk_b, a.sk_h, a.sk_t, a.V, a.sv_b, a.sv_h, a.sv_t, a.O, a.so_b, a.so_h, a.so_t,
                      a.Tq, a.Tk, a.H, a.H * a.B, a.sl2, a.qpos0, a.causal_from);
   return hipGetLastError();
@@ -362,6 +364,29 @@ extern "C" int mx_sdpa_check(const void* Q, long sq_t, const void* K, long sk_t,
   return MX_OK;
 }
 
+// The tiling mx_sdpa runs for a problem, from timings of every (query waves, key waves, block keys, stages) variant
+// on the shapes this library runs (HIP-graph replays, us per launch on MI355X):
+//  * many (batch, head, 128-query) tiles (wg4 >= 512): 4 query waves share each staged key block; with head dim 72
+//    two key waves split every 64-key block as well (vision batch 13: 64.4 -> 61.6, batch 256: 1261 -> 1188);
+//  * few tiles: key waves split each block so the grid still fills the GPU. 2 query waves x 4 key waves (8-wave
+//    workgroups) for the vision tower at batch 1 (11.1 -> 10.6 with a warm L2; 12.6 -> 12.4 on cold buffers), TRecViT
+//    (13.0 -> 12.7) and the yes/no query (10.3 -> 9.9); 4 x 4 (16 waves, 128 queries) for 32 heads of many queries
+//    (text prefix 15.2 -> 12.9); 1 x 4 for at most 64 queries (the 64-token prompt, 8.2: larger tiles leave most of
+//    their query waves empty).
+// t[0..3] = query waves, key waves, keys per staged block, ring stages.
+extern "C" void mx_sdpa_tiling(int B, int H, int Tq, int D, int* t) {
+  const long wg4 = (long)((Tq + 127) / 128) * H * B;
+  int q = 2, k = 4, kb = 128, s = 2;
+  if (wg4 >= 512) {
+    q = 4, k = D == 72 ? 2 : 1, kb = 64, s = D == 72 ? 4 : 3;
+  } else if (Tq <= 64) {
+    q = 1;
+  } else if (D == 64 && wg4 >= 160) {
+    q = 4;
+  }
+  t[0] = q, t[1] = k, t[2] = kb, t[3] = s;
+}
+
 // Strides are in elements; every batch/head stride must keep 16-byte alignment of the rows (multiples of 8).
 extern "C" int mx_sdpa(hipStream_t st, const uint16_t* Q, long sq_b, long sq_h, long sq_t, const uint16_t* K,
                        long sk_b, long sk_h, long sk_t, const uint16_t* V, long sv_b, long sv_h, long sv_t, uint16_t* O,
@@ -372,11 +397,19 @@ extern "C" int mx_sdpa(hipStream_t st, const uint16_t* Q, long sq_b, long sq_h, 
   if ((sq_b | sq_h | sk_b | sk_h | sv_b | sv_h) % 8 || so_h % 4 || so_b % 4) return MX_ESHAPE;
   const Args a{Q, K, V, O, sq_b, sq_h, sq_t, sk_b, sk_h, sk_t, sv_b, sv_h, sv_t, so_b, so_h, so_t,
                B, H, Tq, Tk, D, qpos0, causal_from, scale * 1.4426950408889634f};
-  // many (batch, head, 128-query) tiles: 4 query waves share each staged key block; few: split every 128-key block
-  // over 4 key waves per 32 queries so the grid still fills the GPU
-  const long wg4 = (long)((Tq + 127) / 128) * H * B;
-  hipError_t e;
-  if (D == 72) e = (wg4 >= 512) ? launch<72, 4, 1, 64, 3>(st, a) : launch<72, 1, 4, 128, 2>(st, a);
-  else e = (wg4 >= 512) ? launch<64, 4, 1, 64, 3>(st, a) : launch<64, 1, 4, 128, 2>(st, a);
+  int t[4];
+  mx_sdpa_tiling(B, H, Tq, D, t);
+  const auto is = [&](int q, int k, int kb, int s) { return t[0] == q && t[1] == k && t[2] == kb && t[3] == s; };
+  hipError_t e = hipErrorInvalidValue;
+  if (D == 72) {
+    if (is(4, 2, 64, 4)) e = launch<72, 4, 2, 64, 4>(st, a);
+    else if (is(1, 4, 128, 2)) e = launch<72, 1, 4, 128, 2>(st, a);
+    else if (is(2, 4, 128, 2)) e = launch<72, 2, 4, 128, 2>(st, a);
+  } else {
+    if (is(4, 1, 64, 3)) e = launch<64, 4, 1, 64, 3>(st, a);
+    else if (is(1, 4, 128, 2)) e = launch<64, 1, 4, 128, 2>(st, a);
+    else if (is(4, 4, 128, 2)) e = launch<64, 4, 4, 128, 2>(st, a);
+    else if (is(2, 4, 128, 2)) e = launch<64, 2, 4, 128, 2>(st, a);
+  }
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

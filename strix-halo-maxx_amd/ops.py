@@ -468,6 +468,19 @@ def sdpa(q, k, v, out=None, scale=None, qpos0=0, causal_from=None):
     return out
 
 
+def sdpa_tiling(B, H, Tq, D):
+    """(query waves, key waves, keys per staged block, ring stages) of the kernel sdpa runs for this problem."""
+    import ctypes
+    t = (ctypes.c_int * 4)()
+    _lib.load().mx_sdpa_tiling(B, H, Tq, D, ctypes.cast(t, ctypes.c_void_p))
+    return tuple(t)
+
+
+def sdpa_symbol(B, H, Tq, D):
+    """The attention kernel's name as rocprofv3 prints it."""
+    return "attn_fwd_kernel<{}, {}>".format(D, ", ".join(str(v) for v in sdpa_tiling(B, H, Tq, D)))
+
+
 class Attn:
     """Reference protocol (hattn.py:17-37): Attn(H, T, D)(q, k, v) -> (B, T, H*D). No V^T staging buffer is needed:
     the kernel transposes V through LDS."""

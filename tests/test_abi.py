@@ -18,7 +18,7 @@ A16 = 0x10000  # fake 16-byte aligned device addresses: validation never derefer
 
 def declared():
     src = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|long)\s+(mx_\w+)\s*\(", src, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|long|void)\s+(mx_\w+)\s*\(", src, re.M)))
 
 
 def test_header_declares_entry_points():
@@ -104,6 +104,18 @@ def test_sdpa_validation():
     rc = lib.mx_sdpa(None, A16, 0, 72, 3456, A16, 0, 72, 3456, A16, 0, 72, 3456, A16, 0, 72, 1152, 1, 16, 729, 729, 80,
                      0.1, 0, 729)
     assert rc == -1
+
+
+def test_sdpa_tiling_pick():
+    """The tiling table (host-side, no launch): every pick is a tiling mx_sdpa instantiates."""
+    import strix_halo_maxx_amd.ops as ops
+    assert ops.sdpa_tiling(1, 16, 729, 72) == (2, 4, 128, 2)      # vision tower, batch 1
+    assert ops.sdpa_tiling(13, 16, 729, 72) == (4, 2, 64, 4)      # batch 13 / 256
+    assert ops.sdpa_tiling(1, 32, 64, 64) == (1, 4, 128, 2)       # 64-token prompt
+    assert ops.sdpa_tiling(1, 32, 730, 64) == (4, 4, 128, 2)      # text prefix
+    assert ops.sdpa_tiling(1, 12, 1280, 64) == (2, 4, 128, 2)     # TRecViT
+    assert ops.sdpa_tiling(16, 12, 1280, 64) == (4, 1, 64, 3)     # TRecViT clip
+    assert ops.sdpa_symbol(1, 16, 729, 72) == "attn_fwd_kernel<72, 2, 4, 128, 2>"
 
 
 def test_other_entry_points_refuse_bad_shapes():

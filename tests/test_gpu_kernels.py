@@ -291,6 +291,25 @@ def test_sdpa_prefix_causal_mask(dev):
     assert rel(out3, ref3) < 1e-2
 
 
+@pytest.mark.parametrize("B,L", [(3, 96), (6, 96)])
+def test_sdpa_batched_query_mask(dev, B, L):
+    """The batched yes/no query's mask (every question sees the 730-token prefix and its own ids causally) at a grid
+    size served by 8-wave (B = 3) and 16-wave (B = 6) workgroups."""
+    H, P, D = 32, 730, 64
+    g = gen(13 + B)
+    kc = torch.randn(B, H, P + L, D, generator=g).to(BF)
+    vc = torch.randn(B, H, P + L, D, generator=g).to(BF)
+    q = torch.randn(B, H, L, D, generator=g).to(BF)
+    m = torch.zeros(L, P + L, dtype=torch.bool)
+    m[:, :P] = True
+    m[:, P:] = torch.tril(torch.ones(L, L, dtype=torch.bool))
+    ref = _sdpa_ref(q, kc, vc, 0.125, m[None, None]).transpose(1, 2).reshape(B, L, H * D)
+    print(f"sdpa masked query B={B} L={L}", flush=True)
+    out = ops.sdpa(q.to(dev), kc.to(dev), vc.to(dev), qpos0=P, causal_from=P)
+    assert rel(out, ref) < 1e-2
+    assert (out.float().cpu() - ref).abs().max().item() < 5e-2
+
+
 @pytest.mark.parametrize("rows,D", [(729, 1152), (1458, 1152), (730, 2048), (1, 2048), (1280, 768)])
 def test_layernorm(dev, rows, D):
     g = gen(rows + D)
