@@ -443,13 +443,27 @@ def decode_bench(steps_tokens=128, w8a8=False):
     dec.prefill(img, prompt)
     torch.cuda.synchronize()
     t_pre = time.perf_counter() - t0
-    dec.start_decode()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps_tokens - 1):
-        dec.replay_step()
-    torch.cuda.synchronize()
-    t_dec = (time.perf_counter() - t0) / (steps_tokens - 1)
+    def time_decode():
+        dec.prefill(img, prompt)
+        dec.start_decode()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps_tokens - 1):
+            dec.replay_step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / (steps_tokens - 1)
+    t_dec = time_decode()
+    path = "one launch per step (mx_decode_step_mk)" if dec.use_mk else "per-layer kernels"
+    if dec.mk_error():
+        raise RuntimeError(f"one-launch decode step reported error {dec.mk_error()}")
+    t_layers = None
+    if dec.use_mk:  # the per-layer kernel sequence beside it, on the same decoder
+        dec.use_mk = False
+        dec.graph = None
+        for _ in range(2):
+            dec.generate(img, prompt, 8)
+        t_layers = time_decode()
+        dec.use_mk = True
     # the reference's yes/no query (FastMD2.query, md2fast.py:208-212): a 32-id question over the 730-token prefix,
     # yes / no rows of the LM head, one HIP graph
     dec.encode(img)
@@ -471,7 +485,8 @@ def decode_bench(steps_tokens=128, w8a8=False):
     kvbytes = 2 * 2 * L * ctx_mid * D
     bpt = wbytes + kvbytes
     return {"prefill_ms": round(t_pre * 1e3, 3), "query_ms": round(t_q * 1e3, 3), "decode_tok_s": round(1.0 / t_dec, 1),
-            "decode_ms_per_token": round(t_dec * 1e3, 4),
+            "decode_ms_per_token": round(t_dec * 1e3, 4), "decode_path": path,
+            "decode_tok_s_layer_kernels": round(1.0 / t_layers, 1) if t_layers else None,
             "decode_roofline": {"bound": "hbm", "achieved": round(bpt / t_dec / 1e9, 1), "peak": PEAK_HBM / 1e9,
                                 "unit": "GB/s", "frac": round(bpt / t_dec / PEAK_HBM, 4),
                                 "bytes_per_token": bpt},

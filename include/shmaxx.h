@@ -220,6 +220,24 @@ int mx_decode_attn_fc2_i8(hipStream_t st, const uint16_t* qkv, const float* cs, 
                           int N);
 int mx_gemv_res2_i8(hipStream_t st, const uint16_t* y2, const uint16_t* a, int S, const float* part, const int8_t* Wp,
                     const float* swp, const float* bp, int Kp, const uint16_t* xres, uint16_t* out, int N);
+/* A whole greedy decode step of the 2048-wide, 32-head (64 dims), 8192-MLP text model in ONE launch: every layer of
+ * md2fast.py:173-198 for one token (LN -> [qkv | fc1] + GELU, rope + K/V append at pos = state[1], attention over
+ * keys 0..pos, fc2 / proj and the parallel residual), the final LN + LM head + argmax, and mx_embed_step's
+ * bookkeeping (tokens[state[0]] = token, state advanced, x = wte[token]; nothing recorded at state[0] >= cap).
+ * layers: nl descriptors of mx_decode_mk_layer_bytes() bytes in device memory, each 10 device pointers {ln gamma,
+ * ln beta, Wqf = [Wqkv; Wfc1] (14336 x 2048 bf16), bqf (fp32), W2 (2048 x 8192), b2, Wp (2048 x 2048), bp, K cache,
+ * V cache (slot 0 of [slot][32][ctx][64])}. logits (V bf16) optional. ll: mx_decode_mk_words() exchange words and
+ * ep: 2 words {epoch base, error}, all zeroed once and owned by one decoder; ep[1] != 0 after a step = a wait timed
+ * out (the grid exited; zero ll and ep before the next step). The kernel runs mx_decode_mk_grid() workgroups that
+ * must all be resident: it refuses (MX_ESHAPE) a device with fewer CUs, and ctx > 1024 or V > 65536.
+ * Replaces the per-layer kernel sequence of a greedy step (the reference never decodes, md2fast.py:10-11). */
+int mx_decode_step_mk(hipStream_t st, const void* layers, int nl, int ctx, const uint16_t* lnf_g, const uint16_t* lnf_b,
+                      const uint16_t* wlm, const float* blm, int V, const uint16_t* wte, const float* cs, float eps,
+                      float scale, uint16_t* x, int* state, int pos_base, int* tokens, int cap, uint16_t* logits,
+                      uint64_t* ll, uint32_t* ep);
+int mx_decode_mk_words(void);
+int mx_decode_mk_grid(void);
+int mx_decode_mk_layer_bytes(void);
 
 /* ============================================================================================ TRecViT recurrence
  * One streamed frame of conv_1d + block-diagonal gates + RG-LRU + y-gate (numerics of tapnext/npu/pack8.py:253-279

@@ -56,6 +56,10 @@ SIGNATURES = {
     "mx_gemv_res2": [P, P, P, I, P, P, P, I, P, P, I],
     "mx_decode_attn_fc2_i8": [P, P, P, P, P, I, I, P, F, I, P, P, P, P, P, P, I, P, I],
     "mx_gemv_res2_i8": [P, P, P, I, P, P, P, P, I, P, P, I],
+    "mx_decode_step_mk": [P, P, I, I, P, P, P, P, I, P, P, F, F, P, P, I, P, I, P, P, P],
+    "mx_decode_mk_words": [],
+    "mx_decode_mk_grid": [],
+    "mx_decode_mk_layer_bytes": [],
     "mx_ssm_step": [P, P, P, P, P, L, P, L, P, P, P, P, P, P, P, P, P, P, L, I, I],
     "mx_ssm_prep": [P, P, L, L, P, P, P, P, P, P, P, P, P, P, I, I, I],
     "mx_rglru_scan": [P, P, P, P, I, I, I, P, L, L, P, L, L],

@@ -121,6 +121,41 @@ class TextDecoder:
         self.pos_base = 0
         self.steps = 0
         self.graph = None
+        # one launch per decode step (mx_decode_step_mk) where its shapes hold: the bf16 2048-wide, 32 x 64-head,
+        # 8192-MLP model, a cache of at most 1024 positions, one attention split, and a device with a CU for each of
+        # its workgroups; the per-layer kernels above otherwise (use_mk = False selects them too)
+        self.mk_layers = self.mk_ll = self.mk_ep = None
+        if (dev.type == "cuda" and not w8a8 and attn_splits == 1 and (self.D, self.H, self.hd, c["ff"]) == (2048, 32, 64, 8192)
+                and ctx <= 1024 and self.V <= 65536
+                and torch.cuda.get_device_properties(dev).multi_processor_count >= lib.mx_decode_mk_grid()):
+            self._init_mk()
+        self.use_mk = self.mk_layers is not None
+
+    def _init_mk(self):
+        lib = _lib.load()
+        rows = []
+        for i, b in enumerate(self.blocks):
+            for t, shape in ((b["wqf"], (3 * self.D + 8192, self.D)), (b["w2"], (self.D, 8192)), (b["wp"], (self.D, self.D))):
+                if tuple(t.shape) != shape or not t.is_contiguous():
+                    return
+            rows.append([b["ln"][0].data_ptr(), b["ln"][1].data_ptr(), b["wqf"].data_ptr(), b["bqf"].data_ptr(),
+                         b["w2"].data_ptr(), b["b2"].data_ptr(), b["wp"].data_ptr(), b["bp"].data_ptr(),
+                         self.kc[i].data_ptr(), self.vc[i].data_ptr()])
+        if lib.mx_decode_mk_layer_bytes() != 8 * len(rows[0]):
+            raise RuntimeError("layer descriptor size mismatch with the library")
+        self.mk_layers = torch.tensor(rows, dtype=torch.int64).to(self.dev)
+        self.mk_ll = torch.zeros(lib.mx_decode_mk_words(), dtype=torch.int64, device=self.dev)
+        self.mk_ep = torch.zeros(2, dtype=torch.int32, device=self.dev)
+
+    def mk_error(self):
+        """The one-launch step's error word (0: every wait completed). Synchronises."""
+        return 0 if self.mk_ep is None else int(self.mk_ep[1].item())
+
+    def mk_reset(self):
+        """Clear the exchange words and the epoch after a failed step."""
+        if self.mk_ep is not None:
+            self.mk_ll.zero_()
+            self.mk_ep.zero_()
 
     # ------------------------------------------------------------------ prefill (md2fast.py:169-212)
     def _text_layers(self, x, pos0, causal_from, B=1, bcast=False):
@@ -284,6 +319,16 @@ class TextDecoder:
             self._count_step()
         st = stream()
         lib = _lib.load()
+        if self.use_mk:
+            cap = max(1, min(self.ctx - self.pos_base + 1, self.ctx))
+            _lib.check(lib.mx_decode_step_mk(st, self.mk_layers.data_ptr(), len(self.blocks), self.ctx,
+                                             self.post_ln[0].data_ptr(), self.post_ln[1].data_ptr(),
+                                             self.w_lm.data_ptr(), self.b_lm.data_ptr(), self.V, self.wte.data_ptr(),
+                                             self.cs.data_ptr(), float(self.eps), float(self.hd ** -0.5),
+                                             self.xd[0].data_ptr(), self.state.data_ptr(), self.pos_base,
+                                             self.tokens.data_ptr(), cap, ptr(self.logits) if logits else None,
+                                             self.mk_ll.data_ptr(), self.mk_ep.data_ptr()), "mx_decode_step_mk")
+            return
         xi = 0
         for i, b in enumerate(self.blocks):
             x, xn = self.xd[xi], self.xd[xi ^ 1]
