@@ -59,6 +59,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// DPP lane moves (VALU, no LDS round trip): CTRL quad_perm 0x00-0xff, row_mirror 0x140, row_half_mirror 0x141,
+// row_bcast15 0x142, row_bcast31 0x143; rows outside ROW_MASK return old.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                               CTRL, ROW_MASK, 0xf, false));
+}
+// Sum of v over the 64 lanes, returned wave-uniform: pairs, quads, half rows and rows by DPP butterflies, then rows
+// 0 + 1 and 2 + 3 by row_bcast15 and the whole wave into lane 63 by row_bcast31. ~6 VALU steps instead of 6 LDS
+// permutes; a fixed order (deterministic), not the xor-butterfly order of wave_sum.
+__device__ __forceinline__ float wave_total(float v) {
+  v += dpp_mov<0xb1>(0.f, v);        // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4e>(0.f, v);        // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x141>(0.f, v);       // row_half_mirror
+  v += dpp_mov<0x140>(0.f, v);       // row_mirror
+  v += dpp_mov<0x142, 0xa>(0.f, v);  // row_bcast15 into rows 1, 3
+  v += dpp_mov<0x143, 0xc>(0.f, v);  // row_bcast31 into rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -3,56 +3,103 @@
 //
 // Why: a decode step streams 2.6 GB of weights, ~100 MB per layer. As separate kernels (decode.hip) every layer pays
 // three kernel boundaries, each a launch plus a dependent load -> compute -> store chain during which HBM idles
-// (~9 us of a ~27 us layer). Here the boundaries become data-ready waits between workgroups, and each workgroup has
-// already issued the weight rows (or K/V cache rows) of its next phase when it starts waiting, so HBM keeps
-// streaming through every wait.
+// (~9 us of a ~27 us layer). Here the boundaries become data-ready waits between workgroups, and the weight stream
+// never stops for them.
 //
-// Grid: 256 workgroups of 512 threads (8 waves), one per CU, all resident at once (the host checks the CU count).
-//   * GEMV workgroups g = 0 .. 223, per layer:
-//       A  h = LN(x) (each wave, from x in LDS), rows 64 g .. 64 g + 63 of [Wqkv | Wfc1] (8 rows per wave), + bias,
-//          GELU (tanh) on the fc1 rows -> qkv / g exchange words
-//       B  y2 = bf16(g W2^T + b2) for this workgroup's 8 or 10 fc2 rows (one row per wave, two on waves 0-1 of the
-//          10-row groups), g gathered into LDS
-//       C  x'[n] = bf16(y2[n] + bf16(bf16(a Wp^T + bp)[n] + x[n])) for the same rows (md2fast.py:198's parallel
-//          residual, the roundings of decode.hip's gemv_res2), a gathered into LDS -> x exchange words
-//   * attention workgroups 224 .. 255, one per head: during phase A they load the head's K / V cache rows
-//     0 .. pos - 1 into registers (16 rounds of 8 keys per wave: contexts up to 1024), then wait for the head's q / k /
-//     v, apply the rope (fp32, as rope.hip), append k / v at pos, and run a one-pass softmax over all keys (8 waves
-//     merged in LDS) -> attention output words
-//   * LM head (all 256 workgroups): LN(x) with the final LayerNorm, logits = bf16(x Wlm^T + b) in 8-row jobs, a
+// Grid: 256 workgroups of 9 waves, one per CU, all resident at once (the host checks the CU count). In every
+// workgroup waves 0-7 compute and wave 8 is the exchange wave: it alone waits for other workgroups' results (polls)
+// and publishes most of this workgroup's. Vector-memory completion is in order per wave, so a wave that polled would
+// first wait for every weight row it has in flight; the compute waves never poll and meet the exchange wave at plain
+// s_barriers (no memory wait), so each keeps its next rows in flight through every exchange.
+//   * GEMV workgroups g = 0 .. 223, per layer (compute wave w):
+//       the exchange wave gathers x and computes h = LN(x) into LDS (the proj rows of the workgroup arrive in LDS by
+//          DMA meanwhile)
+//       A  [Wqkv | Wfc1] in row pairs: pair round k gives each wave one pair (qkv pairs in the first rounds), each row
+//          + bias, GELU (tanh) on fc1 rows -> qkv / g exchange words, stored in two bursts
+//       B  the 8 or 10 fc2 rows of the workgroup in 4 KB quarter rows, spread over the waves -> partial sums in LDS
+//       C  the same proj rows from LDS -> partial sums; the exchange wave then forms
+//          x'[n] = bf16(y2[n] + bf16(bf16(a Wp^T + bp)[n] + x[n])), y2 = bf16(g W2^T + b2) (md2fast.py:198's
+//          parallel residual, the roundings of decode.hip's gemv_res2) -> x exchange words
+//     Each compute wave streams A and B through a ring of MK_NB 4 KB units (the next unit issued as soon as one is
+//     reduced, across phase and layer boundaries).
+//   * attention workgroups 224 .. 255, one per head: the compute waves load the head's K cache rows 0 .. pos - 1
+//     into registers and its V rows into LDS (LDS-DMA), 8 keys per wave per round, 16 rounds (contexts up to 1024),
+//     as soon as the previous layer's attention is done; the exchange wave waits for the head's q / k / v, applies
+//     the rope (fp32, as rope.hip), and after the compute waves' one-pass softmax (merged in LDS) publishes the
+//     output and appends k / v at pos.
+//   * LM head (all 256 workgroups): LN(x) with the final LayerNorm, logits = bf16(x Wlm^T + b) in 2-row jobs, a
 //     per-workgroup argmax key; workgroup 0 reduces the 256 keys (first index wins ties, as torch.argmax), records
 //     the token, advances the position and writes the next token's embedding (embed_step_kernel's bookkeeping).
 //
+// What bounds it (measured): every exchange waits behind the requests queued ahead of it in the memory system, so the
+// kernel keeps the queue short (~64 KB per CU in flight: the ring, no deeper) and keeps polls off the weight stream
+// (the exchange wave polls for g only once its own phase A is done; one sentinel per 64 words, then one batch read).
 // Exchange: activation vectors travel as 64-bit words (epoch << 32 | two bf16), written with agent-scope stores and
 // read with agent-scope loads (both bypass the non-coherent per-XCD L2), so a reader polls the data itself: a word
 // with the expected epoch is the new value (8-byte stores are single-copy atomic). Epochs grow by 3 per layer within
-// a step and the base advances by kEpochsPerStep per step (kept in device memory), so a buffer can be reused by every
-// layer: no producer can overwrite a word before all of its readers have consumed it (each next write depends,
-// through the phase chain, on every reader having finished). Every wait is bounded (~50 ms of the 100 MHz clock);
-// a wait that times out records an error code and the workgroup exits, so the grid always drains.
+// a step and the base advances by 3 L + 2 per step (kept in device memory), so a buffer is reused by every layer: no
+// producer can overwrite a word before all of its readers have consumed it (each next write depends, through the
+// phase chain, on every reader having finished). An exchange wave polls one word per 64 until they all carry the
+// epoch, then reads the whole vector (again where a word is still stale). Every wait is bounded (~50 ms of the
+// 100 MHz clock): after a timeout the exchange wave records an error code and stops waiting, so every wave still
+// reaches every barrier and the grid drains (the step's results are then garbage; the host sees the code).
 #include "common.h"
 #include "gemv.h"
+
+#include <utility>
 
 namespace {
 
 constexpr int MK_D = 2048, MK_H = 32, MK_HD = 64, MK_F = 8192;
 constexpr int MK_NQKV = 3 * MK_D, MK_NA = MK_NQKV + MK_F;  // 6144 qkv rows + 8192 fc1 rows
-constexpr int MK_W = 8, MK_T = 64 * MK_W;                   // waves / threads per workgroup
+constexpr int MK_W = 8;                                     // compute waves per workgroup
+constexpr int MK_XW = MK_W;                                 // the exchange wave
+constexpr int MK_T = 64 * (MK_W + 1);                       // 576 threads
 constexpr int MK_NG = 224, MK_G = MK_NG + MK_H;             // GEMV workgroups, all workgroups
-constexpr int MK_RA = MK_NA / MK_NG;                         // 64 phase-A rows per GEMV workgroup
-static_assert(MK_RA == 8 * MK_W, "8 rows per wave");
-constexpr int MK_ROUNDS = 16;                                // key rounds of 8 keys per wave: 1024 keys
+#ifndef MK_GW
+#define MK_GW 8
+#endif
+#ifndef MK_NB
+#define MK_NB 2
+#endif
+// GEMV waves hold MK_NB weight units of 4 KB in flight each (~64 KB per CU): about what saturates HBM, and no more.
+// Requests wait behind everything queued ahead of them, the exchanges between workgroups included: with 128 KB per
+// CU in flight a store -> poll round trip takes ~6 us instead of ~3, for no more bandwidth. (MK_GW < 8 runs the GEMV
+// on fewer waves, the others only meet the barriers.)
+constexpr int GW = MK_GW, NBUF = MK_NB;
+constexpr int MK_NGW = MK_NG * GW;                          // GEMV waves
+constexpr int KA = (MK_NA / 2) / MK_NGW;                    // row pairs per GEMV wave in phase A
+static_assert(KA * MK_NGW * 2 == MK_NA, "whole row pairs per wave");
+constexpr int JB = (4 * 10 + GW - 1) / GW;                  // fc2 quarter-row units per wave (10-row groups)
+constexpr int JC = (10 + GW - 1) / GW;                      // proj rows per wave
+// Slots of the weight ring: [0, SA) phase A, [SA, SA + JB) phase B. Phase C's proj rows go to LDS by DMA at the
+// start of the layer instead (C runs last, when the attention output arrives: rows fetched into the ring only then
+// would add a memory latency to every layer).
+constexpr int SA = 2 * KA, B0 = SA, B1 = SA + JB;
+constexpr int NSLOT = (B1 + NBUF - 1) / NBUF * NBUF;        // slots per layer (a multiple of the ring depth)
+// Barriers per layer in GEMV workgroups: h ready, phase A done, g ready, a ready, partial sums ready. The exchange
+// wave polls for g only once its own workgroup's phase A is done: 224 workgroups polling 64 sentinels each slow the
+// weight stream of phase A down (the polls share each CU's memory pipeline), and g cannot be complete earlier anyway.
+constexpr int NBAR = 5;
+#ifndef MK_ROT
+#define MK_ROT 1
+#endif
+// Row blocks rotate over the 8 workgroups of each group of 8 (consecutive workgroups sit on the 8 XCDs) from one
+// phase-A pair round to the next, so that every XCD reads every part of the address interleave: with a fixed
+// assignment, the XCDs whose blocks fall on some address bits stream up to 1.5x slower than the others, and every
+// workgroup waits for the slowest.
+constexpr int ROT = MK_ROT ? 8 / KA > 0 ? 8 / KA : 1 : 0;
+constexpr int KQ = (MK_NQKV / 2 + MK_NGW - 1) / MK_NGW - 1;  // the last pair round that holds qkv pairs
+// the GEMV wave whose row pairs workgroup wg's wave takes in pair round k
+__device__ __forceinline__ int rot_wave(int wg, int wave, int k) { return ((wg & ~7) + ((wg + ROT * k) & 7)) * GW + wave; }
+constexpr int MK_ROUNDS = 16;                               // key rounds of 8 keys per compute wave: 1024 keys
 constexpr int MK_MAXKEYS = MK_ROUNDS * 8 * MK_W;
+constexpr int MK_MAXL = 32;                                 // layers the LDS copy of the layer table holds
 
 // exchange words (uint64): layout of the LL area
 constexpr int LL_X = 0, LL_QKV = 1024, LL_G = 4096, LL_A = 8192, LL_AM = 9216, LL_WORDS = 9216 + MK_G;
+static_assert(LL_G == LL_QKV + MK_NQKV / 2, "g words follow the qkv words: pair p of [qkv | fc1] is word LL_QKV + p");
 constexpr uint64_t kTimeout = 5000000ull;  // 50 ms at 100 MHz
-
-// fc2 / proj rows of GEMV workgroup g: 128 groups of 10 rows, then 96 of 8 (even sizes: pairs stay together)
-__device__ __forceinline__ void row_group(int g, int& r0, int& n) {
-  if (g < 128) r0 = 10 * g, n = 10;
-  else r0 = 1280 + 8 * (g - 128), n = 8;
-}
 
 // Every pointer here is to device memory: the casts to the global address space keep the loads and stores global
 // (pointers read from the layer table, or passed through the opaque asm below, would otherwise become flat accesses,
@@ -73,35 +120,20 @@ __device__ __forceinline__ void load_vec_g(u32x4 (&xc)[KC], const uint16_t* x, i
 #pragma unroll
   for (int i = 0; i < KC; i++) xc[i] = ldg_vec(x + (lane + 64 * i) * 8);
 }
+// 16-byte chunk of a weight matrix at byte offset off (32-bit) from a wave-uniform base: one offset register per
+// row, the chunk steps as immediates
+__device__ __forceinline__ u32x4 ldw(const uint16_t* base, uint32_t off) {
+  return __builtin_nontemporal_load(GLOBAL(const u32x4, reinterpret_cast<const char*>(base) + off));
+}
 
-// Wait until words buf[0 .. NW) all carry epoch ep and store their payloads to dst[0 .. NW) (LDS). Every thread of
-// the workgroup calls it; each round issues all of a thread's loads before checking any (one round trip per round;
-// words already seen are simply read again). false: the wait timed out (error recorded); the caller returns.
-template <int NW>
-__device__ bool ll_gather(const uint64_t* __restrict__ buf, uint32_t ep, uint32_t* dst, uint32_t* err, int* s_flag) {
-  constexpr int PER = (NW + MK_T - 1) / MK_T;
-  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  for (;;) {
-    uint64_t v[PER];
-#pragma unroll
-    for (int i = 0; i < PER; i++) v[i] = ld_word(buf + min((int)threadIdx.x + MK_T * i, NW - 1));
-    int pending = 0;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int w = threadIdx.x + MK_T * i;
-      if (w < NW) {
-        if ((uint32_t)(v[i] >> 32) == ep) dst[w] = (uint32_t)v[i];
-        else pending = 1;
-      }
-    }
-    if (!__syncthreads_or(pending)) return true;
-    if (threadIdx.x == 0) *s_flag = (__builtin_amdgcn_s_memrealtime() - t0) > kTimeout;
-    __syncthreads();
-    if (*s_flag) {
-      if (threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return false;
-    }
-  }
+// Workgroup barrier without __syncthreads' memory wait: only this wave's LDS accesses complete first, so the rows a
+// compute wave has in flight stay in flight across it.
+__device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// fc2 / proj rows of GEMV workgroup g: 128 groups of 10 rows, then 96 of 8 (even sizes: pairs stay together)
+__device__ __forceinline__ void row_group(int g, int& r0, int& n) {
+  if (g < 128) r0 = 10 * g, n = 10;
+  else r0 = 1280 + 8 * (g - 128), n = 8;
 }
 
 struct MkLayer {  // 10 device pointers, in this order (the host builds the table)
@@ -131,17 +163,8 @@ struct MkArgs {
   uint32_t* ep;         // [0] epoch base, [1] error code (0 = none)
 };
 
-// 16-byte chunk of a weight matrix at byte offset off (32-bit) from a wave-uniform base: one offset register per
-// row, the chunk steps as immediates (64-bit addresses per chunk, hoisted out of the layer loop, spilled)
-__device__ __forceinline__ u32x4 ldw(const uint16_t* base, uint32_t off) {
-  return __builtin_nontemporal_load(GLOBAL(const u32x4, reinterpret_cast<const char*>(base) + off));
-}
-
-constexpr int MK_MAXL = 32;  // layers the LDS copy of the layer table holds
-
 // Layer l's descriptor from the LDS copy of the table, every pointer made wave-uniform (SGPRs): read from global memory
-// inside the loop they would be vector loads, whose waits (in-order with the weight stream) would drain every
-// prefetched weight row.
+// inside the loop they would be vector loads, whose waits (in order with the weight stream) would drain it.
 __device__ __forceinline__ MkLayer layer_of(const uint64_t* tab, int l) {
   uint64_t v[10];
 #pragma unroll
@@ -155,84 +178,164 @@ __device__ __forceinline__ MkLayer layer_of(const uint64_t* tab, int l) {
   return L;
 }
 
+// Dot product of 8 bf16 pairs (one 16-byte chunk of a weight row and of the activation) accumulated into acc with
+// v_dot2_f32_bf16 (two products per instruction, straight from the packed operands: no conversions to hold in
+// registers). The bf16 products are exact in fp32; only the accumulation order differs from a sequential FMA chain.
+// (The components go through plain temporaries: __builtin_bit_cast applied to a vector component directly, w[e],
+// compiles to component 0 for every e with this compiler.)
+__device__ __forceinline__ float dot8d(u32x4 w, u32x4 x, float acc) {
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const uint32_t we = w[e], xe = x[e];
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, we), __builtin_bit_cast(bf16x2, xe), acc, false);
+  }
+  return acc;
+}
+
 __device__ __forceinline__ uint32_t amax_key32(float v, int idx) {
   uint32_t u = __float_as_uint(v);
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return (u & 0xffff0000u) | (0xffffu - (uint32_t)idx);  // v is a bf16 value: its low 16 bits carry no order
 }
 
+// 16 bytes (two exchange words) at byte offset off of buf with an agent-scope load (sc1: past the non-coherent L2).
+// Each 8-byte half is written by one single-copy-atomic store and carries its own epoch, so the two halves are
+// checked separately. The compiler treats these loads as plain reads: a polling loop must pass a fresh (opaque) offset
+// every pass, or the load is hoisted out of it and the loop never sees new data.
+__device__ __forceinline__ u32x4 ld_pair(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+}
+
+// The exchange wave's wait for words buf[0 .. NW) (NW a multiple of 128) with epoch ep, payloads into dst (LDS).
+// Polls word 64 b + 63 of every block b (one load per lane, a few hundred bytes a round) until all carry ep, then
+// reads every word in one batch (NW / 128 16-byte loads per lane, all in flight: one round trip), again where a word
+// is still stale. (Re-reading whole buffers while waiting costs more than it saves: the polls of 224 workgroups share
+// the memory pipeline with the weight stream.) fail: set on a timeout (with the error word); set on entry = return.
+template <int NW>
+__device__ void xgather(const uint64_t* __restrict__ buf, uint32_t ep, uint32_t* dst, uint32_t* err, bool& fail) {
+  static_assert(NW % 128 == 0 && NW / 64 <= 64, "whole blocks, one sentinel per lane");
+  constexpr int NB = NW / 64, NP = NW / 128;
+  if (fail) return;
+  const int lane = threadIdx.x & 63;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(buf), (short)0, NW * 8, 0x00020000);
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  auto timed_out = [&]() __attribute__((always_inline)) {
+    if (__builtin_amdgcn_s_memrealtime() - t0 <= kTimeout) return false;
+    fail = true;
+    if (lane == 0) __hip_atomic_store(GLOBAL(uint32_t, err), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  };
+  for (;;) {  // sentinels: word 64 b + 63 of block b
+    uint32_t so = (uint32_t)min(lane, NB - 1) * 512u + 508u;
+    asm volatile("" : "+v"(so));  // a new offset each pass: the load is not hoisted out of the loop
+    const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(r, so, 0, 16);
+    if (!__any(hi != ep)) break;
+    if (timed_out()) return;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  for (;;) {
+    uint32_t lo = (uint32_t)lane * 16u;
+    asm volatile("" : "+v"(lo));  // as above
+    u32x4 v[NP];
+#pragma unroll
+    for (int j = 0; j < NP; j++) v[j] = ld_pair(r, lo + 1024u * j);
+    int pending = 0;
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+      const u32x4 t = v[j];
+      pending |= (t[1] != ep) | (t[3] != ep);
+    }
+    if (!__any(pending)) {
+#pragma unroll
+      for (int j = 0; j < NP; j++) {
+        const u32x4 t = v[j];
+        *reinterpret_cast<uint2*>(&dst[2 * (lane + 64 * j)]) = make_uint2(t[0], t[2]);
+      }
+      return;
+    }
+    if (timed_out()) return;
+  }
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N - 1, unrolled at compile time (the slot index must be a constant: it
+// selects registers and code paths)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+typedef u32x4 Buf[8];  // one unit in flight: 2 rows x 4 chunks, a half fc2 row (8 chunks) or a proj row (4)
+
 __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
-  __shared__ __attribute__((aligned(16))) uint32_t xs[MK_D / 2];   // x: the layer's input (bf16 pairs)
-  __shared__ __attribute__((aligned(16))) uint32_t gs[MK_F / 2];   // fc1 output g
-  __shared__ __attribute__((aligned(16))) uint32_t as2[MK_D / 2];  // attention output
-  __shared__ __attribute__((aligned(16))) uint16_t qkvh[3 * MK_HD]; // attention: the head's q, k, v (bf16)
+  __shared__ __attribute__((aligned(16))) uint32_t xs[MK_D / 2];  // x: the layer's input (bf16 pairs)
+  // GEMV workgroups: g (fc1 output, 16 KB) then the attention output a (4 KB); attention workgroups: V rows (128 KB)
+  __shared__ __attribute__((aligned(1024))) uint8_t big[MK_MAXKEYS * MK_HD * 2];
+  __shared__ __attribute__((aligned(16))) uint16_t qkvh[3 * MK_HD];  // attention: the head's q, k, v (bf16)
   __shared__ __attribute__((aligned(16))) uint16_t qr[MK_HD], kr[MK_HD];  // roped q, k (bf16)
   __shared__ float rec[MK_W][2 + MK_HD];
-  __shared__ float ys[16];
+  __shared__ __attribute__((aligned(16))) uint32_t hs[MK_D / 2];  // GEMV workgroups: h = LN(x) (bf16 pairs)
+  __shared__ float pb[4 * 10], pc[10];  // GEMV workgroups: fc2 quarter-row and proj partial sums
   __shared__ uint32_t sbest[MK_W];
-  __shared__ int s_flag;
   __shared__ uint64_t stab[MK_MAXL * 10];
+  uint32_t* gs = reinterpret_cast<uint32_t*>(big);
+  uint32_t* as2 = gs + MK_F / 2;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wg = blockIdx.x;
+  // wave-uniform by construction (readfirstlane): the compute / exchange split is a branch, not a predication that
+  // would keep both sides' registers live at once
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), wg = blockIdx.x;
+  const bool xw = wave == MK_XW;  // the exchange wave
+  // The exchange wave issues first when it competes with the compute waves (its polls and publishes are what the
+  // other workgroups wait for): ~5% per step.
+  if (xw) __builtin_amdgcn_s_setprio(3);
   for (int i = tid; i < a.nl * 10; i += MK_T) stab[i] = reinterpret_cast<const uint64_t*>(a.layers)[i];
   __syncthreads();
   const uint32_t base = a.ep[0];
-  const int pos = min(max(a.state[1], 0), a.ctx - 1);
+  const int pos = min(max(a.state[1], 0), a.ctx - 1);  // the new token's position (its cached keys: rows 0 .. pos - 1)
   const int NL = a.nl;
-  auto E = [&](int l, int p) { return base + 3u * (uint32_t)l + (uint32_t)p; };
+  auto E = [&](int l, int p) __attribute__((always_inline)) { return base + 3u * (uint32_t)l + (uint32_t)p; };
   uint32_t* err = a.ep + 1;
+  bool fail = false;  // exchange wave: a wait timed out
 
+  // The exchange wave and the compute waves run separate loops that meet at the same barriers (4 per layer in GEMV
+  // workgroups, 2 in attention workgroups): one loop with both roles as branches would be laid out as one straight
+  // region, both roles' registers live at once.
   if (wg >= MK_NG) {
     // ======================================================================= attention workgroup (one head)
     const int h = wg - MK_NG;
-    const int sub = lane & 7, kg = lane >> 3;
-    const int kmax = max(pos - 1, 0);  // last cache row (rows 0 .. pos - 1 hold earlier tokens)
-    for (int l = 0; l < NL; l++) {
-      const MkLayer L = layer_of(stab, l);
-      uint32_t so = (uint32_t)sub * 8u;  // opaque: addresses rebuilt per layer, not hoisted (they would spill)
-      asm volatile("" : "+v"(so));
-      uint64_t* ll = a.ll;
-      asm volatile("" : "+s"(ll));
-      const uint16_t* kh = L.kc + (long)h * a.ctx * MK_HD;
-      const uint16_t* vh = L.vc + (long)h * a.ctx * MK_HD;
-      // the head's cache rows, issued before the wait for q / k / v (32-bit offsets from the head's base)
-      u32x4 kk[MK_ROUNDS], vv[MK_ROUNDS];
-#pragma unroll
-      for (int r = 0; r < MK_ROUNDS; r++) {
-        const int key = min(wave * 8 + kg + 64 * r, kmax);
-        const unsigned off = (unsigned)key * 64u + so;
-        kk[r] = ldg_vec(kh + off);
-        vv[r] = ldg_vec(vh + off);
-      }
-      // q, k, v of the head (96 words: q at h * 32, k at 1024 + h * 32, v at 2048 + h * 32); the wait also completes
-      // the cache loads above
-      {
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        const int w = (min(tid, 95) >> 5) * 1024 + h * 32 + (tid & 31);
-        for (;;) {
-          const uint64_t v = ld_word(ll + LL_QKV + w);
-          int pending = 0;
-          if (tid < 96) {
-            if ((uint32_t)(v >> 32) == E(l, 1)) reinterpret_cast<uint32_t*>(qkvh)[tid] = (uint32_t)v;
-            else pending = 1;
-          }
-          if (!__syncthreads_or(pending)) break;
-          if (tid == 0) s_flag = (__builtin_amdgcn_s_memrealtime() - t0) > kTimeout;
-          __syncthreads();
-          if (s_flag) {
-            if (tid == 0) __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
+    if (xw) {
+      // ---- exchange wave: q / k / v of the head, rope, output, append
+      const int d = lane, jr = (d & 31) >> 1, d0 = d < 32 ? jr : d;
+      const float cr = ldg(a.cs + (long)pos * 32 + 2 * jr), sr = ldg(a.cs + (long)pos * 32 + 2 * jr + 1);
+      for (int l = 0; l < NL; l++) {
+        const MkLayer L = layer_of(stab, l);
+        uint64_t* ll = a.ll;  // opaque: the exchange addresses are rebuilt per layer, not hoisted
+        asm volatile("" : "+s"(ll));
+        // 96 words: q at h * 32, k at 1024 + h * 32, v at 2048 + h * 32
+        if (!fail) {
+          const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+          const int w1 = (lane >> 5) * 1024 + h * 32 + (lane & 31), w2 = 2048 + h * 32 + (lane & 31);
+          for (;;) {
+            const uint64_t v1 = ld_word(ll + LL_QKV + w1), v2 = ld_word(ll + LL_QKV + w2);
+            const bool ok = (uint32_t)(v1 >> 32) == E(l, 1) && (lane >= 32 || (uint32_t)(v2 >> 32) == E(l, 1));
+            if (!__any(!ok)) {
+              reinterpret_cast<uint32_t*>(qkvh)[lane] = (uint32_t)v1;
+              if (lane < 32) reinterpret_cast<uint32_t*>(qkvh)[64 + lane] = (uint32_t)v2;
+              break;
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kTimeout) {
+              fail = true;
+              if (lane == 0) __hip_atomic_store(GLOBAL(uint32_t, err), 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
           }
         }
-      }
-      // rope of the new token's q and k (fp32, rope.hip's arithmetic): output dim d < 32 pairs input dims
-      // (d >> 1, 16 + (d >> 1)); the roped k and the raw v are appended at pos after the last barrier of the layer
-      uint16_t kapp = 0, vapp = 0;
-      if (tid < MK_HD) {
-        const int d = tid, jr = (d & 31) >> 1;
-        const float* cp = a.cs + (long)pos * 32;
-        const float cr = ldg(cp + 2 * jr), sr = ldg(cp + 2 * jr + 1);
-        const int d0 = d < 32 ? jr : d;
+        // rope of the new token's q and k (fp32, rope.hip's arithmetic): output dim d < 32 pairs input dims
+        // (d >> 1, 16 + (d >> 1)); the roped k and the raw v are appended at pos at the end of the layer
         const float qa = bf2f(qkvh[d0]), qb = bf2f(qkvh[16 + jr]);
         const float ka = bf2f(qkvh[MK_HD + d0]), kb = bf2f(qkvh[MK_HD + 16 + jr]);
         const float qo = __fadd_rn(__fmul_rn(qa, sr), __fmul_rn(qb, cr)), qe = __fsub_rn(__fmul_rn(qa, cr), __fmul_rn(qb, sr));
@@ -240,306 +343,418 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         const float qv = d < 32 ? ((d & 1) ? qo : qe) : qa;
         const float kv = d < 32 ? ((d & 1) ? ko : ke) : ka;
         qr[d] = f2bf(qv);
-        kapp = f2bf(kv);
+        const uint16_t kapp = f2bf(kv);
         kr[d] = kapp;
-        vapp = qkvh[2 * MK_HD + d];
-      }
-      __syncthreads();
-      const u32x4 qp = *reinterpret_cast<const u32x4*>(&qr[sub * 8]);
-      const u32x4 knew = *reinterpret_cast<const u32x4*>(&kr[sub * 8]);
-      const u32x4 vnew = *reinterpret_cast<const u32x4*>(&qkvh[2 * MK_HD + sub * 8]);
-      const u32x4 zero4 = {0u, 0u, 0u, 0u};
-      // one pass over all keys 0 .. pos: scores (8 lanes per key), wave max, exponentials, P V
-      float sv[MK_ROUNDS];
-      float mb = -INFINITY;
+        const uint16_t vapp = qkvh[2 * MK_HD + d];
+        bar();  // q, k, v ready
+        bar();  // the 8 waves' (m, l, o) in rec
+        if (lane < MK_HD / 2) {  // two output dims per lane -> one word
+          float M = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < MK_ROUNDS; r++) {
-        const int key = wave * 8 + kg + 64 * r;
-        if (key == pos) { kk[r] = knew; vv[r] = vnew; }
-        else if (key > pos) { kk[r] = zero4; vv[r] = zero4; }
-        float sc = 0.f;
+          for (int w = 0; w < MK_W; w++) M = fmaxf(M, rec[w][0]);
+          float Lt = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          sc = __builtin_fmaf(lo_bf(kk[r][e]), lo_bf(qp[e]), sc);
-          sc = __builtin_fmaf(hi_bf(kk[r][e]), hi_bf(qp[e]), sc);
+          for (int w = 0; w < MK_W; w++) {
+            const float f = __builtin_amdgcn_exp2f(rec[w][0] - M);
+            Lt += rec[w][1] * f;
+            a0 += rec[w][2 + 2 * lane] * f;
+            a1 += rec[w][3 + 2 * lane] * f;
+          }
+          st_word(ll + LL_A + h * 32 + lane, E(l, 2), pack2(a0 / Lt, a1 / Lt));
         }
-        sc += __shfl_xor(sc, 1, 64);
-        sc += __shfl_xor(sc, 2, 64);
-        sc += __shfl_xor(sc, 4, 64);
-        sc = key <= pos ? sc * a.scale_log2 : -INFINITY;
-        sv[r] = sc;
-        mb = fmaxf(mb, sc);
+        // the append (read by later steps only)
+        *GLOBAL(uint16_t, L.kc + ((long)h * a.ctx + pos) * MK_HD + lane) = kapp;
+        *GLOBAL(uint16_t, L.vc + ((long)h * a.ctx + pos) * MK_HD + lane) = vapp;
+        // rec / qkvh / qr / kr are rewritten only after the next layer's first barrier
       }
-      const float m = fmaxf(wave_max(mb), -1e30f);  // a wave whose keys are all past pos: p = 0, not NaN
-      float lsum = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    } else {
+      // ---- compute waves: the cached keys 0 .. pos - 1 of the head, K rows into registers and V rows into LDS (row
+      // key at byte 128 key), issued before the exchange wave's wait for q / k / v; lane l of wave w takes key
+      // w * 8 + (l >> 3) + 64 r in round r, dims 8 (l & 7) .. + 7. The buffer range of both caches ends at row pos, so
+      // rows at and past pos read as zeros (masked below; the new token's own key is scored by wave 0 from LDS).
+      // One-pass softmax per wave, merged by the exchange wave.
+      const int sub = lane & 7, kg = lane >> 3;
+      const uint32_t koff = (uint32_t)(wave * 8 + kg) * 128u + (uint32_t)sub * 16u;
+      for (int l = 0; l < NL; l++) {
+        const MkLayer L = layer_of(stab, l);
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc(L.kc + (long)h * a.ctx * MK_HD, (short)0, pos * 128, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc(L.vc + (long)h * a.ctx * MK_HD, (short)0, pos * 128, 0x00020000);
+        uint32_t ko = koff;
+        asm volatile("" : "+v"(ko));
+        u32x4 kk[MK_ROUNDS];
 #pragma unroll
-      for (int r = 0; r < MK_ROUNDS; r++) {
-        const float pr = rbf(__builtin_amdgcn_exp2f(sv[r] - m));
-        if (sub == 0) lsum += pr;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          o[2 * e] = __builtin_fmaf(pr, lo_bf(vv[r][e]), o[2 * e]);
-          o[2 * e + 1] = __builtin_fmaf(pr, hi_bf(vv[r][e]), o[2 * e + 1]);
+        for (int r = 0; r < MK_ROUNDS; r++) {
+          kk[r] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 8192u * r, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rv, (__attribute__((address_space(3))) void*)(big + (wave * 8 + 64 * r) * 128), 16, ko + 8192u * r, 0, 0, 0);
         }
-      }
+        bar();  // q, k, v ready
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's K registers and V rows have landed
+        const u32x4 qp = *reinterpret_cast<const u32x4*>(&qr[sub * 8]);
+        float sv[MK_ROUNDS];
+        float mb = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        o[e] += __shfl_xor(o[e], 8, 64);
-        o[e] += __shfl_xor(o[e], 16, 64);
-        o[e] += __shfl_xor(o[e], 32, 64);
-      }
-      lsum = wave_sum(lsum);
-      if (kg == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) rec[wave][2 + sub * 8 + e] = o[e];
-      }
-      if (lane == 0) { rec[wave][0] = m; rec[wave][1] = lsum; }
-      __syncthreads();
-      if (tid < MK_HD / 2) {  // two output dims per thread -> one word
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < MK_W; w++) M = fmaxf(M, rec[w][0]);
-        float Lt = 0.f, a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int w = 0; w < MK_W; w++) {
-          const float f = __builtin_amdgcn_exp2f(rec[w][0] - M);
-          Lt += rec[w][1] * f;
-          a0 += rec[w][2 + 2 * tid] * f;
-          a1 += rec[w][3 + 2 * tid] * f;
+        for (int r = 0; r < MK_ROUNDS; r++) {
+          const int key = wave * 8 + kg + 64 * r;
+          float sc = dot8d(kk[r], qp, 0.f);
+          sc += __shfl_xor(sc, 1, 64);
+          sc += __shfl_xor(sc, 2, 64);
+          sc += __shfl_xor(sc, 4, 64);
+          sc = key < pos ? sc * a.scale_log2 : -INFINITY;
+          sv[r] = sc;
+          mb = fmaxf(mb, sc);
         }
-        st_word(ll + LL_A + h * 32 + tid, E(l, 2), pack2(a0 / Lt, a1 / Lt));
+        float snew = -INFINITY;  // the new token's key, wave 0
+        if (wave == 0) {
+          float sc = dot8d(*reinterpret_cast<const u32x4*>(&kr[sub * 8]), qp, 0.f);
+          sc += __shfl_xor(sc, 1, 64);
+          sc += __shfl_xor(sc, 2, 64);
+          sc += __shfl_xor(sc, 4, 64);
+          snew = sc * a.scale_log2;
+          mb = fmaxf(mb, snew);
+        }
+        const float m = fmaxf(wave_max(mb), -1e30f);  // a wave with no key in range: p = 0, not NaN
+        float lsum = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < MK_ROUNDS; r++) {
+          // rows past the range: p = 0, and the LDS row is zeroed here whatever the copy left in it (0 x NaN = NaN)
+          const u32x4 zero4 = {0u, 0u, 0u, 0u};
+          const u32x4 vl = *reinterpret_cast<const u32x4*>(big + (wave * 8 + kg + 64 * r) * 128 + sub * 16);
+          const u32x4 vv = wave * 8 + kg + 64 * r < pos ? vl : zero4;
+          const float pr = rbf(__builtin_amdgcn_exp2f(sv[r] - m));
+          if (sub == 0) lsum += pr;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const uint32_t ve = vv[e];
+            o[2 * e] = __builtin_fmaf(pr, lo_bf(ve), o[2 * e]);
+            o[2 * e + 1] = __builtin_fmaf(pr, hi_bf(ve), o[2 * e + 1]);
+          }
+        }
+        if (wave == 0 && kg == 0) {
+          const u32x4 vv = *reinterpret_cast<const u32x4*>(&qkvh[2 * MK_HD + sub * 8]);
+          const float pr = rbf(__builtin_amdgcn_exp2f(snew - m));
+          if (sub == 0) lsum += pr;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const uint32_t ve = vv[e];
+            o[2 * e] = __builtin_fmaf(pr, lo_bf(ve), o[2 * e]);
+            o[2 * e + 1] = __builtin_fmaf(pr, hi_bf(ve), o[2 * e + 1]);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          o[e] += __shfl_xor(o[e], 8, 64);
+          o[e] += __shfl_xor(o[e], 16, 64);
+          o[e] += __shfl_xor(o[e], 32, 64);
+        }
+        lsum = wave_sum(lsum);
+        if (kg == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; e++) rec[wave][2 + sub * 8 + e] = o[e];
+        }
+        if (lane == 0) { rec[wave][0] = m; rec[wave][1] = lsum; }
+        bar();  // the 8 waves' (m, l, o) in rec; every V row read (the next layer's V rows may land)
       }
-      if (tid < MK_HD) {  // the append (read by later steps only)
-        *GLOBAL(uint16_t, L.kc + ((long)h * a.ctx + pos) * MK_HD + tid) = kapp;
-        *GLOBAL(uint16_t, L.vc + ((long)h * a.ctx + pos) * MK_HD + tid) = vapp;
-      }
-      // no barrier here: rec, qkvh, qr, kr are next written after the next layer's q / k / v wait, which every
-      // thread reaches only after its reads above (a barrier would also wait for the stores just issued)
     }
   } else {
     // ======================================================================= GEMV workgroup
     int r0, nr;
     row_group(wg, r0, nr);
-    const int gw = wg * MK_W + wave;  // 1792 GEMV waves; phase-A job j covers rows j * 7168 + 4 gw .. + 3
-    u32x4 wa[4][4];                   // one 4-row phase-A job in flight
-    auto issue_a = [&](const MkLayer& L, uint32_t lo, int j) {
+    const uint16_t* xb = reinterpret_cast<const uint16_t*>(xs);
+    if (xw) {
+      // ---- exchange wave: x in, h = LN(x) for the compute waves, g and a in, this workgroup's x' rows out
+      for (int l = 0; l < NL; l++) {
+        const MkLayer L = layer_of(stab, l);
+        uint64_t* ll = a.ll;  // opaque: the exchange addresses are rebuilt per layer, not hoisted
+        asm volatile("" : "+s"(ll));
+        // the LayerNorm parameters and the workgroup's fc2 / proj biases (row r0 + lane), loaded while x is awaited
+        u32x4 xc[4], gc[4], bc[4];
+        load_vec_g<4>(gc, L.ln_g, lane);
+        load_vec_g<4>(bc, L.ln_b, lane);
+        const int ri = r0 + min(lane, nr - 1);
+        const float b2v = ldg(L.b2 + ri), bpv = ldg(L.bp + ri);
+        if (l == 0) {
+          load_vec_g<4>(xc, a.x, lane);
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t o = (uint32_t)(j * 7168 + 4 * gw + r) * (MK_D * 2u) + lo;
-#pragma unroll
-        for (int i = 0; i < 4; i++) wa[r][i] = ldw(L.wqf, o + 1024u * i);
-      }
-    };
-    {
-      uint32_t lo = (uint32_t)lane * 16u;
-      asm volatile("" : "+v"(lo));
-      issue_a(layer_of(stab, 0), lo, 0);
-    }
-    for (int l = 0; l < NL; l++) {
-      const MkLayer L = layer_of(stab, l);
-      // the lane's byte offset, opaque to the compiler: the addresses derived from it are rebuilt every layer instead
-      // of being hoisted out of the loop (live across it, they spill; a spill reload waits for every load before it)
-      uint32_t lo = (uint32_t)lane * 16u;
-      asm volatile("" : "+v"(lo));
-      uint64_t* ll = a.ll;  // the exchange addresses likewise
-      asm volatile("" : "+s"(ll));
-      // ---- phase A: LN(x), then two 4-row jobs of [Wqkv | Wfc1] (job 0 was issued before the wait for x; job 0 of
-      // every wave together covers all qkv rows, so the attention can start after the first job)
-      u32x4 gc[4], bc[4];
-      load_vec_g<4>(gc, L.ln_g, lane);
-      load_vec_g<4>(bc, L.ln_b, lane);
-      if (l == 0) {
-        for (int i = tid; i < MK_D / 8; i += MK_T)
-          reinterpret_cast<u32x4*>(xs)[i] = ldg_vec(a.x + i * 8);
-        __syncthreads();
-      } else if (!ll_gather<MK_D / 2>(ll + LL_X, E(l - 1, 3), xs, err, &s_flag)) {
-        return;
-      }
-      u32x4 xc[4];
-      load_vec<4>(xc, reinterpret_cast<const uint16_t*>(xs), lane);
-      ln_chunks<4>(xc, gc, bc, a.eps, MK_D, lane);
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        float acc[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          acc[r] = 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[r] = dot8(wa[r][i], xc[i], acc[r]);
+          for (int i = 0; i < 4; i++) reinterpret_cast<u32x4*>(xs)[lane + 64 * i] = xc[i];
+        } else {
+          xgather<MK_D / 2>(ll + LL_X, E(l - 1, 3), xs, err, fail);
+          load_vec<4>(xc, xb, lane);
         }
-        __builtin_amdgcn_sched_barrier(0);  // job 0's registers are free before job 1's loads land in them
-        if (j == 0) issue_a(L, lo, 1);
-        const int row = j * 7168 + 4 * gw + (lane >> 4);
-        const float bme = ldg(L.bqf + row);
-        const float tot = reduce_rows<4>(acc, lane);  // lane l: row 4 gw + (l >> 4) of the job
-        float v = rbf(tot + bme);
-        if (row >= MK_NQKV) v = rbf(gelu_tanh(v));
-        const float vn = __shfl_down(v, 16, 64);  // the odd row of the pair
-        if ((lane & 31) == 0) {
-          const uint32_t w = pack2(v, vn);
-          if (row < MK_NQKV) st_word(ll + LL_QKV + row / 2, E(l, 1), w);
-          else st_word(ll + LL_G + (row - MK_NQKV) / 2, E(l, 1), w);
-        }
-      }
-      // ---- phase B: fc2 rows r0 + wave (and r0 + 8 + wave on waves 0-1 of 10-row groups): the first row issued
-      // before the wait for g, the second after it
-      const bool two = wave + 8 < nr;
-      const int n1 = r0 + wave, n2 = two ? r0 + 8 + wave : n1;
-      __builtin_amdgcn_sched_barrier(0);
-      u32x4 w2[16];
-      const uint32_t o2a = (uint32_t)n1 * (MK_F * 2u) + lo;
+        ln_chunks<4, true>(xc, gc, bc, a.eps, MK_D, lane);
 #pragma unroll
-      for (int i = 0; i < 16; i++) w2[i] = ldw(L.w2, o2a + 1024u * i);
-      if (!ll_gather<MK_F / 2>(ll + LL_G, E(l, 1), gs, err, &s_flag)) return;
-      float y2a, y2b = 0.f;
+        for (int i = 0; i < 4; i++) reinterpret_cast<u32x4*>(hs)[lane + 64 * i] = xc[i];
+        bar();  // h ready
+        bar();  // the workgroup's phase A done
+        xgather<MK_F / 2>(ll + LL_G, E(l, 1), gs, err, fail);
+        bar();  // g ready
+        xgather<MK_D / 2>(ll + LL_A, E(l, 2), as2, err, fail);
+        bar();  // a ready
+        bar();  // the partial sums in pb / pc
+        // x'[n] = bf16(y2[n] + bf16(bf16(a Wp^T + bp)[n] + x[n])), y2 = bf16(g W2^T + b2): row r0 + lane
+        float xn = 0.f;
+        if (lane < nr) {
+          const float y2 = rbf(((pb[4 * lane] + pb[4 * lane + 1]) + (pb[4 * lane + 2] + pb[4 * lane + 3])) + b2v);
+          xn = rbf(y2 + rbf(rbf(pc[lane] + bpv) + bf2f(xb[r0 + lane])));
+        }
+        const float xn1 = __shfl_down(xn, 1, 64);
+        if (lane < nr && !(lane & 1)) st_word(ll + LL_X + (r0 + lane) / 2, E(l, 3), pack2(xn, xn1));
+      }
+    } else if (wave < GW) {
+      // ---- GEMV waves: a ring of NBUF 4 KB weight units, slot s of a layer in buffer s % NBUF, the unit NBUF slots
+      // ahead issued as soon as a slot is reduced (across phase and layer boundaries):
+      //   slots [0, SA): phase A, the pair rot_wave(wg, wave, k) + k MK_NGW (k = s / 2) of [Wqkv | Wfc1] rows (qkv
+      //   pairs first), row s % 2
+      //   slots [B0, B1): phase B, unit u = wave + GW (s - B0) < 4 nr: quarter u % 4 of fc2 row r0 + u / 4
+      // and phase C from LDS: proj row r0 + u (u = wave + GW j < nr) at pw + 4 KB u
+      u32x4 buf[NBUF][4];
+      float bqr[NBUF];
+      const uint8_t* pw = big + 24576;  // proj rows of the workgroup (10 x 4 KB), after gs and as2
+      const uint32_t pwo = lds_off(pw);
+      // real = false (the next-layer slots of the last layer): the same loads from the LayerNorm gamma, discarded
+      auto issue = [&](auto sc, const MkLayer& L, uint32_t lo, bool real) __attribute__((always_inline)) {
+        constexpr int s = decltype(sc)::value;
+        u32x4(&b)[4] = buf[s % NBUF];
+        if constexpr (s < SA) {
+          const int row = 2 * (rot_wave(wg, wave, s >> 1) + (s >> 1) * MK_NGW) + (s & 1);
+          const uint32_t o = real ? (uint32_t)row * (MK_D * 2u) + lo : lo;
+#pragma unroll
+          for (int i = 0; i < 4; i++) b[i] = ldw(real ? L.wqf : L.ln_g, o + 1024u * i);
+          bqr[s % NBUF] = ldg(L.bqf + row);
+        } else if constexpr (s >= B0 && s < B1) {
+          // a slot past the workgroup's units reads the LayerNorm gamma (4 KB, in cache) instead: every slot issues
+          // the same loads, so the compiler's wait counts stay exact (a conditional load makes them drain everything)
+          const int u = wave + GW * (s - B0);
+          const bool ok = u < 4 * nr;
+          const uint32_t o = ok ? (uint32_t)(r0 + (u >> 2)) * (MK_F * 2u) + (uint32_t)(u & 3) * (MK_D * 2u) + lo : lo;
+#pragma unroll
+          for (int i = 0; i < 4; i++) b[i] = ldw(ok ? L.w2 : L.ln_g, o + 1024u * i);
+        }
+      };
+      u32x4 hc[4];
+      float accE = 0.f, bE = 0.f;  // phase A: the even row of the current pair
+      // The pair words are published in two bursts, one vector store each: after the last round that holds qkv pairs
+      // and at the end of phase A. A store holds back this wave's later waits until it completes (the counter
+      // completes in order), ~2 us at agent scope under load: one per pair would stall the weight stream KA times.
+      uint32_t wq[KA];
+      auto compute = [&](auto sc, uint64_t* ll, uint32_t ep) __attribute__((always_inline)) {
+        constexpr int s = decltype(sc)::value;
+        const u32x4(&b)[4] = buf[s % NBUF];
+        if constexpr (s < SA) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc = dot8d(b[i], hc[i], acc);
+          if constexpr (!(s & 1)) {
+            accE = acc;
+            bE = bqr[s % NBUF];
+          } else {  // the pair: + bias, GELU on fc1 rows, one exchange word (qkv and g words are contiguous)
+            constexpr int k = s >> 1;
+            const int pr = rot_wave(wg, wave, k) + k * MK_NGW;
+            float ve = rbf(wave_total(accE) + bE), vo = rbf(wave_total(acc) + bqr[s % NBUF]);
+            if (2 * pr >= MK_NQKV) {
+              ve = rbf(gelu_tanh(ve));
+              vo = rbf(gelu_tanh(vo));
+            }
+            wq[k] = pack2(ve, vo);
+            if constexpr (k == KQ || k == KA - 1) {  // burst: lane i publishes the word of round k0 + i
+              constexpr int k0 = k == KQ ? 0 : KQ + 1;
+              uint32_t w = wq[k0];
+#pragma unroll
+              for (int j = k0 + 1; j <= k; j++) w = lane == j - k0 ? wq[j] : w;
+              const int kl = k0 + lane;
+              if (lane <= k - k0) st_word(ll + LL_QKV + rot_wave(wg, wave, kl) + kl * MK_NGW, ep, w);
+            }
+          }
+        } else if constexpr (s >= B0 && s < B1) {
+          const int u = wave + GW * (s - B0);
+          if (u < 4 * nr) {
+            const uint32_t* gq = gs + (u & 3) * (MK_D / 2);
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              acc = dot8d(b[i], *reinterpret_cast<const u32x4*>(&gq[(lane + 64 * i) * 4]), acc);
+            const float t = wave_total(acc);
+            if (lane == 0) pb[u] = t;
+          }
+        }
+      };
       {
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc = dot8(w2[i], *reinterpret_cast<const u32x4*>(&gs[(lane + 64 * i) * 4]), acc);
-        y2a = rbf(wave_sum(acc) + ldg(L.b2 + n1));
+        const MkLayer L0 = layer_of(stab, 0);
+        uint32_t lo = (uint32_t)lane * 16u;
+        asm volatile("" : "+v"(lo));
+        static_for<NBUF>([&](auto sc) __attribute__((always_inline)) { issue(sc, L0, lo, true); });
       }
-      __builtin_amdgcn_sched_barrier(0);
-      if (two) {  // wave-uniform
-        const uint32_t o2b = (uint32_t)n2 * (MK_F * 2u) + lo;
+      for (int l = 0; l < NL; l++) {
+        const MkLayer L = layer_of(stab, l);
+        const bool more = l + 1 < NL;
+        const MkLayer Ln = layer_of(stab, more ? l + 1 : l);
+        // the lane's byte offset and the exchange base, opaque to the compiler: the addresses derived from them are
+        // rebuilt every layer instead of being hoisted out of the loop (live across it, they spill)
+        uint32_t lo = (uint32_t)lane * 16u;
+        asm volatile("" : "+v"(lo));
+        uint64_t* ll = a.ll;
+        asm volatile("" : "+s"(ll));
+        // this wave's proj rows into LDS (DMA), landed before the h barrier: the wait costs nothing there (x comes
+        // later), and none is needed later, when the next layer's first units are in flight
 #pragma unroll
-        for (int i = 0; i < 16; i++) w2[i] = ldw(L.w2, o2b + 1024u * i);
-        float acc = 0.f;
+        for (int j = 0; j < JC; j++) {
+          const int u = wave + GW * j;
+          if (u < nr) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc = dot8(w2[i], *reinterpret_cast<const u32x4*>(&gs[(lane + 64 * i) * 4]), acc);
-        y2b = rbf(wave_sum(acc) + ldg(L.b2 + n2));
-      }
-      // ---- phase C: proj rows n1 (, n2), issued before the wait for the attention output
-      __builtin_amdgcn_sched_barrier(0);
-      u32x4 wpa[4], wpb[4];
-      const uint32_t opa = (uint32_t)n1 * (MK_D * 2u) + lo;
-      const uint32_t opb = (uint32_t)n2 * (MK_D * 2u) + lo;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        wpa[i] = ldw(L.wp, opa + 1024u * i);
-        wpb[i] = ldw(L.wp, opb + 1024u * i);  // n2 == n1 on one-row waves: the same (cached) row
-      }
-      const float bpa = ldg(L.bp + n1), bpb = ldg(L.bp + n2);
-      if (!ll_gather<MK_D / 2>(ll + LL_A, E(l, 2), as2, err, &s_flag)) return;
-      {
-        float acc[2] = {0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const u32x4 av = *reinterpret_cast<const u32x4*>(&as2[(lane + 64 * i) * 4]);
-          acc[0] = dot8(wpa[i], av, acc[0]);
-          acc[1] = dot8(wpb[i], av, acc[1]);
+            for (int i = 0; i < 4; i++)
+              dma16s(L.wp, (uint32_t)(r0 + u) * (MK_D * 2u) + 1024u * i + lo, pwo + (uint32_t)u * 4096u + 1024u * i);
+          }
         }
-        const float ta = wave_sum(acc[0]), tb = wave_sum(acc[1]);
-        const uint16_t* xb = reinterpret_cast<const uint16_t*>(xs);
-        if (lane == 0) {
-          ys[wave] = rbf(y2a + rbf(rbf(ta + bpa) + bf2f(xb[n1])));
-          if (two) ys[8 + wave] = rbf(y2b + rbf(rbf(tb + bpb) + bf2f(xb[n2])));
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        bar();  // h ready
+        load_vec<4>(hc, reinterpret_cast<const uint16_t*>(hs), lane);
+        static_for<NSLOT>([&](auto sc) __attribute__((always_inline)) {
+          constexpr int s = decltype(sc)::value;
+          if constexpr (s == B0) {
+            bar();  // phase A done
+            bar();  // g ready
+          }
+          compute(sc, ll, E(l, 1));
+          // the freed buffer's next unit (sched_barrier: kept after the reduction that frees it; the scheduler would
+          // otherwise hoist the loads and need more buffers)
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (s + NBUF < NSLOT) issue(std::integral_constant<int, s + NBUF>{}, L, lo, true);
+          else issue(std::integral_constant<int, s + NBUF - NSLOT>{}, Ln, lo, more);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        bar();  // a ready
+        // ---- phase C from LDS
+#pragma unroll
+        for (int j = 0; j < JC; j++) {
+          const int u = wave + GW * j;
+          if (u < nr) {
+            const uint8_t* pr = pw + u * 4096;
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              acc = dot8d(*reinterpret_cast<const u32x4*>(pr + (lane + 64 * i) * 16),
+                          *reinterpret_cast<const u32x4*>(&as2[(lane + 64 * i) * 4]), acc);
+            const float t = wave_total(acc);
+            if (lane == 0) pc[u] = t;
+          }
         }
+        bar();  // the partial sums in pb / pc; every read of hs, gs, as2, pw done
       }
-      __syncthreads();
-      if (tid < nr / 2) {
-        // rows r0 + 2 tid, r0 + 2 tid + 1: staged at index (row - r0)
-        st_word(ll + LL_X + r0 / 2 + tid, E(l, 3), pack2(ys[2 * tid], ys[2 * tid + 1]));
-      }
-      // the next layer's first phase-A job, in flight during the wait for x (ys is rewritten only after that wait)
-      __builtin_amdgcn_sched_barrier(0);
-      if (l + 1 < NL) issue_a(layer_of(stab, l + 1), lo, 0);
+    } else {
+      for (int l = 0; l < NL; l++)  // waves past GW: the same barriers per layer
+        for (int i = 0; i < NBAR; i++) bar();
     }
   }
 
   // ========================================================================= LM head + argmax (all workgroups)
   {
-    const int gw = wg * MK_W + wave;  // 2048 waves; 4-row jobs gw, gw + 2048, ...
-    const int njobs = (a.V + 3) / 4;
+    // 2048 compute waves; job round i: 2-row job jidx(i) = SJ i + (this wave's index, rotated over each group of 8
+    // workgroups as in phase A)
+    constexpr int SJ = MK_G * MK_W;
+    auto jidx = [&](int i) __attribute__((always_inline)) {
+      return SJ * i + ((wg & ~7) + ((wg + (MK_ROT ? i : 0)) & 7)) * MK_W + wave;
+    };
+    const int njobs = (a.V + 1) / 2;
     uint32_t lo = (uint32_t)lane * 16u;
     asm volatile("" : "+v"(lo));
     uint64_t* ll = a.ll;
     asm volatile("" : "+s"(ll));
-    u32x4 gc[4], bc[4];
-    load_vec<4>(gc, a.lnf_g, lane);
-    load_vec<4>(bc, a.lnf_b, lane);
-    typedef u32x4 Job[4][4];
-    Job wv0, wv1;  // two 4-row jobs: the next one in flight while one is reduced (static names: no scratch)
-    auto issue = [&](int j, Job& w) {
+    Buf w0, w1;
+    float bj0 = 0.f, bj1 = 0.f;
+    auto issue = [&](Buf& b, float& bj, int j) __attribute__((always_inline)) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t o = (uint32_t)min(4 * j + r, a.V - 1) * (MK_D * 2u) + lo;
+      for (int r = 0; r < 2; r++) {
+        const uint32_t o = (uint32_t)min(2 * j + r, a.V - 1) * (MK_D * 2u) + lo;
 #pragma unroll
-        for (int i = 0; i < 4; i++) w[r][i] = ldw(a.wlm, o + 1024u * i);
+        for (int i = 0; i < 4; i++) b[4 * r + i] = ldw(a.wlm, o + 1024u * i);
       }
+      bj = ldg(a.blm + min(2 * j + (lane >> 5), a.V - 1));
     };
     uint32_t best = 0u;
     u32x4 xc[4];
-    auto reduce_job = [&](int j, const Job& w) {
-      float acc[4];
+    auto job = [&](const Buf& b, float bj, int j) __attribute__((always_inline)) {
+      float acc[2];
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
+      for (int r = 0; r < 2; r++) {
         acc[r] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[r] = dot8(w[r][i], xc[i], acc[r]);
+        for (int i = 0; i < 4; i++) acc[r] = dot8d(b[4 * r + i], xc[i], acc[r]);
       }
-      const int n = 4 * j + (lane >> 4);
-      const float bme = a.blm[min(n, a.V - 1)];
-      const float tot = reduce_rows<4>(acc, lane);
+      const int n = 2 * j + (lane >> 5);
+      const float t0 = wave_total(acc[0]), t1 = wave_total(acc[1]);
+      const float tot = lane < 32 ? t0 : t1;
       if (n < a.V) {
-        const float v = rbf(tot + bme);
-        if (a.logits && (lane & 15) == 0) a.logits[n] = f2bf(v);
+        const float v = rbf(tot + bj);
+        if (a.logits && (lane & 31) == 0) *GLOBAL(uint16_t, a.logits + n) = f2bf(v);
         const uint32_t k = amax_key32(v, n);
         best = k > best ? k : best;
       }
     };
-    constexpr int SJ = MK_G * MK_W;
-    if (gw < njobs) issue(gw, wv0);
-    if (!ll_gather<MK_D / 2>(ll + LL_X, E(NL - 1, 3), xs, err, &s_flag)) return;
-    load_vec<4>(xc, reinterpret_cast<const uint16_t*>(xs), lane);
-    ln_chunks<4>(xc, gc, bc, a.eps, MK_D, lane);
-    for (int j = gw; j < njobs; j += 2 * SJ) {
-      if (j + SJ < njobs) issue(j + SJ, wv1);
-      reduce_job(j, wv0);
-      if (j + SJ < njobs) {
-        if (j + 2 * SJ < njobs) issue(j + 2 * SJ, wv0);
-        reduce_job(j + SJ, wv1);
+    u32x4 gc[4], bc[4];
+    if (!xw) {
+      if (jidx(0) < njobs) issue(w0, bj0, jidx(0));
+      if (jidx(1) < njobs) issue(w1, bj1, jidx(1));
+      load_vec_g<4>(gc, a.lnf_g, lane);
+      load_vec_g<4>(bc, a.lnf_b, lane);
+    } else {
+      xgather<MK_D / 2>(ll + LL_X, E(NL - 1, 3), xs, err, fail);
+    }
+    bar();  // x ready
+    if (!xw) {
+      load_vec<4>(xc, reinterpret_cast<const uint16_t*>(xs), lane);
+      ln_chunks<4, true>(xc, gc, bc, a.eps, MK_D, lane);
+      for (int i = 0; jidx(i) < njobs; i += 2) {
+        job(w0, bj0, jidx(i));
+        __builtin_amdgcn_sched_barrier(0);
+        if (jidx(i + 2) < njobs) issue(w0, bj0, jidx(i + 2));
+        if (jidx(i + 1) < njobs) {
+          job(w1, bj1, jidx(i + 1));
+          __builtin_amdgcn_sched_barrier(0);
+          if (jidx(i + 3) < njobs) issue(w1, bj1, jidx(i + 3));
+        }
       }
-    }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const uint32_t t = __shfl_xor(best, o, 64);
-      best = t > best ? t : best;
+      for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t t = __shfl_xor(best, o, 64);
+        best = t > best ? t : best;
+      }
+      if (lane == 0) sbest[wave] = best;
     }
-    if (lane == 0) sbest[wave] = best;
-    __syncthreads();
-    if (tid == 0) {
+    bar();
+    if (xw && lane == 0) {
       uint32_t b = sbest[0];
 #pragma unroll
       for (int w = 1; w < MK_W; w++) b = sbest[w] > b ? sbest[w] : b;
       st_word(ll + LL_AM + wg, base + 3u * (uint32_t)NL + 1u, b);
     }
   }
-  if (wg != 0) return;
-  // ---- workgroup 0: the token, the bookkeeping of embed_step_kernel, the next embedding, the next epoch base
-  if (!ll_gather<MK_G>(a.ll + LL_AM, base + 3u * (uint32_t)NL + 1u, xs, err, &s_flag)) return;
-  if (tid < 64) {
-    uint32_t b = 0u;
-    for (int i = tid; i < MK_G; i += 64) b = xs[i] > b ? xs[i] : b;
+  if (wg != 0 || !xw) return;
+  // ---- workgroup 0's exchange wave: the token, the bookkeeping of embed_step_kernel, the next embedding, the next
+  // epoch base (every workgroup has read the old ones: their argmax words come after)
+  xgather<MK_G>(a.ll + LL_AM, base + 3u * (uint32_t)NL + 1u, xs, err, fail);
+  uint32_t b = 0u;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const uint32_t t = __shfl_xor(b, o, 64);
-      b = t > b ? t : b;
-    }
-    if (tid == 0) sbest[0] = b;
+  for (int i = 0; i < MK_G / 64; i++) b = xs[lane + 64 * i] > b ? xs[lane + 64 * i] : b;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t t = __shfl_xor(b, o, 64);
+    b = t > b ? t : b;
   }
-  __syncthreads();
-  const int tok = min((int)(0xffffu - (sbest[0] & 0xffffu)), a.V - 1);
-  if (tid == 0) {
+  const int tok = min((int)(0xffffu - (b & 0xffffu)), a.V - 1);
+  if (lane == 0) {
     const int s = a.state[0];
     if (s < a.cap) {
       a.tokens[s] = tok;
       a.state[1] = a.pos_base + s;
       a.state[0] = s + 1;
     }
-    a.ep[0] = base + 3u * (uint32_t)NL + 2u;
+    if (!fail) a.ep[0] = base + 3u * (uint32_t)NL + 2u;
   }
-  for (int i = tid; i < MK_D / 8; i += MK_T)
-    *reinterpret_cast<u32x4*>(a.x + i * 8) = *reinterpret_cast<const u32x4*>(a.wte + (long)tok * MK_D + i * 8);
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    *GLOBAL(u32x4, a.x + (lane + 64 * i) * 8) = ldg_vec(a.wte + (long)tok * MK_D + (lane + 64 * i) * 8);
 }
 
 }  // namespace

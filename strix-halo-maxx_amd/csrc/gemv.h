@@ -19,15 +19,17 @@ __device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc) {
 // LayerNorm of a row held as KC chunks per lane (chunk c = lane + 64 i), with gamma / beta chunks gc / bc loaded by
 // the caller (before its weight rows, so the normalisation need not wait for them): bf16 result in place (torch
 // F.layer_norm numerics: fp32 statistics, biased variance, one rounding).
-template <int KC>
+// (DPP: the wave sums by wave_total, fewer steps than wave_sum's LDS permutes, another fp32 summation order)
+template <int KC, bool DPP = false>
 __device__ __forceinline__ void ln_chunks(u32x4 (&xc)[KC], const u32x4 (&gc)[KC], const u32x4 (&bc)[KC], float eps,
                                           int K, int lane) {
+  auto red = [](float v) { return DPP ? wave_total(v) : wave_sum(v); };
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < KC; i++)
 #pragma unroll
     for (int e = 0; e < 4; e++) s += lo_bf(xc[i][e]) + hi_bf(xc[i][e]);
-  const float mean = wave_sum(s) / (float)K;
+  const float mean = red(s) / (float)K;
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < KC; i++)
@@ -36,7 +38,7 @@ __device__ __forceinline__ void ln_chunks(u32x4 (&xc)[KC], const u32x4 (&gc)[KC]
       const float d0 = lo_bf(xc[i][e]) - mean, d1 = hi_bf(xc[i][e]) - mean;
       ss += d0 * d0 + d1 * d1;
     }
-  const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)K + eps);
+  const float rstd = 1.0f / sqrtf(red(ss) / (float)K + eps);
 #pragma unroll
   for (int i = 0; i < KC; i++) {
     const u32x4 g = gc[i], b = bc[i];
