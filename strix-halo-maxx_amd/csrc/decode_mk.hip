@@ -60,27 +60,48 @@ constexpr int MK_NG = 224, MK_G = MK_NG + MK_H;             // GEMV workgroups, 
 #define MK_GW 8
 #endif
 #ifndef MK_NB
-#define MK_NB 2
+#define MK_NB 5
 #endif
-// GEMV waves hold MK_NB weight units of 4 KB in flight each (~64 KB per CU): about what saturates HBM, and no more.
-// Requests wait behind everything queued ahead of them, the exchanges between workgroups included: with 128 KB per
-// CU in flight a store -> poll round trip takes ~6 us instead of ~3, for no more bandwidth. (MK_GW < 8 runs the GEMV
-// on fewer waves, the others only meet the barriers.)
+// GEMV waves stream 4 KB weight units through a ring of MK_NB register buffers. Within a layer a unit is issued only
+// MK_DIST = 2 slots ahead (~64 KB per CU in flight, about what saturates HBM, and no more): requests wait behind
+// everything queued ahead of them, the exchanges between workgroups included, and with 128 KB per CU in flight a
+// store -> poll round trip takes ~6 us instead of ~3, for no more bandwidth. At the end of a layer, where the next
+// one can only start after the exchange of x, the whole ring is filled with the next layer's first units (MK_PF), so
+// that the stream does not restart from empty. (MK_GW < 8 runs the GEMV on fewer waves, the others only meet the
+// barriers.) Measured, steps per second: ring 2/2/2 1940, 3/2/3 2009, 4/2/4 2058, 5/2/5 2119, 6/2/6 2099, 4/3/4 1887.
 constexpr int GW = MK_GW, NBUF = MK_NB;
+#ifndef MK_DIST
+#define MK_DIST 2
+#endif
+#ifndef MK_PF
+#define MK_PF MK_NB
+#endif
+// Within a layer a unit is issued DIST slots ahead of its use; the first PF units of a layer are issued before its h
+// barrier, at the end of the previous layer (any others up to DIST right after the barrier).
+constexpr int DIST = MK_DIST, PF = MK_PF;
+static_assert(DIST >= 1 && DIST <= NBUF && PF >= 0 && PF <= NBUF, "issue distances within the ring");
 constexpr int MK_NGW = MK_NG * GW;                          // GEMV waves
 constexpr int KA = (MK_NA / 2) / MK_NGW;                    // row pairs per GEMV wave in phase A
 static_assert(KA * MK_NGW * 2 == MK_NA, "whole row pairs per wave");
-constexpr int JB = (4 * 10 + GW - 1) / GW;                  // fc2 quarter-row units per wave (10-row groups)
-constexpr int JC = (10 + GW - 1) / GW;                      // proj rows per wave
-// Slots of the weight ring: [0, SA) phase A, [SA, SA + JB) phase B. Phase C's proj rows go to LDS by DMA at the
-// start of the layer instead (C runs last, when the attention output arrives: rows fetched into the ring only then
-// would add a memory latency to every layer).
-constexpr int SA = 2 * KA, B0 = SA, B1 = SA + JB;
+constexpr int MK_RW = 8;                                    // fc2 / proj rows per workgroup (all 256)
+static_assert(MK_RW * MK_G == MK_D, "the rows split evenly over the workgroups");
+constexpr int JB = (4 * MK_RW + GW - 1) / GW;               // fc2 quarter-row units per wave
+constexpr int JC = (MK_RW + GW - 1) / GW;                   // proj rows per wave
+constexpr int JBA = 4 * MK_RW / MK_W, JCA = MK_RW / MK_W;   // the same in attention workgroups (all 8 waves)
+static_assert(JBA == 4 && JCA == 1, "an attention-workgroup wave takes one whole fc2 row and one proj row");
+// Slots of the weight ring: [0, SA) phase A, [B0, B1) phase B. Phase B is split at the middle of fc2's inputs: its
+// first half [B0, BH) needs g[0, 4096) only, the second [BH, B1) g[4096, 8192). The first half of g is complete a
+// pair round before the end of phase A, so the wait for the second half runs while the first half of B streams.
+// Phase C's proj rows go to LDS by DMA at the start of the layer instead (C runs last, when the attention output
+// arrives: rows fetched into the ring only then would add a memory latency to every layer).
+constexpr int SA = 2 * KA, B0 = SA, B1 = SA + JB, BH = B0 + JB / 2;
+static_assert(JB % 2 == 0, "B splits into two halves");
 constexpr int NSLOT = (B1 + NBUF - 1) / NBUF * NBUF;        // slots per layer (a multiple of the ring depth)
-// Barriers per layer in GEMV workgroups: h ready, phase A done, g ready, a ready, partial sums ready. The exchange
-// wave polls for g only once its own workgroup's phase A is done: 224 workgroups polling 64 sentinels each slow the
-// weight stream of phase A down (the polls share each CU's memory pipeline), and g cannot be complete earlier anyway.
-constexpr int NBAR = 5;
+// Barriers per layer: h ready, phase A done, g1 ready, g2 ready, a ready, partial sums ready (attention workgroups:
+// q / k / v ready and the softmax merged instead of the first two). The exchange wave polls for g only once its own
+// workgroup's phase A is done: 224 workgroups polling 64 sentinels each slow the weight stream of phase A down (the
+// polls share each CU's memory pipeline), and g cannot be complete earlier anyway.
+constexpr int NBAR = 6;
 #ifndef MK_ROT
 #define MK_ROT 1
 #endif
@@ -90,6 +111,12 @@ constexpr int NBAR = 5;
 // workgroup waits for the slowest.
 constexpr int ROT = MK_ROT ? 8 / KA > 0 ? 8 / KA : 1 : 0;
 constexpr int KQ = (MK_NQKV / 2 + MK_NGW - 1) / MK_NGW - 1;  // the last pair round that holds qkv pairs
+constexpr int KG1 = (MK_NQKV / 2 + MK_F / 4 + MK_NGW - 1) / MK_NGW - 1;  // ... that holds pairs of g[0, 4096)
+static_assert(KQ < KG1 && KG1 < KA - 1, "three bursts");
+// fc2 unit j of a wave: half j / (JB / 2) of the inputs, row wave + GW (i / 2) and quarter 2 half + (i & 1) of it
+// (i = j % (JB / 2)): each wave takes whole rows, their first two quarters in B's first half
+__device__ __forceinline__ int b_row(int wave, int j) { return wave + GW * ((j % (JB / 2)) >> 1); }
+__device__ __forceinline__ int b_quarter(int j) { return 2 * (j / (JB / 2)) + (j & 1); }
 // the GEMV wave whose row pairs workgroup wg's wave takes in pair round k
 __device__ __forceinline__ int rot_wave(int wg, int wave, int k) { return ((wg & ~7) + ((wg + ROT * k) & 7)) * GW + wave; }
 constexpr int MK_ROUNDS = 16;                               // key rounds of 8 keys per compute wave: 1024 keys
@@ -130,10 +157,11 @@ __device__ __forceinline__ u32x4 ldw(const uint16_t* base, uint32_t off) {
 // compute wave has in flight stay in flight across it.
 __device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// fc2 / proj rows of GEMV workgroup g: 128 groups of 10 rows, then 96 of 8 (even sizes: pairs stay together)
+// fc2 / proj rows of workgroup g: 8 each, the attention workgroups included (they finish their head before the fc2
+// rows can start, and 2048 rows over the 224 GEMV workgroups alone would leave some with 10 rows, others with 8)
 __device__ __forceinline__ void row_group(int g, int& r0, int& n) {
-  if (g < 128) r0 = 10 * g, n = 10;
-  else r0 = 1280 + 8 * (g - 128), n = 8;
+  r0 = MK_RW * g;
+  n = MK_RW;
 }
 
 struct MkLayer {  // 10 device pointers, in this order (the host builds the table)
@@ -279,7 +307,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t qr[MK_HD], kr[MK_HD];  // roped q, k (bf16)
   __shared__ float rec[MK_W][2 + MK_HD];
   __shared__ __attribute__((aligned(16))) uint32_t hs[MK_D / 2];  // GEMV workgroups: h = LN(x) (bf16 pairs)
-  __shared__ float pb[4 * 10], pc[10];  // GEMV workgroups: fc2 quarter-row and proj partial sums
+  __shared__ float pb[4 * MK_RW], pc[MK_RW];  // fc2 quarter-row and proj partial sums
   __shared__ uint32_t sbest[MK_W];
   __shared__ uint64_t stab[MK_MAXL * 10];
   uint32_t* gs = reinterpret_cast<uint32_t*>(big);
@@ -301,20 +329,29 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
   uint32_t* err = a.ep + 1;
   bool fail = false;  // exchange wave: a wait timed out
 
-  // The exchange wave and the compute waves run separate loops that meet at the same barriers (4 per layer in GEMV
-  // workgroups, 2 in attention workgroups): one loop with both roles as branches would be laid out as one straight
-  // region, both roles' registers live at once.
+  // The exchange wave and the compute waves run separate loops that meet at the same barriers (5 per layer): one
+  // loop with both roles as branches would be laid out as one straight region, both roles' registers live at once.
+  int r0, nr;  // the workgroup's fc2 / proj rows
+  row_group(wg, r0, nr);
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(xs);
+  uint8_t* const pw = big + 24576;  // proj rows of the workgroup (4 KB each), after gs and as2
   if (wg >= MK_NG) {
     // ======================================================================= attention workgroup (one head)
+    // The head's attention, then (V rows no longer needed in LDS) the workgroup's 8 fc2 / proj rows like a GEMV
+    // workgroup's phases B and C.
     const int h = wg - MK_NG;
     if (xw) {
       // ---- exchange wave: q / k / v of the head, rope, output, append
       const int d = lane, jr = (d & 31) >> 1, d0 = d < 32 ? jr : d;
       const float cr = ldg(a.cs + (long)pos * 32 + 2 * jr), sr = ldg(a.cs + (long)pos * 32 + 2 * jr + 1);
+      // x of the workgroup's rows (the residual): the step's input now, this workgroup's own output later
+      if (lane < MK_RW / 2) xs[r0 / 2 + lane] = *GLOBAL(const uint32_t, a.x + r0 + 2 * lane);
       for (int l = 0; l < NL; l++) {
         const MkLayer L = layer_of(stab, l);
         uint64_t* ll = a.ll;  // opaque: the exchange addresses are rebuilt per layer, not hoisted
         asm volatile("" : "+s"(ll));
+        const int ri = r0 + min(lane, nr - 1);
+        const float b2v = ldg(L.b2 + ri), bpv = ldg(L.bp + ri);
         // 96 words: q at h * 32, k at 1024 + h * 32, v at 2048 + h * 32
         if (!fail) {
           const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -366,6 +403,25 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         *GLOBAL(uint16_t, L.kc + ((long)h * a.ctx + pos) * MK_HD + lane) = kapp;
         *GLOBAL(uint16_t, L.vc + ((long)h * a.ctx + pos) * MK_HD + lane) = vapp;
         // rec / qkvh / qr / kr are rewritten only after the next layer's first barrier
+        // ---- the workgroup's fc2 / proj rows (gs, as2 over the V rows: the compute waves are past them)
+        xgather<MK_F / 4>(ll + LL_G, E(l, 1), gs, err, fail);
+        bar();  // g1 ready
+        xgather<MK_F / 4>(ll + LL_G + MK_F / 4, E(l, 1), gs + MK_F / 4, err, fail);
+        bar();  // g2 ready
+        xgather<MK_D / 2>(ll + LL_A, E(l, 2), as2, err, fail);
+        bar();  // a ready
+        bar();  // the partial sums in pb / pc
+        float xn = 0.f;
+        if (lane < nr) {
+          const float y2 = rbf(((pb[4 * lane] + pb[4 * lane + 1]) + (pb[4 * lane + 2] + pb[4 * lane + 3])) + b2v);
+          xn = rbf(y2 + rbf(rbf(pc[lane] + bpv) + bf2f(xb[r0 + lane])));
+        }
+        const float xn1 = __shfl_down(xn, 1, 64);
+        if (lane < nr && !(lane & 1)) {
+          const uint32_t w = pack2(xn, xn1);
+          st_word(ll + LL_X + (r0 + lane) / 2, E(l, 3), w);
+          xs[(r0 + lane) / 2] = w;  // the next layer's residual
+        }
       }
     } else {
       // ---- compute waves: the cached keys 0 .. pos - 1 of the head, K rows into registers and V rows into LDS (row
@@ -455,14 +511,56 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
           for (int e = 0; e < 8; e++) rec[wave][2 + sub * 8 + e] = o[e];
         }
         if (lane == 0) { rec[wave][0] = m; rec[wave][1] = lsum; }
-        bar();  // the 8 waves' (m, l, o) in rec; every V row read (the next layer's V rows may land)
+        bar();  // the 8 waves' (m, l, o) in rec; every V row read
+        // ---- the workgroup's fc2 / proj rows: this wave's quarter rows u = wave + 8 j into registers, its proj row
+        // into LDS (over the V rows, read by now)
+        uint32_t lo = (uint32_t)lane * 16u;
+        asm volatile("" : "+v"(lo));
+        u32x4 wb[JBA][4];
+#pragma unroll
+        for (int j = 0; j < JBA; j++) {  // row r0 + wave, quarter j
+          const uint32_t o = (uint32_t)(r0 + wave) * (MK_F * 2u) + (uint32_t)j * (MK_D * 2u) + lo;
+#pragma unroll
+          for (int i = 0; i < 4; i++) wb[j][i] = ldw(L.w2, o + 1024u * i);
+        }
+#pragma unroll
+        for (int j = 0; j < JCA; j++) {
+          const int u = wave + MK_W * j;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            dma16s(L.wp, (uint32_t)(r0 + u) * (MK_D * 2u) + 1024u * i + lo, lds_off(pw) + (uint32_t)u * 4096u + 1024u * i);
+        }
+#pragma unroll
+        for (int j = 0; j < JBA; j++) {
+          if (j == 0) bar();  // g1 ready
+          if (j == 2) bar();  // g2 ready
+          const uint32_t* gq = gs + j * (MK_D / 2);
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc = dot8d(wb[j][i], *reinterpret_cast<const u32x4*>(&gq[(lane + 64 * i) * 4]), acc);
+          const float t = wave_total(acc);
+          if (lane == 0) pb[4 * wave + j] = t;
+        }
+        bar();  // a ready
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the proj rows have landed
+#pragma unroll
+        for (int j = 0; j < JCA; j++) {
+          const int u = wave + MK_W * j;
+          const uint8_t* pr = pw + u * 4096;
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc = dot8d(*reinterpret_cast<const u32x4*>(pr + (lane + 64 * i) * 16),
+                        *reinterpret_cast<const u32x4*>(&as2[(lane + 64 * i) * 4]), acc);
+          const float t = wave_total(acc);
+          if (lane == 0) pc[u] = t;
+        }
+        bar();  // the partial sums in pb / pc; every read of gs, as2, pw done (the next layer's V rows may land)
       }
     }
   } else {
     // ======================================================================= GEMV workgroup
-    int r0, nr;
-    row_group(wg, r0, nr);
-    const uint16_t* xb = reinterpret_cast<const uint16_t*>(xs);
     if (xw) {
       // ---- exchange wave: x in, h = LN(x) for the compute waves, g and a in, this workgroup's x' rows out
       for (int l = 0; l < NL; l++) {
@@ -488,8 +586,10 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         for (int i = 0; i < 4; i++) reinterpret_cast<u32x4*>(hs)[lane + 64 * i] = xc[i];
         bar();  // h ready
         bar();  // the workgroup's phase A done
-        xgather<MK_F / 2>(ll + LL_G, E(l, 1), gs, err, fail);
-        bar();  // g ready
+        xgather<MK_F / 4>(ll + LL_G, E(l, 1), gs, err, fail);
+        bar();  // g1 ready
+        xgather<MK_F / 4>(ll + LL_G + MK_F / 4, E(l, 1), gs + MK_F / 4, err, fail);
+        bar();  // g2 ready
         xgather<MK_D / 2>(ll + LL_A, E(l, 2), as2, err, fail);
         bar();  // a ready
         bar();  // the partial sums in pb / pc
@@ -511,7 +611,6 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
       // and phase C from LDS: proj row r0 + u (u = wave + GW j < nr) at pw + 4 KB u
       u32x4 buf[NBUF][4];
       float bqr[NBUF];
-      const uint8_t* pw = big + 24576;  // proj rows of the workgroup (10 x 4 KB), after gs and as2
       const uint32_t pwo = lds_off(pw);
       // real = false (the next-layer slots of the last layer): the same loads from the LayerNorm gamma, discarded
       auto issue = [&](auto sc, const MkLayer& L, uint32_t lo, bool real) __attribute__((always_inline)) {
@@ -526,18 +625,19 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         } else if constexpr (s >= B0 && s < B1) {
           // a slot past the workgroup's units reads the LayerNorm gamma (4 KB, in cache) instead: every slot issues
           // the same loads, so the compiler's wait counts stay exact (a conditional load makes them drain everything)
-          const int u = wave + GW * (s - B0);
-          const bool ok = u < 4 * nr;
-          const uint32_t o = ok ? (uint32_t)(r0 + (u >> 2)) * (MK_F * 2u) + (uint32_t)(u & 3) * (MK_D * 2u) + lo : lo;
+          const int rw = b_row(wave, s - B0), q = b_quarter(s - B0);
+          const bool ok = rw < nr;
+          const uint32_t o = ok ? (uint32_t)(r0 + rw) * (MK_F * 2u) + (uint32_t)q * (MK_D * 2u) + lo : lo;
 #pragma unroll
           for (int i = 0; i < 4; i++) b[i] = ldw(ok ? L.w2 : L.ln_g, o + 1024u * i);
         }
       };
       u32x4 hc[4];
       float accE = 0.f, bE = 0.f;  // phase A: the even row of the current pair
-      // The pair words are published in two bursts, one vector store each: after the last round that holds qkv pairs
-      // and at the end of phase A. A store holds back this wave's later waits until it completes (the counter
-      // completes in order), ~2 us at agent scope under load: one per pair would stall the weight stream KA times.
+      // The pair words are published in three bursts, one vector store each: after the last round that holds qkv
+      // pairs, after the last one with pairs of g[0, 4096), and at the end of phase A. A store holds back this wave's
+      // later waits until it completes (the counter completes in order), ~2 us at agent scope under load: one per pair
+      // would stall the weight stream KA times.
       uint32_t wq[KA];
       auto compute = [&](auto sc, uint64_t* ll, uint32_t ep) __attribute__((always_inline)) {
         constexpr int s = decltype(sc)::value;
@@ -558,8 +658,8 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
               vo = rbf(gelu_tanh(vo));
             }
             wq[k] = pack2(ve, vo);
-            if constexpr (k == KQ || k == KA - 1) {  // burst: lane i publishes the word of round k0 + i
-              constexpr int k0 = k == KQ ? 0 : KQ + 1;
+            if constexpr (k == KQ || k == KG1 || k == KA - 1) {  // burst: lane i publishes the word of round k0 + i
+              constexpr int k0 = k == KQ ? 0 : k == KG1 ? KQ + 1 : KG1 + 1;
               uint32_t w = wq[k0];
 #pragma unroll
               for (int j = k0 + 1; j <= k; j++) w = lane == j - k0 ? wq[j] : w;
@@ -568,15 +668,15 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
             }
           }
         } else if constexpr (s >= B0 && s < B1) {
-          const int u = wave + GW * (s - B0);
-          if (u < 4 * nr) {
-            const uint32_t* gq = gs + (u & 3) * (MK_D / 2);
+          const int rw = b_row(wave, s - B0), q = b_quarter(s - B0);
+          if (rw < nr) {
+            const uint32_t* gq = gs + q * (MK_D / 2);
             float acc = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; i++)
               acc = dot8d(b[i], *reinterpret_cast<const u32x4*>(&gq[(lane + 64 * i) * 4]), acc);
             const float t = wave_total(acc);
-            if (lane == 0) pb[u] = t;
+            if (lane == 0) pb[4 * rw + q] = t;
           }
         }
       };
@@ -584,7 +684,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         const MkLayer L0 = layer_of(stab, 0);
         uint32_t lo = (uint32_t)lane * 16u;
         asm volatile("" : "+v"(lo));
-        static_for<NBUF>([&](auto sc) __attribute__((always_inline)) { issue(sc, L0, lo, true); });
+        static_for<PF>([&](auto sc) __attribute__((always_inline)) { issue(sc, L0, lo, true); });
       }
       for (int l = 0; l < NL; l++) {
         const MkLayer L = layer_of(stab, l);
@@ -609,20 +709,31 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         bar();  // h ready
+        static_for<(DIST > PF ? DIST - PF : 0)>([&](auto sc) __attribute__((always_inline)) {
+          issue(std::integral_constant<int, PF + decltype(sc)::value>{}, L, lo, true);
+        });
         load_vec<4>(hc, reinterpret_cast<const uint16_t*>(hs), lane);
         static_for<NSLOT>([&](auto sc) __attribute__((always_inline)) {
           constexpr int s = decltype(sc)::value;
           if constexpr (s == B0) {
             bar();  // phase A done
-            bar();  // g ready
+            bar();  // g1 ready
           }
+          if constexpr (s == BH) bar();  // g2 ready
           compute(sc, ll, E(l, 1));
           // the freed buffer's next unit (sched_barrier: kept after the reduction that frees it; the scheduler would
           // otherwise hoist the loads and need more buffers)
           __builtin_amdgcn_sched_barrier(0);
-          if constexpr (s + NBUF < NSLOT) issue(std::integral_constant<int, s + NBUF>{}, L, lo, true);
-          else issue(std::integral_constant<int, s + NBUF - NSLOT>{}, Ln, lo, more);
+          if constexpr (s + DIST < NSLOT) {
+            if constexpr (s + DIST >= PF) issue(std::integral_constant<int, s + DIST>{}, L, lo, true);
+          } else if constexpr (s + DIST - NSLOT < PF) {
+            issue(std::integral_constant<int, s + DIST - NSLOT>{}, Ln, lo, more);
+          }
           __builtin_amdgcn_sched_barrier(0);
+        });
+        // the next layer's units DIST .. PF - 1 (their buffers are free now)
+        static_for<(PF > DIST ? PF - DIST : 0)>([&](auto sc) __attribute__((always_inline)) {
+          issue(std::integral_constant<int, DIST + decltype(sc)::value>{}, Ln, lo, more);
         });
         bar();  // a ready
         // ---- phase C from LDS
