@@ -167,6 +167,92 @@ def traffic_probe(vt, img, reps=3):
     print("[bench] traffic probe done: " + ", ".join(f"{k}={v[0]}" for k, v in classes.items()), flush=True)
 
 
+def _decoder_for_probe():
+    import torch
+    import strix_halo_maxx_amd.md2text as mt
+    import strix_halo_maxx_amd.synth as S
+    dev = torch.device("cuda:0")
+    dec = mt.TextDecoder(S.text_weights(0), device=dev, ctx=1024)
+    img = S.activations(3, (729, 2048), "img").to(dev)
+    return dec, img, S.prompt_ids(4, 64)
+
+
+def decode_step_bytes(pos):
+    """Algorithmic bytes of one bf16 decode step at position pos: every text weight and the LM head once, and the
+    K / V cache rows 0 .. pos - 1 of every layer (decode_bench's count, at the step's own position)."""
+    import strix_halo_maxx_amd.synth as S
+    c = S.TXT
+    D, F, L, V = c["dim"], c["ff"], c["layers"], c["vocab"]
+    return 2 * L * (3 * D * D + D * D + 2 * D * F) + 2 * V * D + 2 * 2 * L * pos * D
+
+
+def traffic_probe_decode(reps=3):
+    """Eager bf16 decode steps for HBM-traffic counters (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): prefill of
+    730 + 64 tokens and a few warm-up steps, a marker fill of 34567 floats, `reps` one-launch decode steps
+    (mx_decode_step_mk), a marker fill of 45678 floats, then `reps` device copies of 256 MiB for the calibration."""
+    import torch
+    dec, img, prompt = _decoder_for_probe()
+    if not dec.use_mk:
+        raise RuntimeError("the one-launch decode step is not in use on this device")
+    dec.generate(img, prompt, 4)
+    dec.prefill(img, prompt)
+    dec.start_decode()
+    for _ in range(2):
+        dec.decode_step()
+    torch.cuda.synchronize()
+    torch.full((34567,), 1.0, device=img.device)
+    for _ in range(reps):
+        dec.decode_step()
+    torch.cuda.synchronize()
+    torch.full((45678,), 1.0, device=img.device)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=img.device)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    if dec.mk_error():
+        raise RuntimeError(f"one-launch decode step reported error {dec.mk_error()}")
+    print(f"[bench] decode traffic probe done: {reps} steps from position {dec.pos_base + 2}", flush=True)
+
+
+def summarize_traffic_decode(fetch_csv, write_csv, reps=3):
+    """Markdown summary of the two --pmc passes over `bench.py --traffic-probe-decode`: the decode steps sit between
+    the run's last two marker fills, the calibration copies follow the second."""
+    import strix_halo_maxx_amd.synth as S
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        seq = _pmc_sequence(path, counter)
+        fills = [i for i, (k, _) in enumerate(seq) if "FillFunctor" in k]
+        m0, m1 = fills[-2], fills[-1]
+        probe, calib = seq[m0 + 1:m1], seq[m1 + 1:]
+        copies = [v for k, v in calib if "copyBuffer" in k][:reps]  # the first ones: a small read-back follows
+        if len(probe) != reps or len(copies) < reps or any("decode_mk_kernel" not in k for k, _ in probe):
+            raise RuntimeError(f"{counter}: probe dispatches {[k for k, _ in probe]}, {len(copies)} calibration")
+        out[counter] = ([v for _, v in probe], copies)
+    fcal, wcal = (sum(out[c][1]) / reps for c in ("FETCH_SIZE", "WRITE_SIZE"))
+    copy_b = 256 << 20
+    ff, wf = copy_b / (fcal * 1024), copy_b / (wcal * 1024)
+    pos0 = 1 + 729 + 64 + 2  # prefix + prompt, then the two warm-up steps
+    rows = []
+    for i in range(reps):
+        fk, wk = out["FETCH_SIZE"][0][i], out["WRITE_SIZE"][0][i]
+        rd, wr = fk * 1024 * ff, wk * 1024 * wf
+        algo = decode_step_bytes(pos0 + i)
+        rows.append(f"| {i} | {pos0 + i} | {fk:,.1f} | {wk:,.1f} | {rd / 1e6:,.1f} | {wr / 1e6:,.2f} | "
+                    f"{(rd + wr) / 1e6:,.1f} | {algo / 1e6:,.1f} | {(rd + wr) / algo:.3f} |")
+    head = ["| step | position | FETCH_SIZE KiB | WRITE_SIZE KiB | read MB | written MB | traffic MB | algorithmic MB | "
+            "ratio |", "|---|---|---|---|---|---|---|---|---|"]
+    mid = reps // 2
+    fk, wk = out["FETCH_SIZE"][0][mid], out["WRITE_SIZE"][0][mid]
+    blob = {"kernel": "decode_mk_kernel", "position": pos0 + mid, "bytes_per_launch": int(fk * 1024 * ff + wk * 1024 * wf),
+            "algorithmic_bytes": decode_step_bytes(pos0 + mid)}
+    return (f"Calibration (plain copy of 256 MiB = {copy_b:,} B read + the same written): FETCH_SIZE reads "
+            f"{fcal:,.1f} KiB per copy, WRITE_SIZE {wcal:,.1f} KiB. Bytes = FETCH_SIZE x 1024 x {ff:.4f} + "
+            f"WRITE_SIZE x 1024 x {wf:.4f}.\n\n" + "\n".join(head + rows) +
+            "\n\nbench.py reads the JSON block below (`traffic` of the decode roofline):\n\n```json\n" +
+            json.dumps(blob, indent=1) + "\n```\n")
+
+
 def _pmc_sequence(path, counter):
     """[(kernel name, counter value)] per dispatch, in dispatch order, from a rocprofv3 counter_collection CSV."""
     import csv
@@ -316,6 +402,19 @@ def summarize_trace(trace_csv, top=30):
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "vision_tower_b1_hbm_traffic.md")
+DECODE_TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                   "decode_megakernel_hbm_traffic.md")
+
+
+def measured_decode_traffic():
+    """(HBM bytes per one-launch decode step, algorithmic bytes at the same position) from the committed summary of
+    the decode traffic probe, or None."""
+    try:
+        txt = open(DECODE_TRAFFIC_FILE).read()
+        blob = json.loads(txt.split("```json", 1)[1].split("```", 1)[0])
+        return int(blob["bytes_per_launch"]), int(blob["algorithmic_bytes"])
+    except (OSError, IndexError, ValueError, KeyError):
+        return None
 
 
 def measured_traffic(label, sym):
@@ -484,12 +583,17 @@ def decode_bench(steps_tokens=128, w8a8=False):
     ctx_mid = dec.pos_base + steps_tokens // 2
     kvbytes = 2 * 2 * L * ctx_mid * D
     bpt = wbytes + kvbytes
+    traffic = {}
+    mt_ = measured_decode_traffic() if dec.use_mk and not w8a8 else None
+    if mt_:  # counted HBM bytes of one step over its algorithmic bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE)
+        traffic = {"traffic_per_step": mt_[0], "traffic_ratio": round(mt_[0] / mt_[1], 4),
+                   "traffic_source": os.path.relpath(DECODE_TRAFFIC_FILE, os.path.dirname(DECODE_TRAFFIC_FILE) + "/..")}
     return {"prefill_ms": round(t_pre * 1e3, 3), "query_ms": round(t_q * 1e3, 3), "decode_tok_s": round(1.0 / t_dec, 1),
             "decode_ms_per_token": round(t_dec * 1e3, 4), "decode_path": path,
             "decode_tok_s_layer_kernels": round(1.0 / t_layers, 1) if t_layers else None,
             "decode_roofline": {"bound": "hbm", "achieved": round(bpt / t_dec / 1e9, 1), "peak": PEAK_HBM / 1e9,
                                 "unit": "GB/s", "frac": round(bpt / t_dec / PEAK_HBM, 4),
-                                "bytes_per_token": bpt},
+                                "bytes_per_token": bpt, **traffic},
             "workload": "moondream2 text decoder, 24 layers, prefill 730 + 64 tokens, greedy "
                         f"{steps_tokens} tokens, batch 1, one HIP graph per decode step; query_ms: one 32-id "
                         "yes/no query over the 730-token prefix (graph)"
@@ -686,6 +790,10 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="headline tower only (no batch 13 / 256, decoder, TRecViT)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the eager launches that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count (see traffic_probe)")
+    ap.add_argument("--traffic-probe-decode", action="store_true",
+                    help="only the eager one-launch decode steps the --pmc passes count (see traffic_probe_decode)")
+    ap.add_argument("--summarize-traffic-decode", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the traffic summary of two --pmc passes over --traffic-probe-decode")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic summary of two --pmc passes over --traffic-probe (see summarize_traffic)")
     ap.add_argument("--summarize-trace", metavar="TRACE_CSV", help="print a rocprofv3 kernel trace grouped by kernel")
@@ -701,6 +809,9 @@ def main():
     if a.summarize_traffic:
         print(summarize_traffic(*a.summarize_traffic))
         return
+    if a.summarize_traffic_decode:
+        print(summarize_traffic_decode(*a.summarize_traffic_decode))
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (every workload here fits one GPU's "
               "288 GB; the sharding plan is design-only). Run with --gpus 1.", file=sys.stderr)
@@ -710,6 +821,10 @@ def main():
     import strix_halo_maxx_amd.md2 as md2
     import strix_halo_maxx_amd.synth as S
 
+    if a.traffic_probe_decode:
+        with torch.inference_mode():
+            traffic_probe_decode()
+        return
     dev = torch.device("cuda:0")
     w = S.vision_weights(0)
     vt = md2.VisionTower(w, device=dev)
