@@ -552,7 +552,7 @@ def decode_bench(steps_tokens=128, w8a8=False):
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) / (steps_tokens - 1)
     t_dec = time_decode()
-    path = "one launch per step (mx_decode_step_mk)" if dec.use_mk else "per-layer kernels"
+    path = ("one launch per step (mx_decode_step_mk" + ("_i8)" if w8a8 else ")")) if dec.use_mk else "per-layer kernels"
     if dec.mk_error():
         raise RuntimeError(f"one-launch decode step reported error {dec.mk_error()}")
     t_layers = None

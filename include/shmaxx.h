@@ -224,9 +224,9 @@ int mx_gemv_res2_i8(hipStream_t st, const uint16_t* y2, const uint16_t* a, int S
  * md2fast.py:173-198 for one token (LN -> [qkv | fc1] + GELU, rope + K/V append at pos = state[1], attention over
  * keys 0..pos, fc2 / proj and the parallel residual), the final LN + LM head + argmax, and mx_embed_step's
  * bookkeeping (tokens[state[0]] = token, state advanced, x = wte[token]; nothing recorded at state[0] >= cap).
- * layers: nl descriptors of mx_decode_mk_layer_bytes() bytes in device memory, each 10 device pointers {ln gamma,
+ * layers: nl descriptors of mx_decode_mk_layer_bytes() bytes in device memory, each 13 device pointers {ln gamma,
  * ln beta, Wqf = [Wqkv; Wfc1] (14336 x 2048 bf16), bqf (fp32), W2 (2048 x 8192), b2, Wp (2048 x 2048), bp, K cache,
- * V cache (slot 0 of [slot][32][ctx][64])}. logits (V bf16) optional. ll: mx_decode_mk_words() exchange words and
+ * V cache (slot 0 of [slot][32][ctx][64]), and three weight-scale pointers used only by mx_decode_step_mk_i8}. logits (V bf16) optional. ll: mx_decode_mk_words() exchange words and
  * ep: 2 words {epoch base, error}, all zeroed once and owned by one decoder; ep[1] != 0 after a step = a wait timed
  * out (the grid exited; zero ll and ep before the next step). The kernel runs mx_decode_mk_grid() workgroups that
  * must all be resident: it refuses (MX_ESHAPE) a device with fewer CUs, and ctx > 1024 or V > 65536.
@@ -235,6 +235,15 @@ int mx_decode_step_mk(hipStream_t st, const void* layers, int nl, int ctx, const
                       const uint16_t* wlm, const float* blm, int V, const uint16_t* wte, const float* cs, float eps,
                       float scale, uint16_t* x, int* state, int pos_base, int* tokens, int cap, uint16_t* logits,
                       uint64_t* ll, uint32_t* ep);
+/* The same step with the W8A8 text Linears (the reference's default HI8Lin text path, hgemm.py:95-137): each
+ * descriptor's Wqf / W2 / Wp are int8 (the same shapes, one byte per weight, per-row fp32 scales in its last three
+ * pointers sqf, sw2, swp, which must not be null); the LN output, g and the attention output are quantised per token
+ * (tgemm.py:81-91), the int8 dots summed exactly, and each Linear dequantised as ((acc s_x) s_w) + b with GELU on that
+ * fp32 value (i8gemm.hip:181-197); the LM head stays bf16. Replaces the W8A8 per-layer kernel sequence of a step. */
+int mx_decode_step_mk_i8(hipStream_t st, const void* layers, int nl, int ctx, const uint16_t* lnf_g,
+                         const uint16_t* lnf_b, const uint16_t* wlm, const float* blm, int V, const uint16_t* wte,
+                         const float* cs, float eps, float scale, uint16_t* x, int* state, int pos_base, int* tokens,
+                         int cap, uint16_t* logits, uint64_t* ll, uint32_t* ep);
 int mx_decode_mk_words(void);
 int mx_decode_mk_grid(void);
 int mx_decode_mk_layer_bytes(void);

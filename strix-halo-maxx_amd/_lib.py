@@ -57,6 +57,7 @@ SIGNATURES = {
     "mx_decode_attn_fc2_i8": [P, P, P, P, P, I, I, P, F, I, P, P, P, P, P, P, I, P, I],
     "mx_gemv_res2_i8": [P, P, P, I, P, P, P, P, I, P, P, I],
     "mx_decode_step_mk": [P, P, I, I, P, P, P, P, I, P, P, F, F, P, P, I, P, I, P, P, P],
+    "mx_decode_step_mk_i8": [P, P, I, I, P, P, P, P, I, P, P, F, F, P, P, I, P, I, P, P, P],
     "mx_decode_mk_words": [],
     "mx_decode_mk_grid": [],
     "mx_decode_mk_layer_bytes": [],

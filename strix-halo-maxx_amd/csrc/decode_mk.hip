@@ -94,9 +94,19 @@ static_assert(JBA == 4 && JCA == 1, "an attention-workgroup wave takes one whole
 // pair round before the end of phase A, so the wait for the second half runs while the first half of B streams.
 // Phase C's proj rows go to LDS by DMA at the start of the layer instead (C runs last, when the attention output
 // arrives: rows fetched into the ring only then would add a memory latency to every layer).
-constexpr int SA = 2 * KA, B0 = SA, B1 = SA + JB, BH = B0 + JB / 2;
 static_assert(JB % 2 == 0, "B splits into two halves");
-constexpr int NSLOT = (B1 + NBUF - 1) / NBUF * NBUF;        // slots per layer (a multiple of the ring depth)
+// The same ring for the W8A8 form (the reference's default text path: int8 weight rows with fp32 per-row scales,
+// activations quantised per token): a 4 KB unit is then a phase-A row pair or half an fc2 row, and phase B cannot be
+// split (g's quantisation scale is its maximum over all 8192 values).
+template <bool I8>
+struct RingCfg {
+  static constexpr int SA = I8 ? KA : 2 * KA;                 // phase-A slots
+  static constexpr int NB = I8 ? 2 * MK_RW / GW : JB;          // phase-B units per wave
+  static constexpr int B0 = SA, B1 = SA + NB, BH = I8 ? B0 : B0 + NB / 2;
+  static constexpr int NSLOT = (B1 + NBUF - 1) / NBUF * NBUF;  // slots per layer (a multiple of the ring depth)
+};
+static_assert(2 * MK_RW % GW == 0, "whole int8 fc2 half rows per wave");
+static_assert(GW == 8, "the W8A8 form quantises with every wave of the workgroup: no idle waves");
 // Barriers per layer: h ready, phase A done, g1 ready, g2 ready, a ready, partial sums ready (attention workgroups:
 // q / k / v ready and the softmax merged instead of the first two). The exchange wave polls for g only once its own
 // workgroup's phase A is done: 224 workgroups polling 64 sentinels each slow the weight stream of phase A down (the
@@ -122,6 +132,7 @@ __device__ __forceinline__ int rot_wave(int wg, int wave, int k) { return ((wg &
 constexpr int MK_ROUNDS = 16;                               // key rounds of 8 keys per compute wave: 1024 keys
 constexpr int MK_MAXKEYS = MK_ROUNDS * 8 * MK_W;
 constexpr int MK_MAXL = 32;                                 // layers the LDS copy of the layer table holds
+constexpr int MK_LP = 13;                                   // pointers per layer descriptor
 
 // exchange words (uint64): layout of the LL area
 constexpr int LL_X = 0, LL_QKV = 1024, LL_G = 4096, LL_A = 8192, LL_AM = 9216, LL_WORDS = 9216 + MK_G;
@@ -164,15 +175,16 @@ __device__ __forceinline__ void row_group(int g, int& r0, int& n) {
   n = MK_RW;
 }
 
-struct MkLayer {  // 10 device pointers, in this order (the host builds the table)
+struct MkLayer {  // 13 device pointers, in this order (the host builds the table)
   const uint16_t *ln_g, *ln_b;  // LayerNorm (2048)
-  const uint16_t* wqf;          // [6144 + 8192][2048]: qkv rows then fc1 rows
+  const uint16_t* wqf;          // [6144 + 8192][2048]: qkv rows then fc1 rows (int8 in the W8A8 form)
   const float* bqf;
-  const uint16_t* w2;           // [2048][8192]
+  const uint16_t* w2;           // [2048][8192] (int8)
   const float* b2;
-  const uint16_t* wp;           // [2048][2048]
+  const uint16_t* wp;           // [2048][2048] (int8)
   const float* bp;
   uint16_t *kc, *vc;            // [32][ctx][64] (cache slot 0)
+  const float *sqf, *sw2, *swp; // W8A8: per-row weight scales of wqf, w2, wp (unused in the bf16 form)
 };
 
 struct MkArgs {
@@ -194,10 +206,10 @@ struct MkArgs {
 // Layer l's descriptor from the LDS copy of the table, every pointer made wave-uniform (SGPRs): read from global memory
 // inside the loop they would be vector loads, whose waits (in order with the weight stream) would drain it.
 __device__ __forceinline__ MkLayer layer_of(const uint64_t* tab, int l) {
-  uint64_t v[10];
+  uint64_t v[MK_LP];
 #pragma unroll
-  for (int i = 0; i < 10; i++) {
-    const uint64_t t = tab[l * 10 + i];
+  for (int i = 0; i < MK_LP; i++) {
+    const uint64_t t = tab[l * MK_LP + i];
     v[i] = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(t >> 32)) << 32) |
            (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)t);
   }
@@ -218,6 +230,125 @@ __device__ __forceinline__ float dot8d(u32x4 w, u32x4 x, float acc) {
     acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, we), __builtin_bit_cast(bf16x2, xe), acc, false);
   }
   return acc;
+}
+
+// 16 int8 x int8 products (one 16-byte chunk of a weight row and of the quantised activation), added to acc exactly.
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int dot16_i8(u32x4 a, u32x4 w, int acc) {
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const uint32_t ae = a[e], we = w[e];
+    acc = __builtin_amdgcn_sdot4((int)ae, (int)we, acc, false);
+  }
+  return acc;
+}
+// Exact int32 sum over the wave (the DPP pattern of wave_total), returned wave-uniform.
+__device__ __forceinline__ int wave_total_i(int v) {
+  auto mv = [](int old, int x, auto ctrl, auto rm) __attribute__((always_inline)) {
+    return __builtin_amdgcn_update_dpp(old, x, decltype(ctrl)::value, decltype(rm)::value, 0xf, false);
+  };
+  using std::integral_constant;
+  v += mv(0, v, integral_constant<int, 0xb1>{}, integral_constant<int, 0xf>{});
+  v += mv(0, v, integral_constant<int, 0x4e>{}, integral_constant<int, 0xf>{});
+  v += mv(0, v, integral_constant<int, 0x141>{}, integral_constant<int, 0xf>{});
+  v += mv(0, v, integral_constant<int, 0x140>{}, integral_constant<int, 0xf>{});
+  v += mv(0, v, integral_constant<int, 0x142>{}, integral_constant<int, 0xa>{});
+  v += mv(0, v, integral_constant<int, 0x143>{}, integral_constant<int, 0xc>{});
+  return __builtin_amdgcn_readlane(v, 63);
+}
+// Per-token int8 quantisation of a bf16 vector held by one wave, NC chunks of 8 values per lane (chunk c = lane +
+// 64 i at src word 4 c): s = max(max |x|, 1e-5) / 127, q = trunc(x / s + 0.5 sign) with the IEEE quotient
+// (tgemm.py:81-91 _quant_rows, decode.hip's quant_vals_block_i8); q of chunk c to dst bytes 8 c .. 8 c + 7. Returns s
+// (wave-uniform). One wave quantises up to 8192 values here, so the quotient is taken as x * (1 / s), within 1.5e-5
+// of x / s for |x / s| <= 127 (two roundings of 2^-24 relative); only where |t| + 0.5 lies within 1e-4 of an integer
+// could that change the truncated result, and there the exact quotient decides. The q values are those of the IEEE
+// division.
+// 8 values of a bf16 chunk quantised with scale s (rs = 1 / s) into two words; near: set where the multiply form's
+// |t| + 0.5 lies within 1e-4 of an integer (exact = true takes the IEEE quotient instead)
+__device__ __forceinline__ uint2 qpack_i8(const u32x4& v, float s, float rs, bool exact, bool& near) {
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const uint32_t ve = v[e >> 1];
+    const float x = (e & 1) ? hi_bf(ve) : lo_bf(ve);
+    const float t = exact ? x / s : x * rs;
+    const float u = fabsf(t) + 0.5f, fr = u - truncf(u);
+    near |= fr < 1e-4f || fr > 1.0f - 1e-4f;
+    const int qi = (int)(t + (t >= 0.f ? 0.5f : -0.5f));
+    w[e >> 2] |= ((uint32_t)qi & 0xffu) << (8 * (e & 3));
+  }
+  return make_uint2(w[0], w[1]);
+}
+template <int NC>
+__device__ __forceinline__ float quant_wave_i8(const uint32_t* src, uint32_t* dst, int lane) {
+  float amax = 0.f;
+#pragma unroll 4
+  for (int i = 0; i < NC; i++) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(&src[4 * (lane + 64 * i)]);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t ve = v[e];
+      amax = fmaxf(amax, fmaxf(fabsf(lo_bf(ve)), fabsf(hi_bf(ve))));
+    }
+  }
+  const float s = fmaxf(wave_max(amax), 1e-5f) / 127.0f;
+  const float rs = 1.0f / s;
+#pragma unroll 4
+  for (int i = 0; i < NC; i++) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(&src[4 * (lane + 64 * i)]);
+    bool near = false;
+    uint2 q = qpack_i8(v, s, rs, false, near);
+    if (__any(near)) {  // wave-uniform and rare: the chunk again with the IEEE quotient
+      bool unused = false;
+      q = qpack_i8(v, s, rs, true, unused);
+    }
+    *reinterpret_cast<uint2*>(&dst[2 * (lane + 64 * i)]) = q;
+  }
+  return s;
+}
+
+// The same quantisation by all the workgroup's waves (every wave calls it at the same point; it holds two barriers):
+// one wave alone spends ~6 us on 8192 values, the workgroup ~0.6 us. red: one float per wave.
+template <int NCH>
+__device__ __forceinline__ float quant_block_i8(const uint32_t* src, uint32_t* dst, float* red, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+  float amax = 0.f;
+#pragma unroll
+  for (int c0 = 0; c0 < NCH; c0 += MK_T) {
+    const int c = c0 + tid;
+    if (c < NCH) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&src[4 * c]);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t ve = v[e];
+        amax = fmaxf(amax, fmaxf(fabsf(lo_bf(ve)), fabsf(hi_bf(ve))));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  if (lane == 0) red[wave] = amax;
+  bar();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < MK_W + 1; w++) m = fmaxf(m, red[w]);
+  const float s = fmaxf(m, 1e-5f) / 127.0f;
+  const float rs = 1.0f / s;
+#pragma unroll
+  for (int c0 = 0; c0 < NCH; c0 += MK_T) {
+    const int c = c0 + tid;
+    if (c < NCH) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&src[4 * c]);
+      bool near = false;
+      uint2 q = qpack_i8(v, s, rs, false, near);
+      if (__any(near)) {
+        bool unused = false;
+        q = qpack_i8(v, s, rs, true, unused);
+      }
+      *reinterpret_cast<uint2*>(&dst[2 * c]) = q;
+    }
+  }
+  bar();
+  return s;
 }
 
 __device__ __forceinline__ uint32_t amax_key32(float v, int idx) {
@@ -299,7 +430,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 typedef u32x4 Buf[8];  // one unit in flight: 2 rows x 4 chunks, a half fc2 row (8 chunks) or a proj row (4)
 
+template <bool I8>
 __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
+  using RC = RingCfg<I8>;
+  constexpr int SA = RC::SA, B0 = RC::B0, B1 = RC::B1, BH = RC::BH, NSLOT = RC::NSLOT;
   __shared__ __attribute__((aligned(16))) uint32_t xs[MK_D / 2];  // x: the layer's input (bf16 pairs)
   // GEMV workgroups: g (fc1 output, 16 KB) then the attention output a (4 KB); attention workgroups: V rows (128 KB)
   __shared__ __attribute__((aligned(1024))) uint8_t big[MK_MAXKEYS * MK_HD * 2];
@@ -309,9 +443,14 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t hs[MK_D / 2];  // GEMV workgroups: h = LN(x) (bf16 pairs)
   __shared__ float pb[4 * MK_RW], pc[MK_RW];  // fc2 quarter-row and proj partial sums
   __shared__ uint32_t sbest[MK_W];
-  __shared__ uint64_t stab[MK_MAXL * 10];
+  __shared__ uint64_t stab[MK_MAXL * MK_LP];
+  __shared__ __attribute__((aligned(16))) uint32_t hq[MK_D / 4];  // W8A8: h quantised (int8)
+  __shared__ float qred[MK_W + 1];                                // W8A8: per-wave maxima of a quantisation
+  __shared__ int pbi[2 * MK_RW], pci[MK_RW];                      // W8A8: fc2 half-row and proj int32 sums
   uint32_t* gs = reinterpret_cast<uint32_t*>(big);
   uint32_t* as2 = gs + MK_F / 2;
+  uint32_t* gq = reinterpret_cast<uint32_t*>(big + 65536);  // W8A8: g quantised (8 KB)
+  uint32_t* aq = reinterpret_cast<uint32_t*>(big + 73728);  // W8A8: a quantised (2 KB)
 
   // wave-uniform by construction (readfirstlane): the compute / exchange split is a branch, not a predication that
   // would keep both sides' registers live at once
@@ -320,7 +459,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
   // The exchange wave issues first when it competes with the compute waves (its polls and publishes are what the
   // other workgroups wait for): ~5% per step.
   if (xw) __builtin_amdgcn_s_setprio(3);
-  for (int i = tid; i < a.nl * 10; i += MK_T) stab[i] = reinterpret_cast<const uint64_t*>(a.layers)[i];
+  for (int i = tid; i < a.nl * MK_LP; i += MK_T) stab[i] = reinterpret_cast<const uint64_t*>(a.layers)[i];
   __syncthreads();
   const uint32_t base = a.ep[0];
   const int pos = min(max(a.state[1], 0), a.ctx - 1);  // the new token's position (its cached keys: rows 0 .. pos - 1)
@@ -334,7 +473,8 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
   int r0, nr;  // the workgroup's fc2 / proj rows
   row_group(wg, r0, nr);
   const uint16_t* xb = reinterpret_cast<const uint16_t*>(xs);
-  uint8_t* const pw = big + 24576;  // proj rows of the workgroup (4 KB each), after gs and as2
+  uint8_t* const pw = big + 24576;  // proj rows of the workgroup (4 KB each, 2 KB int8), after gs and as2
+  constexpr uint32_t PROW = I8 ? MK_D : 2 * MK_D;  // bytes of a proj row
   if (wg >= MK_NG) {
     // ======================================================================= attention workgroup (one head)
     // The head's attention, then (V rows no longer needed in LDS) the workgroup's 8 fc2 / proj rows like a GEMV
@@ -352,6 +492,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         asm volatile("" : "+s"(ll));
         const int ri = r0 + min(lane, nr - 1);
         const float b2v = ldg(L.b2 + ri), bpv = ldg(L.bp + ri);
+        const float sw2v = I8 ? ldg(L.sw2 + ri) : 0.f, swpv = I8 ? ldg(L.swp + ri) : 0.f;
         // 96 words: q at h * 32, k at 1024 + h * 32, v at 2048 + h * 32
         if (!fail) {
           const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -405,16 +546,24 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         // rec / qkvh / qr / kr are rewritten only after the next layer's first barrier
         // ---- the workgroup's fc2 / proj rows (gs, as2 over the V rows: the compute waves are past them)
         xgather<MK_F / 4>(ll + LL_G, E(l, 1), gs, err, fail);
-        bar();  // g1 ready
+        if (!I8) bar();  // g1 ready
         xgather<MK_F / 4>(ll + LL_G + MK_F / 4, E(l, 1), gs + MK_F / 4, err, fail);
-        bar();  // g2 ready
+        float sg = 0.f, sa = 0.f;
+        bar();  // g2 ready (W8A8: g gathered, then quantised by all waves)
+        if (I8) sg = quant_block_i8<MK_F / 8>(gs, gq, qred, tid);
         xgather<MK_D / 2>(ll + LL_A, E(l, 2), as2, err, fail);
+        if (I8) sa = quant_wave_i8<MK_D / 512>(as2, aq, lane);  // alone: the compute waves are in phase B
         bar();  // a ready
         bar();  // the partial sums in pb / pc
         float xn = 0.f;
         if (lane < nr) {
-          const float y2 = rbf(((pb[4 * lane] + pb[4 * lane + 1]) + (pb[4 * lane + 2] + pb[4 * lane + 3])) + b2v);
-          xn = rbf(y2 + rbf(rbf(pc[lane] + bpv) + bf2f(xb[r0 + lane])));
+          if (I8) {
+            const float y2 = rbf(((float)(pbi[2 * lane] + pbi[2 * lane + 1]) * sg) * sw2v + b2v);
+            xn = rbf(y2 + rbf(rbf(((float)pci[lane] * sa) * swpv + bpv) + bf2f(xb[r0 + lane])));
+          } else {
+            const float y2 = rbf(((pb[4 * lane] + pb[4 * lane + 1]) + (pb[4 * lane + 2] + pb[4 * lane + 3])) + b2v);
+            xn = rbf(y2 + rbf(rbf(pc[lane] + bpv) + bf2f(xb[r0 + lane])));
+          }
         }
         const float xn1 = __shfl_down(xn, 1, 64);
         if (lane < nr && !(lane & 1)) {
@@ -512,14 +661,15 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         }
         if (lane == 0) { rec[wave][0] = m; rec[wave][1] = lsum; }
         bar();  // the 8 waves' (m, l, o) in rec; every V row read
-        // ---- the workgroup's fc2 / proj rows: this wave's quarter rows u = wave + 8 j into registers, its proj row
-        // into LDS (over the V rows, read by now)
+        // ---- the workgroup's fc2 / proj rows: this wave's row r0 + wave of fc2 into registers (4 KB units: quarters,
+        // or int8 halves), its proj row into LDS (over the V rows, read by now)
         uint32_t lo = (uint32_t)lane * 16u;
         asm volatile("" : "+v"(lo));
-        u32x4 wb[JBA][4];
+        constexpr int NU = I8 ? 2 : JBA;
+        u32x4 wb[NU][4];
 #pragma unroll
-        for (int j = 0; j < JBA; j++) {  // row r0 + wave, quarter j
-          const uint32_t o = (uint32_t)(r0 + wave) * (MK_F * 2u) + (uint32_t)j * (MK_D * 2u) + lo;
+        for (int j = 0; j < NU; j++) {
+          const uint32_t o = (uint32_t)(r0 + wave) * (I8 ? MK_F : MK_F * 2u) + (uint32_t)j * 4096u + lo;
 #pragma unroll
           for (int i = 0; i < 4; i++) wb[j][i] = ldw(L.w2, o + 1024u * i);
         }
@@ -527,34 +677,58 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         for (int j = 0; j < JCA; j++) {
           const int u = wave + MK_W * j;
 #pragma unroll
-          for (int i = 0; i < 4; i++)
-            dma16s(L.wp, (uint32_t)(r0 + u) * (MK_D * 2u) + 1024u * i + lo, lds_off(pw) + (uint32_t)u * 4096u + 1024u * i);
+          for (int i = 0; i < (int)PROW / 1024; i++)
+            dma16s(L.wp, (uint32_t)(r0 + u) * PROW + 1024u * i + lo, lds_off(pw) + (uint32_t)u * PROW + 1024u * i);
         }
+        if constexpr (I8) {
+          bar();  // g gathered
+          quant_block_i8<MK_F / 8>(gs, gq, qred, tid);
 #pragma unroll
-        for (int j = 0; j < JBA; j++) {
-          if (j == 0) bar();  // g1 ready
-          if (j == 2) bar();  // g2 ready
-          const uint32_t* gq = gs + j * (MK_D / 2);
-          float acc = 0.f;
+          for (int j = 0; j < NU; j++) {  // half j of the row
+            int acc = 0;
 #pragma unroll
-          for (int i = 0; i < 4; i++)
-            acc = dot8d(wb[j][i], *reinterpret_cast<const u32x4*>(&gq[(lane + 64 * i) * 4]), acc);
-          const float t = wave_total(acc);
-          if (lane == 0) pb[4 * wave + j] = t;
+            for (int i = 0; i < 4; i++)
+              acc = dot16_i8(*reinterpret_cast<const u32x4*>(&gq[j * 1024 + 4 * (lane + 64 * i)]), wb[j][i], acc);
+            const int t = wave_total_i(acc);
+            if (lane == 0) pbi[2 * wave + j] = t;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < NU; j++) {
+            if (j == 0) bar();  // g1 ready
+            if (j == 2) bar();  // g2 ready
+            const uint32_t* gh = gs + j * (MK_D / 2);
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              acc = dot8d(wb[j][i], *reinterpret_cast<const u32x4*>(&gh[(lane + 64 * i) * 4]), acc);
+            const float t = wave_total(acc);
+            if (lane == 0) pb[4 * wave + j] = t;
+          }
         }
         bar();  // a ready
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the proj rows have landed
 #pragma unroll
         for (int j = 0; j < JCA; j++) {
           const int u = wave + MK_W * j;
-          const uint8_t* pr = pw + u * 4096;
-          float acc = 0.f;
+          const uint8_t* pr = pw + u * PROW;
+          if constexpr (I8) {
+            int acc = 0;
 #pragma unroll
-          for (int i = 0; i < 4; i++)
-            acc = dot8d(*reinterpret_cast<const u32x4*>(pr + (lane + 64 * i) * 16),
-                        *reinterpret_cast<const u32x4*>(&as2[(lane + 64 * i) * 4]), acc);
-          const float t = wave_total(acc);
-          if (lane == 0) pc[u] = t;
+            for (int i = 0; i < 2; i++)
+              acc = dot16_i8(*reinterpret_cast<const u32x4*>(&aq[4 * (lane + 64 * i)]),
+                             *reinterpret_cast<const u32x4*>(pr + (lane + 64 * i) * 16), acc);
+            const int t = wave_total_i(acc);
+            if (lane == 0) pci[u] = t;
+          } else {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              acc = dot8d(*reinterpret_cast<const u32x4*>(pr + (lane + 64 * i) * 16),
+                          *reinterpret_cast<const u32x4*>(&as2[(lane + 64 * i) * 4]), acc);
+            const float t = wave_total(acc);
+            if (lane == 0) pc[u] = t;
+          }
         }
         bar();  // the partial sums in pb / pc; every read of gs, as2, pw done (the next layer's V rows may land)
       }
@@ -573,6 +747,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         load_vec_g<4>(bc, L.ln_b, lane);
         const int ri = r0 + min(lane, nr - 1);
         const float b2v = ldg(L.b2 + ri), bpv = ldg(L.bp + ri);
+        const float sw2v = I8 ? ldg(L.sw2 + ri) : 0.f, swpv = I8 ? ldg(L.swp + ri) : 0.f;
         if (l == 0) {
           load_vec_g<4>(xc, a.x, lane);
 #pragma unroll
@@ -584,20 +759,30 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         ln_chunks<4, true>(xc, gc, bc, a.eps, MK_D, lane);
 #pragma unroll
         for (int i = 0; i < 4; i++) reinterpret_cast<u32x4*>(hs)[lane + 64 * i] = xc[i];
-        bar();  // h ready
+        bar();  // h ready (W8A8: then quantised by all waves, shared by qkv and fc1, md2fast.py:174)
+        if (I8) quant_block_i8<MK_D / 8>(hs, hq, qred, tid);
         bar();  // the workgroup's phase A done
         xgather<MK_F / 4>(ll + LL_G, E(l, 1), gs, err, fail);
-        bar();  // g1 ready
+        if (!I8) bar();  // g1 ready
         xgather<MK_F / 4>(ll + LL_G + MK_F / 4, E(l, 1), gs + MK_F / 4, err, fail);
-        bar();  // g2 ready
+        float sg = 0.f, sa = 0.f;
+        bar();  // g2 ready (W8A8: g gathered, then quantised by all waves)
+        if (I8) sg = quant_block_i8<MK_F / 8>(gs, gq, qred, tid);
         xgather<MK_D / 2>(ll + LL_A, E(l, 2), as2, err, fail);
+        if (I8) sa = quant_wave_i8<MK_D / 512>(as2, aq, lane);  // alone: the compute waves are in phase B
         bar();  // a ready
         bar();  // the partial sums in pb / pc
-        // x'[n] = bf16(y2[n] + bf16(bf16(a Wp^T + bp)[n] + x[n])), y2 = bf16(g W2^T + b2): row r0 + lane
+        // x'[n] = bf16(y2[n] + bf16(bf16(a Wp^T + bp)[n] + x[n])), y2 = bf16(g W2^T + b2): row r0 + lane (W8A8: each
+        // Linear's fp32 dequant ((acc s_act) s_w) + b rounded once, i8gemm.hip:181-197)
         float xn = 0.f;
         if (lane < nr) {
-          const float y2 = rbf(((pb[4 * lane] + pb[4 * lane + 1]) + (pb[4 * lane + 2] + pb[4 * lane + 3])) + b2v);
-          xn = rbf(y2 + rbf(rbf(pc[lane] + bpv) + bf2f(xb[r0 + lane])));
+          if (I8) {
+            const float y2 = rbf(((float)(pbi[2 * lane] + pbi[2 * lane + 1]) * sg) * sw2v + b2v);
+            xn = rbf(y2 + rbf(rbf(((float)pci[lane] * sa) * swpv + bpv) + bf2f(xb[r0 + lane])));
+          } else {
+            const float y2 = rbf(((pb[4 * lane] + pb[4 * lane + 1]) + (pb[4 * lane + 2] + pb[4 * lane + 3])) + b2v);
+            xn = rbf(y2 + rbf(rbf(pc[lane] + bpv) + bf2f(xb[r0 + lane])));
+          }
         }
         const float xn1 = __shfl_down(xn, 1, 64);
         if (lane < nr && !(lane & 1)) st_word(ll + LL_X + (r0 + lane) / 2, E(l, 3), pack2(xn, xn1));
@@ -610,13 +795,27 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
       //   slots [B0, B1): phase B, unit u = wave + GW (s - B0) < 4 nr: quarter u % 4 of fc2 row r0 + u / 4
       // and phase C from LDS: proj row r0 + u (u = wave + GW j < nr) at pw + 4 KB u
       u32x4 buf[NBUF][4];
-      float bqr[NBUF];
+      float bqr[NBUF], bqr2[NBUF], sqr[NBUF], sqr2[NBUF];  // phase A: the unit's biases (W8A8: both rows', and scales)
       const uint32_t pwo = lds_off(pw);
       // real = false (the next-layer slots of the last layer): the same loads from the LayerNorm gamma, discarded
       auto issue = [&](auto sc, const MkLayer& L, uint32_t lo, bool real) __attribute__((always_inline)) {
         constexpr int s = decltype(sc)::value;
         u32x4(&b)[4] = buf[s % NBUF];
-        if constexpr (s < SA) {
+        if constexpr (I8 && s < SA) {  // the row pair of round s: 2 x 2 KB, rows 2 p, 2 p + 1
+          const int p = rot_wave(wg, wave, s) + s * MK_NGW;
+          const uint32_t o = real ? (uint32_t)p * (MK_D * 2u) + lo : lo;
+#pragma unroll
+          for (int i = 0; i < 4; i++) b[i] = ldw(real ? L.wqf : L.ln_g, o + 1024u * i);
+          bqr[s % NBUF] = ldg(L.bqf + 2 * p);
+          bqr2[s % NBUF] = ldg(L.bqf + 2 * p + 1);
+          sqr[s % NBUF] = ldg(L.sqf + 2 * p);
+          sqr2[s % NBUF] = ldg(L.sqf + 2 * p + 1);
+        } else if constexpr (I8 && s >= B0 && s < B1) {  // half u & 1 of int8 fc2 row r0 + u / 2
+          const int u = wave + GW * (s - B0);
+          const uint32_t o = (uint32_t)(r0 + (u >> 1)) * (uint32_t)MK_F + (uint32_t)(u & 1) * 4096u + lo;
+#pragma unroll
+          for (int i = 0; i < 4; i++) b[i] = ldw(L.w2, o + 1024u * i);
+        } else if constexpr (s < SA) {
           const int row = 2 * (rot_wave(wg, wave, s >> 1) + (s >> 1) * MK_NGW) + (s & 1);
           const uint32_t o = real ? (uint32_t)row * (MK_D * 2u) + lo : lo;
 #pragma unroll
@@ -639,10 +838,45 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
       // later waits until it completes (the counter completes in order), ~2 us at agent scope under load: one per pair
       // would stall the weight stream KA times.
       uint32_t wq[KA];
+      u32x4 hqv[2];  // W8A8: this lane's chunks (16 int8 each) of the quantised h
+      float sh = 0.f;
+      // the burst that ends with pair round k (lane i publishes the word of round k0 + i)
+      auto burst = [&](auto kc, uint64_t* ll, uint32_t ep) __attribute__((always_inline)) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k == KQ || k == KG1 || k == KA - 1) {
+          constexpr int k0 = k == KQ ? 0 : k == KG1 ? KQ + 1 : KG1 + 1;
+          uint32_t w = wq[k0];
+#pragma unroll
+          for (int j = k0 + 1; j <= k; j++) w = lane == j - k0 ? wq[j] : w;
+          const int kl = k0 + lane;
+          if (lane <= k - k0) st_word(ll + LL_QKV + rot_wave(wg, wave, kl) + kl * MK_NGW, ep, w);
+        }
+      };
       auto compute = [&](auto sc, uint64_t* ll, uint32_t ep) __attribute__((always_inline)) {
         constexpr int s = decltype(sc)::value;
         const u32x4(&b)[4] = buf[s % NBUF];
-        if constexpr (s < SA) {
+        if constexpr (I8 && s < SA) {  // the pair: exact int32 sums, dequant ((acc s_h) s_w) + b, GELU on fc1 rows
+          const int p = rot_wave(wg, wave, s) + s * MK_NGW;
+          int a0 = dot16_i8(hqv[0], b[0], 0), a1 = dot16_i8(hqv[0], b[2], 0);
+          a0 = dot16_i8(hqv[1], b[1], a0);
+          a1 = dot16_i8(hqv[1], b[3], a1);
+          float ve = ((float)wave_total_i(a0) * sh) * sqr[s % NBUF] + bqr[s % NBUF];
+          float vo = ((float)wave_total_i(a1) * sh) * sqr2[s % NBUF] + bqr2[s % NBUF];
+          if (2 * p >= MK_NQKV) {
+            ve = gelu_tanh(ve);
+            vo = gelu_tanh(vo);
+          }
+          wq[s] = pack2(ve, vo);
+          burst(std::integral_constant<int, s>{}, ll, ep);
+        } else if constexpr (I8 && s >= B0 && s < B1) {
+          const int u = wave + GW * (s - B0);
+          int acc = 0;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc = dot16_i8(*reinterpret_cast<const u32x4*>(&gq[(u & 1) * 1024 + 4 * (lane + 64 * i)]), b[i], acc);
+          const int t = wave_total_i(acc);
+          if (lane == 0) pbi[u] = t;  // row u / 2, half u & 1
+        } else if constexpr (s < SA) {
           float acc = 0.f;
 #pragma unroll
           for (int i = 0; i < 4; i++) acc = dot8d(b[i], hc[i], acc);
@@ -658,14 +892,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
               vo = rbf(gelu_tanh(vo));
             }
             wq[k] = pack2(ve, vo);
-            if constexpr (k == KQ || k == KG1 || k == KA - 1) {  // burst: lane i publishes the word of round k0 + i
-              constexpr int k0 = k == KQ ? 0 : k == KG1 ? KQ + 1 : KG1 + 1;
-              uint32_t w = wq[k0];
-#pragma unroll
-              for (int j = k0 + 1; j <= k; j++) w = lane == j - k0 ? wq[j] : w;
-              const int kl = k0 + lane;
-              if (lane <= k - k0) st_word(ll + LL_QKV + rot_wave(wg, wave, kl) + kl * MK_NGW, ep, w);
-            }
+            burst(std::integral_constant<int, k>{}, ll, ep);
           }
         } else if constexpr (s >= B0 && s < B1) {
           const int rw = b_row(wave, s - B0), q = b_quarter(s - B0);
@@ -703,8 +930,8 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
           const int u = wave + GW * j;
           if (u < nr) {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-              dma16s(L.wp, (uint32_t)(r0 + u) * (MK_D * 2u) + 1024u * i + lo, pwo + (uint32_t)u * 4096u + 1024u * i);
+            for (int i = 0; i < (int)PROW / 1024; i++)
+              dma16s(L.wp, (uint32_t)(r0 + u) * PROW + 1024u * i + lo, pwo + (uint32_t)u * PROW + 1024u * i);
           }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -712,14 +939,21 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         static_for<(DIST > PF ? DIST - PF : 0)>([&](auto sc) __attribute__((always_inline)) {
           issue(std::integral_constant<int, PF + decltype(sc)::value>{}, L, lo, true);
         });
-        load_vec<4>(hc, reinterpret_cast<const uint16_t*>(hs), lane);
+        if constexpr (I8) {
+          sh = quant_block_i8<MK_D / 8>(hs, hq, qred, tid);
+          hqv[0] = *reinterpret_cast<const u32x4*>(&hq[4 * lane]);
+          hqv[1] = *reinterpret_cast<const u32x4*>(&hq[4 * (lane + 64)]);
+        } else {
+          load_vec<4>(hc, reinterpret_cast<const uint16_t*>(hs), lane);
+        }
         static_for<NSLOT>([&](auto sc) __attribute__((always_inline)) {
           constexpr int s = decltype(sc)::value;
           if constexpr (s == B0) {
             bar();  // phase A done
-            bar();  // g1 ready
+            bar();  // g1 ready (W8A8: all of g gathered)
+            if constexpr (I8) quant_block_i8<MK_F / 8>(gs, gq, qred, tid);
           }
-          if constexpr (s == BH) bar();  // g2 ready
+          if constexpr (!I8 && s == BH) bar();  // g2 ready
           compute(sc, ll, E(l, 1));
           // the freed buffer's next unit (sched_barrier: kept after the reduction that frees it; the scheduler would
           // otherwise hoist the loads and need more buffers)
@@ -741,14 +975,24 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         for (int j = 0; j < JC; j++) {
           const int u = wave + GW * j;
           if (u < nr) {
-            const uint8_t* pr = pw + u * 4096;
-            float acc = 0.f;
+            const uint8_t* pr = pw + u * PROW;
+            if constexpr (I8) {
+              int acc = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-              acc = dot8d(*reinterpret_cast<const u32x4*>(pr + (lane + 64 * i) * 16),
-                          *reinterpret_cast<const u32x4*>(&as2[(lane + 64 * i) * 4]), acc);
-            const float t = wave_total(acc);
-            if (lane == 0) pc[u] = t;
+              for (int i = 0; i < 2; i++)
+                acc = dot16_i8(*reinterpret_cast<const u32x4*>(&aq[4 * (lane + 64 * i)]),
+                               *reinterpret_cast<const u32x4*>(pr + (lane + 64 * i) * 16), acc);
+              const int t = wave_total_i(acc);
+              if (lane == 0) pci[u] = t;
+            } else {
+              float acc = 0.f;
+#pragma unroll
+              for (int i = 0; i < 4; i++)
+                acc = dot8d(*reinterpret_cast<const u32x4*>(pr + (lane + 64 * i) * 16),
+                            *reinterpret_cast<const u32x4*>(&as2[(lane + 64 * i) * 4]), acc);
+              const float t = wave_total(acc);
+              if (lane == 0) pc[u] = t;
+            }
           }
         }
         bar();  // the partial sums in pb / pc; every read of hs, gs, as2, pw done
@@ -874,15 +1118,12 @@ extern "C" int mx_decode_mk_words(void) { return LL_WORDS; }
 
 extern "C" int mx_decode_mk_grid(void) { return MK_G; }
 
-// One greedy decode step of the 2048-wide, 32-head text model in one launch (decode_mk_kernel): layers[nl] describes
-// every layer's weights and cache (device memory), x the step's input embedding (replaced by the next step's), state /
-// tokens / cap / pos_base as mx_embed_step; logits optional (V bf16). ll: mx_decode_mk_words() zeroed words, ep: 2
-// words {epoch base, error} zeroed once, both owned by one decoder (the kernel advances the base). Needs
-// mx_decode_mk_grid() CUs (one workgroup on each, all resident) and ctx <= 1024 (the keys one pass holds).
-extern "C" int mx_decode_step_mk(hipStream_t st, const void* layers, int nl, int ctx, const uint16_t* lnf_g,
-                                 const uint16_t* lnf_b, const uint16_t* wlm, const float* blm, int V,
-                                 const uint16_t* wte, const float* cs, float eps, float scale, uint16_t* x, int* state,
-                                 int pos_base, int* tokens, int cap, uint16_t* logits, uint64_t* ll, uint32_t* ep) {
+namespace {
+template <bool I8>
+int launch_mk(hipStream_t st, const void* layers, int nl, int ctx, const uint16_t* lnf_g, const uint16_t* lnf_b,
+              const uint16_t* wlm, const float* blm, int V, const uint16_t* wte, const float* cs, float eps, float scale,
+              uint16_t* x, int* state, int pos_base, int* tokens, int cap, uint16_t* logits, uint64_t* ll,
+              uint32_t* ep) {
   if (!layers || !lnf_g || !lnf_b || !wlm || !blm || !wte || !cs || !x || !state || !tokens || !ll || !ep)
     return MX_ENULL;
   if (nl < 1 || nl > MK_MAXL || ctx < 1 || ctx > MK_MAXKEYS || V < 1 || V > 65536 || cap < 1 || pos_base < 0)
@@ -899,10 +1140,35 @@ extern "C" int mx_decode_step_mk(hipStream_t st, const void* layers, int nl, int
   a.eps = eps, a.scale_log2 = scale * 1.4426950408889634f;
   a.lnf_g = lnf_g, a.lnf_b = lnf_b, a.wlm = wlm, a.blm = blm, a.wte = wte, a.cs = cs;
   a.x = x, a.state = state, a.tokens = tokens, a.logits = logits, a.ll = ll, a.ep = ep;
-  hipLaunchKernelGGL(decode_mk_kernel, dim3(MK_G), dim3(MK_T), 0, st, a);
+  hipLaunchKernelGGL(decode_mk_kernel<I8>, dim3(MK_G), dim3(MK_T), 0, st, a);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
+}  // namespace
 
-// Bytes of one layer descriptor in the layers array of mx_decode_step_mk: 10 device pointers (ln_g, ln_b, wqf, bqf,
-// w2, b2, wp, bp, kc, vc), in that order, 8 bytes each.
+// One greedy decode step of the 2048-wide, 32-head text model in one launch (decode_mk_kernel): layers[nl] describes
+// every layer's weights and cache (device memory), x the step's input embedding (replaced by the next step's), state /
+// tokens / cap / pos_base as mx_embed_step; logits optional (V bf16). ll: mx_decode_mk_words() zeroed words, ep: 2
+// words {epoch base, error} zeroed once, both owned by one decoder (the kernel advances the base). Needs
+// mx_decode_mk_grid() CUs (one workgroup on each, all resident) and ctx <= 1024 (the keys one pass holds).
+extern "C" int mx_decode_step_mk(hipStream_t st, const void* layers, int nl, int ctx, const uint16_t* lnf_g,
+                                 const uint16_t* lnf_b, const uint16_t* wlm, const float* blm, int V,
+                                 const uint16_t* wte, const float* cs, float eps, float scale, uint16_t* x, int* state,
+                                 int pos_base, int* tokens, int cap, uint16_t* logits, uint64_t* ll, uint32_t* ep) {
+  return launch_mk<false>(st, layers, nl, ctx, lnf_g, lnf_b, wlm, blm, V, wte, cs, eps, scale, x, state, pos_base,
+                          tokens, cap, logits, ll, ep);
+}
+
+// The same step with the W8A8 text Linears: each descriptor's wqf / w2 / wp are int8 (the same shapes, one byte per
+// weight) and its sqf / sw2 / swp hold their fp32 per-row scales; the LM head stays bf16.
+extern "C" int mx_decode_step_mk_i8(hipStream_t st, const void* layers, int nl, int ctx, const uint16_t* lnf_g,
+                                    const uint16_t* lnf_b, const uint16_t* wlm, const float* blm, int V,
+                                    const uint16_t* wte, const float* cs, float eps, float scale, uint16_t* x,
+                                    int* state, int pos_base, int* tokens, int cap, uint16_t* logits, uint64_t* ll,
+                                    uint32_t* ep) {
+  return launch_mk<true>(st, layers, nl, ctx, lnf_g, lnf_b, wlm, blm, V, wte, cs, eps, scale, x, state, pos_base,
+                         tokens, cap, logits, ll, ep);
+}
+
+// Bytes of one layer descriptor in the layers array of mx_decode_step_mk(_i8): 13 device pointers (ln_g, ln_b, wqf,
+// bqf, w2, b2, wp, bp, kc, vc, sqf, sw2, swp), in that order, 8 bytes each (the last three only for the W8A8 form).
 extern "C" int mx_decode_mk_layer_bytes(void) { return (int)sizeof(MkLayer); }

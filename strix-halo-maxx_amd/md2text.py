@@ -121,11 +121,12 @@ class TextDecoder:
         self.pos_base = 0
         self.steps = 0
         self.graph = None
-        # one launch per decode step (mx_decode_step_mk) where its shapes hold: the bf16 2048-wide, 32 x 64-head,
-        # 8192-MLP model, a cache of at most 1024 positions, one attention split, and a device with a CU for each of
-        # its workgroups; the per-layer kernels above otherwise (use_mk = False selects them too)
+        # one launch per decode step (mx_decode_step_mk, or mx_decode_step_mk_i8 for the W8A8 Linears) where its
+        # shapes hold: the 2048-wide, 32 x 64-head, 8192-MLP model, a cache of at most 1024 positions, one attention
+        # split, and a device with a CU for each of its workgroups; the per-layer kernels above otherwise (use_mk =
+        # False selects them too)
         self.mk_layers = self.mk_ll = self.mk_ep = None
-        if (dev.type == "cuda" and not w8a8 and attn_splits == 1 and (self.D, self.H, self.hd, c["ff"]) == (2048, 32, 64, 8192)
+        if (dev.type == "cuda" and attn_splits == 1 and (self.D, self.H, self.hd, c["ff"]) == (2048, 32, 64, 8192)
                 and ctx <= 1024 and self.V <= 65536
                 and torch.cuda.get_device_properties(dev).multi_processor_count >= lib.mx_decode_mk_grid()):
             self._init_mk()
@@ -138,9 +139,10 @@ class TextDecoder:
             for t, shape in ((b["wqf"], (3 * self.D + 8192, self.D)), (b["w2"], (self.D, 8192)), (b["wp"], (self.D, self.D))):
                 if tuple(t.shape) != shape or not t.is_contiguous():
                     return
+            scales = [b["sqf"].data_ptr(), b["sw2"].data_ptr(), b["swp"].data_ptr()] if self.w8a8 else [0, 0, 0]
             rows.append([b["ln"][0].data_ptr(), b["ln"][1].data_ptr(), b["wqf"].data_ptr(), b["bqf"].data_ptr(),
                          b["w2"].data_ptr(), b["b2"].data_ptr(), b["wp"].data_ptr(), b["bp"].data_ptr(),
-                         self.kc[i].data_ptr(), self.vc[i].data_ptr()])
+                         self.kc[i].data_ptr(), self.vc[i].data_ptr()] + scales)
         if lib.mx_decode_mk_layer_bytes() != 8 * len(rows[0]):
             raise RuntimeError("layer descriptor size mismatch with the library")
         self.mk_layers = torch.tensor(rows, dtype=torch.int64).to(self.dev)
@@ -321,7 +323,8 @@ class TextDecoder:
         lib = _lib.load()
         if self.use_mk:
             cap = max(1, min(self.ctx - self.pos_base + 1, self.ctx))
-            _lib.check(lib.mx_decode_step_mk(st, self.mk_layers.data_ptr(), len(self.blocks), self.ctx,
+            fn = lib.mx_decode_step_mk_i8 if self.w8a8 else lib.mx_decode_step_mk
+            _lib.check(fn(st, self.mk_layers.data_ptr(), len(self.blocks), self.ctx,
                                              self.post_ln[0].data_ptr(), self.post_ln[1].data_ptr(),
                                              self.w_lm.data_ptr(), self.b_lm.data_ptr(), self.V, self.wte.data_ptr(),
                                              self.cs.data_ptr(), float(self.eps), float(self.hd ** -0.5),
