@@ -22,7 +22,10 @@
 //  * Head dim 72 pads to 80 along the QK contraction (5 k-steps; Q's padding is zero, so the neighbouring LDS bytes
 //    that K's padding reads are multiplied by 0) and to 96 output rows for PV (3 row tiles; rows >= 72 are dropped).
 // Numerics: fp32 scores and accumulators; P is rounded to bf16 before the PV product and the softmax denominator is
-// summed over those rounded values, so numerator and denominator use the same weights.
+// summed over those rounded values, so numerator and denominator use the same weights. With D = 72 the PV product
+// computes the denominator itself: the V^T operand rows 72..95 (padding, dropped) are replaced by ones, so those
+// output rows accumulate sum_j P[i, j] in fp32 inside the MFMA (and are rescaled with O), which takes the per-score
+// unpack-and-add off the VALU, the unit that bounds the small-grid shapes.
 #include "common.h"
 
 namespace {
@@ -148,6 +151,11 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
     }
   };
 
+  // D = 72: the PV operand's padding rows carry ones, and O^T row 72 (+ 4 hk) = register 4 of the last row tile holds
+  // the denominator; D = 64 has no padding rows and sums the rounded P on the VALU
+  constexpr bool ONES = DV > D;
+  static_assert(!ONES || DV - 32 + 8 >= D, "register 4 of the last row tile is a padding row");
+  const bool ones_lane = ONES && (lane & 31) >= D - (DV - 32);
   float m_run = -1e30f, l_run = 0.f;
   bool first = true;  // no key block consumed yet by this wave (O and l are still zero)
   f32x16 oacc[DV / 32];
@@ -214,7 +222,7 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
       const float mnew = grow ? mx : m_run;
       if (!first) {
         const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
-        l_run *= alpha;
+        if constexpr (!ONES) l_run *= alpha;
 #pragma unroll
         for (int i = 0; i < DV / 32; i++)
 #pragma unroll
@@ -231,10 +239,10 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
       for (int r2 = 0; r2 < 16; r2 += 2) {
         const uint32_t w = pack2(__builtin_amdgcn_exp2f(__builtin_fmaf(st[kt][r2], scale_log2, -m_run)),
                                  __builtin_amdgcn_exp2f(__builtin_fmaf(st[kt][r2 + 1], scale_log2, -m_run)));
-        sum += lo_bf(w) + hi_bf(w);
+        if constexpr (!ONES) sum += lo_bf(w) + hi_bf(w);
         pk[kt][r2 >> 1] = w;
       }
-    l_run += halves_sum(sum);
+    if constexpr (!ONES) l_run += halves_sum(sum);
 
     // ---- O^T += V^T P^T ; k-step (kt, s) covers keys kt*32 + 16 s + {4hk..4hk+3, 8+4hk..8+4hk+3}. The V^T
     // operand comes from two transpose reads: lane j = lane & 15 of each 16-lane group points at
@@ -261,7 +269,11 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
             lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(Vst + r0 * ROWB + col * 2));
             hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(Vst + (r0 + 8) * ROWB + col * 2));
           }
-          const u32x4 va = {lo.x, lo.y, hi.x, hi.y};
+          u32x4 va = {lo.x, lo.y, hi.x, hi.y};
+          if (ONES && dt == DV / 32 - 1) {
+            constexpr uint32_t one2 = 0x3f803f80u;  // two bf16 1.0
+            va = ones_lane ? u32x4{one2, one2, one2, one2} : va;
+          }
           oacc[dt] = mfma32(as_bf16x8(va), bp, oacc[dt]);
         }
       }
@@ -278,6 +290,7 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
     wait_vm<0>();
     __syncthreads();
     const int slot = kw * NQW + qg;
+    if constexpr (ONES) l_run = oacc[DV / 32 - 1][4];
     cm[slot * 64 + lane] = m_run;
     cl[slot * 64 + lane] = l_run;
 #pragma unroll
@@ -317,6 +330,7 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
   }
 
   if (qi >= Tq) return;
+  if constexpr (ONES) l_run = oacc[DV / 32 - 1][4];
   const float inv = 1.f / l_run;
   uint16_t* orow = O + b * so_b + (long)qi * so_t + h * so_h;
 #pragma unroll
