@@ -90,18 +90,6 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
   const uint16_t* Vb = V + b * sv_b + h * sv_h;
   const uint32_t sbase = lds_off(smem);
 
-  bf16x8 qf[DK / 16];
-  {
-    const uint16_t* qrow = Qb + (long)min(qi, Tq - 1) * sq_t;
-#pragma unroll
-    for (int s = 0; s < DK / 16; s++) {
-      const int d = 16 * s + 8 * hk;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (d < D) v = *reinterpret_cast<const u32x4*>(qrow + d);
-      qf[s] = as_bf16x8(v);
-    }
-  }
-
   int kend = Tk;
   if (causal_from < Tk) {
     const int qlast = min((qx + 1) * 32 * NQW, Tq) - 1;
@@ -164,8 +152,25 @@ __global__ __launch_bounds__(64 * NQW * NKW) void attn_fwd_kernel(
 #pragma unroll
     for (int e = 0; e < 16; e++) oacc[i][e] = 0.f;
 
+  // Stage 0, then this lane's Q fragments, then one wait for both, then the other prefetched stages. The compiler
+  // does not count the LDS-DMA loads (inline asm), so a Q fragment still in flight at its first use would make it wait
+  // with a count that assumes nothing was issued after Q, i.e. for every prefetched stage, on every pass of the key
+  // loop; waiting for Q here (a wait the compiler sees) leaves the loop with the ring's own waits only.
+  if (nkb > 0) issue(0, 0);
+  bf16x8 qf[DK / 16];
+  {
+    const uint16_t* qrow = Qb + (long)min(qi, Tq - 1) * sq_t;
 #pragma unroll
-  for (int s = 0; s < S - 1; s++)
+    for (int s = 0; s < DK / 16; s++) {
+      const int d = 16 * s + 8 * hk;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (d < D) v = *reinterpret_cast<const u32x4*>(qrow + d);
+      qf[s] = as_bf16x8(v);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0); expcnt, lgkmcnt not waited (gfx9 encoding)
+#pragma unroll
+  for (int s = 1; s < S - 1; s++)
     if (s < nkb) issue(s, s);
 
   for (int kb = 0; kb < nkb; kb++) {
