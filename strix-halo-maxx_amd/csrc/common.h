@@ -38,18 +38,16 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// tanh(u) = 1 - 2 / (exp(2 u) + 1) on the hardware exp2 (v_exp_f32) and reciprocal (v_rcp_f32): saturates to +-1
-// for large |u| (exp2 -> inf / 0) and is within ~2e-7 of tanh everywhere in absolute terms, far below the bf16
-// rounding that follows every use here. A handful of VALU ops instead of a libm polynomial with range reduction.
-__device__ __forceinline__ float tanh_fast(float u) {
-  const float e = __builtin_amdgcn_exp2f(u * 2.885390081777927f);  // 2 / ln 2
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-}
-// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), evaluated in fp32 like torch's
-// F.gelu(x, approximate="tanh") on a bf16 tensor (upcast, compute, round once).
+// GELU, tanh form: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated in fp32 like torch's
+// F.gelu(x, approximate="tanh") on a bf16 tensor (upcast, compute, round once). Since 1 + tanh(u) = 2 / (1 + exp(-2u)),
+// this is x / (1 + exp(-2u)) with -2u / ln 2 = x (c1 + c2 x^2): one hardware exp2 (v_exp_f32), one reciprocal
+// (v_rcp_f32) and five plain operations, and no cancellation in 1 + tanh(u) for negative u. Within a few fp32 ulp of
+// the formula; saturates to x for large u (exp2 -> 0) and to -0 for very negative u (exp2 -> inf, rcp -> 0).
 __device__ __forceinline__ float gelu_tanh(float x) {
-  float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanh_fast(u));
+  constexpr float c1 = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634);  // -2 sqrt(2/pi) / ln 2
+  constexpr float c2 = (float)(-2.0 * 0.7978845608028654 * 1.4426950408889634 * 0.044715);
+  const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(c2, x * x, c1));
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 // GELU, erf form (torch nn.GELU() default): 0.5 x (1 + erf(x / sqrt 2)).
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }

@@ -64,9 +64,13 @@ struct IntC {
 };
 // I8: s holds int32 accumulator bits; the linear output is ((float)acc * sa) * sw + bias in fp32 and any GELU applies
 // to that fp32 value before the one bf16 rounding (the W8A8 epilogue); a residual is then added to the rounded value.
-template <int ACT, bool I8 = false>
+// HR: 0 / 1 = no residual / a residual, known at compile time; 2 = has_r decides. The activation is computed for every
+// column and then selected (act_ncols varies across the lanes of a wave: a branch per group would serialise the
+// exp / rcp chains of the groups instead of interleaving them).
+template <int ACT, bool I8 = false, int HR = 2>
 __device__ __forceinline__ u32x2 epi_val(const f32x4& s, const f32x4& bv, const u32x2& rv, bool has_r, int n,
                                          int act_ncols, float sa = 0.f, const f32x4& sw = f32x4{0.f, 0.f, 0.f, 0.f}) {
+  const bool hr = HR == 2 ? has_r : HR == 1;
   float v[4];
   if constexpr (I8) {
     static_assert(ACT != 3, "no gated GELU in the int8 path");
@@ -76,12 +80,14 @@ __device__ __forceinline__ u32x2 epi_val(const f32x4& s, const f32x4& bv, const 
       v[e] = t * sw[e] + bv[e];
     }
     if constexpr (ACT == 1 || ACT == 2) {
-      if (act_ncols <= 0 || n < act_ncols) {
+      const bool on = act_ncols <= 0 || n < act_ncols;
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = ACT == 1 ? gelu_tanh(v[e]) : gelu_erf(v[e]);
+      for (int e = 0; e < 4; e++) {
+        const float g = ACT == 1 ? gelu_tanh(v[e]) : gelu_erf(v[e]);
+        v[e] = on ? g : v[e];
       }
     }
-    if (has_r) {
+    if (hr) {
       v[0] = rbf(v[0]) + lo_bf(rv.x);
       v[1] = rbf(v[1]) + hi_bf(rv.x);
       v[2] = rbf(v[2]) + lo_bf(rv.y);
@@ -97,12 +103,16 @@ __device__ __forceinline__ u32x2 epi_val(const f32x4& s, const f32x4& bv, const 
     o.y = 0;
   } else {
     if constexpr (ACT == 1 || ACT == 2) {
-      if (act_ncols <= 0 || n < act_ncols) {
+      // the activation's bf16 rounding: explicit before a residual add, else the final pack's own rounding
+      const bool on = act_ncols <= 0 || n < act_ncols;
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = rbf(ACT == 1 ? gelu_tanh(v[e]) : gelu_erf(v[e]));
+      for (int e = 0; e < 4; e++) {
+        float g = ACT == 1 ? gelu_tanh(v[e]) : gelu_erf(v[e]);
+        if (hr) g = rbf(g);
+        v[e] = on ? g : v[e];
       }
     }
-    if (has_r) {
+    if (hr) {
       v[0] += lo_bf(rv.x);
       v[1] += hi_bf(rv.x);
       v[2] += lo_bf(rv.y);
@@ -308,6 +318,43 @@ __device__ __forceinline__ void gemm_body(
 #endif
   };
 
+  // The epilogue's operands: bias, per-row / per-column scales and, on 4-wave tiles, the residual. Tiles of at most 2 x 2
+  // MFMA blocks per wave load them before the k loop, so their latency hides under it (nothing in the loop uses them,
+  // so the compiler puts no wait for them there); larger tiles load them after it (their registers are taken). Each
+  // pointer is checked: the raw-sum modes (P) return before the epilogue and may pass null scales, bias or residual.
+  constexpr bool HOIST_R = FN * FM <= 4;
+  constexpr bool EARLY = NW == 4 && FN * FM <= 4;
+  f32x4 bv[FN][4];
+  f32x4 swv[I8 ? FN : 1][4];
+  float sav[I8 ? FM : 1];
+  u32x2 rv[HOIST_R ? FN : 1][HOIST_R ? FM : 1][4];
+  if constexpr (EARLY) {
+    if constexpr (I8) {
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          swv[i][g] = sw ? bias4(sw, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < FM; j++) sav[j] = sa ? sa[min(m0 + wm * WTM + j * 32 + lr, M - 1)] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        bv[i][g] = bias ? bias4(bias, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N) : f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (HOIST_R) {
+      if (R) {
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+          for (int j = 0; j < FM; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+              rv[i][j][g] = res4(R, ldr, r_rows, m0 + wm * WTM + j * 32 + lr, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, M, N);
+      }
+    }
+  }
 #pragma unroll
   for (int s = 0; s < S; s++)
     if (s < nkl) issue(kt0 + s, s);
@@ -428,61 +475,68 @@ __device__ __forceinline__ void gemm_body(
 
   // ---- epilogue: lane holds output row m, columns n .. n+3 for each 8-row group g of the MFMA result. Results go
   // through an LDS staging tile (the ring is free once every wave is past its last k-step) and reach C only in the
-  // final copy, so the bias / residual loads here never queue behind stores. They are all issued up front (one
-  // latency for the lot) where the registers allow: always for the bias, for the residual on 4-wave tiles.
-  constexpr bool HOIST_R = FN * FM <= 4;
-  f32x4 bv[FN][4];
-  f32x4 swv[I8 ? FN : 1][4];
-  float sav[I8 ? FM : 1];
-  if constexpr (I8) {
+  // final copy. The bias, scales and residual were loaded before the k loop (small tiles) or are loaded here.
+  if constexpr (!EARLY) {
+    if constexpr (I8) {
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          swv[i][g] = sw ? bias4(sw, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < FM; j++) sav[j] = sa ? sa[min(m0 + wm * WTM + j * 32 + lr, M - 1)] : 0.f;
+    }
 #pragma unroll
     for (int i = 0; i < FN; i++)
 #pragma unroll
-      for (int g = 0; g < 4; g++) swv[i][g] = bias4(sw, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N);
+      for (int g = 0; g < 4; g++)
+        bv[i][g] = bias ? bias4(bias, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N) : f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (HOIST_R) {
+      if (R) {
 #pragma unroll
-    for (int j = 0; j < FM; j++) sav[j] = sa[min(m0 + wm * WTM + j * 32 + lr, M - 1)];
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+          for (int j = 0; j < FM; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+              rv[i][j][g] = res4(R, ldr, r_rows, m0 + wm * WTM + j * 32 + lr, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, M, N);
+      }
+    }
   }
-  u32x2 rv[HOIST_R ? FN : 1][HOIST_R ? FM : 1][4];
-#pragma unroll
-  for (int i = 0; i < FN; i++)
-#pragma unroll
-    for (int g = 0; g < 4; g++)
-      bv[i][g] = bias ? bias4(bias, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, N) : f32x4{0.f, 0.f, 0.f, 0.f};
-  if constexpr (HOIST_R) {
-    if (R) {
+  __syncthreads();
+  // the activation and the residual's presence are compile-time in the loop (one straight run per case)
+  if (owner) with_act(act, [&](auto ac) {
+    constexpr int ACT = decltype(ac)::value;
+    auto run = [&](auto hrc) {
+      constexpr int HR = decltype(hrc)::value;
 #pragma unroll
       for (int i = 0; i < FN; i++)
 #pragma unroll
         for (int j = 0; j < FM; j++)
 #pragma unroll
-          for (int g = 0; g < 4; g++)
-            rv[i][j][g] = res4(R, ldr, r_rows, m0 + wm * WTM + j * 32 + lr, n0 + wn * WTN + i * 32 + 8 * g + 4 * hk, M, N);
-    }
-  }
-  __syncthreads();
-  if (owner) with_act(act, [&](auto ac) {
-    constexpr int ACT = decltype(ac)::value;
-#pragma unroll
-    for (int i = 0; i < FN; i++)
-#pragma unroll
-      for (int j = 0; j < FM; j++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int r = wm * WTM + j * 32 + lr, c = wn * WTN + i * 32 + 8 * g + 4 * hk;
-          u32x2 rg = {0u, 0u};
-          if constexpr (HOIST_R)
-            rg = rv[i][j][g];
-          else if (R)
-            rg = res4(R, ldr, r_rows, m0 + r, n0 + c, M, N);
-          const f32x4 a4 = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          if constexpr (I8) {
-            if constexpr (ACT != 3)
-              stage_val<ACT, SP>(smem, r, c, epi_val<ACT, true>(a4, bv[i][g], rg, R != nullptr, n0 + c, act_ncols,
-                                                                 sav[j], swv[i][g]));
-          } else {
-            stage_val<ACT, SP>(smem, r, c, epi_val<ACT>(a4, bv[i][g], rg, R != nullptr, n0 + c, act_ncols));
+          for (int g = 0; g < 4; g++) {
+            const int r = wm * WTM + j * 32 + lr, c = wn * WTN + i * 32 + 8 * g + 4 * hk;
+            u32x2 rg = {0u, 0u};
+            if constexpr (HR == 1) {
+              if constexpr (HOIST_R)
+                rg = rv[i][j][g];
+              else
+                rg = res4(R, ldr, r_rows, m0 + r, n0 + c, M, N);
+            }
+            const f32x4 a4 = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+            if constexpr (I8) {
+              if constexpr (ACT != 3)
+                stage_val<ACT, SP>(smem, r, c, epi_val<ACT, true, HR>(a4, bv[i][g], rg, HR == 1, n0 + c, act_ncols,
+                                                                       sav[j], swv[i][g]));
+            } else {
+              stage_val<ACT, SP>(smem, r, c, epi_val<ACT, false, HR>(a4, bv[i][g], rg, HR == 1, n0 + c, act_ncols));
+            }
           }
-        }
+    };
+    if (R)
+      run(IntC<1>{});
+    else
+      run(IntC<0>{});
   });
   __syncthreads();
   if (act == 3)

@@ -230,6 +230,29 @@ def _fp32_oracle(w):
     return ot.Text({k: v.float() for k, v in w.items()}, 1024, S.freqs_cis(32, 2048), dtype=torch.float32)
 
 
+def compare_free_running(out, tol, gap_max=0.05):
+    """out[mk] = (tokens[:7], logits per step, next embedding) of two greedy decoders run free from one prefill.
+    tokens[0] comes from the shared prefill; step t reads tokens[t] and its argmax is tokens[t + 1]. The logits are
+    compared while both decoders read the same tokens (steps t < d, d the first index where the tokens differ). If they
+    part, the step that chose differently must be a near tie: its top-2 gap below gap_max, the threshold above which
+    the tokens must agree. With no parting the next step's embedding must be identical. Returns the per-step rel-L2."""
+    tk0, lg0, x0 = out[False]
+    tk1, lg1, x1 = out[True]
+    d = next((i for i in range(len(tk0)) if tk0[i] != tk1[i]), len(tk0))
+    assert d >= 1, "the prefill's token differs"
+    rs = [rel(lg1[t], lg0[t]) for t in range(min(d, len(lg0)))]
+    print("rel-L2 of the logits per step:", [f"{r:.1e}" for r in rs], "tokens part at", d, flush=True)
+    assert max(rs) < tol, rs
+    if d < len(tk0):
+        v = torch.topk(lg0[d - 1], 2).values
+        gap = (v[0] - v[1]).item()
+        print(f"tokens part after step {d - 1}: top-2 gap {gap:.3g}", flush=True)
+        assert gap < gap_max, (d, gap)
+    else:
+        assert torch.equal(x1, x0)  # the next step's embedding
+    return rs
+
+
 def _check_decode(dec, ora, ora32, img, prompt, n_tokens, tol=1e-2):
     """Teacher-forced on the HIP path's tokens: the bf16 oracle and its fp32 arbiter step in lockstep. Checks the
     logits (rel-L2 tol) and the token rule of the module docstring at every step. Returns (HIP tokens, steps where the
@@ -285,8 +308,9 @@ def test_decoder_two_layers(dev, mk):
 
 def test_decode_one_launch_step_equals_layer_kernels(dev):
     """The one-launch step and the per-layer kernels on the same weights and inputs, 2 layers, 6 steps from the same
-    prefill: the same tokens while the logits agree within a few bf16 roundings (their fp32 sums run in other
-    orders: fc2 / proj row sums and the attention's key partition differ)."""
+    prefill: the logits agree within a few bf16 roundings (their fp32 sums run in other orders: fc2 / proj row sums
+    and the attention's key partition differ) while both read the same tokens, and the tokens part only at a near tie
+    (compare_free_running)."""
     w, _, dec = _models(2, seed=1)
     img = S.activations(5, (729, 2048), "img")
     prompt = S.prompt_ids(6, 48)
@@ -301,12 +325,7 @@ def test_decode_one_launch_step_equals_layer_kernels(dev):
             lg.append(dec.logits.float().cpu().clone())
         out[mk] = (dec.tokens[:7].cpu().tolist(), lg, dec.xd[0].cpu().clone())
     assert dec.mk_error() == 0
-    for t in range(6):
-        assert rel(out[True][1][t], out[False][1][t]) < 5e-3, t
-    top2 = [torch.topk(l, 2).values for l in out[False][1]]
-    if all((v[0] - v[1]).item() > 0.05 for v in top2):
-        assert out[True][0] == out[False][0]
-        assert torch.equal(out[True][2], out[False][2])  # the next step's embedding
+    compare_free_running(out, 5e-3)
 
 
 def test_decoder_full_config_greedy_128(dev):

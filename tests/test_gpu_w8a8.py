@@ -208,11 +208,13 @@ def test_decode_w8a8_one_launch_step_equals_layer_kernels(dev):
     """The W8A8 one-launch step and the W8A8 per-layer kernels on the same weights and inputs, 2 layers, 6 steps from
     the same prefill. The int8 sums are exact in both and the quantisations of g and the attention output see the
     same values; the LayerNorm's fp32 sums run in another order (DPP against a workgroup sum), which can move an int8
-    value of h by one step. So: logits within rel-L2 2e-2, the same tokens and next embedding where the top-2 gap
-    exceeds 0.05. The bound is the W8A8 decoder's own tolerance against the oracle (2e-2): one int8 step of h moves a
-    whole row's sum by a weight times the scale, far more than a bf16 rounding (measured: 7e-3 at the first step)."""
+    value of h by one step. So: logits within rel-L2 2e-2 while both read the same tokens, which part only at a near
+    tie (top-2 gap below 0.05), and the same next embedding when they never part (compare_free_running). The bound
+    is the W8A8 decoder's own tolerance against the oracle (2e-2): one int8 step of h moves a whole row's sum by a
+    weight times the scale, far more than a bf16 rounding (measured: 7e-3 at the first step)."""
     import strix_halo_maxx_amd.md2text as mt
     import strix_halo_maxx_amd.synth as S
+    from test_gpu_decoder import compare_free_running
     w = S.text_weights(1, layers=2)
     dec = mt.TextDecoder(w, ctx=1024, w8a8=True)
     assert dec.use_mk
@@ -230,10 +232,4 @@ def test_decode_w8a8_one_launch_step_equals_layer_kernels(dev):
             lg.append(dec.logits.float().cpu().clone())
         out[mk] = (dec.tokens[:7].cpu().tolist(), lg, dec.xd[0].cpu().clone())
     assert dec.mk_error() == 0
-    rs = [((out[True][1][t] - out[False][1][t]).norm() / out[False][1][t].norm()).item() for t in range(6)]
-    print("rel-L2 of the logits per step:", [f"{r:.1e}" for r in rs], flush=True)
-    assert max(rs) < 2e-2, rs
-    top2 = [torch.topk(l, 2).values for l in out[False][1]]
-    if all((v[0] - v[1]).item() > 0.05 for v in top2):
-        assert out[True][0] == out[False][0]
-        assert torch.equal(out[True][2], out[False][2])
+    compare_free_running(out, 2e-2)
