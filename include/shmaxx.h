@@ -60,6 +60,23 @@ int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const uint16_t* A,
 int mx_gemm_reduce(hipStream_t st, const float* P, int nsplit, long p_split, long ldp, const float* bias,
                    const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int act,
                    int act_ncols);
+/* Residual Linear and the LayerNorm that reads it, in one launch: X = bf16(bf16(A W^T + bias) + R) and
+ * Y = LayerNorm(X; gamma, beta, eps), the roundings of mx_gemm_bf16_partial + mx_residual_layernorm. Replaces the
+ * block's lin_res(proj) + ln2 and lin_res(fc2) + the next block's ln1 (moondream/gpu/md2fast.py:153-157, the post-LN
+ * at :158 for the last block). The 64 x 64 output tiles of a row block exchange their rows' sums and centred square
+ * sums through stats (>= mx_gemm_res_ln_stats_words(M, N) 64-bit words) and wait for each other, so the whole grid
+ * must be resident: N % 64 == 0, N <= 4096 and ((M + 63) / 64) * (N / 64) <= the device's CU count, else
+ * MX_ESHAPE. sync (>= mx_gemm_res_ln_sync_words(M) 32-bit words) and stats are zeroed once by the caller and then
+ * kept ready by the kernel; calls that share them must be ordered on one stream. sync[0] != 0 after a call: a wait
+ * timed out and the results are undefined (zero both before the next call). The statistics combine per-tile sums in
+ * fp32 in another order than mx_residual_layernorm's row sums (Y within a bf16 rounding of it; X identical for the
+ * same k-loop). */
+int mx_gemm_bf16_res_ln(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* bias,
+                        const uint16_t* R, long ldr, uint16_t* X, long ldx, const uint16_t* gamma,
+                        const uint16_t* beta, uint16_t* Y, long ldy, int M, int N, int K, int Kw, float eps,
+                        uint64_t* stats, long stats_words, uint32_t* sync, long sync_words);
+long mx_gemm_res_ln_stats_words(int M, int N);
+long mx_gemm_res_ln_sync_words(int M);
 
 /* mx_gemm_bf16 without a caller workspace: in-kernel split-K (splits > 1, or a split pick when cfg < 0) uses a fixed
  * device array of the library (mx_gemm_noalloc_max_ws() fp32 partial elements, 16 MiB, plus 65,536 tile counters)

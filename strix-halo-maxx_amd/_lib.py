@@ -67,13 +67,17 @@ SIGNATURES = {
     "mx_counter_add": [P, P, I],
     "mx_gemm_bf16_noalloc": [P, I, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I, I, I],
     "mx_gemm_noalloc_max_ws": [],
+    "mx_gemm_bf16_res_ln": [P, P, L, P, L, P, P, L, P, L, P, P, P, L, I, I, I, I, F, P, L, P, L],
+    "mx_gemm_res_ln_stats_words": [I, I],
+    "mx_gemm_res_ln_sync_words": [I],
 }
 
 STATUS = {0: "ok", -1: "bad config", -2: "unsupported shape/stride", -3: "split-K workspace too small",
           -4: "operand layout/alignment", -5: "HIP launch failed", -6: "null pointer"}
 
 RESTYPE = {"mx_gemm_ws_elems": L, "mx_gemm_ws_counters": L, "mx_track_head_blob_elems": L,
-           "mx_gemm_noalloc_max_ws": L, "mx_sdpa_tiling": None}
+           "mx_gemm_noalloc_max_ws": L, "mx_sdpa_tiling": None, "mx_gemm_res_ln_stats_words": L,
+           "mx_gemm_res_ln_sync_words": L}
 
 _lib = None
 

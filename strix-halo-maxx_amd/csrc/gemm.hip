@@ -193,6 +193,30 @@ __device__ __forceinline__ void interleave_reads_mfma() {
   }
 }
 
+// ---- fused residual + LayerNorm epilogue (mx_gemm_bf16_res_ln): x' = bf16(bf16(acc + bias) + R) and Y = LN(x').
+// A row's LayerNorm needs all N columns, which tiles_n workgroups hold. Each publishes, for each of its BM rows, the
+// sum of its BN values of x' and their centred square sum as two 64-bit words (epoch << 32 | fp32 bits), written
+// with single-copy-atomic agent-scope stores and read with agent-scope loads (past the per-XCD L2s), and waits only
+// for the other tiles of its row block. The epoch is the row block's generation + 1; the generation lives in device
+// memory and the row block's last workgroup to finish advances it, so every launch (graph replays included) uses
+// new epochs and nothing is ever cleared. The waits are bounded (kRlnTimeout); a timeout sets sync[0] and the
+// launch's results are garbage. Every workgroup of a row block must be resident at once: the host allows this mode
+// only for grids of at most one workgroup per CU.
+struct RlnArgs {
+  const uint16_t* gamma;
+  const uint16_t* beta;
+  uint16_t* X;   // x' (ldx)
+  long ldx;
+  uint16_t* Y;   // LN(x') (ldy)
+  long ldy;
+  float eps;
+  uint64_t* stats;  // [tiles_m][tiles_n][BM][2] words
+  uint32_t* sync;   // [0] error word, then {generation, departures} per row block
+};
+constexpr uint64_t kRlnTimeout = 5000000ull;  // 50 ms at 100 MHz (s_memrealtime)
+constexpr int kRlnMaxTiles = 64;             // column tiles per row (N <= 64 BN)
+#define GPTR(T, p) ((__attribute__((address_space(1))) T*)(p))
+
 // The kernel body, shared by the bf16 GEMM and the W8A8 int8 GEMM (I8). In the int8 form A and W hold int8 values and
 // every K / stride argument counts 16-bit units (2 int8): an LDS row is still 128 bytes (128 int8 of one k-step), a
 // fragment is still 16 bytes (16 consecutive k for the 32x32x32 int8 MFMA instead of 8 for the 32x32x16 bf16 one), so
@@ -200,13 +224,14 @@ __device__ __forceinline__ void interleave_reads_mfma() {
 // KS = 2: 8 waves, the spatial WGM x WGN split twice over, each wave group taking half of every k-step's substeps
 // (same LDS bytes per k-step as KS = 1, twice the waves to pull them: a CU holding one workgroup reads its LDS at the
 // 8-wave rate); the second group's accumulators are added to the first's through LDS after the k loop.
-template <int BM, int BN, int WGM, int WGN, int S, bool I8, int KS = 1>
+template <int BM, int BN, int WGM, int WGN, int S, bool I8, int KS = 1, bool RLN = false>
 __device__ __forceinline__ void gemm_body(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
     const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
     uint16_t* __restrict__ C, long ldc, int M, int N, int K, int Kw, int act, int act_ncols,
     int tiles_m, int tiles_n, int splits, int kt_per_split, float* __restrict__ ws, int* __restrict__ cnt,
-    float* __restrict__ P, long ldp, long p_split, const float* __restrict__ sa, const float* __restrict__ sw) {
+    float* __restrict__ P, long ldp, long p_split, const float* __restrict__ sa, const float* __restrict__ sw,
+    const RlnArgs rl = RlnArgs{}) {
   constexpr int NWS = WGM * WGN, NW = NWS * KS, NT = 64 * NW;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
   static_assert(KS == 1 || KS == 2, "one or two k groups");
@@ -328,6 +353,17 @@ __device__ __forceinline__ void gemm_body(
   f32x4 swv[I8 ? FN : 1][4];
   float sav[I8 ? FM : 1];
   u32x2 rv[HOIST_R ? FN : 1][HOIST_R ? FM : 1][4];
+  u32x2 gmv[RLN ? FN : 1][4], btv[RLN ? FN : 1][4];
+  if constexpr (RLN) {
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int c = n0 + wn * WTN + i * 32 + 8 * g + 4 * hk;  // < N: N is a multiple of BN in this mode
+        gmv[i][g] = *reinterpret_cast<const u32x2*>(rl.gamma + c);
+        btv[i][g] = *reinterpret_cast<const u32x2*>(rl.beta + c);
+      }
+  }
   if constexpr (EARLY) {
     if constexpr (I8) {
 #pragma unroll
@@ -384,6 +420,181 @@ __device__ __forceinline__ void gemm_body(
     __builtin_amdgcn_sched_barrier(0);
   }
   static_assert(SPW % 2 == 0, "the tail reads into buffer 0");
+
+  if constexpr (RLN) {
+    static_assert(KS == 1 && !I8 && NWS == 4 && WGN == 2 && EARLY && HOIST_R, "4-wave 2 x 2 tiles, small");
+    static_assert(NT % BM == 0 && BM <= NT, "whole row groups of threads");
+    constexpr int QG = NT / BM;  // thread groups per row when the statistics are gathered
+    const int rb = tile_m;
+    uint32_t* gen = rl.sync + 1 + 2 * rb;
+    // every workgroup of the row block reads the generation before it publishes; none advances it before all have
+    // read the statistics, so all of them use the same epoch
+    const uint32_t ep = __hip_atomic_load(GPTR(uint32_t, gen), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    // x' in registers: bf16(bf16(acc + bias) + residual), the rounding of residual_layernorm_kernel
+    float xv[FN][FM][16];
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float r4[4] = {lo_bf(rv[i][j][g].x), hi_bf(rv[i][j][g].x), lo_bf(rv[i][j][g].y), hi_bf(rv[i][j][g].y)};
+#pragma unroll
+          for (int e = 0; e < 4; e++) xv[i][j][4 * g + e] = rbf(rbf(acc[i][j][4 * g + e] + bv[i][g][e]) + r4[e]);
+        }
+    float* red = reinterpret_cast<float*>(smem);  // [QG][BM] partials (the ring is free past the k loop)
+    float* red2 = red + QG * BM;
+    float* smean = red2 + QG * BM;                // [BM] mean, [BM] rstd
+    float* srstd = smean + BM;
+    uint16_t* stx = reinterpret_cast<uint16_t*>(srstd + BM);  // staging tile of x', then of Y (BM x SP)
+    static_assert((4 * QG * BM + 2 * BM) * 4 + BM * SP * 2 <= SMEM * 2, "the epilogue fits the ring");
+    // this tile's row sums, then centred square sums (two passes over registers, waves wn = 0, 1 combined in order)
+    float tsum[FM], tm2[FM];
+    __syncthreads();  // every wave is past its last ring read
+#pragma unroll
+    for (int j = 0; j < FM; j++) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) a += xv[i][j][e];
+      a = halves_sum(a);
+      if (hk == 0) red[wn * BM + wm * WTM + j * 32 + lr] = a;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FM; j++) {
+      const int r = wm * WTM + j * 32 + lr;
+      tsum[j] = red[r] + red[BM + r];
+      const float mt = tsum[j] * (1.0f / BN);
+      float q = 0.f;
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const float d = xv[i][j][e] - mt;
+          q += d * d;
+        }
+      q = halves_sum(q);
+      if (hk == 0) red2[wn * BM + r] = q;
+    }
+    // x' to the staging tile meanwhile
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int r = wm * WTM + j * 32 + lr, c = wn * WTN + i * 32 + 8 * g + 4 * hk;
+          *reinterpret_cast<u32x2*>(stx + r * SP + c) =
+              u32x2{pack2(xv[i][j][4 * g], xv[i][j][4 * g + 1]), pack2(xv[i][j][4 * g + 2], xv[i][j][4 * g + 3])};
+        }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FM; j++) tm2[j] = red2[wm * WTM + j * 32 + lr] + red2[BM + wm * WTM + j * 32 + lr];
+    // publish (one lane per row: the wn = 0, hk = 0 lanes)
+    uint64_t* sbase = rl.stats + ((size_t)rb * tiles_n) * BM * 2;
+    if (wn == 0 && hk == 0) {
+#pragma unroll
+      for (int j = 0; j < FM; j++) {
+        const int r = wm * WTM + j * 32 + lr;
+        uint64_t* w = sbase + ((size_t)tile_n * BM + r) * 2;
+        __hip_atomic_store(GPTR(uint64_t, w), ((uint64_t)ep << 32) | __float_as_uint(tsum[j]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(GPTR(uint64_t, w + 1), ((uint64_t)ep << 32) | __float_as_uint(tm2[j]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    // x' out while the other tiles publish
+    store_staged<BM, BN, SP, NT>(stx, rl.X, rl.ldx, m0, n0, M, N, tid);
+    // gather: thread (q, r) reads the entries of tiles q, q + QG, ... for row r, until all carry this epoch
+    {
+      const int r = tid % BM, q = tid / BM;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(sbase, (short)0, (int)(tiles_n * BM * 16), 0x00020000);
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      float ssum = 0.f;
+      constexpr int KMAX = (kRlnMaxTiles + QG - 1) / QG;
+      float es[KMAX], em2[KMAX];  // fixed indices only (unrolled, predicated): registers, not scratch
+      const int nmine = (tiles_n - q + QG - 1) / QG;
+      for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < KMAX; k++) {
+          es[k] = 0.f;
+          em2[k] = 0.f;
+          if (k < nmine) {
+            uint32_t off = (uint32_t)(((q + k * QG) * BM + r) * 16);
+            asm volatile("" : "+v"(off));  // a new offset each pass: the load is not hoisted out of the loop
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16);
+            ok = ok && v.y == ep && v.w == ep;
+            es[k] = __uint_as_float(v.x);
+            em2[k] = __uint_as_float(v.z);
+          }
+        }
+        if (ok) break;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kRlnTimeout) {
+          __hip_atomic_store(GPTR(uint32_t, rl.sync), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+#pragma unroll
+      for (int k = 0; k < KMAX; k++) ssum += es[k];  // zeros past nmine
+      red[q * BM + r] = ssum;
+      __syncthreads();
+      float tot = 0.f;
+#pragma unroll
+      for (int k2 = 0; k2 < QG; k2++) tot += red[k2 * BM + r];
+      const float mean = tot / (float)N;
+      // M2 = sum over tiles of (M2_t + BN (mean_t - mean)^2): the centred square sum over the whole row
+      float m2 = 0.f;
+#pragma unroll
+      for (int k = 0; k < KMAX; k++) {
+        const float d = es[k] * (1.0f / BN) - mean;
+        m2 += k < nmine ? em2[k] + (float)BN * d * d : 0.f;
+      }
+      red2[q * BM + r] = m2;
+      __syncthreads();
+      if (q == 0) {
+        float t2 = 0.f;
+#pragma unroll
+        for (int k2 = 0; k2 < QG; k2++) t2 += red2[k2 * BM + r];
+        smean[r] = mean;
+        srstd[r] = 1.0f / sqrtf(t2 / (float)N + rl.eps);
+      }
+    }
+    __syncthreads();  // statistics read by every thread of this workgroup; the staging tile of x' is stored
+    if (tid == 0) {
+      uint32_t* dep = gen + 1;
+      const uint32_t old = __hip_atomic_fetch_add(GPTR(uint32_t, dep), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == (uint32_t)tiles_n - 1) {  // the row block's last: re-arm for the next launch
+        __hip_atomic_store(GPTR(uint32_t, dep), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(GPTR(uint32_t, gen), ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    // Y = (x' - mean) rstd gamma + beta, the order of residual_layernorm_kernel
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++) {
+        const int r = wm * WTM + j * 32 + lr;
+        const float mu = smean[r], rs2 = srstd[r];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float gg[4] = {lo_bf(gmv[i][g].x), hi_bf(gmv[i][g].x), lo_bf(gmv[i][g].y), hi_bf(gmv[i][g].y)};
+          const float bb[4] = {lo_bf(btv[i][g].x), hi_bf(btv[i][g].x), lo_bf(btv[i][g].y), hi_bf(btv[i][g].y)};
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) y[e] = (xv[i][j][4 * g + e] - mu) * rs2 * gg[e] + bb[e];
+          const int c = wn * WTN + i * 32 + 8 * g + 4 * hk;
+          *reinterpret_cast<u32x2*>(stx + r * SP + c) = u32x2{pack2(y[0], y[1]), pack2(y[2], y[3])};
+        }
+      }
+    __syncthreads();
+    store_staged<BM, BN, SP, NT>(stx, rl.Y, rl.ldy, m0, n0, M, N, tid);
+    return;
+  }
 
   // ---- KS = 2: the second k group's partial tiles join the first's, in a fixed order
   if constexpr (KS == 2) {
@@ -568,6 +779,17 @@ __global__ __launch_bounds__(512) void gemm_bf16_kh2_kernel(
   gemm_body<BM, BN, 2, 2, S, false, 2>(A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols,
                                        tiles_m, tiles_n, splits, kt_per_split, ws, cnt, P, ldp, p_split, nullptr,
                                        nullptr);
+}
+
+// The residual + LayerNorm form (RlnArgs): one k range per tile (no split-K), 4-wave 2 x 2 tiles
+template <int BM, int BN, int S>
+__global__ __launch_bounds__(256) void gemm_rln_kernel(const uint16_t* __restrict__ A, long lda,
+                                                       const uint16_t* __restrict__ W, long ldw,
+                                                       const float* __restrict__ bias, const uint16_t* __restrict__ R,
+                                                       long ldr, int M, int N, int K, int Kw, int tiles_m, int tiles_n,
+                                                       RlnArgs rl) {
+  gemm_body<BM, BN, 2, 2, S, false, 1, true>(A, lda, W, ldw, bias, R, ldr, 0, nullptr, 0, M, N, K, Kw, 0, 0, tiles_m,
+                                             tiles_n, 1, Kw / BK, nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, rl);
 }
 
 // W8A8: C = epi(((float)(Aq Wq^T) * sa[m]) * sw[n] + bias[n]) (K, Kw, lda, ldw in 16-bit units); P (raw int32
@@ -1306,4 +1528,40 @@ extern "C" int mx_gemm_i8(hipStream_t st, int cfg, const int8_t* A, long lda, co
   }
 #undef I_
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// Residual Linear + LayerNorm in one launch: X = bf16(bf16(A W^T + bias) + R) (the residual stream) and
+// Y = LayerNorm(X) with gamma, beta, eps (the next normalisation). Replaces the Linear with the residual
+// (md2fast.py:154, :157 lin_res) and the LayerNorm that reads its output (:155 ln2, the next block's ln1 at :153),
+// i.e. mx_gemm_bf16_partial + mx_residual_layernorm with one split. The row statistics combine the tiles' sums and
+// centred square sums (exact identity for the centred sum of squares; fp32 summation in another order than the
+// row kernel). stats: stats_words >= mx_gemm_res_ln_stats_words(M, N) 64-bit words; sync: sync_words >=
+// mx_gemm_res_ln_sync_words(M) 32-bit words, zeroed once by the caller, then owned by it: calls that share them
+// must be ordered on one stream. sync[0] != 0 after a call means a wait timed out (results undefined; zero sync
+// and stats before the next call). Needs N a multiple of 64 (at most 4096) and a grid of at most one workgroup per
+// CU ((M / 64 rounded up) x (N / 64) <= the device's CU count), else MX_ESHAPE.
+extern "C" long mx_gemm_res_ln_stats_words(int M, int N) { return (long)((M + 63) / 64) * (N / 64) * 64 * 2; }
+extern "C" long mx_gemm_res_ln_sync_words(int M) { return 1 + 2L * ((M + 63) / 64); }
+
+extern "C" int mx_gemm_bf16_res_ln(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                                   const float* bias, const uint16_t* R, long ldr, uint16_t* X, long ldx,
+                                   const uint16_t* gamma, const uint16_t* beta, uint16_t* Y, long ldy, int M, int N,
+                                   int K, int Kw, float eps, uint64_t* stats, long stats_words, uint32_t* sync,
+                                   long sync_words) {
+  if (!R || !X || !gamma || !beta || !Y || !stats || !sync) return MX_ENULL;
+  int rc = mx_gemm_check(3, 1, A, lda, W, ldw, bias, R, ldr, X, ldx, M, N, K, Kw, 0, nullptr, 0, nullptr, 0);
+  if (rc) return rc;
+  if (N % 64 || N / 64 > kRlnMaxTiles) return MX_ESHAPE;
+  if (ldy % 4 || ldy < N || ((uintptr_t)Y & 7) || (((uintptr_t)gamma | (uintptr_t)beta) & 7)) return MX_ELAYOUT;
+  if (stats_words < mx_gemm_res_ln_stats_words(M, N) || sync_words < mx_gemm_res_ln_sync_words(M)) return MX_ESHAPE;
+  if ((uintptr_t)stats & 15) return MX_ELAYOUT;
+  const int tm = (M + 63) / 64, tn = N / 64;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return MX_ELAUNCH;
+  if ((long)tm * tn > cus) return MX_ESHAPE;  // every tile of a row block resident at once
+  const RlnArgs rl{gamma, beta, X, ldx, Y, ldy, eps, stats, sync};
+  hipLaunchKernelGGL((gemm_rln_kernel<64, 64, 4>), dim3(tm * tn), dim3(256), 0, st, A, lda, W, ldw, bias, R, ldr, M,
+                     N, K, Kw, tm, tn, rl);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }

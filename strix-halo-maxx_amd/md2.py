@@ -53,6 +53,11 @@ class VisionTower:
         # tiles, and there the fp32 partials would only add traffic)
         self.splitk = hasattr(self.blocks[0]["proj"], "partial") if self.blocks else False
         self.splitk_max_rows = 8192
+        # which residual Linears run with their LayerNorm fused in (one launch instead of two) where the grid fits: the
+        # attention projection (1152 x 1152, 64 x 64 tiles: 8.4 + 4.9 us -> one launch, 16-19 us less per frame). fc2
+        # would need its 4304-deep k loop on 64 x 64 tiles without split-K, slower than its split-K GEMM plus the
+        # separate residual LayerNorm (2.31 against 2.21 ms per frame), so it keeps the two launches.
+        self.fuse_res_ln = {"proj"}
 
     def _attn(self, b, h, B):
         T, H, hd, D = self.T, self.H, self.hd, self.D
@@ -61,13 +66,27 @@ class VisionTower:
         q, k, v = (q5[:, :, i].transpose(1, 2) for i in range(3))   # (B, H, T, hd) strided views
         return self.attn(q, k, v).view(B * T, D)            # (B*T, D)
 
+    def _fuse(self, lin, B, which):
+        return (which in self.fuse_res_ln and hasattr(lin, "res_ln")
+                and ops.res_ln_fits(B * self.T, lin.N, self.dev))
+
     def _block_sk(self, b, x, h, B, next_ln):
         """Split-K form of one block: x (residual stream) and h = ln1(x) in; the block output and next_ln(output)
-        out (the second is None when next_ln is None)."""
+        out (the second is None when next_ln is None). Where the grid fits (a few crops), a residual Linear and the
+        LayerNorm after it are one launch (MxLin.res_ln)."""
         a = self._attn(b, h, B)
-        x1, h2 = ops.residual_layernorm(b["proj"].partial(a), b["proj"].b, x, b["ln2"], eps=self.eps)
+        if self._fuse(b["proj"], B, "proj"):
+            x1, h2 = b["proj"].res_ln(a, x, b["ln2"], eps=self.eps)
+        else:
+            x1, h2 = ops.residual_layernorm(b["proj"].partial(a), b["proj"].b, x, b["ln2"], eps=self.eps)
         f = b["fc1"](h2, gelu=True)
+        if next_ln is not None and self._fuse(b["fc2"], B, "fc2"):
+            return b["fc2"].res_ln(f, x1, next_ln, eps=self.eps)
         return ops.residual_layernorm(b["fc2"].partial(f), b["fc2"].b, x1, next_ln, eps=self.eps)
+
+    def rln_error(self):
+        """Non-zero if a fused residual-LayerNorm launch timed out waiting for its row block (results undefined)."""
+        return ops.RlnWorkspace.get(self.dev).error()
 
     # ---- one pre-LN block (md2fast.py:152-157)
     def _use_splitk(self, B):

@@ -208,6 +208,25 @@ class MxLin:
         _lib.check(_partial(self, cfg, sp, x2, P, M), "mx_gemm_bf16_partial")
         return P
 
+    def res_ln(self, x, res, ln, eps=1e-5, x_out=None, y_out=None):
+        """x' = bf16(bf16(x W^T + b) + res) and y = LayerNorm(x'; ln = (gamma, beta)) in one launch
+        (mx_gemm_bf16_res_ln): the residual Linear and the normalisation that reads its output. Only where
+        res_ln_fits(M, N); returns (x', y)."""
+        x2 = _rows(x, self.K)
+        if x2.shape[1] != self.K:
+            raise ValueError(f"input width {x2.shape[1]} != {self.K}")
+        M, N = x2.shape[0], self.N
+        r2 = _rows(res, N)
+        X = x_out if x_out is not None else torch.empty(M, N, device=x2.device, dtype=BF)
+        Y = y_out if y_out is not None else torch.empty(M, N, device=x2.device, dtype=BF)
+        ws = RlnWorkspace.get(x2.device)
+        _lib.check(_lib.load().mx_gemm_bf16_res_ln(
+            stream(), x2.data_ptr(), x2.stride(0), self.w.data_ptr(), self.w.stride(0), ptr(self.b), r2.data_ptr(),
+            r2.stride(0), X.data_ptr(), X.stride(0), ln[0].data_ptr(), ln[1].data_ptr(), Y.data_ptr(), Y.stride(0), M,
+            N, self.K, self.Kw, float(eps), ws.stats.data_ptr(), ws.stats.numel(), ws.sync.data_ptr(),
+            ws.sync.numel()), "mx_gemm_bf16_res_ln")
+        return X, Y
+
 
 _TUNED_P = {}  # (M, N, Kw) -> (cfg, splits) of the split-K partial GEMM
 
@@ -500,6 +519,41 @@ def layernorm(x, w, b, eps=1e-5, out=None):
     call("mx_layernorm", stream(), x2.data_ptr(), x2.stride(0), w.data_ptr(), b.data_ptr(), y.data_ptr(),
          y.reshape(-1, D).stride(0), x2.shape[0], D, float(eps))
     return y.view(*x.shape) if out is None else y
+
+
+class RlnWorkspace:
+    """Row statistics and their generation counters for mx_gemm_bf16_res_ln on one device, allocated zeroed once at
+    their largest size (the launch allows at most one 64 x 64 tile per CU, so at most 256 tiles: 256 x 128 stats
+    words; 1 + 2 x 256 sync words) and then owned by the kernel, which leaves them ready for the next call. Calls on
+    one stream serialise; two streams must not share them."""
+    _by_dev = {}
+
+    def __init__(self, device):
+        self.stats = torch.zeros(256 * 128, device=device, dtype=torch.int64)
+        self.sync = torch.zeros(1024, device=device, dtype=torch.int32)
+
+    @classmethod
+    def get(cls, device):
+        d = torch.device(device)
+        key = d.index if d.index is not None else torch.cuda.current_device()
+        if key not in cls._by_dev:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("the residual-LayerNorm workspace must exist before graph capture")
+            cls._by_dev[key] = cls(d)
+        return cls._by_dev[key]
+
+    def error(self):
+        """Non-zero if a wait of a fused residual-LayerNorm GEMM timed out (its results are then undefined)."""
+        return int(self.sync[0].item())
+
+
+def _cu_count(device):
+    return torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
+
+
+def res_ln_fits(M, N, device):
+    """mx_gemm_bf16_res_ln's shape rule: N a multiple of 64 (at most 4096) and one 64 x 64 tile per CU at most."""
+    return N % 64 == 0 and N <= 4096 and ((M + 63) // 64) * (N // 64) <= _cu_count(device)
 
 
 def residual_layernorm(P, bias, res, ln=None, eps=1e-5, x_out=None, y_out=None):

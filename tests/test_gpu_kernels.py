@@ -195,6 +195,58 @@ def test_residual_layernorm_matches_unfused(dev):
     assert torch.equal(yo.cpu(), ops.layernorm(xo, gam, bet, eps=1e-6).cpu())
 
 
+@pytest.mark.parametrize("M,K", [(729, 1152), (729, 4304), (100, 1152)])
+def test_gemm_res_ln_matches_unfused(dev, M, K):
+    """mx_gemm_bf16_res_ln (residual Linear + LayerNorm in one launch, row statistics exchanged between the tiles of
+    a row block): x' within one ulp of the pre-rounding sum plus one of x' of the CPU restatement (another summation
+    order than the CPU's, as test_residual_layernorm_matches_unfused); y within one bf16 ulp (of the largest operand
+    of its last step) of the row LayerNorm kernel applied to the same x' (statistics summed in another order), on at
+    most 0.1 % of the elements, and as close to an fp32 LayerNorm as that
+    kernel's output (its bf16 rounding, ~1.5e-3 rel-L2, within 5 %). Three calls
+    in a row with new inputs (each launch takes new epochs from the row blocks' generation counters), no timeout."""
+    N = 1152
+    g = gen(M + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    gam = (1 + 0.1 * torch.randn(N, generator=g)).to(BF).to(dev)
+    bet = (0.1 * torch.randn(N, generator=g)).to(BF).to(dev)
+    lin = ops.MxLin(w, b)
+    assert ops.res_ln_fits(M, N, dev)
+    ws = ops.RlnWorkspace.get(dev)
+    for call in range(3):
+        x = torch.randn(M, K, generator=g).to(BF).to(dev)
+        r = (torch.randn(M, N, generator=g) * 4).to(BF).to(dev)
+        print(f"res_ln M={M} K={K} call {call}", flush=True)
+        xo, yo = lin.res_ln(x, r, (gam, bet), eps=1e-6)
+        torch.cuda.synchronize()
+        assert ws.error() == 0
+        gsum = x.cpu().float() @ w.float().t() + lin.b.cpu().float()
+        exp = (gsum.to(BF).float() + r.cpu().float()).to(BF)
+        a, f = xo.float().cpu(), exp.float()
+        tol = 2.0 ** -7 * (gsum.abs() + torch.maximum(a.abs(), f.abs())) + 1e-30
+        over, frac = int(((a - f).abs() > tol).sum()), (a != f).float().mean().item()
+        assert over == 0 and frac <= 2e-2, (over, frac)
+        y_row = ops.layernorm(xo, gam, bet, eps=1e-6)
+        y32 = F.layer_norm(xo.float().cpu(), (N,), gam.float().cpu(), bet.float().cpu(), eps=1e-6)
+        # one bf16 ulp of the largest operand of y = t + beta, t = (x' - mean) rstd gamma: where beta cancels t, a
+        # last-bit change of the statistics moves a tiny y by more than one of its own ulps
+        yb, yr, bb = yo.float().cpu(), y_row.float().cpu(), bet.float().cpu().expand(M, N)
+        scale = torch.maximum(torch.maximum(yb.abs(), yr.abs()), torch.maximum(bb.abs(), (y32 - bb).abs()))
+        assert bool(((yb - yr).abs() <= 2.0 ** -7 * scale + 1e-30).all()), (yb - yr).abs().max().item()
+        assert (yb != yr).float().mean().item() <= 1e-3
+        assert rel(yo, y32) <= 1.05 * rel(y_row, y32) + 1e-5, (rel(yo, y32), rel(y_row, y32))
+
+
+def test_gemm_res_ln_refuses_a_grid_larger_than_the_gpu(dev):
+    """Two crops (1458 rows: 23 x 18 tiles > 256 CUs) cannot all be resident: refused before launching."""
+    lin = ops.MxLin(torch.zeros(1152, 1152, dtype=BF), torch.zeros(1152))
+    x = torch.zeros(1458, 1152, dtype=BF, device=dev)
+    ln = (torch.ones(1152, dtype=BF, device=dev), torch.zeros(1152, dtype=BF, device=dev))
+    assert not ops.res_ln_fits(1458, 1152, dev)
+    with pytest.raises(_lib.MxError, match="-2"):
+        lin.res_ln(x, x, ln)
+
+
 @pytest.mark.parametrize("cfg", [None, 0, 7, 8, 12, 15, 16, 17])
 def test_gemm_epilogues_match_unfused(dev, cfg):
     """GELU applied to the bf16-rounded linear output, then + residual (md2fast.py:55-67; i8gemm.hip:378); the gated
