@@ -53,10 +53,11 @@ def gemm_symbol(cfg):
 
 
 def op_classes(vt, img):
-    """The tower's batch-1 op classes (its split-K form: partial GEMMs for the two residual Linears, each reduced by
-    the fused residual-LayerNorm kernel) as {label: (kernel symbol, flops per launch, algorithmic HBM bytes per launch,
-    fn(i, block))}; one eager pass
-    keeps every block's real operands, and fn(i, block) relaunches op `label` of block i on them."""
+    """The tower's batch-1 op classes, the launches its blocks run: the attention projection with its residual and
+    ln2 in one launch (mx_gemm_bf16_res_ln) where the tower fuses it, else as a partial GEMM plus the residual-
+    LayerNorm kernel; fc2 as a split-K partial GEMM plus the residual-LayerNorm kernel (the next block's ln1). As
+    {label: (kernel symbol, flops per launch, algorithmic HBM bytes per launch, fn(i, block))}; one eager pass keeps
+    every block's real operands, and fn(i, block) relaunches op `label` of block i on them."""
     import torch
     import strix_halo_maxx_amd.ops as ops
     B = img.shape[0]
@@ -64,6 +65,7 @@ def op_classes(vt, img):
     M = B * T
     blocks = vt.blocks
     saved = []
+    fused_proj = vt._fuse(blocks[0]["proj"], B, "proj")
     x = vt.embed(img)
     h = ops.layernorm(x, *blocks[0]["ln1"], eps=vt.eps)
     for i, b in enumerate(blocks):
@@ -71,8 +73,12 @@ def op_classes(vt, img):
         q5 = qkv.view(B, T, 3, H, hd)
         q, k, v = (q5[:, :, j].transpose(1, 2) for j in range(3))
         a = vt.attn(q, k, v).view(M, D)
-        pp = b["proj"].partial(a)
-        x1, h2 = ops.residual_layernorm(pp, b["proj"].b, x, b["ln2"], eps=vt.eps)
+        if fused_proj:
+            pp = None
+            x1, h2 = b["proj"].res_ln(a, x, b["ln2"], eps=vt.eps)
+        else:
+            pp = b["proj"].partial(a)
+            x1, h2 = ops.residual_layernorm(pp, b["proj"].b, x, b["ln2"], eps=vt.eps)
         f = b["fc1"](h2, gelu=True)
         pf = b["fc2"].partial(f)
         nxt = blocks[i + 1]["ln1"] if i + 1 < len(blocks) else vt.post_ln
@@ -82,7 +88,8 @@ def op_classes(vt, img):
     outs = {n: torch.empty(M, w, device=x.device, dtype=torch.bfloat16)
             for n, w in (("h", D), ("qkv", 3 * D), ("x", D), ("f", blocks[0]["fc1"].N))}
     a_out = torch.empty(B, T, D, device=x.device, dtype=torch.bfloat16)
-    pp_out, pf_out = torch.empty_like(saved[0][4]), torch.empty_like(saved[0][8])
+    pp_out = None if fused_proj else torch.empty_like(saved[0][4])
+    pf_out = torch.empty_like(saved[0][8])
 
     def sym(l):
         cfg = l.cfgs.get(M) or ops._TUNED.get((M, l.N, l.Kw))
@@ -93,23 +100,31 @@ def op_classes(vt, img):
         return f"{gemm_symbol(cfg)} x{sp} splits"
     attn_sym = ops.sdpa_symbol(B, H, T, hd)
     F, Kw2 = blocks[0]["fc1"].N, blocks[0]["fc2"].Kw
-    sp_proj, sp_fc2 = saved[0][4].shape[0], saved[0][8].shape[0]
+    sp_proj, sp_fc2 = (0 if fused_proj else saved[0][4].shape[0]), saved[0][8].shape[0]
     # algorithmic HBM bytes per launch: every operand once (bf16 activations / weights, fp32 split-K partials)
     classes = {
         "qkv": (sym(blocks[0]["qkv"]), 2 * M * D * 3 * D, 2 * (M * D + 3 * D * D + M * 3 * D),
                 lambda i, b: b["qkv"](saved[i][1], out=outs["qkv"])),
         "attn": (attn_sym, 4 * B * H * T * T * hd, 8 * M * D, lambda i, b: ops.sdpa(*saved[i][2], out=a_out)),
-        "proj": (psym(blocks[0]["proj"]), 2 * M * D * D, 2 * (M * D + D * D) + 4 * sp_proj * M * D,
-                 lambda i, b: b["proj"].partial(saved[i][3], out=pp_out)),
-        "res_ln2": ("residual_layernorm_kernel<3>", 0, (4 * sp_proj + 6) * M * D, lambda i, b: ops.residual_layernorm(
-            saved[i][4], b["proj"].b, saved[i][0], b["ln2"], eps=vt.eps, x_out=outs["x"], y_out=outs["h"])),
+    }
+    if fused_proj:  # a, W, the residual in; x' and ln2(x') out
+        classes["proj"] = ("gemm_rln_kernel<64, 64, 4>", 2 * M * D * D, 2 * (M * D + D * D + 3 * M * D),
+                           lambda i, b: b["proj"].res_ln(saved[i][3], saved[i][0], b["ln2"], eps=vt.eps,
+                                                         x_out=outs["x"], y_out=outs["h"]))
+    else:
+        classes["proj"] = (psym(blocks[0]["proj"]), 2 * M * D * D, 2 * (M * D + D * D) + 4 * sp_proj * M * D,
+                           lambda i, b: b["proj"].partial(saved[i][3], out=pp_out))
+        classes["res_ln2"] = ("residual_layernorm_kernel<3>", 0, (4 * sp_proj + 6) * M * D,
+                              lambda i, b: ops.residual_layernorm(saved[i][4], b["proj"].b, saved[i][0], b["ln2"],
+                                                                  eps=vt.eps, x_out=outs["x"], y_out=outs["h"]))
+    classes.update({
         "fc1": (sym(blocks[0]["fc1"]), 2 * M * D * F, 2 * (M * D + F * D + M * F),
                 lambda i, b: b["fc1"](saved[i][6], gelu=True, out=outs["f"])),
         "fc2": (psym(blocks[0]["fc2"]), 2 * M * blocks[0]["fc2"].K * D, 2 * (M * F + D * Kw2) + 4 * sp_fc2 * M * D,
                 lambda i, b: b["fc2"].partial(saved[i][7], out=pf_out)),
         "res_ln1": ("residual_layernorm_kernel<3>", 0, (4 * sp_fc2 + 6) * M * D, lambda i, b: ops.residual_layernorm(
             saved[i][8], b["fc2"].b, saved[i][5], saved[i][9], eps=vt.eps, x_out=outs["x"], y_out=outs["h"])),
-    }
+    })
     return classes
 
 

@@ -343,12 +343,14 @@ __device__ __forceinline__ void gemm_body(
 #endif
   };
 
-  // The epilogue's operands: bias, per-row / per-column scales and, on 4-wave tiles, the residual. Tiles of at most 2 x 2
-  // MFMA blocks per wave load them before the k loop, so their latency hides under it (nothing in the loop uses them,
-  // so the compiler puts no wait for them there); larger tiles load them after it (their registers are taken). Each
+  // The epilogue's operands: bias, per-row / per-column scales and, on 4-wave tiles, the residual. Small 4-wave tiles
+  // load them before the k loop, so their latency hides under it (nothing in the loop uses them, so the compiler puts
+  // no wait for them there); larger tiles load them after it (their registers are taken). Each
   // pointer is checked: the raw-sum modes (P) return before the epilogue and may pass null scales, bias or residual.
   constexpr bool HOIST_R = FN * FM <= 4;
-  constexpr bool EARLY = NW == 4 && FN * FM <= 4;
+  // 2 x 2 blocks per wave hold 47 more VGPRs through the loop: only where the ring already keeps the CU to one
+  // workgroup (more than 80 KB of LDS); with a smaller ring they would halve the workgroups per CU (> 256 registers)
+  constexpr bool EARLY = NW == 4 && (FN * FM <= 2 || (FN * FM <= 4 && S * STAGE * 2 > 80 * 1024));
   f32x4 bv[FN][4];
   f32x4 swv[I8 ? FN : 1][4];
   float sav[I8 ? FM : 1];
