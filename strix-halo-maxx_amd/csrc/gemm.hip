@@ -1014,7 +1014,10 @@ constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0, 4}, {64, 128, 4, 1, 0, 4}, {128, 64
                          // 8-wave forms of the 2 x 2 tiles, two k groups (kh = 2): batch-1 grids, one workgroup per
                          // CU, whose k loop waits on LDS reads at the 4-wave rate
                          {128, 128, 4, 1, 0, 8, 2}, {64, 128, 4, 1, 0, 8, 2}, {128, 64, 4, 1, 0, 8, 2},
-                         {64, 64, 4, 2, 0, 8, 2}};
+                         {64, 64, 4, 2, 0, 8, 2},
+                         // one wave row x 4 wave columns, 3 x 1 MFMA blocks per wave: 96-row tiles for M = 729
+                         // (8 row tiles, the same 768 padded rows as 128 and a third more workgroups)
+                         {96, 128, 4, 1, 0, 4}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -1255,6 +1258,7 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
     case 5: e = L_(128, 256, 3); break;
     case 6: e = L_(64, 64, 3); break;
     case 7: e = L_(128, 128, 2); break;
+    case 23: e = launch<96, 128, 1, 4, 4>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 15: e = launch<256, 256, 2, 4, 2>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 16: e = launch<256, 128, 4, 2, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 17: e = launch<128, 256, 2, 4, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
@@ -1407,6 +1411,7 @@ extern "C" int mx_gemm_i8_partial(hipStream_t st, int cfg, int splits, const int
     case 5: e = I_(128, 256, 2, 2, 3); break;
     case 6: e = I_(64, 64, 2, 2, 3); break;
     case 7: e = I_(128, 128, 2, 2, 2); break;
+    case 23: e = I_(96, 128, 1, 4, 4); break;
     default: return MX_EBADCFG;
   }
 #undef I_
@@ -1464,6 +1469,7 @@ extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const u
     case 5: e = L_(128, 256, 3); break;
     case 6: e = L_(64, 64, 3); break;
     case 7: e = L_(128, 128, 2); break;
+    case 23: e = launch<96, 128, 1, 4, 4>(st, splits, A, lda, W, ldw, nullptr, nullptr, 0, 0, nullptr, 0, M, N, K, Kw, 0, 0, nullptr, nullptr, P, ldp, p_split); break;
 #define H_(BM, BN, S) launch_kh2<BM, BN, S>(st, splits, A, lda, W, ldw, nullptr, nullptr, 0, 0, nullptr, 0, M, N, K, Kw, 0, 0, P, ldp, p_split)
     case 19: e = H_(128, 128, 4); break;
     case 20: e = H_(64, 128, 4); break;
@@ -1522,6 +1528,7 @@ extern "C" int mx_gemm_i8(hipStream_t st, int cfg, const int8_t* A, long lda, co
     case 5: e = I_(128, 256, 2, 2, 3); break;
     case 6: e = I_(64, 64, 2, 2, 3); break;
     case 7: e = I_(128, 128, 2, 2, 2); break;
+    case 23: e = I_(96, 128, 1, 4, 4); break;
     case 15: e = I_(256, 256, 2, 4, 2); break;
     case 16: e = I_(256, 128, 4, 2, 3); break;
     case 17: e = I_(128, 256, 2, 4, 3); break;
