@@ -76,11 +76,18 @@ __device__ __forceinline__ float wave_total(float v) {
   v += dpp_mov<0x143, 0xc>(0.f, v);  // row_bcast31 into rows 2, 3
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+// Max of v over the 64 lanes, wave-uniform, by the same DPP steps as wave_total (exact in any order; rows a broadcast
+// skips keep their own value). Every lane must be active.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_mov<0xb1>(v, v));
+  v = fmaxf(v, dpp_mov<0x4e>(v, v));
+  v = fmaxf(v, dpp_mov<0x141>(v, v));
+  v = fmaxf(v, dpp_mov<0x140>(v, v));
+  v = fmaxf(v, dpp_mov<0x142, 0xa>(v, v));
+  v = fmaxf(v, dpp_mov<0x143, 0xc>(v, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 

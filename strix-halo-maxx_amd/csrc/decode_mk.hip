@@ -256,13 +256,11 @@ __device__ __forceinline__ int wave_total_i(int v) {
   v += mv(0, v, integral_constant<int, 0x143>{}, integral_constant<int, 0xc>{});
   return __builtin_amdgcn_readlane(v, 63);
 }
-// Per-token int8 quantisation of a bf16 vector held by one wave, NC chunks of 8 values per lane (chunk c = lane +
-// 64 i at src word 4 c): s = max(max |x|, 1e-5) / 127, q = trunc(x / s + 0.5 sign) with the IEEE quotient
-// (tgemm.py:81-91 _quant_rows, decode.hip's quant_vals_block_i8); q of chunk c to dst bytes 8 c .. 8 c + 7. Returns s
-// (wave-uniform). One wave quantises up to 8192 values here, so the quotient is taken as x * (1 / s), within 1.5e-5
-// of x / s for |x / s| <= 127 (two roundings of 2^-24 relative); only where |t| + 0.5 lies within 1e-4 of an integer
-// could that change the truncated result, and there the exact quotient decides. The q values are those of the IEEE
-// division.
+// Per-token int8 quantisation of a bf16 vector: s = max(max |x|, 1e-5) / 127, q = trunc(x / s + 0.5 sign) with the
+// IEEE quotient (tgemm.py:81-91 _quant_rows, decode.hip's quant_vals_block_i8). The quotient is taken as x * (1 / s),
+// within 1.5e-5 of x / s for |x / s| <= 127 (two roundings of 2^-24 relative); only where |t| + 0.5 lies within 1e-4
+// of an integer could that change the truncated result, and there the exact quotient decides. The q values are those
+// of the IEEE division.
 // 8 values of a bf16 chunk quantised with scale s (rs = 1 / s) into two words; near: set where the multiply form's
 // |t| + 0.5 lies within 1e-4 of an integer (exact = true takes the IEEE quotient instead)
 __device__ __forceinline__ uint2 qpack_i8(const u32x4& v, float s, float rs, bool exact, bool& near) {
@@ -279,36 +277,9 @@ __device__ __forceinline__ uint2 qpack_i8(const u32x4& v, float s, float rs, boo
   }
   return make_uint2(w[0], w[1]);
 }
-template <int NC>
-__device__ __forceinline__ float quant_wave_i8(const uint32_t* src, uint32_t* dst, int lane) {
-  float amax = 0.f;
-#pragma unroll 4
-  for (int i = 0; i < NC; i++) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(&src[4 * (lane + 64 * i)]);
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint32_t ve = v[e];
-      amax = fmaxf(amax, fmaxf(fabsf(lo_bf(ve)), fabsf(hi_bf(ve))));
-    }
-  }
-  const float s = fmaxf(wave_max(amax), 1e-5f) / 127.0f;
-  const float rs = 1.0f / s;
-#pragma unroll 4
-  for (int i = 0; i < NC; i++) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(&src[4 * (lane + 64 * i)]);
-    bool near = false;
-    uint2 q = qpack_i8(v, s, rs, false, near);
-    if (__any(near)) {  // wave-uniform and rare: the chunk again with the IEEE quotient
-      bool unused = false;
-      q = qpack_i8(v, s, rs, true, unused);
-    }
-    *reinterpret_cast<uint2*>(&dst[2 * (lane + 64 * i)]) = q;
-  }
-  return s;
-}
-
-// The same quantisation by all the workgroup's waves (every wave calls it at the same point; it holds two barriers):
-// one wave alone spends ~6 us on 8192 values, the workgroup ~0.6 us. red: one float per wave.
+// The quantisation of NCH chunks of 8 values (chunk c at src word 4 c, q to dst bytes 8 c .. 8 c + 7) by all the
+// workgroup's waves (every wave calls it at the same point; it holds two barriers); returns s to every thread. One
+// wave alone spent ~6 us on 8192 values (1.9 us on 2048), the workgroup ~0.6 us. red: one float per wave.
 template <int NCH>
 __device__ __forceinline__ float quant_block_i8(const uint32_t* src, uint32_t* dst, float* red, int tid) {
   const int lane = tid & 63, wave = tid >> 6;
@@ -552,8 +523,8 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         bar();  // g2 ready (W8A8: g gathered, then quantised by all waves)
         if (I8) sg = quant_block_i8<MK_F / 8>(gs, gq, qred, tid);
         xgather<MK_D / 2>(ll + LL_A, E(l, 2), as2, err, fail);
-        if (I8) sa = quant_wave_i8<MK_D / 512>(as2, aq, lane);  // alone: the compute waves are in phase B
-        bar();  // a ready
+        bar();  // a ready (W8A8: then quantised by all waves; the compute waves are done with phase B)
+        if (I8) sa = quant_block_i8<MK_D / 8>(as2, aq, qred, tid);
         bar();  // the partial sums in pb / pc
         float xn = 0.f;
         if (lane < nr) {
@@ -707,6 +678,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
           }
         }
         bar();  // a ready
+        if constexpr (I8) quant_block_i8<MK_D / 8>(as2, aq, qred, tid);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the proj rows have landed
 #pragma unroll
         for (int j = 0; j < JCA; j++) {
@@ -769,8 +741,8 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
         bar();  // g2 ready (W8A8: g gathered, then quantised by all waves)
         if (I8) sg = quant_block_i8<MK_F / 8>(gs, gq, qred, tid);
         xgather<MK_D / 2>(ll + LL_A, E(l, 2), as2, err, fail);
-        if (I8) sa = quant_wave_i8<MK_D / 512>(as2, aq, lane);  // alone: the compute waves are in phase B
-        bar();  // a ready
+        bar();  // a ready (W8A8: then quantised by all waves; the compute waves are done with phase B)
+        if (I8) sa = quant_block_i8<MK_D / 8>(as2, aq, qred, tid);
         bar();  // the partial sums in pb / pc
         // x'[n] = bf16(y2[n] + bf16(bf16(a Wp^T + bp)[n] + x[n])), y2 = bf16(g W2^T + b2): row r0 + lane (W8A8: each
         // Linear's fp32 dequant ((acc s_act) s_w) + b rounded once, i8gemm.hip:181-197)
@@ -970,6 +942,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
           issue(std::integral_constant<int, DIST + decltype(sc)::value>{}, Ln, lo, more);
         });
         bar();  // a ready
+        if constexpr (I8) quant_block_i8<MK_D / 8>(as2, aq, qred, tid);
         // ---- phase C from LDS
 #pragma unroll
         for (int j = 0; j < JC; j++) {
