@@ -277,6 +277,49 @@ __device__ __forceinline__ uint2 qpack_i8(const u32x4& v, float s, float rs, boo
   }
   return make_uint2(w[0], w[1]);
 }
+// |x| maxima of bf16 pairs, two per register: with the sign bit cleared, bf16 bit patterns order as unsigned 16-bit
+// integers the way their values do, so one AND and one packed 16-bit max (v_pk_max_u16) cover a pair of values.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 absmax2(u16x2 m, uint32_t p) {
+  return __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, p & 0x7fff7fffu));
+}
+__device__ __forceinline__ float absmax_value(u16x2 m) { return __uint_as_float((uint32_t)max(m.x, m.y) << 16); }
+
+// The exchange wave's side of a quantisation whose maximum it already holds (one float per lane: the LayerNorm's
+// output h, in its registers): the wave-uniform scale and its reciprocal to qs[0], qs[1] for quant_pass_i8, written
+// before the barrier that publishes the vector. Returns s. (Taking g's or a's maximum on the exchange wave while it
+// gathers them was measured slower than the workgroup's own pass: 2263 / 2276 against 2285 tok/s.)
+__device__ __forceinline__ float quant_scale_i8(float lane_amax, float* qs, int lane) {
+  const float s = fmaxf(wave_max(lane_amax), 1e-5f) / 127.0f;
+  if (lane == 0) {
+    qs[0] = s;
+    qs[1] = 1.0f / s;
+  }
+  return s;
+}
+// The quantising pass alone, by all the workgroup's waves after that barrier (every wave calls it at the same point;
+// one barrier at the end): chunks of 8 values as quant_block_i8, scale from qs. Returns s.
+template <int NCH>
+__device__ __forceinline__ float quant_pass_i8(const uint32_t* src, uint32_t* dst, const float* qs, int tid) {
+  const float s = qs[0], rs = qs[1];
+#pragma unroll
+  for (int c0 = 0; c0 < NCH; c0 += MK_T) {
+    const int c = c0 + tid;
+    if (c < NCH) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&src[4 * c]);
+      bool near = false;
+      uint2 q = qpack_i8(v, s, rs, false, near);
+      if (__any(near)) {
+        bool unused = false;
+        q = qpack_i8(v, s, rs, true, unused);
+      }
+      *reinterpret_cast<uint2*>(&dst[2 * c]) = q;
+    }
+  }
+  bar();
+  return s;
+}
+
 // The quantisation of NCH chunks of 8 values (chunk c at src word 4 c, q to dst bytes 8 c .. 8 c + 7) by all the
 // workgroup's waves (every wave calls it at the same point; it holds two barriers); returns s to every thread. One
 // wave alone spent ~6 us on 8192 values (1.9 us on 2048), the workgroup ~0.6 us. red: one float per wave.
@@ -416,7 +459,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
   __shared__ uint32_t sbest[MK_W];
   __shared__ uint64_t stab[MK_MAXL * MK_LP];
   __shared__ __attribute__((aligned(16))) uint32_t hq[MK_D / 4];  // W8A8: h quantised (int8)
-  __shared__ float qred[MK_W + 1];                                // W8A8: per-wave maxima of a quantisation
+  __shared__ float qred[MK_W + 1];                                // W8A8: per-wave maxima / a scale and reciprocal
   __shared__ int pbi[2 * MK_RW], pci[MK_RW];                      // W8A8: fc2 half-row and proj int32 sums
   uint32_t* gs = reinterpret_cast<uint32_t*>(big);
   uint32_t* as2 = gs + MK_F / 2;
@@ -729,10 +772,18 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
           load_vec<4>(xc, xb, lane);
         }
         ln_chunks<4, true>(xc, gc, bc, a.eps, MK_D, lane);
+        u16x2 hm = {0, 0};  // W8A8: this lane's |h| maximum, for the scale
 #pragma unroll
-        for (int i = 0; i < 4; i++) reinterpret_cast<u32x4*>(hs)[lane + 64 * i] = xc[i];
-        bar();  // h ready (W8A8: then quantised by all waves, shared by qkv and fc1, md2fast.py:174)
-        if (I8) quant_block_i8<MK_D / 8>(hs, hq, qred, tid);
+        for (int i = 0; i < 4; i++) {
+          reinterpret_cast<u32x4*>(hs)[lane + 64 * i] = xc[i];
+          if (I8) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) hm = absmax2(hm, xc[i][e]);
+          }
+        }
+        if (I8) quant_scale_i8(absmax_value(hm), qred, lane);
+        bar();  // h ready (W8A8: with its scale; then quantised by all waves, shared by qkv and fc1, md2fast.py:174)
+        if (I8) quant_pass_i8<MK_D / 8>(hs, hq, qred, tid);
         bar();  // the workgroup's phase A done
         xgather<MK_F / 4>(ll + LL_G, E(l, 1), gs, err, fail);
         if (!I8) bar();  // g1 ready
@@ -912,7 +963,7 @@ __global__ __launch_bounds__(MK_T) void decode_mk_kernel(MkArgs a) {
           issue(std::integral_constant<int, PF + decltype(sc)::value>{}, L, lo, true);
         });
         if constexpr (I8) {
-          sh = quant_block_i8<MK_D / 8>(hs, hq, qred, tid);
+          sh = quant_pass_i8<MK_D / 8>(hs, hq, qred, tid);
           hqv[0] = *reinterpret_cast<const u32x4*>(&hq[4 * lane]);
           hqv[1] = *reinterpret_cast<const u32x4*>(&hq[4 * (lane + 64)]);
         } else {
