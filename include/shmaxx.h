@@ -45,7 +45,8 @@ int mx_gemm_cfg_tile(int cfg, int* bm, int* bn);
  * mx_gemm_bf16; mx_gemm_bf16_partial splits K over workgroups), or MX_EBADCFG. No counterpart in the reference (its
  * configs are all one kind). */
 int mx_gemm_cfg_kind(int cfg);
-/* Raw split-K partials for a 4-wave cfg (either kind; 8-wave cfgs return MX_EBADCFG): P[s][m][n] = sum over split
+/* Raw split-K partials for a 4-wave cfg (either kind) or a two-k-group 8-wave cfg (19-22; the other 8-wave cfgs return
+ * MX_EBADCFG): P[s][m][n] = sum over split
  * s's k-steps of A[m,k] W[n,k] (fp32; row stride ldp, split stride p_split), no bias / activation / residual; the
  * consumer adds the splits in order
  * (mx_residual_layernorm). No counterpart in the reference (no split-K there): it replaces the GEMM half of the
