@@ -198,8 +198,9 @@ __device__ __forceinline__ void interleave_reads_mfma() {
 // sum of its BN values of x' and their centred square sum as two 64-bit words (epoch << 32 | fp32 bits), written
 // with single-copy-atomic agent-scope stores and read with agent-scope loads (past the per-XCD L2s), and waits only
 // for the other tiles of its row block. The epoch is the row block's generation + 1; the generation lives in device
-// memory and the row block's last workgroup to finish advances it, so every launch (graph replays included) uses
-// new epochs and nothing is ever cleared. The waits are bounded (kRlnTimeout); a timeout sets sync[0] and the
+// memory, every workgroup reads it after its k loop, and the row block's first column tile writes the epoch back as
+// the generation once it has seen all of the row block's words, so every launch (graph replays included) uses new
+// epochs and nothing is ever cleared. The waits are bounded (kRlnTimeout); a timeout sets sync[0] and the
 // launch's results are garbage. Every workgroup of a row block must be resident at once: the host allows this mode
 // only for grids of at most one workgroup per CU.
 struct RlnArgs {
@@ -211,7 +212,7 @@ struct RlnArgs {
   long ldy;
   float eps;
   uint64_t* stats;  // [tiles_m][tiles_n][BM][2] words
-  uint32_t* sync;   // [0] error word, then {generation, departures} per row block
+  uint32_t* sync;   // [0] error word, then the generation of each row block
 };
 constexpr uint64_t kRlnTimeout = 5000000ull;  // 50 ms at 100 MHz (s_memrealtime)
 constexpr int kRlnMaxTiles = 64;             // column tiles per row (N <= 64 BN)
@@ -428,9 +429,11 @@ __device__ __forceinline__ void gemm_body(
     static_assert(NT % BM == 0 && BM <= NT, "whole row groups of threads");
     constexpr int QG = NT / BM;  // thread groups per row when the statistics are gathered
     const int rb = tile_m;
-    uint32_t* gen = rl.sync + 1 + 2 * rb;
+    uint32_t* gen = rl.sync + 1 + rb;
     // every workgroup of the row block reads the generation before it publishes; none advances it before all have
-    // read the statistics, so all of them use the same epoch
+    // published, so all of them use the same epoch. (Read here, its round trip hides under the statistics below; read
+    // before the k loop, the loads of 216 workgroups at one address held up the ring's first loads: 2.31 against
+    // 2.19 ms per frame.)
     const uint32_t ep = __hip_atomic_load(GPTR(uint32_t, gen), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     // x' in registers: bf16(bf16(acc + bias) + residual), the rounding of residual_layernorm_kernel
     float xv[FN][FM][16];
@@ -567,14 +570,11 @@ __device__ __forceinline__ void gemm_body(
       }
     }
     __syncthreads();  // statistics read by every thread of this workgroup; the staging tile of x' is stored
-    if (tid == 0) {
-      uint32_t* dep = gen + 1;
-      const uint32_t old = __hip_atomic_fetch_add(GPTR(uint32_t, dep), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == (uint32_t)tiles_n - 1) {  // the row block's last: re-arm for the next launch
-        __hip_atomic_store(GPTR(uint32_t, dep), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(GPTR(uint32_t, gen), ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    // every tile of the row block has published this epoch (so every workgroup of it has read the generation): the
+    // row block's first column tile writes it as the next launch's generation. (No departure counter, whose returning
+    // atomic held every wave at the barrier before the Y store; and one writer per row block: 216 agent-scope stores
+    // into one cache line, one per workgroup, made the tower 2.33 against 2.21 ms per frame.)
+    if (tid == 0 && tile_n == 0) __hip_atomic_store(GPTR(uint32_t, gen), ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Y = (x' - mean) rstd gamma + beta, the order of residual_layernorm_kernel
 #pragma unroll
     for (int i = 0; i < FN; i++)
@@ -1550,7 +1550,7 @@ extern "C" int mx_gemm_i8(hipStream_t st, int cfg, const int8_t* A, long lda, co
 // and stats before the next call). Needs N a multiple of 64 (at most 4096) and a grid of at most one workgroup per
 // CU ((M / 64 rounded up) x (N / 64) <= the device's CU count), else MX_ESHAPE.
 extern "C" long mx_gemm_res_ln_stats_words(int M, int N) { return (long)((M + 63) / 64) * (N / 64) * 64 * 2; }
-extern "C" long mx_gemm_res_ln_sync_words(int M) { return 1 + 2L * ((M + 63) / 64); }
+extern "C" long mx_gemm_res_ln_sync_words(int M) { return 1 + (long)((M + 63) / 64); }
 
 extern "C" int mx_gemm_bf16_res_ln(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw,
                                    const float* bias, const uint16_t* R, long ldr, uint16_t* X, long ldx,
