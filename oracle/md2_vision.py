@@ -7,6 +7,14 @@ Restates moondream/gpu/md2fast.py:
   * _vision: normalise, patchify, patch_emb + pos, 27 blocks, post_ln, cat[x,x] projection   md2fast.py:147-160
 Everything runs in torch bf16 on the CPU, exactly the op sequence of the reference (F.scaled_dot_product_attention
 on (1, H, T, D) transposed views, as md2fast.py:155).
+
+`tower_with` runs the same tower with the Linear and attention operator classes injected (the reference's plug-in
+point, FastMD2(model, lin_cls=..., hattn=...), md2fast.py:71, 87-94): a Linear follows hgemm.HLin's protocol
+(`cls(weight, bias, dtype)`, `__call__(x, gelu=False, res=None)`, flags `fused_gelu` / `fused_res`,
+hgemm.py:139-178) and the attention hattn.Attn's (`cls(H, T, D)`, `__call__(q, k, v)` on (1, H, T, D) views ->
+(1, T, H*D), hattn.py:17-37). GELU and residual adds move into a Linear's epilogue exactly when its flags (and, for
+the residual, the USE_FUSED_RES switch, md2fast.py:51) say so (md2fast.py:55-67). Test infrastructure: it drives an
+operator binding under test through the reference's dataflow; with the default torch operators it is `tower`.
 """
 import torch
 import torch.nn.functional as F
@@ -70,3 +78,69 @@ def tower(w, img_u8, layers=None, project=False, return_blocks=False):
         feats = torch.cat([x, x], dim=-1)
         x = lin(gelu(lin(feats, w["proj_mlp.fc1.weight"], w["proj_mlp.fc1.bias"])), w["proj_mlp.fc2.weight"], w["proj_mlp.fc2.bias"])
     return (x, hs) if return_blocks else x
+
+
+class TorchLinear:
+    """F.linear in bf16 with the HLin protocol and no fused epilogues (what the oracle's `lin` computes)."""
+    fused_gelu = False
+    fused_res = False
+
+    def __init__(self, weight, bias, dtype):
+        self.weight, self.bias = weight.to(dtype), None if bias is None else bias.to(dtype)
+
+    def __call__(self, x, gelu=False, res=None):
+        if gelu or res is not None:
+            raise ValueError("TorchLinear has no fused epilogue")
+        return F.linear(x, self.weight, self.bias)
+
+
+class TorchAttention:
+    """F.scaled_dot_product_attention with hattn.Attn's protocol: (1, H, T, D) views -> (1, T, H*D)."""
+
+    def __init__(self, H, T, D):
+        self.H, self.D = H, D
+
+    def __call__(self, q, k, v):
+        B, H, T, D = q.shape
+        return F.scaled_dot_product_attention(q, k, v).transpose(1, 2).reshape(B, T, H * D)
+
+
+def _run_linear(layer, x, act=False, res=None, fuse_res=False):
+    """One Linear of the block with an optional tanh GELU after it and an optional residual add after that. Each of
+    the two goes into the layer's epilogue when the layer advertises it (fused_gelu; fused_res with the fuse_res
+    switch on), as md2fast.mlp / lin_res decide (md2fast.py:55-67); otherwise it is torch's separate bf16 op on the
+    layer's bf16 output."""
+    epi = {}
+    if act and getattr(layer, "fused_gelu", False):
+        epi["gelu"], act = True, False
+    if res is not None and fuse_res and getattr(layer, "fused_res", False):
+        epi["res"], res = res, None
+    y = layer(x, **epi)
+    if act:
+        y = gelu(y)
+    return y if res is None else y + res
+
+
+def tower_with(w, img_u8, linear_cls, attention_cls, device="cpu", fuse_res=False, H=16):
+    """md2fast.py:147-160 (batch of one crop) with injected operator classes; returns (729, 1152) post-LN features.
+    Weights are moved to `device` and wrapped once per Linear, as FastMD2's constructor does (md2fast.py:87-94)."""
+    dev = torch.device(device)
+    wt = lambda n: w[n].to(dev)
+    make = lambda n: linear_cls(wt(n + ".weight"), wt(n + ".bias"), BF)
+    n_blocks = 0
+    while f"blocks.{n_blocks}.ln1.weight" in w:
+        n_blocks += 1
+    layers = []
+    for i in range(n_blocks):
+        p = f"blocks.{i}."
+        layers.append({k: make(p + name) for k, name in
+                       (("qkv", "attn.qkv"), ("proj", "attn.proj"), ("fc1", "mlp.fc1"), ("fc2", "mlp.fc2"))})
+        for k in ("ln1", "ln2"):
+            layers[-1][k] = (wt(p + k + ".weight"), wt(p + k + ".bias"))
+    attend = attention_cls(H, NTOK, 1152 // H)
+    x = _run_linear(make("patch_emb"), normalize_patchify(img_u8[None].to(dev)), res=wt("pos_emb"), fuse_res=False)
+    for L in layers:
+        heads = [t.view(1, NTOK, H, -1).transpose(1, 2) for t in _run_linear(L["qkv"], ln(x, *L["ln1"])).chunk(3, -1)]
+        x = _run_linear(L["proj"], attend(*heads), res=x, fuse_res=fuse_res)
+        x = _run_linear(L["fc2"], _run_linear(L["fc1"], ln(x, *L["ln2"]), act=True), res=x, fuse_res=fuse_res)
+    return ln(x, wt("post_ln.weight"), wt("post_ln.bias"))[0]

@@ -1,12 +1,12 @@
 """The reference-side binding (strix_halo_maxx_amd.refbind, the module a maintainer adds next to hgemm.py) driven
-the way the reference drives its own op classes: a `_vision` loop shaped exactly like FastMD2._vision
-(moondream/gpu/md2fast.py:147-160, with _ln / gelu / mlp / lin_res of md2fast.py:43-67 restated below as the
-harness) with lin_cls = refbind.MxLin and hattn = refbind.Attn, in both USE_FUSED_RES settings, against the oracle's
-tower; and refbind.MxI8Lin (the HI8Lin protocol) against the oracle's W8A8 restatement bit for bit.
+through the reference's own dataflow: the oracle's operator-injected tower (oracle.md2_vision.tower_with, the
+FastMD2._vision loop of md2fast.py:147-160 with lin_cls / hattn plugged in, md2fast.py:71, 87-94) runs with
+linear_cls = refbind.MxLin and attention_cls = refbind.Attn, with the residual adds fused into the GEMM epilogue and
+without (USE_FUSED_RES, md2fast.py:51), against the oracle's all-torch tower; and refbind.MxI8Lin (the HI8Lin
+protocol) against the oracle's W8A8 restatement bit for bit.
 Tolerances as in the vision tests: end to end (27 blocks + post-LN) rel-L2 <= 2e-2."""
 import pytest
 import torch
-import torch.nn.functional as F
 
 import oracle.md2_text as ot
 import oracle.md2_vision as ov
@@ -15,7 +15,6 @@ import strix_halo_maxx_amd.synth as S
 
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
-GRID, PATCH, NTOK = 27, 14, 729
 
 
 def rel(a, b):
@@ -23,80 +22,16 @@ def rel(a, b):
     return ((a - b).norm() / b.norm()).item()
 
 
-# ---- the reference's helpers (md2fast.py:43-67), as the harness the op classes plug into
-class Flags:
-    USE_FUSED_RES = False
-
-
-def _ln(x, wb):
-    return F.layer_norm(x, (x.shape[-1],), wb[0], wb[1])
-
-
-def gelu(x):
-    return F.gelu(x, approximate="tanh")
-
-
-def mlp(fc1, fc2, h, res=None, pre=None):
-    kw = {"pre": pre} if pre is not None else {}
-    a = fc1(h, gelu=True, **kw) if getattr(fc1, "fused_gelu", False) else gelu(fc1(h, **kw))
-    if res is not None and Flags.USE_FUSED_RES and getattr(fc2, "fused_res", False):
-        return fc2(a, res=res)
-    out = fc2(a)
-    return out if res is None else out + res
-
-
-def lin_res(l, x, res):
-    if Flags.USE_FUSED_RES and getattr(l, "fused_res", False):
-        return l(x, res=res)
-    return l(x) + res
-
-
-class RefShapedVision:
-    """FastMD2's vision half with `lin_cls` and `hattn` plugged in (md2fast.py:87-94, 147-157)."""
-
-    def __init__(self, w, lin_cls, attn_cls, dev, H=16):
-        g = lambda n: w[n].to(dev)
-        L = lambda n: lin_cls(g(n + ".weight"), g(n + ".bias"), BF)
-        self.patch_emb, self.pos_emb = L("patch_emb"), g("pos_emb")
-        n = 0
-        while f"blocks.{n}.ln1.weight" in w:
-            n += 1
-        self.vblocks = [dict(ln1=(g(f"blocks.{i}.ln1.weight"), g(f"blocks.{i}.ln1.bias")), qkv=L(f"blocks.{i}.attn.qkv"),
-                             proj=L(f"blocks.{i}.attn.proj"),
-                             ln2=(g(f"blocks.{i}.ln2.weight"), g(f"blocks.{i}.ln2.bias")),
-                             fc1=L(f"blocks.{i}.mlp.fc1"), fc2=L(f"blocks.{i}.mlp.fc2")) for i in range(n)]
-        self.post_ln = (g("post_ln.weight"), g("post_ln.bias"))
-        self.vh = H
-        self.attn_v = attn_cls(H, NTOK, 1152 // H)
-
-    def _vision(self, img_u8):
-        x = img_u8.permute(2, 0, 1)[None].to(BF).div_(255.0).sub_(0.5).div_(0.5)
-        x = x.reshape(1, 3, GRID, PATCH, GRID, PATCH).permute(0, 2, 4, 1, 3, 5).reshape(1, NTOK, 3 * PATCH * PATCH)
-        x = self.patch_emb(x) + self.pos_emb
-        H = self.vh
-        for b in self.vblocks:
-            h = _ln(x, b["ln1"])
-            q, k, v = [t.view(1, NTOK, H, -1).transpose(1, 2) for t in b["qkv"](h).chunk(3, dim=-1)]
-            a = self.attn_v(q, k, v)
-            x = lin_res(b["proj"], a, x)
-            x = mlp(b["fc1"], b["fc2"], _ln(x, b["ln2"]), res=x)
-        return _ln(x, self.post_ln)[0]
-
-
 @pytest.mark.parametrize("fused_res", [True, False])
-def test_reference_shaped_vision_loop_with_refbind(dev, fused_res):
+def test_reference_dataflow_tower_with_refbind(dev, fused_res):
     w = S.vision_weights(0)
     img = S.images_u8(1, 1)
     ref = ov.tower(w, img)[0]
-    m = RefShapedVision(w, rb.MxLin, rb.Attn, dev)
-    Flags.USE_FUSED_RES = fused_res
-    try:
-        out = m._vision(img[0].to(dev))
-    finally:
-        Flags.USE_FUSED_RES = False
+    print(f"refbind tower, fused residual {fused_res}", flush=True)
+    out = ov.tower_with(w, img[0].to(dev), rb.MxLin, rb.Attn, device=dev, fuse_res=fused_res)
     r = rel(out, ref)
-    print(f"reference-shaped _vision, USE_FUSED_RES={fused_res}: rel-L2 vs oracle {r:.2e}", flush=True)
-    assert out.shape == (NTOK, 1152)
+    print(f"refbind tower, fused residual {fused_res}: rel-L2 vs oracle {r:.2e}", flush=True)
+    assert out.shape == (729, 1152) and out.device.type == "cuda"
     assert r <= 2e-2
 
 
