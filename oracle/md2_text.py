@@ -72,23 +72,38 @@ def quant_rows(x):
     return q.to(torch.int8), s
 
 
-def i8_linear(q, sx, wq, sw, bias, gelu_tanh=False):
-    """i8gemm.hip:181-197: exact int32 accumulation (int64 matmul here), fp32 ((acc * s_x) * s_w) + b, optional GELU
-    on the fp32 value, one bf16 rounding. q (M, K) int8, wq (N, K) int8."""
-    acc = (q.long() @ wq.long().t()).to(torch.int32)
+def _int8_dot(q, wq, kc=1024):
+    """Exact int32 q wq^T of int8 values on the CPU's fp32 BLAS: every partial sum over a 1024-wide slice of K is an
+    integer below 1024 * 127^2 < 2^24, exact in fp32 in any summation order; the slices are added in int64."""
+    K = q.shape[1]
+    qf = q.float()
+    wf = wq if wq.dtype == torch.float32 else wq.float()
+    acc = torch.zeros(q.shape[0], wq.shape[0], dtype=torch.int64)
+    for k0 in range(0, K, kc):
+        acc += (qf[:, k0:k0 + kc] @ wf[:, k0:k0 + kc].t()).to(torch.int64)
+    return acc.to(torch.int32)
+
+
+def i8_linear(q, sx, wq, sw, bias, gelu_tanh=False, out_dtype=BF):
+    """i8gemm.hip:181-197: exact int32 accumulation, fp32 ((acc * s_x) * s_w) + b, optional GELU on the fp32 value,
+    one bf16 rounding (none with out_dtype float32: the fp32 arbiter). q (M, K) int8, wq (N, K) int8 (or the same
+    values as float32, to skip the conversion)."""
+    acc = _int8_dot(q, wq)
     v = acc.float() * sx[:, None]
     v = v * sw[None, :]
     if bias is not None:
         v = v + bias.float()[None, :]
     if gelu_tanh:
         v = gelu(v)
-    return v.to(BF)
+    return v.to(out_dtype)
 
 
 class Text:
     def __init__(self, w, ctx, freqs, bos=50256, H=32, w8a8=False, dtype=BF):
         """dtype: the activation / cache type. BF is the reference's bf16 path; torch.float32 (with fp32 weights)
-        is the same op sequence without bf16 roundings, used as the arbiter of near-tied greedy steps."""
+        is the same op sequence without bf16 roundings, used as the arbiter of near-tied greedy steps (with w8a8, the
+        int8 quantisation stays: the weights quantise to the same int8 values, the activations are quantised from
+        fp32 values and the dequantised outputs are not rounded)."""
         self.w = w
         self.H = H
         self.w8a8 = w8a8
@@ -106,6 +121,7 @@ class Text:
         if w8a8:
             self.q = {f"blocks.{i}.{m}": quant_weight(w[f"blocks.{i}.{m}.weight"])
                       for i in range(n) for m in ("attn.qkv", "attn.proj", "mlp.fc1", "mlp.fc2")}
+        self.qf = {}
 
     def _lin(self, name, x, pre=None, gelu_tanh=False):
         """A text Linear: bf16 F.linear (+ separate GELU), or the W8A8 path (pre = the shared quantised input)."""
@@ -116,7 +132,9 @@ class Text:
         shp = x.shape
         q, sx = pre if pre is not None else quant_rows(x.reshape(-1, shp[-1]))
         wq, sw = self.q[name]
-        return i8_linear(q, sx, wq, sw, w[name + ".bias"], gelu_tanh).view(*shp[:-1], wq.shape[0])
+        if name not in self.qf:  # the int8 values as float32 once (the exact dot runs on the fp32 BLAS)
+            self.qf[name] = wq.float()
+        return i8_linear(q, sx, self.qf[name], sw, w[name + ".bias"], gelu_tanh, self.dt).view(*shp[:-1], wq.shape[0])
 
     def layers(self, x, pos0, mask):
         """md2fast.py:169-199 (fuse=False). x (1, n, D)."""

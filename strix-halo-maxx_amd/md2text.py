@@ -15,6 +15,8 @@ nq questions share the image prefix, whose K/V the prefix prefill writes into ev
 questions, zero-padded to L tokens, run as one batch of nq * L rows under the prefix + causal mask; the last real
 token of each question goes through the final LN and the LM head restricted to the yes / no token rows.
 """
+import warnings
+
 import torch
 
 from . import _lib, ops
@@ -131,6 +133,7 @@ class TextDecoder:
                 and torch.cuda.get_device_properties(dev).multi_processor_count >= lib.mx_decode_mk_grid()):
             self._init_mk()
         self.use_mk = self.mk_layers is not None
+        self.mk_fallbacks = 0  # generations redone on the per-layer kernels after a one-launch step timed out
 
     def _init_mk(self):
         lib = _lib.load()
@@ -403,6 +406,23 @@ class TextDecoder:
         """Prefill + greedy decode; returns the n_tokens generated ids (the first comes from the prompt prefill).
         Raises ValueError, before any work, when the prefill plus n_tokens - 1 decode steps would not fit the cache."""
         self._check_room(1 + img_emb.shape[0] + prompt_ids.shape[0], n_tokens)
+        self._generate(img_emb, prompt_ids, n_tokens, use_graph)
+        if self.use_mk and self.mk_error():
+            # a one-launch step's wait timed out (e.g. another process held CUs, so its 256 workgroups were not all
+            # resident): its tokens and the cache rows it wrote are undefined. Clear the exchange words and redo the
+            # whole generation on the per-layer kernels, which have no cross-workgroup waits.
+            err = self.mk_error()
+            self.mk_reset()
+            self.mk_fallbacks += 1
+            warnings.warn(f"one-launch decode step timed out (error {err}); regenerating on the per-layer kernels")
+            self.use_mk, self.graph = False, None
+            try:
+                self._generate(img_emb, prompt_ids, n_tokens, use_graph)
+            finally:
+                self.use_mk, self.graph = True, None
+        return self.tokens[:n_tokens]
+
+    def _generate(self, img_emb, prompt_ids, n_tokens, use_graph):
         self.prefill(img_emb, prompt_ids)
         self.start_decode()
         if use_graph:
@@ -413,4 +433,3 @@ class TextDecoder:
         else:
             for _ in range(n_tokens - 1):
                 self.decode_step()
-        return self.tokens[:n_tokens]

@@ -9,12 +9,13 @@ Model level (seeded weights N(0, 0.02), image tokens N(0, 1), prompt ids uniform
     layers) of the oracle's;
   * greedy tokens: at every step the HIP token is the bf16 oracle's argmax, except where that choice is not decidable
     at bf16 precision. The arbiter is the same oracle run in fp32 (fp32 weights, no bf16 roundings) on the same
-    tokens: a HIP token t may differ from the bf16 oracle's argmax only if the fp32 logit gap between the fp32 argmax
-    f and t is no larger than the bf16 oracle's own error at that step, max_j |bf16_j - fp32_j| over the logits. The
-    bound is derived per step from the oracle's own rounding error, not a fixed constant. (The oracle's error on the
-    two decisive logits alone is a single draw of that noise: at 24 layers a HIP path whose logits are as far from
-    fp32 as the oracle's are on average, max |hip - fp32| 0.051 against the oracle's 0.051, still lands above it on
-    one pair now and then.)
+    tokens. The step is decided by a handful of logits: the fp32 arbiter's top 16 plus the bf16 oracle's argmax and
+    the HIP token. e = max |bf16 - fp32| over those logits is the bf16 oracle's own error where it matters, and a
+    bf16-precision path with that error on two logits can reorder them when their fp32 gap is below 2 e (each of the
+    pair may be off by e, in opposite directions). So a HIP token t may differ from the bf16 oracle's argmax only if
+    the fp32 gap between the fp32 argmax f and t is at most 2 e (t == f is always allowed: the HIP path then picked
+    the exact argmax and the oracle did not). Every such step is printed with the gap, e and the HIP path's own error
+    on the pair, and the number of steps where the HIP token differs from both argmaxes is bounded per test.
 Yes/no query: decide() agrees with the bf16 oracle except where the fp32 arbiter's margin is no larger than the bf16
 oracle's own margin error (the same derived rule)."""
 import pytest
@@ -120,7 +121,7 @@ def test_lm_argmax_first_index_on_ties(dev):
     assert torch.equal(xe, wte[777]) and state.tolist() == [1, 100]
 
 
-@pytest.mark.parametrize("L", [1, 7, 300, 922])
+@pytest.mark.parametrize("L", [1, 7, 300, 922, 1023, 1024])
 def test_decode_attn_vs_fp32(dev, L):
     H, ctx, pos = 32, 1024, L - 1
     g = gen(L)
@@ -253,10 +254,14 @@ def compare_free_running(out, tol, gap_max=0.05):
     return rs
 
 
+TOPK = 16  # fp32 candidates whose logits decide a greedy step
+
+
 def _check_decode(dec, ora, ora32, img, prompt, n_tokens, tol=1e-2):
     """Teacher-forced on the HIP path's tokens: the bf16 oracle and its fp32 arbiter step in lockstep. Checks the
     logits (rel-L2 tol) and the token rule of the module docstring at every step. Returns (HIP tokens, steps where the
-    HIP token equals the bf16 oracle's argmax, steps where it equals the fp32 argmax, the undecidable steps)."""
+    HIP token equals the bf16 oracle's argmax, steps where it equals the fp32 argmax, the undecidable steps as
+    (step, fp32 gap, 2 e, HIP error on the pair), steps where the HIP token equals neither argmax)."""
     lg0, hp, xp = ora.prefill(img, prompt, return_hidden=True)
     lf = ora32.prefill(img, prompt)
     xg = dec.prefill(img.to(dec.dev), prompt)
@@ -269,24 +274,28 @@ def _check_decode(dec, ora, ora32, img, prompt, n_tokens, tol=1e-2):
         gl.append(dec.logits.cpu().clone())
     toks = dec.tokens[:n_tokens].cpu().tolist()
     lg = lg0
-    same_b, same_f, undecidable = [], [], []
+    same_b, same_f, undecidable, neither = [], [], [], []
     for t in range(n_tokens):
         assert rel(gl[t], lg) <= tol, (t, rel(gl[t], lg))
-        lb, l32, tk = lg.float(), lf.float(), toks[t]
+        lb, l32, lh, tk = lg.float(), lf.float(), gl[t].float(), toks[t]
         ob, of = int(torch.argmax(lb)), int(torch.argmax(l32))
         if tk == ob:
             same_b.append(t)
         else:
+            cand = torch.tensor(sorted(set(torch.topk(l32, TOPK).indices.tolist()) | {ob, tk}))
+            e = (lb[cand] - l32[cand]).abs().max().item()
             gap = (l32[of] - l32[tk]).item()
-            err = (lb - l32).abs().max().item()
-            assert gap <= err, (t, tk, ob, of, gap, err)
-            undecidable.append((t, round(gap, 4), round(err, 4)))
+            hip_pair = ((lh[of] - l32[of]).abs() + (lh[tk] - l32[tk]).abs()).item()
+            assert gap <= 2 * e, (t, tk, ob, of, gap, e)
+            undecidable.append((t, round(gap, 4), round(2 * e, 4), round(hip_pair, 4)))
+            if tk != of:
+                neither.append(t)
         if tk == of:
             same_f.append(t)
         if t + 1 < n_tokens:
             lg = ora.step(tk)
             lf = ora32.step(tk)
-    return toks, same_b, same_f, undecidable
+    return toks, same_b, same_f, undecidable, neither
 
 
 @pytest.mark.parametrize("mk", [True, False])
@@ -298,12 +307,14 @@ def test_decoder_two_layers(dev, mk):
     img = S.activations(3, (729, 2048), "img")
     prompt = S.prompt_ids(4, 64)
     print(f"decoder 2 layers, one-launch step {mk}", flush=True)
-    toks, same_b, _, und = _check_decode(dec, ora, _fp32_oracle(w), img, prompt, 24)
-    print(f"2 layers, 24 tokens: {len(same_b)} equal the bf16 oracle's argmax; undecidable steps {und}", flush=True)
+    toks, same_b, _, und, neither = _check_decode(dec, ora, _fp32_oracle(w), img, prompt, 24)
+    print(f"2 layers, 24 tokens: {len(same_b)} equal the bf16 oracle's argmax; undecidable steps "
+          f"(step, fp32 gap, 2e, HIP pair error) {und}", flush=True)
+    assert len(neither) == 0 and len(same_b) >= 23
     # the graph-replayed loop gives the same tokens as the eager loop
     g_toks = dec.generate(img.to(dev), prompt, 24).cpu().tolist()
     assert g_toks == toks
-    assert dec.mk_error() == 0
+    assert dec.mk_error() == 0 and dec.mk_fallbacks == 0
 
 
 def test_decode_one_launch_step_equals_layer_kernels(dev):
@@ -324,28 +335,106 @@ def test_decode_one_launch_step_equals_layer_kernels(dev):
             dec.decode_step(logits=True)
             lg.append(dec.logits.float().cpu().clone())
         out[mk] = (dec.tokens[:7].cpu().tolist(), lg, dec.xd[0].cpu().clone())
-    assert dec.mk_error() == 0
+    assert dec.mk_error() == 0 and dec.mk_fallbacks == 0
     compare_free_running(out, 5e-3)
+
+
+def _report_greedy(tag, same_b, same_f, und, neither, n):
+    n_same = next((t for t in range(n) if t not in set(same_b)), n)
+    print(f"{tag}: {len(same_b)}/{n} equal the bf16 oracle's argmax, {len(same_f)}/{n} the fp32 arbiter's; "
+          f"free-running identical prefix {n_same}; undecidable steps (step, fp32 gap, 2e, HIP pair error) {und}; "
+          f"equal to neither argmax at steps {neither}", flush=True)
 
 
 def test_decoder_full_config_greedy_128(dev):
     """Config 2: 24 layers, prefill 1 + 729 image tokens + 64 prompt ids, greedy 128 tokens (graph replay). The
-    graph-replayed tokens equal the eager ones; teacher-forced on them, every token obeys the derived rule of the
-    module docstring. Reports how many tokens equal the bf16 oracle's and the fp32 arbiter's argmax, and the length of
-    the prefix over which the free-running bf16 oracle would produce the same sequence (up to and including the first
-    step where the HIP token differs from the oracle's argmax, the two free-running sequences coincide)."""
+    graph-replayed tokens equal the eager ones; teacher-forced on them, every token obeys the rule of the module
+    docstring, at most 4 of the 128 tokens equal neither the bf16 oracle's nor the fp32 arbiter's argmax, and at least
+    120 equal the bf16 oracle's (measured on this seed: 3 and 123, at steps 68, 75 and 94, fp32 gaps 0.007-0.023
+    against 2e = 0.042-0.087). Reports both counts, every undecidable step, and the length of the prefix over which
+    the free-running bf16 oracle would produce the same sequence (up to and including the first step where the HIP
+    token differs from the oracle's argmax, the two free-running sequences coincide)."""
     w, ora, dec = _models(None)
     img = S.activations(3, (729, 2048), "img")
     prompt = S.prompt_ids(4, 64)
     toks = dec.generate(img.to(dev), prompt, 128).cpu().tolist()
+    assert dec.mk_error() == 0 and dec.mk_fallbacks == 0
     dec.graph = None
-    toks_e, same_b, same_f, und = _check_decode(dec, ora, _fp32_oracle(w), img, prompt, 128, tol=2e-2)
+    toks_e, same_b, same_f, und, neither = _check_decode(dec, ora, _fp32_oracle(w), img, prompt, 128, tol=2e-2)
     assert toks_e == toks
-    assert dec.use_mk and dec.mk_error() == 0
-    n_same = next((t for t in range(128) if t not in set(same_b)), 128)
-    print(f"greedy 128: {len(same_b)}/128 equal the bf16 oracle's argmax, {len(same_f)}/128 the fp32 arbiter's; "
-          f"free-running identical prefix {n_same}; undecidable steps (step, fp32 gap, bf16 error) {und}", flush=True)
-    assert len(same_b) + len(und) == 128
+    assert dec.use_mk and dec.mk_error() == 0 and dec.mk_fallbacks == 0
+    _report_greedy("greedy 128", same_b, same_f, und, neither, 128)
+    assert len(neither) <= 4
+    assert len(same_b) >= 120
+
+
+def _fp32_w8a8_oracle(w):
+    return ot.Text({k: v.float() for k, v in w.items()}, 1024, S.freqs_cis(32, 2048), w8a8=True,
+                   dtype=torch.float32)
+
+
+def test_decoder_w8a8_full_config_greedy_128(dev):
+    """Config 2 with the reference's W8A8 text Linears (int8 weights per channel, int8 activations per token, bf16 LM
+    head): 24 layers, prefill 1 + 729 + 64, greedy 128 tokens through the one-launch W8A8 step (graph replay) against
+    oracle.Text(w8a8=True), teacher-forced on the HIP tokens: hidden states and per-step logits within rel-L2 5e-2 (the
+    quantisation is discontinuous: the LayerNorm's fp32 summation order moves an occasional int8 value of h by one
+    step, already 2e-2 at 2 layers, and 24 layers compound it as the bf16 path's 1e-2 becomes 2e-2; measured 3.2e-2
+    for the prompt's hidden states), and the token rule of the module docstring with the W8A8 arbiter (the same
+    quantised Linears with fp32 activations and no bf16 roundings: the quantisation is part of the function, the bf16
+    roundings around it are the noise, about three times the bf16 path's: 2e = 0.10-0.19 on the deciding logits). At
+    most 8 tokens equal neither argmax and at least 112 equal the W8A8 oracle's (measured on this seed: 5 and 116,
+    every one of them within the rule with fp32 gaps 0.004-0.062)."""
+    w = S.text_weights(0)
+    ora = ot.Text(w, 1024, S.freqs_cis(32, 2048), w8a8=True)
+    dec = mt.TextDecoder(w, ctx=1024, w8a8=True)
+    assert dec.use_mk
+    img = S.activations(3, (729, 2048), "img")
+    prompt = S.prompt_ids(4, 64)
+    print("w8a8 decoder, 24 layers, 128 tokens", flush=True)
+    toks = dec.generate(img.to(dev), prompt, 128).cpu().tolist()
+    assert dec.mk_error() == 0 and dec.mk_fallbacks == 0
+    dec.graph = None
+    toks_e, same_b, same_f, und, neither = _check_decode(dec, ora, _fp32_w8a8_oracle(w), img, prompt, 128, tol=5e-2)
+    assert toks_e == toks
+    assert dec.mk_error() == 0 and dec.mk_fallbacks == 0
+    _report_greedy("w8a8 greedy 128", same_b, same_f, und, neither, 128)
+    assert len(neither) <= 8
+    assert len(same_b) >= 112
+
+
+def test_decode_reaches_the_last_cache_row(dev):
+    """A 970-position prefill (1 + 729 image tokens + 240 prompt ids) into a 1024-entry cache, then 54 greedy steps
+    at positions 970 .. 1023: the last key round of both decode attention paths (keys 960 .. 1023) and the final
+    cache row. The one-launch step and the per-layer kernels agree (compare_free_running), the one-launch step obeys
+    the token rule against the oracle (2 layers), a 55th step and a generate() one token longer are refused on the
+    host before any work, and the device state stopped exactly at the cache's end (55 tokens, next position 1024)."""
+    w, ora, dec = _models(2, seed=2)
+    img = S.activations(7, (729, 2048), "img")
+    prompt = S.prompt_ids(8, 240)
+    n = 1024 - (1 + 729 + 240) + 1  # tokens: the prefill's plus one per decode step at positions 970 .. 1023
+    out = {}
+    for mk in (False, True):
+        dec.use_mk = mk
+        print(f"decode to the last cache row, one-launch step {mk}", flush=True)
+        dec.prefill(img.to(dev), prompt)
+        dec.start_decode()
+        lg = []
+        for _ in range(n - 1):
+            dec.decode_step(logits=True)
+            lg.append(dec.logits.float().cpu().clone())
+        assert dec.state.cpu().tolist() == [n, 1024]
+        with pytest.raises(ValueError):
+            dec.decode_step()
+        out[mk] = (dec.tokens[:n].cpu().tolist(), lg, dec.xd[0].cpu().clone())
+    assert dec.mk_error() == 0 and dec.mk_fallbacks == 0
+    compare_free_running(out, 5e-3)
+    with pytest.raises(ValueError):
+        dec.generate(img.to(dev), prompt, n + 1)
+    dec.use_mk = True
+    toks, same_b, _, und, neither = _check_decode(dec, ora, _fp32_oracle(w), img, prompt, n)
+    print(f"to row 1023: {len(same_b)}/{n} equal the bf16 oracle's argmax; undecidable steps {und}", flush=True)
+    assert toks == out[True][0]
+    assert len(neither) == 0 and dec.mk_error() == 0 and dec.mk_fallbacks == 0
 
 
 YES, NO = [11, 222, 3333, 44444], [55, 666, 7777, 50000]
