@@ -478,6 +478,63 @@ def cpu_baseline(budget_s=20.0):
                       f"median of {n} frames after 1 warm-up, torch.set_num_threads({threads})"}
 
 
+def block_bench(reps=200, cpu=True):
+    """One SigLIP block (729 tokens x 1152, 16 heads x 72, MLP 4304, GELU-tanh, residuals; weights N(0, 0.02),
+    activations N(0, 1)): the GPU block (ln1 -> qkv -> attention -> proj + residual + ln2 -> fc1 + GELU -> fc2 +
+    residual, the tower's own kernels) as one HIP graph replayed `reps` times between two HIP events on its stream,
+    and the oracle's block (the reference's torch bf16 block restated) on the host cores, median of 5 after 2
+    warm-ups."""
+    import torch
+    import oracle.md2_vision as ov
+    import strix_halo_maxx_amd.md2 as md2
+    import strix_halo_maxx_amd.synth as S
+    w = S.vision_weights(0, layers=1)
+    x_cpu = S.activations(11, (729, 1152), "x")
+    dev = torch.device("cuda:0")
+    vt = md2.VisionTower(w, device=dev)
+    b = vt.blocks[0]
+    x = x_cpu.to(dev)
+    for _ in range(3):
+        vt.block(b, x, 1)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        vt.block(b, x, 1)
+    st = torch.cuda.current_stream()
+    for _ in range(5):
+        g.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
+    e1.synchronize()
+    if vt.rln_error():
+        raise RuntimeError(f"fused residual-LayerNorm GEMM reported error {vt.rln_error()}")
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    fl = vision_flops_per_frame(layers=1, Kp=0)
+    out = {"us_per_block": round(us, 2), "tflops": round(fl / us / 1e6, 1), "mfma_frac": round(fl / us / 1e6 / (PEAK_BF16 / 1e12), 4),
+           "gflop_per_block": round(fl / 1e9, 3),
+           "workload": "one SigLIP block, 729 tokens x 1152, bf16, batch 1, one HIP graph per block"}
+    if cpu:
+        threads = _cpu_threads()
+        torch.set_num_threads(threads)
+        xb = x_cpu[None]
+        with torch.inference_mode():
+            for _ in range(2):
+                ov.block(w, 0, xb)
+            ts = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                ov.block(w, 0, xb)
+                ts.append(time.perf_counter() - t0)
+        out["cpu_baseline"] = {"value": round(statistics.median(ts) * 1e3, 2), "unit": "ms/block", "cores": threads,
+                               "kind": "port", "threads": threads, "host_logical_cpus": os.cpu_count(),
+                               "sample": f"oracle block (md2fast.py:153-157 restated), 729 tokens, median of 5 after "
+                                         f"2 warm-ups, torch.set_num_threads({threads})"}
+    return out
+
+
 def cpu_baseline_decoder(n_tokens=8):
     """Config 2 on the host cores: the oracle decoder (the reference's torch bf16 text path restated), prefill of
     1 + 729 image tokens + 64 prompt ids once, then n_tokens greedy steps; tok/s over the decode steps."""
@@ -738,31 +795,11 @@ def large_batch_ops(vt, imgs, reps=5):
     (+ residual), each on block 0's real operands, `reps` launches between HIP events on the launching stream.
     Returns {op: {"us", "tflops", "mfma_frac"}} (LN: GB/s instead)."""
     import torch
-    import strix_halo_maxx_amd.ops as ops
-    B = imgs.shape[0]
-    T, D, H, hd = vt.T, vt.D, vt.H, vt.hd
-    M = B * T
-    b = vt.blocks[0]
-    x = vt.embed(imgs)
-    h = ops.layernorm(x, *b["ln1"], eps=vt.eps)
-    qkv = b["qkv"](h)
-    q5 = qkv.view(B, T, 3, H, hd)
-    q, k, v = (q5[:, :, j].transpose(1, 2) for j in range(3))
-    a = vt.attn(q, k, v).view(M, D)
-    x1 = b["proj"](a, res=x)
-    h2 = ops.layernorm(x1, *b["ln2"], eps=vt.eps)
-    f = b["fc1"](h2, gelu=True)
-    F = f.shape[1]
-    y = torch.empty_like(x)
-    ops_ = {"qkv": (2 * M * D * 3 * D, lambda: b["qkv"](h, out=qkv)),
-            "attn": (4 * B * H * T * T * hd, lambda: ops.sdpa(q, k, v, out=a.view(B, T, D))),
-            "proj": (2 * M * D * D, lambda: b["proj"](a, res=x, out=y)),
-            "ln": (0, lambda: ops.layernorm(x1, *b["ln2"], eps=vt.eps, out=h2)),
-            "fc1": (2 * M * D * F, lambda: b["fc1"](h2, gelu=True, out=f)),
-            "fc2": (2 * M * F * D, lambda: b["fc2"](f, res=x1, out=y))}
+    ops_ = large_batch_block_ops(vt, imgs)
+    M, D = imgs.shape[0] * vt.T, vt.D
     st = torch.cuda.current_stream()
     res = {}
-    for name, (fl, fn) in ops_.items():
+    for name, (fl, _, fn) in ops_.items():
         fn()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(st)
@@ -779,6 +816,227 @@ def large_batch_ops(vt, imgs, reps=5):
     gemm_us = sum(res[k]["us"] for k in ("qkv", "proj", "fc1", "fc2"))
     res["gemms"] = {"tflops": round(gemm_fl / gemm_us / 1e6, 1), "mfma_frac": round(gemm_fl / gemm_us / 1e6 / (PEAK_BF16 / 1e12), 4)}
     return res
+
+
+def large_batch_block_ops(vt, imgs):
+    """Block 0's ops at a large batch on its real operands: {op: (flops, algorithmic HBM bytes, fn)}, fn relaunching
+    the op into fixed outputs (every operand once: bf16 activations and weights)."""
+    import torch
+    import strix_halo_maxx_amd.ops as ops
+    B = imgs.shape[0]
+    T, D, H, hd = vt.T, vt.D, vt.H, vt.hd
+    M = B * T
+    b = vt.blocks[0]
+    x = vt.embed(imgs)
+    h = ops.layernorm(x, *b["ln1"], eps=vt.eps)
+    qkv = b["qkv"](h)
+    q5 = qkv.view(B, T, 3, H, hd)
+    q, k, v = (q5[:, :, j].transpose(1, 2) for j in range(3))
+    a = vt.attn(q, k, v).view(M, D)
+    x1 = b["proj"](a, res=x)
+    h2 = ops.layernorm(x1, *b["ln2"], eps=vt.eps)
+    f = b["fc1"](h2, gelu=True)
+    F = f.shape[1]
+    y = torch.empty_like(x)
+    return {"qkv": (2 * M * D * 3 * D, 2 * (M * D + 3 * D * D + 3 * M * D), lambda: b["qkv"](h, out=qkv)),
+            "attn": (4 * B * H * T * T * hd, 2 * 4 * M * D, lambda: ops.sdpa(q, k, v, out=a.view(B, T, D))),
+            "proj": (2 * M * D * D, 2 * (3 * M * D + D * D), lambda: b["proj"](a, res=x, out=y)),
+            "ln": (0, 2 * 2 * M * D, lambda: ops.layernorm(x1, *b["ln2"], eps=vt.eps, out=h2)),
+            "fc1": (2 * M * D * F, 2 * (M * D + F * D + M * F), lambda: b["fc1"](h2, gelu=True, out=f)),
+            "fc2": (2 * M * F * D, 2 * (M * F + D * F + 2 * M * D), lambda: b["fc2"](f, res=x1, out=y))}
+
+
+PROBES = ("tower_b256", "trecvit", "scan", "decode_w8a8")
+
+
+def _probe_classes(workload):
+    """Launch classes of a profiling probe: (title, [(label, fn, algorithmic HBM bytes per call or None, flops per
+    call)]), built on the device with every warm-up (tile tuning, first-touch) done. fn() launches one call of the
+    class eagerly (no graph)."""
+    import torch
+    import strix_halo_maxx_amd.synth as S
+    dev = torch.device("cuda:0")
+    if workload == "tower_b256":
+        import strix_halo_maxx_amd.md2 as md2
+        vt = md2.VisionTower(S.vision_weights(0), device=dev)
+        imgs = S.images_u8(2, 256).to(dev)
+        vt(imgs)
+        ops_ = large_batch_block_ops(vt, imgs)
+        for _, _, fn in ops_.values():
+            fn()
+        return ("moondream2 vision tower at batch 256 (186,624 tokens), block 0's ops on its own operands",
+                [(k, fn, algo, fl) for k, (fl, algo, fn) in ops_.items()])
+    if workload == "trecvit":
+        import strix_halo_maxx_amd.trecvit as tv
+        m = tv.TRecViT(S.trecvit_weights(0), device=dev)
+        fr = S.frames_u8(1, 4).to(dev)
+        qf = (S.query_points(5, 256)[:, 1:] / 256.0).to(torch.bfloat16).to(dev)
+        m.reset()
+        for t in range(3):
+            m.step(fr[t], qf)
+        return ("TRecViT streamed frame (12 blocks, 1024 patch + 256 query tokens, hidden 768) with the tracking "
+                "heads, eager launches", [("frame", lambda: m.step(fr[3], qf), None, None)])
+    if workload == "scan":
+        T, C, F = 1280, 768, 16
+        g = torch.Generator(device=dev).manual_seed(3)
+        bufs = [(torch.rand(F, T, C, device=dev, generator=g), torch.randn(F, T, C, device=dev, generator=g),
+                 torch.zeros(T, C, device=dev),
+                 torch.randn(F, T, 2 * C, device=dev, generator=g).to(torch.bfloat16),
+                 torch.empty(F, T, C, device=dev, dtype=torch.bfloat16)) for _ in range(4)]
+        it = iter(range(1 << 30))
+        from strix_halo_maxx_amd import _lib
+
+        def run():
+            b = bufs[next(it) % len(bufs)]
+            _lib.call("mx_rglru_scan", _lib.stream(), b[0].data_ptr(), b[1].data_ptr(), b[2].data_ptr(), F, T, C,
+                      b[3].data_ptr(), 2 * C, T * 2 * C, b[4].data_ptr(), C, T * C)
+        run()
+        return (f"RG-LRU clip scan (mx_rglru_scan, {F} frames x {T} tokens x {C} channels), each call on its own "
+                "buffers", [("scan", run, 12 * F * T * C + 8 * T * C, None)])
+    if workload == "decode_w8a8":
+        import strix_halo_maxx_amd.md2text as mt
+        dec = mt.TextDecoder(S.text_weights(0), device=dev, ctx=1024, w8a8=True)
+        if not dec.use_mk:
+            raise RuntimeError("the one-launch decode step is not in use on this device")
+        img = S.activations(3, (729, 2048), "img").to(dev)
+        prompt = S.prompt_ids(4, 64)
+        dec.generate(img, prompt, 4)
+        dec.prefill(img, prompt)
+        dec.start_decode()
+        for _ in range(2):
+            dec.decode_step()
+        c = S.TXT
+        D, F_, L, V = c["dim"], c["ff"], c["layers"], c["vocab"]
+        lin = L * (3 * D * D + D * D + 2 * D * F_)
+        algo = lin + 4 * L * (3 * D + D + F_ + D) + 2 * V * D + 2 * 2 * L * (dec.pos_base + 3) * D
+        return ("moondream2 W8A8 one-launch decode step (mx_decode_step_mk_i8), 24 layers, from position "
+                f"{dec.pos_base + 2}", [("step", dec.decode_step, algo, None)])
+    raise ValueError(f"unknown probe {workload}; one of {PROBES}")
+
+
+def probe(workload, reps=3):
+    """Eager launches for rocprofv3 --pmc passes over one workload: after the warm-ups, for class i a marker fill of
+    10000 + i floats then `reps` calls of the class; then a marker fill of 99999 floats and the calibration: `reps`
+    device copies of 256 MiB (known traffic: 256 MiB read + 256 MiB written each)."""
+    import torch
+    title, classes = _probe_classes(workload)
+    torch.cuda.synchronize()
+    for i, (label, fn, _, _) in enumerate(classes):
+        torch.full((10000 + i,), 1.0, device="cuda:0")
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+    torch.full((99999,), 1.0, device="cuda:0")
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[bench] probe {workload} done: {title}", flush=True)
+
+
+def _pmc_dispatches(path):
+    """{counter: [(kernel, grid threads, value)] in dispatch order} from a rocprofv3 counter_collection CSV (values
+    of one dispatch summed over their dimension rows; MfmaUtil, a percentage, averaged)."""
+    import csv
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            c = r["Counter_Name"]
+            d = int(r["Dispatch_Id"])
+            k = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "")
+            k = k[:k.rfind(">") + 1] if ">" in k else k.split("(")[0]
+            e = per.setdefault(c, {}).setdefault(d, [k, int(r.get("Grid_Size", 0) or 0), 0.0, 0])
+            e[2] += float(r["Counter_Value"])
+            e[3] += 1
+    out = {}
+    for c, m in per.items():
+        out[c] = [(k, g, v / n if c == "MfmaUtil" else v) for _, (k, g, v, n) in sorted(m.items())]
+    return out
+
+
+def summarize_probe(workload, paths, reps=3):
+    """Markdown summary of rocprofv3 --pmc passes (one CSV each) over `bench.py --probe WORKLOAD`: per class, per
+    (kernel, grid): dispatches per call, HBM traffic per dispatch from FETCH_SIZE / WRITE_SIZE (scaled by what the
+    counters read for the 256 MiB calibration copies), and whichever of MfmaUtil, the waiting / issue fractions of
+    wave time, LDS bank conflicts and the L2 hit rate the CSVs hold."""
+    title, classes = _probe_classes(workload)
+    vals = {}
+    for p in paths:
+        vals.update(_pmc_dispatches(p))
+    segs = {}
+    for c, seq in vals.items():
+        fills = [i for i, (k, _, _) in enumerate(seq) if "FillFunctor" in k]
+        marks = fills[-(len(classes) + 1):]
+        if len(marks) != len(classes) + 1:
+            raise RuntimeError(f"{c}: {len(fills)} marker fills for {len(classes)} classes")
+        parts = [seq[marks[i] + 1:marks[i + 1]] for i in range(len(classes))]
+        segs[c] = (parts, [v for k, _, v in seq[marks[-1] + 1:] if "copyBuffer" in k][:reps])
+    cal = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        if c in segs:
+            cp = segs[c][1]
+            if len(cp) < reps:
+                raise RuntimeError(f"{c}: {len(cp)} calibration copies")
+            cal[c] = (256 << 20) / (sum(cp) / reps * 1024)
+    rows, blob = [], {"workload": workload, "title": title, "calibration": {k: round(v, 4) for k, v in cal.items()},
+                      "kernels": []}
+    any_c = next(iter(segs))
+    for j, (label, _, algo, fl) in enumerate(classes):
+        order = []
+        groups = {}
+        for idx, (k, g, _) in enumerate(segs[any_c][0][j]):
+            key = (k, g)
+            if key not in groups:
+                order.append(key)
+                groups[key] = []
+            groups[key].append(idx)
+        for key in order:
+            idxs = groups[key]
+            stat = lambda c: sum(segs[c][0][j][i][2] for i in idxs) / len(idxs) if c in segs else None
+            e = {"class": label, "kernel": key[0], "grid_threads": key[1], "dispatches_per_call": len(idxs) / reps}
+            if cal:
+                rd, wr = stat("FETCH_SIZE") * 1024 * cal["FETCH_SIZE"], stat("WRITE_SIZE") * 1024 * cal["WRITE_SIZE"]
+                e.update(read_bytes=int(rd), write_bytes=int(wr))
+            for c in ("MfmaUtil", "SQ_WAIT_ANY", "SQ_WAVE_CYCLES", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_VALU",
+                      "SQ_ACTIVE_INST_LDS", "SQ_LDS_BANK_CONFLICT", "TCC_HIT_sum", "TCC_MISS_sum"):
+                if c in segs:
+                    e[c] = stat(c)
+            if algo and len(order) == 1:
+                e["algorithmic_bytes"] = algo
+            if fl and len(order) == 1:
+                e["flops"] = fl
+            blob["kernels"].append(e)
+    cols = [("dispatches / call", lambda e: f"{e['dispatches_per_call']:g}")]
+    if cal:
+        cols += [("read MB", lambda e: f"{e['read_bytes'] / 1e6:,.2f}"), ("written MB", lambda e: f"{e['write_bytes'] / 1e6:,.2f}"),
+                 ("algorithmic MB", lambda e: f"{e['algorithmic_bytes'] / 1e6:,.2f}" if "algorithmic_bytes" in e else "")
+                 , ("traffic / algorithmic", lambda e: f"{(e['read_bytes'] + e['write_bytes']) / e['algorithmic_bytes']:.2f}"
+                    if "algorithmic_bytes" in e else "")]
+    have = set(blob["kernels"][0]) if blob["kernels"] else set()
+    if "MfmaUtil" in have:
+        cols.append(("MfmaUtil %", lambda e: f"{e['MfmaUtil']:.1f}"))
+    if "SQ_WAVE_CYCLES" in have:
+        for c, lab in (("SQ_WAIT_ANY", "waiting / wave time"), ("SQ_WAIT_INST_ANY", "issue-stalled / wave time"),
+                       ("SQ_ACTIVE_INST_VALU", "VALU + MFMA issue / wave time"),
+                       ("SQ_ACTIVE_INST_LDS", "LDS issue / wave time")):
+            if c in have:
+                cols.append((lab, lambda e, c=c: f"{e[c] / e['SQ_WAVE_CYCLES']:.2f}" if e["SQ_WAVE_CYCLES"] else ""))
+    if "SQ_LDS_BANK_CONFLICT" in have:
+        cols.append(("LDS bank-conflict cycles", lambda e: f"{e['SQ_LDS_BANK_CONFLICT']:,.0f}"))
+    if "TCC_HIT_sum" in have and "TCC_MISS_sum" in have:
+        cols.append(("L2 hit rate", lambda e: f"{e['TCC_HIT_sum'] / max(1.0, e['TCC_HIT_sum'] + e['TCC_MISS_sum']):.2f}"))
+    lines = ["| class | kernel | grid threads | " + " | ".join(c for c, _ in cols) + " |",
+             "|" + "---|" * (len(cols) + 3)]
+    for e in blob["kernels"]:
+        lines.append(f"| {e['class']} | `{e['kernel'][:70]}` | {e['grid_threads']:,} | " +
+                     " | ".join(fn(e) for _, fn in cols) + " |")
+    head = f"Workload: {title}.\n\n"
+    if cal:
+        head += (f"Calibration: a 256 MiB device copy reads {256 * 1024 / cal['FETCH_SIZE']:,.1f} KiB of FETCH_SIZE and "
+                 f"{256 * 1024 / cal['WRITE_SIZE']:,.1f} KiB of WRITE_SIZE; bytes = FETCH_SIZE x 1024 x "
+                 f"{cal['FETCH_SIZE']:.4f} + WRITE_SIZE x 1024 x {cal['WRITE_SIZE']:.4f}.\n\n")
+    return head + "\n".join(lines) + "\n\n```json\n" + json.dumps(blob, indent=1, default=float) + "\n```\n"
 
 
 def tower_time(vt, img, steps, warmup):
@@ -814,7 +1072,21 @@ def main():
     ap.add_argument("--summarize-trace", metavar="TRACE_CSV", help="print a rocprofv3 kernel trace grouped by kernel")
     ap.add_argument("--summarize-counters", nargs="+", metavar="PMC_CSV",
                     help="print per-op MFMA / wait / LDS / L2 counters of --pmc passes over --traffic-probe")
+    ap.add_argument("--probe", choices=PROBES, help="only the eager launches of one workload that rocprofv3 --pmc "
+                    "passes count (see probe)")
+    ap.add_argument("--summarize-probe", nargs="+", metavar=("WORKLOAD", "PMC_CSV"),
+                    help="print the per-kernel summary of --pmc passes (one CSV each) over --probe WORKLOAD")
     a = ap.parse_args()
+    if a.summarize_probe:
+        import torch
+        with torch.inference_mode():
+            print(summarize_probe(a.summarize_probe[0], a.summarize_probe[1:]))
+        return
+    if a.probe:
+        import torch
+        with torch.inference_mode():
+            probe(a.probe)
+        return
     if a.summarize_counters:
         print(summarize_counters(a.summarize_counters))
         return
@@ -852,6 +1124,8 @@ def main():
     with torch.inference_mode():
         s = tower_time(vt, img, a.steps, a.warmup)
         agg = op_timing(vt, img)
+    if vt.rln_error():  # a timed-out row-block wait of the fused residual-LayerNorm GEMM leaves undefined results
+        raise RuntimeError(f"fused residual-LayerNorm GEMM reported error {vt.rln_error()}")
     ms = s * 1e3
     label, (tot_ms, n, fl, sym) = max(agg.items(), key=lambda kv: kv[1][0])
     avg_s = tot_ms / n / 1e3
@@ -886,9 +1160,15 @@ def main():
                 del imgs
                 vt.graphs.clear()
                 torch.cuda.empty_cache()
+        if vt.rln_error():
+            raise RuntimeError(f"fused residual-LayerNorm GEMM reported error {vt.rln_error()}")
     del vt
     torch.cuda.empty_cache()
     if not a.no_extra:
+        print("[bench] one vision block", file=sys.stderr, flush=True)
+        with torch.inference_mode():
+            out.setdefault("extra", {})["vision_block"] = block_bench(cpu=not a.no_cpu)
+        torch.cuda.empty_cache()
         print("[bench] decoder", file=sys.stderr, flush=True)
         with torch.inference_mode():
             out.setdefault("extra", {})["decoder"] = decode_bench()

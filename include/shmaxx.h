@@ -68,7 +68,9 @@ int mx_gemm_reduce(hipStream_t st, const float* P, int nsplit, long p_split, lon
  * sums through stats (>= mx_gemm_res_ln_stats_words(M, N) 64-bit words) and wait for each other, so the whole grid
  * must be resident: N % 64 == 0, N <= 4096 and ((M + 63) / 64) * (N / 64) <= the device's CU count, else
  * MX_ESHAPE. sync (>= mx_gemm_res_ln_sync_words(M) 32-bit words) and stats are zeroed once by the caller and then
- * kept ready by the kernel; calls that share them must be ordered on one stream. sync[0] != 0 after a call: a wait
+ * kept ready by the kernel; calls that share them must be ordered on one stream and have the same N (any M): where
+ * a row block's words sit depends on N / 64, so a call of another N could meet old words carrying the epoch it
+ * expects and accept stale statistics. Give each N its own stats / sync. sync[0] != 0 after a call: a wait
  * timed out and the results are undefined (zero both before the next call). The statistics combine per-tile sums in
  * fp32 in another order than mx_residual_layernorm's row sums (Y within a bf16 rounding of it; X identical for the
  * same k-loop). */
@@ -286,6 +288,15 @@ int mx_ssm_step_rows(hipStream_t st, const uint16_t* x0, const uint16_t* x1, con
                      const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT, const uint16_t* ba,
                      const uint16_t* sp, const int* frame, float* h, uint16_t* z, long ld_z, int T, int C,
                      const int* rows, int* stamps, int srows, uint16_t* xsave, long ld_save);
+/* The RG-LRU layer alone: TAPNext's RGLRU.forward(x, h0) -> (y, h) (tapnext/npu/r9/cpuemu.py:33-47, the layer the
+ * reference swaps at :110-116; the Python binding is refbind.rglru_forward / trecvit.RGLRU). x [T][ld_x] bf16 is
+ * the layer's input (the temporal conv's output), h0 [T][C] fp32 the state or NULL on the first frame (then
+ * h = bf(x * bf(sigmoid(gx)))); h [T][C] fp32 receives the new state (h == h0 updates in place) and y [T][ld_y]
+ * bf16 = bf(h). Gates as in mx_ssm_step (wxT / waT [H][64 out][64 in], bx / ba [C], sp = bf16(softplus(a_param))).
+ * x and the gate weights 16-byte aligned, ld_x % 8 == 0, C % 64 == 0. */
+int mx_rglru_step(hipStream_t st, const uint16_t* x, long ld_x, const float* h0, const uint16_t* wxT,
+                  const uint16_t* bx, const uint16_t* waT, const uint16_t* ba, const uint16_t* sp, float* h,
+                  uint16_t* y, long ld_y, int T, int C);
 /* Clip form of the same recurrence: per-frame affine maps h -> A h + B for F frames (x_stack = 3 history frames then
  * the F frames, frame stride fs_x), then the time scan. No reference counterpart (the reference only streams):
  * a frame-parallel restatement of the same recurrence. */

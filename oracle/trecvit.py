@@ -85,6 +85,31 @@ def ssm(yg, xx, hist, h0, conv_w, conv_b, a_param, wx, bx, wa, ba, first):
     return z.to(BF), h
 
 
+def rglru(x, h0, wx, bx, wa, ba, a_param):
+    """RGLRU.forward(x, h0) -> (y, h) of tapnext/npu/r9/cpuemu.py:33-47 with the exact transcendentals (its "exact"
+    variant, :66-72: fp64 sigmoid / exp / sqrt, one bf16 rounding each). x bf16 [T, C] (the layer's input, the conv
+    output xc), h0 fp32 [T, C] or None (first frame); wx / wa [H, 64 in, 64 out], bx / ba [H, 64]. The gate products
+    accumulate in fp64 and round once to bf16, as in `ssm`. Returns (y bf16 = h rounded, h fp32)."""
+    T, C = x.shape
+    H = wx.shape[0]
+    xd = x.double().view(T, H, 64)
+
+    def gate(w, b):  # BlockDiagonalLinear in bf16, then the sigmoid on the bf16 value, rounded
+        pre = f(torch.einsum("thi,hij->thj", xd, w.double()).float()) + f(b.float())[None]
+        return f(torch.sigmoid(f(pre).double()).float()).reshape(T, C)
+
+    gate_x, gate_a = gate(wx, bx), gate(wa, ba)
+    log_a = f(f(-8.0 * gate_a) * f(torch.log1p(torch.exp(a_param.double())).float())[None])
+    gated = f(x.float() * gate_x)
+    if h0 is None:
+        return gated.to(BF), gated
+    a = f(torch.exp(log_a.double()).float())
+    om = f(1.0 - f(torch.exp(2.0 * log_a.double()).float()))
+    mult = f(torch.sqrt(om.double()).float())
+    h = a * h0 + f(gated * mult)
+    return h.to(BF), h
+
+
 class Model:
     def __init__(self, w, H=12):
         self.w = w

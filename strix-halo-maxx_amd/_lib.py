@@ -64,6 +64,7 @@ SIGNATURES = {
     "mx_ssm_step": [P, P, P, P, P, L, P, L, P, P, P, P, P, P, P, P, P, P, L, I, I],
     "mx_ssm_prep": [P, P, L, L, P, P, P, P, P, P, P, P, P, P, I, I, I],
     "mx_rglru_scan": [P, P, P, P, I, I, I, P, L, L, P, L, L],
+    "mx_rglru_step": [P, P, L, P, P, P, P, P, P, P, P, L, I, I],
     "mx_counter_add": [P, P, I],
     "mx_gemm_bf16_noalloc": [P, I, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I, I, I],
     "mx_gemm_noalloc_max_ws": [],

@@ -1179,8 +1179,9 @@ extern "C" long mx_gemm_ws_counters(int cfg, int splits, int M, int N) {
 // Default (cfg, splits) when the caller passes cfg < 0: minimise estimated time = rounds of workgroups over the
 // 256 CUs x per-tile time, with per-tile time ~ BM*BN*(k-steps)/efficiency. Returns cfg * 16 + splits.
 extern "C" int mx_gemm_pick(int M, int N, int Kw) {
-  static const float eff[kNCfg] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f,
-                                   1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f, 1.4f, 1.1f, 0.9f, 0.9f, 0.7f};
+  static const float eff[] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f, 1.0f, 1.0f, 1.0f,
+                              1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f, 1.4f, 1.1f, 0.9f, 0.9f, 0.7f, 0.9f};
+  static_assert(sizeof eff / sizeof eff[0] == kNCfg, "one efficiency per tile config");
   const int nk = Kw / BK;
   int best = 0, bsplit = 1;
   float bt = 1e30f;

@@ -22,6 +22,8 @@
 //                * wave-parallel (too few chains to fill the GPU): one lane per frame, the maps composed with a
 //                  64-lane shuffle scan (steps 1, 2, 4, .., 32); same h as the streamed loop up to fp32
 //                  reassociation.
+// RG-LRU form (mx_rglru_step, the RGLRU.forward(x, h0) -> (y, h) layer of tapnext/npu/r9/cpuemu.py:33-47 on its
+// own): the conv and the y gate drop out (xc = x, y = bf(h)); the first frame is the host's h0 == null.
 // Crop form (mx_ssm_step_rows, one streamed frame of a moving crop of patch tokens): token t's state lives in row
 // rows[t] of the absolute state buffers (h, the history taps, the 32 x 32 patch grid + query rows), so the state
 // moves with the image content and nothing is copied. Tokens that leave the crop drop their state and tokens that
@@ -52,6 +54,8 @@ struct SsmArgs {
   const uint16_t* sp;      // [C] bf16(softplus(a_param))
   const int* frame;        // global index of frame 0 of this launch (first frame of the video <=> index 0)
   float* h; long fs_h;     // fp32 state [T][C] (step form) / unused (prep form)
+  const float* h0;         // the state read before the update (== h except in the RG-LRU form)
+  int first;               // RG-LRU form: 1 = first frame (no h0), in place of the device frame counter
   uint16_t* z; long ld_z; long fs_z;
   float* A; float* B; long fs_ab;  // prep form outputs [F][T][C]
   int T, C, mode;          // mode 0 = step, 1 = prep
@@ -68,13 +72,15 @@ __device__ __forceinline__ void row_stamp(const SsmArgs& p, int row, int tnow, b
   enter = fresh ? tnow : s.x;
 }
 
+// RG: the RG-LRU form (no conv, no y gate, first frame from p.first).
+template <bool RG>
 __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[64 * XS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, hk = lane >> 5;
   const int t0 = blockIdx.x * 64, q = blockIdx.y, f = blockIdx.z;
   const int c0 = q * 64;
-  const int tnow = *p.frame + f;
+  const int tnow = RG ? (p.first ? 0 : 1) : *p.frame + f;
   const bool first = tnow == 0;
   // this thread's slots in the gate products' result layout (lane = channel, registers = 16 tokens)
   const int tm = wave >> 1, tn = wave & 1;
@@ -125,8 +131,13 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int token = min(t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3), p.T - 1);
-      hraw[r] = p.h[(long)rw[r] * p.C + c];
-      yraw[r] = p.yg[f * p.fs_y + (long)token * p.ld_y + c];
+      if (RG) {
+        hraw[r] = first ? 0.f : p.h0[(long)rw[r] * p.C + c];  // no h0 on the first frame
+        yraw[r] = 0x3f80u;                                     // bf16 1.0: z = bf(h)
+      } else {
+        hraw[r] = p.h0[(long)rw[r] * p.C + c];
+        yraw[r] = p.yg[f * p.fs_y + (long)token * p.ld_y + c];
+      }
     }
   }
 
@@ -141,7 +152,7 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
     const int tok = (tid + 256 * it) >> 3;
     const int token = min(t0 + tok, p.T - 1);
     const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;  // clamped: never out of bounds
-    int ntap = first ? 1 : 4;  // taps 0 .. ntap - 1 carry data; the older ones are zero
+    int ntap = (first || RG) ? 1 : 4;  // taps 0 .. ntap - 1 carry data; the older ones are zero
     int enter = tnow;
     if (p.rows && !first) {
       bool fresh;
@@ -158,10 +169,13 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
     rowv[it] = row;
     enterv[it] = enter;
   }
-  const u32x4 bb = *reinterpret_cast<const u32x4*>(p.conv_b + c0 + cc);
-  u32x4 w[4];
+  u32x4 bb = {0u, 0u, 0u, 0u};
+  u32x4 w[4] = {bb, bb, bb, bb};
+  if (!RG) {
+    bb = *reinterpret_cast<const u32x4*>(p.conv_b + c0 + cc);
 #pragma unroll
-  for (int i = 0; i < 4; i++) w[i] = *reinterpret_cast<const u32x4*>(p.conv_w + i * p.C + c0 + cc);
+    for (int i = 0; i < 4; i++) w[i] = *reinterpret_cast<const u32x4*>(p.conv_w + i * p.C + c0 + cc);
+  }
 #pragma unroll
   for (int it = 0; it < 2; it++) {
     const int tok = (tid + 256 * it) >> 3;
@@ -169,9 +183,9 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
       *reinterpret_cast<u32x4*>(p.xsave + (long)rowv[it] * p.ld_save + c0 + cc) = xv[it][0];
       if (q == 0 && cc == 0) p.stamps[(tnow & 1) * p.srows + rowv[it]] = make_int2(enterv[it], tnow);
     }
-    u32x4 o;
+    u32x4 o = xv[it][0];  // RG-LRU form: xc = x
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
+    for (int e = 0; e < 4 && !RG; e++) {
       float r[2];
 #pragma unroll
       for (int hl = 0; hl < 2; hl++) {
@@ -361,12 +375,12 @@ extern "C" int mx_ssm_step(hipStream_t st, const uint16_t* x0, const uint16_t* x
                            const uint16_t* conv_b, const uint16_t* wxT, const uint16_t* bx, const uint16_t* waT,
                            const uint16_t* ba, const uint16_t* sp, const int* frame, float* h, uint16_t* z, long ld_z,
                            int T, int C) {
-  SsmArgs p{{x0, x1, x2, x3}, ld_x, 0, yg, ld_y, 0, conv_w, conv_b, wxT, bx, waT, ba, sp, frame, h, 0, z, ld_z, 0,
-            nullptr, nullptr, 0, T, C, 0, nullptr, nullptr, 0, nullptr, 0};
+  SsmArgs p{{x0, x1, x2, x3}, ld_x, 0, yg, ld_y, 0, conv_w, conv_b, wxT, bx, waT, ba, sp, frame, h, 0, h, 0,
+            z, ld_z, 0, nullptr, nullptr, 0, T, C, 0, nullptr, nullptr, 0, nullptr, 0};
   int rc = check_common(p, 1);
   if (rc) return rc;
   if (!yg || !h || !z) return MX_ENULL;
-  hipLaunchKernelGGL(ssm_kernel, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
@@ -379,13 +393,28 @@ extern "C" int mx_ssm_step_rows(hipStream_t st, const uint16_t* x0, const uint16
                                 const uint16_t* ba, const uint16_t* sp, const int* frame, float* h, uint16_t* z,
                                 long ld_z, int T, int C, const int* rows, int* stamps, int srows, uint16_t* xsave,
                                 long ld_save) {
-  SsmArgs p{{x0, x1, x2, x3}, ld_x, 0, yg, ld_y, 0, conv_w, conv_b, wxT, bx, waT, ba, sp, frame, h, 0, z, ld_z, 0,
-            nullptr, nullptr, 0, T, C, 0, rows, reinterpret_cast<int2*>(stamps), srows, xsave, ld_save};
+  SsmArgs p{{x0, x1, x2, x3}, ld_x, 0, yg, ld_y, 0, conv_w, conv_b, wxT, bx, waT, ba, sp, frame, h, 0, h, 0,
+            z, ld_z, 0, nullptr, nullptr, 0, T, C, 0, rows, reinterpret_cast<int2*>(stamps), srows, xsave, ld_save};
   int rc = check_common(p, 1);
   if (rc) return rc;
   if (!yg || !h || !z || !rows || !stamps || !xsave) return MX_ENULL;
   if (srows < T || ld_save % 8 || ((uintptr_t)xsave & 15) || ((uintptr_t)stamps & 7)) return MX_ESHAPE;
-  hipLaunchKernelGGL(ssm_kernel, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+
+// The RG-LRU layer alone (tapnext/npu/r9/cpuemu.py:33-47, RGLRU.forward(x, h0) -> (y, h)): x [T][ld_x] bf16 (the
+// conv output the layer receives), h0 [T][C] fp32 or null for the first frame (h = x * sigmoid(gate_x)), h [T][C]
+// fp32 written (may be h0: in place), y [T][ld_y] = bf16(h).
+extern "C" int mx_rglru_step(hipStream_t st, const uint16_t* x, long ld_x, const float* h0, const uint16_t* wxT,
+                             const uint16_t* bx, const uint16_t* waT, const uint16_t* ba, const uint16_t* sp, float* h,
+                             uint16_t* y, long ld_y, int T, int C) {
+  if (!x || !wxT || !bx || !waT || !ba || !sp || !h || !y) return MX_ENULL;
+  if (T < 1 || C % 64 || C > 65535 * 64 || ld_x % 8 || ld_x < C || ld_y < C || T > 65535 * 64) return MX_ESHAPE;
+  if (((uintptr_t)x | (uintptr_t)wxT | (uintptr_t)waT) & 15) return MX_ELAYOUT;
+  SsmArgs p{{x, x, x, x}, ld_x, 0, nullptr, 0, 0, nullptr, nullptr, wxT, bx, waT, ba, sp, nullptr, h, 0, h0,
+            h0 ? 0 : 1, y, ld_y, 0, nullptr, nullptr, 0, T, C, 0, nullptr, nullptr, 0, nullptr, 0};
+  hipLaunchKernelGGL(ssm_kernel<true>, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
@@ -396,13 +425,13 @@ extern "C" int mx_ssm_prep(hipStream_t st, const uint16_t* x_stack, long ld_x, l
                            const uint16_t* ba, const uint16_t* sp, const int* frame, float* A, float* B, int F, int T,
                            int C) {
   SsmArgs p{{x_stack + 3 * fs_x, x_stack + 2 * fs_x, x_stack + fs_x, x_stack}, ld_x, fs_x, nullptr, 0, 0, conv_w,
-            conv_b, wxT, bx, waT, ba, sp, frame, nullptr, 0, nullptr, 0, 0, A, B, (long)T * C, T, C, 1,
+            conv_b, wxT, bx, waT, ba, sp, frame, nullptr, 0, nullptr, 0, nullptr, 0, 0, A, B, (long)T * C, T, C, 1,
             nullptr, nullptr, 0, nullptr, 0};
   int rc = check_common(p, F);
   if (rc) return rc;
   if (!A || !B) return MX_ENULL;
   if (fs_x % 8 || F > 65535) return MX_ESHAPE;
-  hipLaunchKernelGGL(ssm_kernel, dim3((T + 63) / 64, C / 64, F), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, F), dim3(256), 0, st, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 

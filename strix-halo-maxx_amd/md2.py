@@ -85,8 +85,18 @@ class VisionTower:
         return ops.residual_layernorm(b["fc2"].partial(f), b["fc2"].b, x1, next_ln, eps=self.eps)
 
     def rln_error(self):
-        """Non-zero if a fused residual-LayerNorm launch timed out waiting for its row block (results undefined)."""
-        return ops.RlnWorkspace.get(self.dev).error()
+        """Non-zero if a fused residual-LayerNorm launch timed out waiting for its row block (results undefined).
+        Synchronises."""
+        return ops.RlnWorkspace.device_error(self.dev)
+
+    def check(self):
+        """Raise if a fused residual-LayerNorm launch since the last reset timed out (its outputs are undefined),
+        after zeroing the words so the next call starts clean. One small device read (synchronises)."""
+        err = self.rln_error()
+        if err:
+            ops.RlnWorkspace.reset_device(self.dev)
+            raise RuntimeError(f"fused residual-LayerNorm GEMM: a row-block wait timed out (error {err}); the last "
+                               "tower outputs are undefined")
 
     # ---- one pre-LN block (md2fast.py:152-157)
     def _use_splitk(self, B):
@@ -139,6 +149,7 @@ class VisionTower:
                 self._vision(img_buf)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
+        self.check()  # the eager warm-up runs finished without a timed-out wait
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             out = self._vision(img_buf)

@@ -59,6 +59,9 @@ class FastMD2:
         return self.td.query()
 
     def decide(self, logits):
+        """Per question (pred_yes, argmax or -1, margin); raises first if the frame's fused residual-LayerNorm
+        launches reported a timed-out wait (decide reads the logits on the host anyway)."""
+        self.vt.check()
         return self.td.decide(logits)
 
     def frame(self, img_u8):

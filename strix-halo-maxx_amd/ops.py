@@ -219,7 +219,7 @@ class MxLin:
         r2 = _rows(res, N)
         X = x_out if x_out is not None else torch.empty(M, N, device=x2.device, dtype=BF)
         Y = y_out if y_out is not None else torch.empty(M, N, device=x2.device, dtype=BF)
-        ws = RlnWorkspace.get(x2.device)
+        ws = RlnWorkspace.get(x2.device, N)
         _lib.check(_lib.load().mx_gemm_bf16_res_ln(
             stream(), x2.data_ptr(), x2.stride(0), self.w.data_ptr(), self.w.stride(0), ptr(self.b), r2.data_ptr(),
             r2.stride(0), X.data_ptr(), X.stride(0), ln[0].data_ptr(), ln[1].data_ptr(), Y.data_ptr(), Y.stride(0), M,
@@ -522,29 +522,55 @@ def layernorm(x, w, b, eps=1e-5, out=None):
 
 
 class RlnWorkspace:
-    """Row statistics and their generation counters for mx_gemm_bf16_res_ln on one device, allocated zeroed once at
-    their largest size (the launch allows at most one 64 x 64 tile per CU, so at most 256 tiles: 256 x 128 stats
-    words; 1 + 2 x 256 sync words) and then owned by the kernel, which leaves them ready for the next call. Calls on
-    one stream serialise; two streams must not share them."""
-    _by_dev = {}
+    """Row statistics and their generation counters for mx_gemm_bf16_res_ln, one per (device, N), allocated zeroed
+    once at their largest size (the launch allows at most one 64 x 64 tile per CU, so at most 256 tiles: 256 x 128
+    stats words; 1 + 2 x 256 sync words) and then owned by the kernel, which leaves them ready for the next call.
+    Keyed by N because where a row block's statistics sit depends on the tiles per row block (N / 64): calls of
+    another N on the same words could meet old words that carry the epoch they expect. Calls of one N may have any
+    M. Calls on one stream serialise; two streams must not share them."""
+    _by_key = {}
 
     def __init__(self, device):
         self.stats = torch.zeros(256 * 128, device=device, dtype=torch.int64)
         self.sync = torch.zeros(1024, device=device, dtype=torch.int32)
 
-    @classmethod
-    def get(cls, device):
+    @staticmethod
+    def _dev_index(device):
         d = torch.device(device)
-        key = d.index if d.index is not None else torch.cuda.current_device()
-        if key not in cls._by_dev:
+        return d.index if d.index is not None else torch.cuda.current_device()
+
+    @classmethod
+    def get(cls, device, N):
+        key = (cls._dev_index(device), int(N))
+        if key not in cls._by_key:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError("the residual-LayerNorm workspace must exist before graph capture")
-            cls._by_dev[key] = cls(d)
-        return cls._by_dev[key]
+            cls._by_key[key] = cls(torch.device(device))
+        return cls._by_key[key]
+
+    @classmethod
+    def device_error(cls, device):
+        """Non-zero if a wait of any fused residual-LayerNorm GEMM on the device timed out (its results are then
+        undefined). Synchronises."""
+        i = cls._dev_index(device)
+        return max((ws.error() for (d, _), ws in cls._by_key.items() if d == i), default=0)
+
+    @classmethod
+    def reset_device(cls, device):
+        """Zero every workspace of the device (after a timed-out wait)."""
+        i = cls._dev_index(device)
+        for (d, _), ws in cls._by_key.items():
+            if d == i:
+                ws.reset()
 
     def error(self):
-        """Non-zero if a wait of a fused residual-LayerNorm GEMM timed out (its results are then undefined)."""
+        """Non-zero if a wait of a fused residual-LayerNorm GEMM on these words timed out."""
         return int(self.sync[0].item())
+
+    def reset(self):
+        """Zero both buffers (after a timed-out wait, before the next call)."""
+        self.stats.zero_()
+        self.sync.zero_()
 
 
 def _cu_count(device):

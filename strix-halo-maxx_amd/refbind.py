@@ -11,6 +11,8 @@ protocols exactly:
     (hgemm.HI8Lin, hgemm.py:95-137; the shared quantisation of md2fast.py:52, 174)
   * Attn(H, T, D); __call__(q, k, v, out=None) with (1, H, T, D) views whose last dim is contiguous -> (1, T, H*D)
     (hattn.Attn, hattn.py:17-37; md2fast.py:155)
+  * rglru_forward(self, x, h0) -> (y, h): TAPNext's RGLRU.forward (tapnext/npu/r9/cpuemu.py:33-47), assigned the
+    way the reference swaps it (`tn.RGLRU.forward = refbind.rglru_forward`, cpuemu.py:110-116)
 Every call launches on torch's current stream and checks the library's status (the reference's `assert rc == 0`).
 Usage in the reference: FastMD2(model, lin_cls=refbind.MxLin, tlin_cls=refbind.MxI8Lin, hattn=True) with
 md2fast.HAttn = refbind.Attn (and md2fast.USE_FUSED_RES = True to run the residual adds in the GEMM epilogue).
@@ -28,6 +30,7 @@ _ARGS = {
     "mx_quant_weight_i8": [_P, _P, _L, _P, _L, _P, _I, _I],
     "mx_quant_rows_i8": [_P, _P, _L, _P, _L, _P, _I, _I],
     "mx_gemm_i8": [_P, _I, _P, _L, _P, _L, _P, _P, _P, _P, _L, _I, _P, _L, _I, _I, _I, _I, _I, _P, _L],
+    "mx_rglru_step": [_P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I],
 }
 _lib = None
 
@@ -151,3 +154,29 @@ class Attn:
                           out.data_ptr(), out.stride(0), D, out.stride(1), B, H, T, Tk, D, D ** -0.5, 0, Tk),
             "mx_sdpa")
         return out
+
+
+def rglru_forward(self, x, h0):
+    """RGLRU.forward(x, h0) -> (h.to(x.dtype), h) on mx_rglru_step, for assignment to the model's RGLRU class
+    (tapnext/npu/r9/cpuemu.py:33-47, swapped in at :110-116). Reads the module's input_gate.w / .b, a_gate.w / .b
+    ((H, 64, 64) block-diagonal weights and (H, 64) biases) and a_param once, on the first call, and keeps their
+    kernel layout on the module (the weights are frozen at inference). x: bf16 (..., C) on the GPU; h0: fp32 state of
+    x's shape, or None on the first frame (then h = x * sigmoid(gate_x), returned as (bf16, fp32))."""
+    prep = getattr(self, "_mx_rglru", None)
+    if prep is None:
+        dev = x.device
+        bf = lambda t: t.detach().to(dev, torch.bfloat16).contiguous()
+        prep = dict(wxT=bf(self.input_gate.w.transpose(-1, -2)), bx=bf(self.input_gate.b.reshape(-1)),
+                    waT=bf(self.a_gate.w.transpose(-1, -2)), ba=bf(self.a_gate.b.reshape(-1)),
+                    sp=torch.log1p(torch.exp(self.a_param.detach().double().cpu())).to(torch.bfloat16).to(dev))
+        self._mx_rglru = prep
+    C = prep["bx"].numel()
+    x2 = x.reshape(-1, C).to(torch.bfloat16).contiguous()
+    T = x2.shape[0]
+    h = torch.empty(T, C, device=x2.device, dtype=torch.float32)
+    y = torch.empty(T, C, device=x2.device, dtype=torch.bfloat16)
+    hp = None if h0 is None else h0.reshape(T, C).float().contiguous()
+    _ok(lib().mx_rglru_step(_st(), x2.data_ptr(), C, _p(hp), prep["wxT"].data_ptr(), prep["bx"].data_ptr(),
+                            prep["waT"].data_ptr(), prep["ba"].data_ptr(), prep["sp"].data_ptr(), h.data_ptr(),
+                            y.data_ptr(), C, T, C), "mx_rglru_step")
+    return y.view(x.shape).to(x.dtype), h.view(x.shape)

@@ -52,6 +52,57 @@ def _interleave_rows(w, b):
     return wi, bi
 
 
+class RGLRU:
+    """TAPNext's RG-LRU layer on its own, the interface the reference swaps numerics at:
+    RGLRU.forward(x, h0) -> (y, h) (tapnext/npu/r9/cpuemu.py:33-47, monkey-patched in at :110-116), one launch of
+    mx_rglru_step. x: bf16 (..., C), the layer's input (the temporal conv's output); h0: fp32 (..., C) state or None
+    on a video's first frame (then h = x * sigmoid(gate_x)); returns y = bf16(h) and h fp32, both new tensors of x's
+    shape. Parameters as the module holds them: input_gate / a_gate BlockDiagonalLinear weights (H, 64, 64) (in, out)
+    and biases (H, 64), a_param (C,)."""
+
+    def __init__(self, input_gate_w, input_gate_b, a_gate_w, a_gate_b, a_param, device="cuda"):
+        dev = torch.device(device)
+        H, bi, bo = input_gate_w.shape
+        if (bi, bo) != (64, 64) or tuple(a_gate_w.shape) != (H, 64, 64):
+            raise ValueError("block-diagonal gates must be (H, 64, 64)")
+        self.C = 64 * H
+        bf = lambda t: t.detach().to(dev, BF).contiguous()
+        self.wxT = bf(input_gate_w.transpose(-1, -2))   # [head][out][in]
+        self.waT = bf(a_gate_w.transpose(-1, -2))
+        self.bx = bf(input_gate_b.reshape(-1))
+        self.ba = bf(a_gate_b.reshape(-1))
+        # bf16(softplus(a_param)) from the exact value (F.softplus on the module's parameter, rounded once)
+        self.sp = torch.log1p(torch.exp(a_param.detach().double().cpu())).to(BF).to(dev).contiguous()
+
+    def forward(self, x, h0=None):
+        C = self.C
+        if x.shape[-1] != C:
+            raise ValueError(f"input width {x.shape[-1]} != {C}")
+        x2 = x.reshape(-1, C)
+        if x2.dtype != BF or x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.to(BF).contiguous()
+        T = x2.shape[0]
+        h = torch.empty(T, C, device=x2.device, dtype=torch.float32)
+        y = torch.empty(T, C, device=x2.device, dtype=BF)
+        hp = None
+        if h0 is not None:
+            if h0.shape != x.shape:
+                raise ValueError(f"h0 {tuple(h0.shape)} != x {tuple(x.shape)}")
+            hp = h0.reshape(T, C).to(torch.float32).contiguous()
+        call("mx_rglru_step", stream(), x2.data_ptr(), x2.stride(0), ptr(hp), self.wxT.data_ptr(), self.bx.data_ptr(),
+             self.waT.data_ptr(), self.ba.data_ptr(), self.sp.data_ptr(), h.data_ptr(), y.data_ptr(), C, T, C)
+        return y.view(x.shape), h.view(x.shape)
+
+    __call__ = forward
+
+
+def rglru_step(x, h0, params):
+    """(y bf16, h fp32) = the RG-LRU layer on x with state h0 (None: first frame); params: an RGLRU, or a dict with
+    the module's tensors (input_gate_w, input_gate_b, a_gate_w, a_gate_b, a_param)."""
+    layer = params if isinstance(params, RGLRU) else RGLRU(device=x.device, **params)
+    return layer(x, h0)
+
+
 class TRecViT:
     def __init__(self, weights, n_tokens=None, device="cuda", lin_cls=ops.MxLin):
         c = TRV

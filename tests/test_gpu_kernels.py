@@ -212,7 +212,7 @@ def test_gemm_res_ln_matches_unfused(dev, M, K):
     bet = (0.1 * torch.randn(N, generator=g)).to(BF).to(dev)
     lin = ops.MxLin(w, b)
     assert ops.res_ln_fits(M, N, dev)
-    ws = ops.RlnWorkspace.get(dev)
+    ws = ops.RlnWorkspace.get(dev, N)
     for call in range(3):
         x = torch.randn(M, K, generator=g).to(BF).to(dev)
         r = (torch.randn(M, N, generator=g) * 4).to(BF).to(dev)
@@ -235,6 +235,37 @@ def test_gemm_res_ln_matches_unfused(dev, M, K):
         assert bool(((yb - yr).abs() <= 2.0 ** -7 * scale + 1e-30).all()), (yb - yr).abs().max().item()
         assert (yb != yr).float().mean().item() <= 1e-3
         assert rel(yo, y32) <= 1.05 * rel(y_row, y32) + 1e-5, (rel(yo, y32), rel(y_row, y32))
+
+
+def test_gemm_res_ln_interleaved_widths(dev):
+    """Calls of different N and M in one process: (729, 1152), (100, 2048), (729, 1152), (100, 2048). Each N has
+    its own statistics words (the tiles per row block decide where a row block's words sit, so words left by another
+    N could carry an expected epoch); every call's x' is the unfused residual sum of its own inputs bit for bit
+    (k loop of the same tile) and y within the row LayerNorm tolerance, with no timeout."""
+    g = gen(77)
+    lins = {}
+    for call, (M, N) in enumerate([(729, 1152), (100, 2048), (729, 1152), (100, 2048)]):
+        if N not in lins:
+            w = (torch.randn(N, 1152, generator=g) * 0.02).to(BF)
+            lins[N] = (ops.MxLin(w, (torch.randn(N, generator=g) * 0.02).to(BF)),
+                       (1 + 0.1 * torch.randn(N, generator=g)).to(BF).to(dev), (0.1 * torch.randn(N, generator=g)).to(BF).to(dev))
+        lin, gam, bet = lins[N]
+        assert ops.res_ln_fits(M, N, dev)
+        x = torch.randn(M, 1152, generator=g).to(BF).to(dev)
+        r = (torch.randn(M, N, generator=g) * 4).to(BF).to(dev)
+        print(f"res_ln interleaved call {call}: M={M} N={N}", flush=True)
+        xo, yo = lin.res_ln(x, r, (gam, bet), eps=1e-6)
+        xs, ys = ops.residual_layernorm(lin.partial(x), lin.b, r, (gam, bet), eps=1e-6)
+        torch.cuda.synchronize()
+        assert ops.RlnWorkspace.device_error(dev) == 0
+        gsum = x.cpu().float() @ lins[N][0].w[:, :1152].cpu().float().t() + lin.b.cpu().float()
+        a, f = xo.float().cpu(), xs.float().cpu()
+        tol = 2.0 ** -7 * (gsum.abs() + torch.maximum(a.abs(), f.abs())) + 1e-30
+        assert int(((a - f).abs() > tol).sum()) == 0, call
+        y_row = ops.layernorm(xo, gam, bet, eps=1e-6).float().cpu()
+        scale = torch.maximum(y_row.abs(), bet.float().cpu().abs().expand(M, N)) + y_row.abs()
+        assert bool(((yo.float().cpu() - y_row).abs() <= 2.0 ** -7 * scale + 1e-30).all()), call
+        assert (yo.float().cpu() != y_row).float().mean().item() <= 1e-3, call
 
 
 def test_gemm_res_ln_refuses_a_grid_larger_than_the_gpu(dev):

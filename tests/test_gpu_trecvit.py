@@ -91,6 +91,43 @@ def test_ssm_step_vs_fp64_closed_form(dev, case):
     assert ((h.double() - wrong).abs() > bound).double().mean().item() > 0.3
 
 
+@pytest.mark.parametrize("first", [True, False])
+def test_rglru_layer_dropin_vs_oracle(dev, first):
+    """The RG-LRU layer on its own (trecvit.RGLRU and refbind.rglru_forward, both on mx_rglru_step) against the
+    oracle's RGLRU.forward restatement (cpuemu.py:33-47) on the SSM test's inputs: h within 1e-3 (the state
+    tolerance: the gate products sum in fp32 here, fp64 there, which can move a gate's bf16 rounding), y exactly
+    bf16(h), so y within one bf16 rounding plus the state tolerance of the oracle's y everywhere (near-zero h, where
+    a_t h0 and the input term cancel, turns the absolute state error into many ulps), rel-L2 1e-3, and more than one
+    ulp apart on at most 0.2 % of the elements; on the first frame (h0 None) h = x * sigmoid(gate_x). The
+    monkey-patch form on a module-shaped object returns the same tensors bit for bit, for a (1, T, C) batch view
+    too."""
+    import types
+    import strix_halo_maxx_amd.refbind as rb
+    d = ssm_inputs(21)
+    x, h0 = d["xx"], None if first else d["h0"]
+    y_ref, h_ref = otr.rglru(x, h0, d["wx"], d["bx"], d["wa"], d["ba"], d["a_param"])
+    layer = tv.RGLRU(d["wx"], d["bx"], d["wa"], d["ba"], d["a_param"], device=dev)
+    y, h = layer(x.to(dev), None if first else h0.to(dev))
+    torch.cuda.synchronize()
+    err = (h.cpu() - h_ref).abs().max().item()
+    print(f"RG-LRU layer first={first}: h max err {err:.2e}", flush=True)
+    assert y.dtype == BF and h.dtype == torch.float32 and y.shape == x.shape
+    assert err <= 1e-3
+    assert torch.equal(y, h.to(BF))
+    yf, yr = y.float().cpu(), y_ref.float()
+    ulp = torch.ldexp(torch.ones_like(yr), torch.frexp(yr)[1] - 8)
+    dy = (yf - yr).abs()
+    assert bool((dy <= ulp + 1e-3).all()) and rel(yf, yr) <= 1e-3
+    assert (dy > ulp).float().mean().item() <= 2e-3
+    mod = types.SimpleNamespace(input_gate=types.SimpleNamespace(w=d["wx"].to(dev), b=d["bx"].to(dev)),
+                                a_gate=types.SimpleNamespace(w=d["wa"].to(dev), b=d["ba"].to(dev)),
+                                a_param=d["a_param"].to(dev))
+    y2, h2 = rb.rglru_forward(mod, x[None].to(dev), None if first else h0[None].to(dev))
+    assert y2.shape == (1,) + tuple(x.shape) and torch.equal(y2[0], y) and torch.equal(h2[0], h)
+    y3, h3 = tv.rglru_step(x.to(dev), None if first else h0.to(dev), layer)
+    assert torch.equal(y3, y) and torch.equal(h3, h)
+
+
 def test_rmsnorm_random_scale_vs_oracle(dev):
     """mx_rmsnorm with a random scale (sc1 = bf16(scale + 1)) against the oracle's rmsnorm (pack8.py:222-229): at
     most one bf16 ulp anywhere (the fp32 sum of the rounded squares runs in another order), and a kernel that
@@ -313,41 +350,50 @@ def test_one_block_480p_frames_resized_on_device(dev):
 
 
 def test_twelve_blocks_streamed_graph_and_clip(dev):
-    """Config 3 shape (12 blocks, 1280 tokens): 4 streamed frames through HIP graphs vs the oracle; then the clip
-    form on the same 4 frames from a reset state, vs the oracle too (its attention runs another tile variant and its
-    recurrence is a reassociated scan, so it matches the streamed run to the same end-to-end tolerance, not bitwise)
-    with RG-LRU states close to the streamed ones."""
+    """Config 3 shape (12 blocks, 1280 tokens), free-running for 16 frames (the bench's clip length): the streamed
+    step through HIP graphs vs the oracle at every frame; then the clip form on the same 16 frames from a reset state,
+    vs the oracle too (its attention runs another tile variant and its recurrence is a reassociated scan, so it
+    matches the streamed run to the same end-to-end tolerance, not bitwise), with RG-LRU states close to the streamed
+    ones. Compounding bound: every frame within the 12-block end-to-end bound, rel-L2 2e-2, the same bound as the
+    first frame. The recurrence forgets (a = sigmoid(gate)^(8 softplus(p)), mostly far below 1 at these weights), so
+    a frame's error is its own blocks' rounding plus a decaying share of the earlier frames'; the test prints the
+    per-frame error so that growth would show."""
     w = S.trecvit_weights(0)
-    frames = S.frames_u8(1, 4)
+    NF = 16
+    frames = S.frames_u8(1, NF)
     qf = _qfeat()
     ora = otr.Model(w)
     m = tv.TRecViT(w, device=dev)
     m.reset()
-    outs, refs = [], []
-    for t in range(4):
+    outs, refs, errs = [], [], []
+    for t in range(NF):
         fin_ref = ora.step(frames[t], qf)
         refs.append(fin_ref)
         fin = m.step(frames[t].to(dev), qf.to(dev), use_graph=True).clone()
         outs.append(fin)
-        print(f"frame {t}: 12-block rel {rel(fin, fin_ref):.2e}", flush=True)
-        assert rel(fin, fin_ref) <= 2e-2
+        errs.append(rel(fin, fin_ref))
+        print(f"frame {t}: 12-block rel {errs[-1]:.2e}", flush=True)
+        assert errs[-1] <= 2e-2, (t, errs[-1])
     h_stream = [h.clone() for h in m.h]
     m.reset()
-    m.clip_state(4)
+    m.clip_state(NF)
     clip = m.forward_clip(frames.to(dev), qf.to(dev))
-    for t in range(4):
-        print(f"clip frame {t}: vs oracle {rel(clip[t], refs[t]):.2e}, vs streamed {rel(clip[t], outs[t]):.2e}", flush=True)
-        assert rel(clip[t], refs[t]) <= 2e-2
+    for t in range(NF):
+        r = rel(clip[t], refs[t])
+        print(f"clip frame {t}: vs oracle {r:.2e}, vs streamed {rel(clip[t], outs[t]):.2e}", flush=True)
+        assert r <= 2e-2, (t, r)
     for i in range(12):
         assert (m.h[i] - h_stream[i]).abs().max().item() <= 5e-2
+    print(f"streamed: first-4 mean {sum(errs[:4]) / 4:.2e}, last-4 mean {sum(errs[-4:]) / 4:.2e}", flush=True)
 
 
 def test_twelve_blocks_state_per_block_vs_oracle(dev):
-    """Config 3 shape (12 blocks, 1280 tokens) streamed for 16 frames, each GPU block fed the oracle's block input
-    and the oracle's previous state (conv history and RG-LRU h): every block's new fp32 state within 1e-3 of the
-    oracle's (max abs), every block's output within rel-L2 1e-2, at every frame."""
+    """Config 3 (12 blocks, 1280 tokens, 64 frames) streamed for all 64 frames, each GPU block fed the oracle's block
+    input and the oracle's previous state (conv history and RG-LRU h): every block's new fp32 state within 1e-3 of
+    the oracle's (max abs), every block's output within rel-L2 1e-2, at every frame (the fp32 state of frames 17-64
+    included)."""
     w = S.trecvit_weights(0)
-    NF = 16
+    NF = 64
     frames = S.frames_u8(11, NF)
     qf = _qfeat()
     ora = otr.Model(w)

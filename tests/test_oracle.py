@@ -116,6 +116,44 @@ def test_vision_block_structure_vs_fp64():
     assert ((out - no_res).norm() / ref.norm()) > 0.3
 
 
+class _EpilogueLinear(ov.TorchLinear):
+    """HLin-protocol Linear that takes GELU and the residual into its epilogue (the same bf16 roundings as torch's
+    separate ops) and records which epilogue each call asked for."""
+    fused_gelu = True
+    fused_res = True
+    calls = []
+
+    def __call__(self, x, gelu=False, res=None):
+        _EpilogueLinear.calls.append((self.weight.shape, gelu, res is not None))
+        y = F.linear(x, self.weight, self.bias)
+        y = ov.gelu(y) if gelu else y
+        return y if res is None else y + res
+
+
+def test_tower_with_injected_operators():
+    """tower_with (the operator-injected tower the reference-side binding is tested through) with torch's operators
+    is the oracle's tower bit for bit; with a Linear advertising fused_gelu / fused_res, fc1 gets gelu=True every
+    time, proj and fc2 get the residual only with fuse_res on (USE_FUSED_RES, md2fast.py:51-67), qkv and the patch
+    embedding never get either, and the result is unchanged."""
+    w = S.vision_weights(0, layers=2)
+    img = S.images_u8(1, 1)
+    ref = ov.tower(w, img)[0]
+    assert torch.equal(ov.tower_with(w, img[0], ov.TorchLinear, ov.TorchAttention), ref)
+    for fuse in (False, True):
+        _EpilogueLinear.calls = []
+        out = ov.tower_with(w, img[0], _EpilogueLinear, ov.TorchAttention, fuse_res=fuse)
+        assert torch.equal(out, ref)
+        by_shape = {}
+        for shape, g, r in _EpilogueLinear.calls:
+            by_shape.setdefault(tuple(shape), set()).add((g, r))
+        assert by_shape[(4304, 1152)] == {(True, False)}                      # fc1
+        assert by_shape[(1152, 4304)] == {(False, fuse)}                      # fc2
+        assert by_shape[(3456, 1152)] == {(False, False)}                     # qkv
+        assert by_shape[(1152, 1152)] == {(False, fuse)}                      # proj
+        assert by_shape[(1152, 588)] == {(False, False)}                      # patch embedding (+ pos, separate)
+        assert len(_EpilogueLinear.calls) == 1 + 4 * 2
+
+
 # ---------------------------------------------------------------------------------------------- text
 def test_rope_against_explicit_rotation():
     """rope (md2fast.py:162-167 / fused.py:53-58): a = x[0:16], b = x[16:32] (halves), output pairs interleaved
@@ -294,6 +332,24 @@ def _run_ssm(d, first, **over):
     a = dict(d, **over)
     return otr.ssm(a["yg"], a["xx"], a["hist"], a["h0"], a["conv_w"], a["conv_b"], a["a_param"], a["wx"], a["bx"],
                    a["wa"], a["ba"], first)
+
+
+def test_rglru_layer_is_the_ssm_core_with_identity_conv():
+    """rglru (RGLRU.forward, cpuemu.py:33-47) is the SSM core with the conv and the y gate taken out: ssm with conv
+    taps (0, 0, 0, 1), a zero conv bias and yg = 1 gives xc = x and z = bf(h), so both restatements agree bit for
+    bit, first frame (h0 None: y = gated x, h = its fp32 value) and later frames; a later frame also differs from the
+    first-frame rule (h0 is used)."""
+    d = _ssm_case()
+    T, C = d["xx"].shape
+    ident = torch.zeros(4, C, dtype=BF)
+    ident[3] = 1.0
+    ones = torch.ones(T, C, dtype=BF)
+    for first in (True, False):
+        z, h = _run_ssm(d, first, conv_w=ident, conv_b=torch.zeros(C, dtype=BF), yg=ones)
+        y2, h2 = otr.rglru(d["xx"], None if first else d["h0"], d["wx"], d["bx"], d["wa"], d["ba"], d["a_param"])
+        assert torch.equal(h, h2) and torch.equal(z, y2) and torch.equal(y2, h2.to(BF)), first
+    y1, h1 = otr.rglru(d["xx"], None, d["wx"], d["bx"], d["wa"], d["ba"], d["a_param"])
+    assert (h1 - h2).abs().max() > 0.1
 
 
 def test_ssm_first_frame_is_gated_input():

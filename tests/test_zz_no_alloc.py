@@ -51,9 +51,16 @@ def test_noalloc_gemm_equals_workspace_gemm_twice(dev, cfg, splits):
 
 
 def test_noalloc_gemm_refuses_beyond_its_workspace(dev):
+    """A split whose partials exceed the fixed array is refused (-3) before any launch, on real operand buffers: the
+    output keeps its NaN fill."""
     lib = _lib.load()
-    M, N, Kw = 186624, 4304, 1152
+    M, N, Kw = 1024, 1024, 1152
     assert lib.mx_gemm_ws_elems(0, 8, M, N) > lib.mx_gemm_noalloc_max_ws()
-    rc = lib.mx_gemm_bf16_noalloc(_lib.stream(), 0, 8, 0x10000, Kw, 0x10000, Kw, None, None, 0, 0, 0x10000, N, M, N,
-                                  Kw, Kw, 0, 0)
+    A = torch.zeros(M, Kw, device=dev, dtype=torch.bfloat16)
+    W = torch.zeros(N, Kw, device=dev, dtype=torch.bfloat16)
+    C = torch.full((M, N), float("nan"), device=dev, dtype=torch.bfloat16)
+    rc = lib.mx_gemm_bf16_noalloc(_lib.stream(), 0, 8, A.data_ptr(), Kw, W.data_ptr(), Kw, None, None, 0, 0,
+                                  C.data_ptr(), N, M, N, Kw, Kw, 0, 0)
     assert rc == -3
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(C.float()).all())
