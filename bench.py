@@ -916,17 +916,18 @@ def _probe_classes(workload):
 
 def probe(workload, reps=3):
     """Eager launches for rocprofv3 --pmc passes over one workload: after the warm-ups, for class i a marker fill of
-    10000 + i floats then `reps` calls of the class; then a marker fill of 99999 floats and the calibration: `reps`
-    device copies of 256 MiB (known traffic: 256 MiB read + 256 MiB written each)."""
+    10000 + i int16 values (a fill kernel no workload runs: FillFunctor<short>) then `reps` calls of the class; then
+    a marker fill of 99999 int16 values and the calibration: `reps` device copies of 256 MiB (known traffic: 256 MiB
+    read + 256 MiB written each)."""
     import torch
     title, classes = _probe_classes(workload)
     torch.cuda.synchronize()
     for i, (label, fn, _, _) in enumerate(classes):
-        torch.full((10000 + i,), 1.0, device="cuda:0")
+        torch.full((10000 + i,), 1, dtype=torch.int16, device="cuda:0")
         for _ in range(reps):
             fn()
         torch.cuda.synchronize()
-    torch.full((99999,), 1.0, device="cuda:0")
+    torch.full((99999,), 1, dtype=torch.int16, device="cuda:0")
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0")
     dst = torch.empty_like(src)
     for _ in range(reps):
@@ -966,7 +967,7 @@ def summarize_probe(workload, paths, reps=3):
         vals.update(_pmc_dispatches(p))
     segs = {}
     for c, seq in vals.items():
-        fills = [i for i, (k, _, _) in enumerate(seq) if "FillFunctor" in k]
+        fills = [i for i, (k, _, _) in enumerate(seq) if "FillFunctor<short>" in k]
         marks = fills[-(len(classes) + 1):]
         if len(marks) != len(classes) + 1:
             raise RuntimeError(f"{c}: {len(fills)} marker fills for {len(classes)} classes")

@@ -155,6 +155,13 @@ int mx_layernorm(hipStream_t st, const uint16_t* X, long ldx, const uint16_t* ga
 int mx_residual_layernorm(hipStream_t st, const float* P, int nsplit, long p_split, long ldp, const float* bias,
                           const uint16_t* R, long ldr, uint16_t* Xo, long ldxo, const uint16_t* gamma,
                           const uint16_t* beta, uint16_t* Y, long ldy, int rows, int D, float eps);
+/* The same reduction with the TRecViT RMSNorm of x -> Y (sc1 = bf16(scale + 1), required): the residual Linear of a
+ * TRecViT block fused with the RMSNorm that reads its output, i.e. `res = linear_out(z) + x; channel_pre_norm(res)`
+ * and `x3 = mlp3(...) + x2; next block's temporal_pre_norm(x3)` (tapnext/npu/step8.py:470-488; the RMSNorm numerics of
+ * tapnext/npu/pack8.py:222-229). At most 4 splits, D <= 2048. */
+int mx_residual_rmsnorm(hipStream_t st, const float* P, int nsplit, long p_split, long ldp, const float* bias,
+                        const uint16_t* R, long ldr, uint16_t* Xo, long ldxo, const uint16_t* sc1, uint16_t* Y,
+                        long ldy, int rows, int D, float eps);
 /* TRecViT RMSNorm with torch's bf16 rounding; sc1 = bf16(scale + 1). Replaces temporal_pre_norm / channel_pre_norm
  * (tapnext/npu/step8.py:474, :480; numerics tapnext/npu/pack8.py:222-229). */
 int mx_rmsnorm(hipStream_t st, const uint16_t* X, long ldx, const uint16_t* sc1, uint16_t* Y, long ldy, int rows, int D,

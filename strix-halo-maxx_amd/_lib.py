@@ -41,6 +41,7 @@ SIGNATURES = {
     "mx_sdpa_tiling": [I, I, I, I, P],
     "mx_layernorm": [P, P, L, P, P, P, L, I, I, F],
     "mx_residual_layernorm": [P, P, I, L, L, P, P, L, P, L, P, P, P, L, I, I, F],
+    "mx_residual_rmsnorm": [P, P, I, L, L, P, P, L, P, L, P, P, L, I, I, F],
     "mx_rmsnorm": [P, P, L, P, P, L, I, I, F],
     "mx_patchify_u8": [P, P, P, L, I, I, I, I],
     "mx_rope_kv": [P, P, L, P, P, P, P, I, I, I, I, I, I, I],

@@ -115,9 +115,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
 // Split-K reduction + bias + residual, then LayerNorm, one wave per row:
 //   x = bf16(bf16(sum_s P[s] + bias) + R)      (the Linear output rounded to bf16, then the fp32 residual add,
 //                                               rounded once more: torch's order for `linear(...) + res` in bf16)
-//   y = LayerNorm(x) as in layernorm_kernel (skipped when gamma is null)
+//   y = LayerNorm(x) as in layernorm_kernel (skipped when gamma is null), or with RMS the TRecViT RMSNorm of
+//   rmsnorm_kernel (gamma = sc1 = bf16(scale + 1), beta unused)
 // The partials are added in split order, so the result does not depend on scheduling.
-template <int MAXC, int NS>
+template <int MAXC, int NS, bool RMS = false>
 __global__ __launch_bounds__(256) void residual_layernorm_kernel(
     const float* __restrict__ P, long p_split, long ldp, const float* __restrict__ bias,
     const uint16_t* __restrict__ R, long ldr, uint16_t* __restrict__ Xo, long ldxo, const uint16_t* __restrict__ gamma,
@@ -182,9 +183,24 @@ __global__ __launch_bounds__(256) void residual_layernorm_kernel(
     }
     if (ok) *reinterpret_cast<u32x4*>(Xo + (long)row * ldxo + c * 8) = o;
 #pragma unroll
-    for (int e = 0; e < 8; e++) s += ok ? v[i][e] : 0.f;
+    for (int e = 0; e < 8; e++) s += ok ? (RMS ? rbf(v[i][e] * v[i][e]) : v[i][e]) : 0.f;
   }
   if (!gamma) return;
+  if constexpr (RMS) {  // s = sum_fp32 bf16(x^2); rstd = bf16(1 / sqrt(bf16(bf16(s / D) + eps))); y = bf16(bf16(x rstd) sc1)
+    const float ms = rbf(wave_sum(s) / (float)D);
+    const float rstd = rbf(1.0f / sqrtf(rbf(ms + eps)));
+    uint16_t* y = Y + (long)row * ldy;
+#pragma unroll
+    for (int i = 0; i < MAXC; i++) {
+      const int c = lane + 64 * i;
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        o[e] = pack2(rbf(v[i][2 * e] * rstd) * lo_bf(gv[i][e]), rbf(v[i][2 * e + 1] * rstd) * hi_bf(gv[i][e]));
+      if (c < nch) *reinterpret_cast<u32x4*>(y + c * 8) = o;
+    }
+    return;
+  }
   const float mean = wave_sum(s) / (float)D;
   float ss = 0.f;
 #pragma unroll
@@ -217,6 +233,24 @@ int check(const void* X, long ldx, const void* Y, long ldy, int rows, int D) {
   if (rows < 1 || D < 8 || D % 8 || D > 8192 || ldx % 8 || ldy % 8 || ldx < D || ldy < D) return MX_ESHAPE;
   if (((uintptr_t)X | (uintptr_t)Y) & 15) return MX_ELAYOUT;
   return MX_OK;
+}
+
+// residual_layernorm_kernel for a validated call: chunks per lane from D (<= 2048), splits 1..4.
+template <bool RMS>
+int launch_residual_norm(hipStream_t st, const float* P, int nsplit, long p_split, long ldp, const float* bias,
+                         const uint16_t* R, long ldr, uint16_t* Xo, long ldxo, const uint16_t* gamma,
+                         const uint16_t* beta, uint16_t* Y, long ldy, int rows, int D, float eps) {
+  dim3 g((rows + 3) / 4);
+  const int nch = D / 8;
+#define L2_(C, NS) hipLaunchKernelGGL((residual_layernorm_kernel<C, NS, RMS>), g, dim3(256), 0, st, P, p_split, ldp, bias, R, ldr, Xo, ldxo, gamma, beta, Y, ldy, rows, D, eps)
+#define L_(C) switch (nsplit) { case 1: L2_(C, 1); break; case 2: L2_(C, 2); break; case 3: L2_(C, 3); break; default: L2_(C, 4); }
+  if (nch <= 128) { L_(2); }
+  else if (nch <= 192) { L_(3); }
+  else if (nch <= 256) { L_(4); }
+  else return MX_ESHAPE;
+#undef L2_
+#undef L_
+  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
 }  // namespace
@@ -268,15 +302,25 @@ extern "C" int mx_residual_layernorm(hipStream_t st, const float* P, int nsplit,
     if (((uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)Y) & 15) return MX_ELAYOUT;
   }
   if (nsplit > 4) return MX_ESHAPE;
-  dim3 g((rows + 3) / 4);
-  const int nch = D / 8;
-#define L2_(C, NS) hipLaunchKernelGGL((residual_layernorm_kernel<C, NS>), g, dim3(256), 0, st, P, p_split, ldp, bias, R, ldr, Xo, ldxo, gamma, beta, Y, ldy, rows, D, eps)
-#define L_(C) switch (nsplit) { case 1: L2_(C, 1); break; case 2: L2_(C, 2); break; case 3: L2_(C, 3); break; default: L2_(C, 4); }
-  if (nch <= 128) { L_(2); }
-  else if (nch <= 192) { L_(3); }
-  else if (nch <= 256) { L_(4); }
-  else return MX_ESHAPE;
-#undef L2_
-#undef L_
-  return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+  return launch_residual_norm<false>(st, P, nsplit, p_split, ldp, bias, R, ldr, Xo, ldxo, gamma, beta, Y, ldy, rows,
+                                     D, eps);
+}
+
+// x = bf16(bf16(sum_s P[s] + bias) + R) -> Xo; y = the TRecViT RMSNorm of x (sc1 = bf16(scale + 1)) -> Y. The
+// epilogue of a residual Linear fused with the RMSNorm that reads its output (tapnext/npu/step8.py:470-488: the
+// ssm block's linear_out + x, then the channel pre-norm; the ViT block's mlp3 + x2, then the next block's temporal
+// pre-norm). Same operands and rules as mx_residual_layernorm, sc1 in place of gamma / beta (required).
+extern "C" int mx_residual_rmsnorm(hipStream_t st, const float* P, int nsplit, long p_split, long ldp,
+                                   const float* bias, const uint16_t* R, long ldr, uint16_t* Xo, long ldxo,
+                                   const uint16_t* sc1, uint16_t* Y, long ldy, int rows, int D, float eps) {
+  if (!P || !R || !Xo || !sc1 || !Y) return MX_ENULL;
+  if (nsplit < 1 || nsplit > 4 || rows < 1 || D < 8 || D % 8 || D > 2048) return MX_ESHAPE;
+  if (ldp % 4 || ldp < D || ldr % 8 || ldr < D || ldxo % 8 || ldxo < D || ldy % 8 || ldy < D ||
+      (nsplit > 1 && (p_split % 4 || p_split < (long)rows * ldp)))
+    return MX_ESHAPE;
+  if ((((uintptr_t)P | (uintptr_t)R | (uintptr_t)Xo | (uintptr_t)sc1 | (uintptr_t)Y) & 15) ||
+      (bias && ((uintptr_t)bias & 15)))
+    return MX_ELAYOUT;
+  return launch_residual_norm<true>(st, P, nsplit, p_split, ldp, bias, R, ldr, Xo, ldxo, sc1, nullptr, Y, ldy, rows,
+                                    D, eps);
 }

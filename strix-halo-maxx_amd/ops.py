@@ -597,6 +597,18 @@ def residual_layernorm(P, bias, res, ln=None, eps=1e-5, x_out=None, y_out=None):
     return x, y
 
 
+def residual_rmsnorm(P, bias, res, sc1, eps=1e-6, x_out=None, y_out=None):
+    """Reduce split-K partials P (splits, M, D) fp32: x = bf16(bf16(sum P + bias) + res); y = the TRecViT RMSNorm of
+    x with sc1 = bf16(scale + 1). Returns (x, y)."""
+    S, M, D = P.shape
+    r2 = _rows(res, D)
+    x = x_out if x_out is not None else torch.empty(M, D, device=P.device, dtype=BF)
+    y = y_out if y_out is not None else torch.empty(M, D, device=P.device, dtype=BF)
+    call("mx_residual_rmsnorm", stream(), P.data_ptr(), S, P.stride(0), P.stride(1), ptr(bias), r2.data_ptr(),
+         r2.stride(0), x.data_ptr(), x.stride(0), sc1.data_ptr(), y.data_ptr(), y.stride(0), M, D, float(eps))
+    return x, y
+
+
 def rmsnorm(x, sc1, eps=1e-6, out=None):
     """TRecViT RMSNorm; sc1 = bf16(scale + 1)."""
     D = x.shape[-1]

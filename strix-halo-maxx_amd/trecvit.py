@@ -174,6 +174,13 @@ class TRecViT:
         self.t = 0  # host copy of the frame index (selects the ring phase)
         self.graphs = {}
         self.out = None
+        # residual Linears whose epilogue runs as split-K fp32 partials + one row kernel that adds them, the bias and
+        # the residual and applies the norm that reads the result (the next block's temporal pre-norm or the encoder
+        # norm for mlp3): the two 3072-deep ones, whose 64 x 64 tiles otherwise stream 3072-wide rows per workgroup
+        # (N = 768 leaves too few output tiles for larger ones). At most splitk_max_rows rows: larger batches (the
+        # clip form) have enough tiles, and there the fp32 partials would only add traffic.
+        self.fuse_norm = {"down", "mlp3"}
+        self.splitk_max_rows = 8192
 
     def reset(self):
         """A new video: zero every block's conv history and RG-LRU state and mark the next frame first
@@ -198,12 +205,17 @@ class TRecViT:
         return out
 
     # ------------------------------------------------------------------ one block, one frame
-    def block_step(self, i, x, phase):
+    def block_step(self, i, x, phase, t0=None, next_norm=None):
+        """Block i on one streamed frame. t0: the block's temporal pre-norm of x when the previous block's tail
+        already computed it (else computed here). next_norm: None returns the block output; ("rms", sc1) or
+        ("ln", (gamma, beta)) returns (output, that norm of the output), the next block's temporal pre-norm or the
+        encoder norm, fused into the last Linear's residual epilogue where it pays."""
         b = self.blocks[i]
         T, D = self.T, self.D
         ring = self.ring[i]
         cur = ring[phase]
-        t0 = ops.rmsnorm(x, b["sc0"], eps=self.rms_eps)
+        if t0 is None:
+            t0 = ops.rmsnorm(x, b["sc0"], eps=self.rms_eps)
         b["yx"](t0, gelu=True, act_cols=D, out=cur)             # [gelu(y) | xx] into this frame's ring slot
         z = torch.empty(T, D, device=self.dev, dtype=BF)
         taps = [ring[(phase - k) % 4][:, D:] for k in range(4)]
@@ -211,20 +223,47 @@ class TRecViT:
              b["conv_w"].data_ptr(), b["conv_b"].data_ptr(), b["wxT"].data_ptr(), b["bx"].data_ptr(),
              b["waT"].data_ptr(), b["ba"].data_ptr(), b["sp"].data_ptr(), self.frame.data_ptr(), self.h[i].data_ptr(),
              z.data_ptr(), D, T, D)
-        return self._block_tail(b, z, x, 1)
+        return self._block_tail(b, z, x, 1, next_norm=next_norm)
 
-    def _block_tail(self, b, z, x, B, T=None):
+    def _norm(self, x, norm):
+        kind, p = norm
+        if kind == "rms":
+            return ops.rmsnorm(x, p, eps=self.rms_eps)
+        return ops.layernorm(x, *p, eps=self.ln_eps)
+
+    def _linres_norm(self, name, lin, a, res, norm):
+        """x = lin(a) + res with torch's roundings and norm(x). For the Linears in fuse_norm (and at most
+        splitk_max_rows rows) the GEMM writes split-K fp32 partials and one row kernel adds them, the bias and the
+        residual and applies the norm; otherwise the GEMM's residual epilogue, then the norm kernel."""
+        M = a.shape[0]
+        if name in self.fuse_norm and M <= self.splitk_max_rows and hasattr(lin, "partial"):
+            P = lin.partial(a)
+            kind, p = norm
+            if kind == "rms":
+                return ops.residual_rmsnorm(P, lin.b, res, p, eps=self.rms_eps)
+            return ops.residual_layernorm(P, lin.b, res, p, eps=self.ln_eps)
+        x = lin(a, res=res)
+        return x, self._norm(x, norm)
+
+    def _block_tail(self, b, z, x, B, T=None, next_norm=None):
         T = self.T if T is None else T
         D, H = self.D, self.H
-        res = b["out"](z, res=x)
-        g = b["up"](ops.rmsnorm(res, b["sc1"], eps=self.rms_eps), act="glu")
-        x1 = b["down"](g, res=res)
-        qkv = b["qkv"](ops.layernorm(x1, *b["ln1"], eps=self.ln_eps))
+        res, t1 = self._linres_norm("out", b["out"], z, x, ("rms", b["sc1"]))
+        g = b["up"](t1, act="glu")
+        x1, h1 = self._linres_norm("down", b["down"], g, res, ("ln", b["ln1"]))
+        qkv = b["qkv"](h1)
         q5 = qkv.view(B, T, 3, H, self.hd)
         q, k, v = (q5[:, :, j].transpose(1, 2) for j in range(3))
         a = ops.sdpa(q, k, v, scale=1.0 / 8.0)
-        x2 = b["oproj"](a.view(B * T, D), res=x1)
-        return b["mlp3"](b["mlp0"](ops.layernorm(x2, *b["ln2"], eps=self.ln_eps), act="erf"), res=x2)
+        x2, h2 = self._linres_norm("oproj", b["oproj"], a.view(B * T, D), x1, ("ln", b["ln2"]))
+        f = b["mlp0"](h2, act="erf")
+        if next_norm is None:
+            return b["mlp3"](f, res=x2)
+        return self._linres_norm("mlp3", b["mlp3"], f, x2, next_norm)
+
+    def _next_norm(self, i):
+        """The norm applied to block i's output: the next block's temporal pre-norm, or the encoder norm."""
+        return ("rms", self.blocks[i + 1]["sc0"]) if i + 1 < len(self.blocks) else ("ln", self.enc_norm)
 
     def heads(self, xq, tracks=None, logits=None, vis=None):
         """model.heads on the encoder-normed query rows xq (Q, D) bf16: tracks (Q, 2) fp32 (first-half / second-half
@@ -241,9 +280,10 @@ class TRecViT:
 
     def _frame(self, phase):
         x = self.embed(self.img, self.qfeat, self.x0)
+        t = ops.rmsnorm(x, self.blocks[0]["sc0"], eps=self.rms_eps) if self.blocks else None
         for i in range(len(self.blocks)):
-            x = self.block_step(i, x, phase)
-        fin = ops.layernorm(x, *self.enc_norm, eps=self.ln_eps)
+            x, t = self.block_step(i, x, phase, t0=t, next_norm=self._next_norm(i))
+        fin = t if self.blocks else ops.layernorm(x, *self.enc_norm, eps=self.ln_eps)
         if self.has_heads:
             self.heads(fin[self.n_img:self.n_img + self.n_q], self.tracks, self.logits, self.vis)
         call("mx_counter_add", stream(), self.frame.data_ptr(), 1)
@@ -304,9 +344,9 @@ class TRecViT:
         for f in range(F):
             self.embed(frames_u8[f], qfeat, x[f])
         x = x.view(F * T, D)
+        t0 = ops.rmsnorm(x, self.blocks[0]["sc0"], eps=self.rms_eps)
         for i, b in enumerate(self.blocks):
             st = self.stack[i]
-            t0 = ops.rmsnorm(x, b["sc0"], eps=self.rms_eps)
             b["yx"](t0, gelu=True, act_cols=D, out=st[3:].view(F * T, 2 * D))
             xs = st[:, :, D:]
             call("mx_ssm_prep", stream(), xs.data_ptr(), 2 * D, T * 2 * D, b["conv_w"].data_ptr(), b["conv_b"].data_ptr(),
@@ -316,8 +356,8 @@ class TRecViT:
             call("mx_rglru_scan", stream(), self.Ab.data_ptr(), self.Bb.data_ptr(), self.h[i].data_ptr(), F, T, D,
                  st[3:].data_ptr(), 2 * D, T * 2 * D, z.data_ptr(), D, T * D)
             st[:3].copy_(st[F:F + 3])  # the last 3 frames become the next clip's history
-            x = self._block_tail(b, z.view(F * T, D), x, F)
-        fin = ops.layernorm(x, *self.enc_norm, eps=self.ln_eps)
+            x, t0 = self._block_tail(b, z.view(F * T, D), x, F, next_norm=self._next_norm(i))
+        fin = t0
         call("mx_counter_add", stream(), self.frame.data_ptr(), F)
         self.t += F
         return fin.view(F, T, D)
@@ -361,11 +401,12 @@ class CropTracker:
         idx = ((r0 + ar)[:, None] * G + (c0 + ar)[None]).flatten()
         return torch.cat([idx, self.m.n_img + torch.arange(self.m.n_q)]).to(torch.int32)
 
-    def _block(self, i, x, phase, T):
+    def _block(self, i, x, t0, phase, T):
+        """Block i over the crop's T tokens; t0 = its temporal pre-norm of x. Returns (output, the next norm of it)."""
         m = self.m
         b, D, ring = m.blocks[i], m.D, m.ring[i]
         cur = self.cur[:T]
-        b["yx"](ops.rmsnorm(x, b["sc0"], eps=m.rms_eps), gelu=True, act_cols=D, out=cur)
+        b["yx"](t0, gelu=True, act_cols=D, out=cur)
         z = torch.empty(T, D, device=m.dev, dtype=BF)
         taps = [cur[:, D:]] + [ring[(phase - k) % 4][:, D:] for k in (1, 2, 3)]
         call("mx_ssm_step_rows", stream(), *(t.data_ptr() for t in taps), 2 * D, cur.data_ptr(), 2 * D,
@@ -373,16 +414,17 @@ class CropTracker:
              b["waT"].data_ptr(), b["ba"].data_ptr(), b["sp"].data_ptr(), m.frame.data_ptr(), m.h[i].data_ptr(),
              z.data_ptr(), D, T, D, self.rows.data_ptr(), self.stamps.data_ptr(), m.T,
              ring[phase][:, D:].data_ptr(), 2 * D)
-        return m._block_tail(b, z, x, 1, T)
+        return m._block_tail(b, z, x, 1, T, next_norm=m._next_norm(i))
 
     def _frame(self, phase, n):
         m = self.m
         T = n * n + m.n_q
         x = m.embed(m.img, m.qfeat, m.x0)  # the whole grid: a patch's embedding only depends on its own pixels
         xc = torch.index_select(x, 0, self.rows[:T], out=self.xc[:T])
+        t = ops.rmsnorm(xc, m.blocks[0]["sc0"], eps=m.rms_eps)
         for i in range(len(m.blocks)):
-            xc = self._block(i, xc, phase, T)
-        fin = ops.layernorm(xc, *m.enc_norm, eps=m.ln_eps)
+            xc, t = self._block(i, xc, t, phase, T)
+        fin = t
         if m.has_heads:
             m.heads(fin[n * n:], m.tracks, m.logits, m.vis)
         call("mx_counter_add", stream(), m.frame.data_ptr(), 1)

@@ -195,6 +195,41 @@ def test_residual_layernorm_matches_unfused(dev):
     assert torch.equal(yo.cpu(), ops.layernorm(xo, gam, bet, eps=1e-6).cpu())
 
 
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_residual_rmsnorm_matches_oracle(dev, splits):
+    """mx_residual_rmsnorm on TRecViT's down / mlp3 shape (1280 x 768, K = 3072): x = bf16(bf16(sum P + bias) + res)
+    bit for bit against the CPU restatement of the partials in split order; y against the oracle's RMSNorm chain
+    (pack8.py:222-229) applied to that x: at most one bf16 ulp anywhere (its fp32 sum of the rounded squares runs in
+    another order), on at most 1 % of the elements, and the rmsnorm kernel on the same x exactly."""
+    import oracle.trecvit as otr
+    M, K, N = 1280, 3072, 768
+    g = gen(31 + splits)
+    a = torch.randn(M, K, generator=g).to(BF).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF).to(dev)
+    b = (torch.randn(N, generator=g) * 0.02).to(dev)
+    r = (torch.randn(M, N, generator=g) * 2).to(BF).to(dev)
+    scale = (torch.randn(N, generator=g) * 0.3).to(BF)
+    sc1 = (scale.float() + 1).to(BF).to(dev)
+    kt = K // 64
+    P = torch.empty(splits, M, N, device=dev)
+    _lib.call("mx_gemm_bf16_partial", _lib.stream(), 0, splits, a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
+              P.data_ptr(), N, M * N, M, N, K, K)
+    print(f"residual rmsnorm, {splits} splits of {kt} k-steps", flush=True)
+    xo, yo = ops.residual_rmsnorm(P, b, r, sc1, eps=1e-6)
+    Pc = P.cpu()
+    acc = Pc[0].clone()
+    for i in range(1, splits):
+        acc += Pc[i]
+    exp = ((acc + b.cpu()).to(BF).float() + r.cpu().float()).to(BF)
+    assert torch.equal(xo.cpu(), exp)
+    ref = otr.rmsnorm(exp, scale)
+    d = (yo.cpu().view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert d.max().item() <= 1 and (d > 0).float().mean().item() <= 1e-2
+    assert torch.equal(yo.cpu(), ops.rmsnorm(xo, sc1, eps=1e-6).cpu())
+    full = (a.float() @ w.float().t()).cpu()
+    assert rel(acc, full) < 1e-5  # the partials cover the whole K range
+
+
 @pytest.mark.parametrize("M,K", [(729, 1152), (729, 4304), (100, 1152)])
 def test_gemm_res_ln_matches_unfused(dev, M, K):
     """mx_gemm_bf16_res_ln (residual Linear + LayerNorm in one launch, row statistics exchanged between the tiles of

@@ -410,7 +410,11 @@ def test_twelve_blocks_state_per_block_vs_oracle(dev):
                 for k in (1, 2, 3):
                     m.ring[i][(phase - k) % 4][:, D:].copy_(ora.hist[i][k - 1])
             m.frame.fill_(t)
-            y = m.block_step(i, x.to(dev), phase)
+            if t % 2:  # the form the streamed frame runs: mlp3 with the next norm fused into its epilogue
+                y, tn = m.block_step(i, x.to(dev), phase, next_norm=m._next_norm(i))
+                assert torch.equal(tn, m._norm(y, m._next_norm(i))), (t, i)
+            else:
+                y = m.block_step(i, x.to(dev), phase)
             x = ora.block(i, x)
             eh = (m.h[i].cpu() - ora.h[i]).abs().max().item()
             ex = rel(y, x)
