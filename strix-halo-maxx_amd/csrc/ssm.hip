@@ -31,14 +31,16 @@
 // buffered by frame parity (read the previous frame's buffer, write this frame's), decides which state the row
 // still has: h0 only if it was in the crop on the previous frame, history tap k only if it has been in the crop
 // without a gap since frame t - k. The current frame's conv input is saved to its absolute row for later frames.
-// Tile: a workgroup owns 64 tokens x one 64-channel head of one frame; the conv output tile is staged in LDS as the
-// MFMA row operand; the gate weights are pre-transposed [head][out][in] so both operands are 16-byte lane reads; the
-// MFMA result layout (lane = output channel, registers = tokens) makes the elementwise tail coalesced along channels.
+// Tile: a 1024-thread workgroup owns 64 tokens x one 64-channel head of one frame; the conv output tile is staged in
+// LDS as the MFMA row operand; the gate weights are pre-transposed [head][out][in] so both operands are 16-byte lane
+// reads; the gate sums go through LDS to the elementwise tail, which runs 4 consecutive channels of one token per
+// thread (16- / 8-byte state, yg and z accesses).
 #include "common.h"
 
 namespace {
 
 constexpr int XS = 72;  // LDS row stride of the conv tile (64 + 8)
+constexpr int GS = 68;  // LDS row stride of the gate-sum tiles (fp32; 16-byte rows for the tail's vector reads)
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
@@ -73,22 +75,28 @@ __device__ __forceinline__ void row_stamp(const SsmArgs& p, int row, int tnow, b
 }
 
 // RG: the RG-LRU form (no conv, no y gate, first frame from p.first).
+// 1024 threads (16 waves) per 64-token x 64-channel tile. The conv tile goes to LDS (512 threads, one 8-channel item
+// each); waves 0-3 run the gate products (MFMA 32x32x16, wave -> 32 tokens x 32 channels) and leave the raw fp32
+// sums in LDS; then all 1024 threads run the elementwise RG-LRU tail on 4 (token, channel) elements each: thread ->
+// token tid / 16, channels 4 (tid % 16) .. + 3, so the state / yg / z accesses are 16- / 8-byte vectors and each
+// thread's serial chain of transcendentals is 4 elements long, with 4 waves per SIMD to hide its latency.
 template <bool RG>
-__global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
+__global__ __launch_bounds__(1024) void ssm_kernel(SsmArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[64 * XS];
+  __shared__ __attribute__((aligned(16))) float gsh[2][64 * GS];  // gate sums [token][channel], x then a
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, hk = lane >> 5;
   const int t0 = blockIdx.x * 64, q = blockIdx.y, f = blockIdx.z;
   const int c0 = q * 64;
   const int tnow = RG ? (p.first ? 0 : 1) : *p.frame + f;
   const bool first = tnow == 0;
-  // this thread's slots in the gate products' result layout (lane = channel, registers = 16 tokens)
-  const int tm = wave >> 1, tn = wave & 1;
-  const int cl = tn * 32 + lr, c = c0 + cl;
-  // the gate products' weight fragments and the per-channel RG-LRU parameters depend on nothing below: issued first
-  // (the 16-bit parameters held unpacked, so no wait is needed to pack them)
+  // tail element group of this thread
+  const int tl = tid >> 4, cl = (tid & 15) * 4;
+  const int token = t0 + tl, tok_c = min(token, p.T - 1);
+  // the gate products' weight fragments (waves 0-3: wave -> tm = token half, tn = channel half), issued first
+  const int tm = (wave >> 1) & 1, tn = wave & 1;
   u32x4 wxf[4], waf[4];
-  {
+  if (wave < 4) {
     const uint16_t* wxr = p.wxT + ((long)q * 64 + tn * 32 + lr) * 64;
     const uint16_t* war = p.waT + ((long)q * 64 + tn * 32 + lr) * 64;
 #pragma unroll
@@ -97,93 +105,62 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
       waf[s4] = *reinterpret_cast<const u32x4*>(war + 16 * s4 + 8 * hk);
     }
   }
-  const uint32_t spw = p.sp[c], bxw = p.bx[c], baw = p.ba[c];
+  // per-channel RG-LRU parameters of the thread's 4 channels (held as packed bf16 pairs)
+  const u32x2 spw = *reinterpret_cast<const u32x2*>(p.sp + c0 + cl);
+  const u32x2 bxw = *reinterpret_cast<const u32x2*>(p.bx + c0 + cl);
+  const u32x2 baw = *reinterpret_cast<const u32x2*>(p.ba + c0 + cl);
 
-  // ---- step form: the fp32 state and yg of this thread's 16 (token, channel) slots are loaded first, so their
-  // latency runs under the conv and the gate products (each slot belongs to this thread alone). The loads take
-  // clamped indices and no branch separates them (a per-slot branch made the compiler wait for each slot's loads in
-  // turn); which slots count (token < T, first frame, fresh crop row) is applied where the values are used. The crop
-  // form's row map, stamps and state are three dependent rounds, each issued for all 16 slots.
-  float hraw[16];
-  uint32_t yraw[16];    // the yg bf16 word of each slot, held unpacked (packing two per register would wait for them)
-  int rw[16];           // state row of each slot
-  uint32_t freshm = 0u;  // bit r: slot r's crop row was not in the crop on the previous frame (its state reads as 0)
+  // ---- step form: the state row and yg of the thread's 4 elements, loaded first (their latency runs under the conv
+  // and the gate products). Clamped indices, no branch around the loads; which of them count (token < T, first frame,
+  // fresh crop row) is applied where the values are used. The crop form's row map and stamp are dependent rounds.
+  f32x4 hraw = {0.f, 0.f, 0.f, 0.f};
+  u32x2 yraw = {0x3f803f80u, 0x3f803f80u};  // bf16 1.0 pairs: the RG-LRU form's z = bf(h)
+  int rw = tok_c;                            // state row of the thread's token
+  bool fresh = false;                        // its crop row was not in the crop on the previous frame (state 0)
   if (p.mode == 0) {
     if (p.rows) {
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int token = min(t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3), p.T - 1);
-        rw[r] = min(max(p.rows[token], 0), p.srows - 1);
-      }
+      rw = min(max(p.rows[tok_c], 0), p.srows - 1);
       if (!first) {
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          bool fresh;
-          int enter;
-          row_stamp(p, rw[r], tnow, fresh, enter);
-          freshm |= (fresh ? 1u : 0u) << r;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; r++) rw[r] = min(t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3), p.T - 1);
-    }
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int token = min(t0 + tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3), p.T - 1);
-      if (RG) {
-        hraw[r] = first ? 0.f : p.h0[(long)rw[r] * p.C + c];  // no h0 on the first frame
-        yraw[r] = 0x3f80u;                                     // bf16 1.0: z = bf(h)
-      } else {
-        hraw[r] = p.h0[(long)rw[r] * p.C + c];
-        yraw[r] = p.yg[f * p.fs_y + (long)token * p.ld_y + c];
+        int enter;
+        row_stamp(p, rw, tnow, fresh, enter);
       }
     }
+    if (!(RG && first)) hraw = *reinterpret_cast<const f32x4*>(p.h0 + (long)rw * p.C + c0 + cl);
+    if (!RG) yraw = *reinterpret_cast<const u32x2*>(p.yg + f * p.fs_y + (long)tok_c * p.ld_y + c0 + cl);
   }
 
-  // ---- temporal conv of this 64 x 64 tile into LDS (8 channels per item, 2 items per thread). Both items' loads go
-  // out before either item's arithmetic (one memory round trip, not two); both items share the channel group cc
-  // (256 is a multiple of 8), so the conv weights and bias are loaded once.
-  const int cc = (tid & 7) * 8;
-  u32x4 xv[2][4];
-  int rowv[2], enterv[2];
-#pragma unroll
-  for (int it = 0; it < 2; it++) {
-    const int tok = (tid + 256 * it) >> 3;
-    const int token = min(t0 + tok, p.T - 1);
-    const int row = p.rows ? min(max(p.rows[token], 0), p.srows - 1) : token;  // clamped: never out of bounds
+  // ---- temporal conv of the 64 x 64 tile into LDS: threads 0-511, one 8-channel item each
+  if (tid < 512) {
+    const int tok = tid >> 3, cc = (tid & 7) * 8;
+    const int tk = min(t0 + tok, p.T - 1);
+    const int row = p.rows ? min(max(p.rows[tk], 0), p.srows - 1) : tk;  // clamped: never out of bounds
     int ntap = (first || RG) ? 1 : 4;  // taps 0 .. ntap - 1 carry data; the older ones are zero
     int enter = tnow;
     if (p.rows && !first) {
-      bool fresh;
-      row_stamp(p, row, tnow, fresh, enter);
-      ntap = fresh ? 1 : min(4, tnow - enter + 1);  // tap k (frame tnow - k) needs enter <= tnow - k
+      bool fr;
+      row_stamp(p, row, tnow, fr, enter);
+      ntap = fr ? 1 : min(4, tnow - enter + 1);  // tap k (frame tnow - k) needs enter <= tnow - k
     }
+    u32x4 xv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      const long r = i == 0 ? token : row;  // the current frame's rows are the launch's tokens
+      const long r = i == 0 ? tk : row;  // the current frame's rows are the launch's tokens
       if (i < ntap) v = *reinterpret_cast<const u32x4*>(p.tap[i] + f * p.fs_x + r * p.ld_x + c0 + cc);
-      xv[it][i] = v;
+      xv[i] = v;
     }
-    rowv[it] = row;
-    enterv[it] = enter;
-  }
-  u32x4 bb = {0u, 0u, 0u, 0u};
-  u32x4 w[4] = {bb, bb, bb, bb};
-  if (!RG) {
-    bb = *reinterpret_cast<const u32x4*>(p.conv_b + c0 + cc);
+    u32x4 bb = {0u, 0u, 0u, 0u};
+    u32x4 w[4] = {bb, bb, bb, bb};
+    if (!RG) {
+      bb = *reinterpret_cast<const u32x4*>(p.conv_b + c0 + cc);
 #pragma unroll
-    for (int i = 0; i < 4; i++) w[i] = *reinterpret_cast<const u32x4*>(p.conv_w + i * p.C + c0 + cc);
-  }
-#pragma unroll
-  for (int it = 0; it < 2; it++) {
-    const int tok = (tid + 256 * it) >> 3;
+      for (int i = 0; i < 4; i++) w[i] = *reinterpret_cast<const u32x4*>(p.conv_w + i * p.C + c0 + cc);
+    }
     if (p.rows && t0 + tok < p.T) {
-      *reinterpret_cast<u32x4*>(p.xsave + (long)rowv[it] * p.ld_save + c0 + cc) = xv[it][0];
-      if (q == 0 && cc == 0) p.stamps[(tnow & 1) * p.srows + rowv[it]] = make_int2(enterv[it], tnow);
+      *reinterpret_cast<u32x4*>(p.xsave + (long)row * p.ld_save + c0 + cc) = xv[0];
+      if (q == 0 && cc == 0) p.stamps[(tnow & 1) * p.srows + row] = make_int2(enter, tnow);
     }
-    u32x4 o = xv[it][0];  // RG-LRU form: xc = x
+    u32x4 o = xv[0];  // RG-LRU form: xc = x
 #pragma unroll
     for (int e = 0; e < 4 && !RG; e++) {
       float r[2];
@@ -191,10 +168,10 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
       for (int hl = 0; hl < 2; hl++) {
         auto get = [&](u32x4 v) { return hl ? hi_bf(v[e]) : lo_bf(v[e]); };
         // w row i = tap (t-3+i): oldest first; xv index 3-i holds frame t-3+i
-        float sum = rbf(get(xv[it][3]) * get(w[0]));
-        sum = sum + rbf(get(xv[it][2]) * get(w[1]));
-        sum = sum + rbf(get(xv[it][1]) * get(w[2]));
-        sum = sum + rbf(get(xv[it][0]) * get(w[3]));
+        float sum = rbf(get(xv[3]) * get(w[0]));
+        sum = sum + rbf(get(xv[2]) * get(w[1]));
+        sum = sum + rbf(get(xv[1]) * get(w[2]));
+        sum = sum + rbf(get(xv[0]) * get(w[3]));
         r[hl] = rbf(sum) + get(bb);
       }
       o[e] = pack2(r[0], r[1]);
@@ -203,27 +180,40 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
   }
   __syncthreads();
 
-  // ---- gates: wave -> 32 tokens (tm) x 32 output channels (tn) of both gates
-  f32x16 gx, ga;
+  // ---- gates: waves 0-3 -> 32 tokens (tm) x 32 output channels (tn) of both gates; raw fp32 sums to LDS
+  if (wave < 4) {
+    f32x16 gx, ga;
 #pragma unroll
-  for (int e = 0; e < 16; e++) { gx[e] = 0.f; ga[e] = 0.f; }
+    for (int e = 0; e < 16; e++) { gx[e] = 0.f; ga[e] = 0.f; }
 #pragma unroll
-  for (int s = 0; s < 4; s++) {
-    const int k = 16 * s + 8 * hk;
-    const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(&xs[(tm * 32 + lr) * XS + k]));
-    gx = mfma32(a, as_bf16x8(wxf[s]), gx);
-    ga = mfma32(a, as_bf16x8(waf[s]), ga);
+    for (int s = 0; s < 4; s++) {
+      const int k = 16 * s + 8 * hk;
+      const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(&xs[(tm * 32 + lr) * XS + k]));
+      gx = mfma32(a, as_bf16x8(wxf[s]), gx);
+      ga = mfma32(a, as_bf16x8(waf[s]), ga);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int tr = tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
+      gsh[0][tr * GS + tn * 32 + lr] = gx[r];
+      gsh[1][tr * GS + tn * 32 + lr] = ga[r];
+    }
   }
+  __syncthreads();
 
-  // ---- elementwise RG-LRU: lane = channel, registers = 16 tokens
-  const float spc = bf2f((uint16_t)spw), bxc = bf2f((uint16_t)bxw), bac = bf2f((uint16_t)baw);
+  // ---- elementwise RG-LRU: 4 channels of one token per thread
+  if (token >= p.T) return;
+  const f32x4 gxv = *reinterpret_cast<const f32x4*>(&gsh[0][tl * GS + cl]);
+  const f32x4 gav = *reinterpret_cast<const f32x4*>(&gsh[1][tl * GS + cl]);
+  const u32x2 xcw = *reinterpret_cast<const u32x2*>(&xs[tl * XS + cl]);
+  f32x4 hv, Av, Bv;
+  float zv[4];
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int tl = tm * 32 + 8 * (r >> 2) + 4 * hk + (r & 3);
-    const int token = t0 + tl;
-    if (token >= p.T) continue;
-    const float xcv = bf2f(xs[tl * XS + cl]);
-    const float gxp = rbf(rbf(gx[r]) + bxc), gap = rbf(rbf(ga[r]) + bac);
+  for (int e = 0; e < 4; e++) {
+    const uint32_t pick = (e >> 1) ? 1 : 0;
+    auto half = [&](const u32x2& w) { return (e & 1) ? hi_bf(pick ? w.y : w.x) : lo_bf(pick ? w.y : w.x); };
+    const float xcv = half(xcw), spc = half(spw), bxc = half(bxw), bac = half(baw);
+    const float gxp = rbf(rbf(gxv[e]) + bxc), gap = rbf(rbf(gav[e]) + bac);
     const float sx = rbf(sigm(gxp)), sa = rbf(sigm(gap));
     const float loga = rbf(rbf(-8.0f * sa) * spc);
     const float av = rbf(expf(loga));
@@ -238,16 +228,21 @@ __global__ __launch_bounds__(256) void ssm_kernel(SsmArgs p) {
       Am = av;
       Bm = rbf(g * mult);
     }
-    const long idx = (long)token * p.C + c;
-    if (p.mode == 0) {
-      const float hp = ((freshm >> r) & 1u) ? 0.f : hraw[r];  // a fresh crop row starts from 0
-      const float h = first ? g : __fadd_rn(__fmul_rn(Am, hp), Bm);
-      p.h[(long)rw[r] * p.C + c] = h;
-      p.z[f * p.fs_z + (long)token * p.ld_z + c] = f2bf(rbf(h) * bf2f((uint16_t)yraw[r]));
-    } else {
-      p.A[f * p.fs_ab + idx] = Am;
-      p.B[f * p.fs_ab + idx] = Bm;
-    }
+    const float hp = fresh ? 0.f : hraw[e];  // a fresh crop row starts from 0
+    const float h = first ? g : __fadd_rn(__fmul_rn(Am, hp), Bm);
+    hv[e] = h;
+    zv[e] = rbf(h) * half(yraw);
+    Av[e] = Am;
+    Bv[e] = Bm;
+  }
+  if (p.mode == 0) {
+    *reinterpret_cast<f32x4*>(p.h + (long)rw * p.C + c0 + cl) = hv;
+    *reinterpret_cast<u32x2*>(p.z + f * p.fs_z + (long)token * p.ld_z + c0 + cl) =
+        u32x2{pack2(zv[0], zv[1]), pack2(zv[2], zv[3])};
+  } else {
+    const long idx = (long)token * p.C + c0 + cl;
+    *reinterpret_cast<f32x4*>(p.A + f * p.fs_ab + idx) = Av;
+    *reinterpret_cast<f32x4*>(p.B + f * p.fs_ab + idx) = Bv;
   }
 }
 
@@ -363,6 +358,16 @@ int check_common(const SsmArgs& p, int F) {
   for (int i = 0; i < 4; i++)
     if ((uintptr_t)p.tap[i] & 15) return MX_ELAYOUT;
   if (((uintptr_t)p.conv_w | (uintptr_t)p.conv_b | (uintptr_t)p.wxT | (uintptr_t)p.waT) & 15) return MX_ELAYOUT;
+  if (((uintptr_t)p.sp | (uintptr_t)p.bx | (uintptr_t)p.ba) & 7) return MX_ELAYOUT;  // 4-channel vector reads
+  return MX_OK;
+}
+
+// The step / RG-LRU forms' per-element operands, read and written as 4-channel vectors: fp32 state rows 16-byte
+// aligned, yg / z rows 8-byte aligned with strides of whole 4-element groups.
+int check_step_io(const float* h, const float* h0, const uint16_t* yg, long ld_y, const uint16_t* z, long ld_z) {
+  if (((uintptr_t)h | (uintptr_t)h0) & 15) return MX_ELAYOUT;
+  if (yg && (((uintptr_t)yg & 7) || ld_y % 4)) return MX_ELAYOUT;
+  if (((uintptr_t)z & 7) || ld_z % 4) return MX_ELAYOUT;
   return MX_OK;
 }
 
@@ -380,7 +385,9 @@ extern "C" int mx_ssm_step(hipStream_t st, const uint16_t* x0, const uint16_t* x
   int rc = check_common(p, 1);
   if (rc) return rc;
   if (!yg || !h || !z) return MX_ENULL;
-  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
+  rc = check_step_io(h, h, yg, ld_y, z, ld_z);
+  if (rc) return rc;
+  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, 1), dim3(1024), 0, st, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
@@ -399,7 +406,9 @@ extern "C" int mx_ssm_step_rows(hipStream_t st, const uint16_t* x0, const uint16
   if (rc) return rc;
   if (!yg || !h || !z || !rows || !stamps || !xsave) return MX_ENULL;
   if (srows < T || ld_save % 8 || ((uintptr_t)xsave & 15) || ((uintptr_t)stamps & 7)) return MX_ESHAPE;
-  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
+  rc = check_step_io(h, h, yg, ld_y, z, ld_z);
+  if (rc) return rc;
+  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, 1), dim3(1024), 0, st, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
@@ -412,9 +421,12 @@ extern "C" int mx_rglru_step(hipStream_t st, const uint16_t* x, long ld_x, const
   if (!x || !wxT || !bx || !waT || !ba || !sp || !h || !y) return MX_ENULL;
   if (T < 1 || C % 64 || C > 65535 * 64 || ld_x % 8 || ld_x < C || ld_y < C || T > 65535 * 64) return MX_ESHAPE;
   if (((uintptr_t)x | (uintptr_t)wxT | (uintptr_t)waT) & 15) return MX_ELAYOUT;
+  if (((uintptr_t)sp | (uintptr_t)bx | (uintptr_t)ba) & 7) return MX_ELAYOUT;
+  const int rc = check_step_io(h, h0 ? h0 : h, nullptr, 0, y, ld_y);
+  if (rc) return rc;
   SsmArgs p{{x, x, x, x}, ld_x, 0, nullptr, 0, 0, nullptr, nullptr, wxT, bx, waT, ba, sp, nullptr, h, 0, h0,
             h0 ? 0 : 1, y, ld_y, 0, nullptr, nullptr, 0, T, C, 0, nullptr, nullptr, 0, nullptr, 0};
-  hipLaunchKernelGGL(ssm_kernel<true>, dim3((T + 63) / 64, C / 64, 1), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(ssm_kernel<true>, dim3((T + 63) / 64, C / 64, 1), dim3(1024), 0, st, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
@@ -431,7 +443,8 @@ extern "C" int mx_ssm_prep(hipStream_t st, const uint16_t* x_stack, long ld_x, l
   if (rc) return rc;
   if (!A || !B) return MX_ENULL;
   if (fs_x % 8 || F > 65535) return MX_ESHAPE;
-  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, F), dim3(256), 0, st, p);
+  if (((uintptr_t)A | (uintptr_t)B) & 15) return MX_ELAYOUT;
+  hipLaunchKernelGGL(ssm_kernel<false>, dim3((T + 63) / 64, C / 64, F), dim3(1024), 0, st, p);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
 
