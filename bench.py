@@ -33,11 +33,11 @@ def vision_flops_per_frame(layers=27, T=729, D=1152, F=4304, H=16, hd=72, Kp=588
 
 # LDS ring depth of each GEMM tile config (the kernel template's last argument)
 GEMM_STAGES = {0: 4, 1: 4, 2: 4, 3: 4, 4: 3, 5: 3, 6: 3, 7: 2, 8: 4, 9: 4, 10: 4, 11: 3, 12: 2, 13: 6, 14: 2,
-               15: 2, 16: 3, 17: 3, 18: 2, 19: 4, 20: 4, 21: 4, 22: 4, 23: 4}
+               15: 2, 16: 3, 17: 3, 18: 2, 19: 4, 20: 4, 21: 4, 22: 4, 23: 4, 24: 3, 25: 2}
 # wave grid (WGM, WGN) of the kind-0 configs that do not use 2 x 2
-GEMM_WAVES = {15: (2, 4), 16: (4, 2), 17: (2, 4), 23: (1, 4)}
+GEMM_WAVES = {15: (2, 4), 16: (4, 2), 17: (2, 4), 23: (1, 4), 25: (4, 2)}
 # 2 x 2 tiles over two k groups of waves (8 waves)
-GEMM_KH2 = {19, 20, 21, 22}
+GEMM_KH2 = {19, 20, 21, 22, 24}
 
 
 def gemm_symbol(cfg):

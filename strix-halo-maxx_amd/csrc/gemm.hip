@@ -41,7 +41,8 @@ constexpr int BK = 64;
 // (split-major, then tile). Inside a run, tiles go in groups of GM row panels, column-major within a group: the 32
 // workgroups an XCD runs at once then share GM panels of A and a few panels of W in that XCD's L2, instead of
 // sweeping every row panel of A past one W panel. Grids with at most GM row panels keep plain column-major order.
-constexpr int GM = 8;
+// GM = 8, and 4 for the 192- and 256-row tiles of large grids (1-3 % faster there than 8; 16 and 32 were slower).
+template <int GM = 8>
 __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int splits, int& tm, int& tn, int& split) {
   const int nt = tiles_m * tiles_n, ntot = nt * splits;
   const int per = ntot / 8, rem = ntot % 8, xcd = b % 8, idx = b / 8;
@@ -253,8 +254,10 @@ __device__ __forceinline__ void gemm_body(
   constexpr int SMEM = PSUM && BM * SPF * 2 > SMEM0 ? BM * SPF * 2 : SMEM0;
   __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
 
+  // large tiles: row groups of 4, and the refill of the ring interleaved with the last substep's MFMAs (below)
+  constexpr bool BIG = BM * BN >= 192 * 192;
   int tile_m, tile_n, split;
-  tile_of(blockIdx.x, tiles_m, tiles_n, splits, tile_m, tile_n, split);
+  tile_of<BIG ? 4 : 8>(blockIdx.x, tiles_m, tiles_n, splits, tile_m, tile_n, split);
   const int tile = tile_n * tiles_m + tile_m;  // split-K workspace slot
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   const int nk_all = Kw / BK;
@@ -321,21 +324,22 @@ __device__ __forceinline__ void gemm_body(
       wf[buf][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Ws[r * BK + ((c ^ ((r >> 1) & 7)) << 3)]));
     }
   };
+  auto mfma1 = [&](int buf, int i, int j) {
+    if constexpr (I8) {
+      typedef int i32x4 __attribute__((ext_vector_type(4)));
+      typedef int i32x16 __attribute__((ext_vector_type(16)));
+      acc[i][j] = __builtin_bit_cast(f32x16, __builtin_amdgcn_mfma_i32_32x32x32_i8(
+          __builtin_bit_cast(i32x4, wf[buf][i]), __builtin_bit_cast(i32x4, af[buf][j]),
+          __builtin_bit_cast(i32x16, acc[i][j]), 0, 0, 0));
+    } else {
+      acc[i][j] = mfma32(wf[buf][i], af[buf][j], acc[i][j]);
+    }
+  };
   auto mfmas = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < FN; i++)
 #pragma unroll
-      for (int j = 0; j < FM; j++) {
-        if constexpr (I8) {
-          typedef int i32x4 __attribute__((ext_vector_type(4)));
-          typedef int i32x16 __attribute__((ext_vector_type(16)));
-          acc[i][j] = __builtin_bit_cast(f32x16, __builtin_amdgcn_mfma_i32_32x32x32_i8(
-              __builtin_bit_cast(i32x4, wf[buf][i]), __builtin_bit_cast(i32x4, af[buf][j]),
-              __builtin_bit_cast(i32x16, acc[i][j]), 0, 0, 0));
-        } else {
-          acc[i][j] = mfma32(wf[buf][i], af[buf][j], acc[i][j]);
-        }
-      }
+      for (int j = 0; j < FM; j++) mfma1(buf, i, j);
   };
   // interleave the FM + FN reads of the next substep with the FM * FN MFMAs of this one
   auto interleave = [&]() {
@@ -416,10 +420,43 @@ __device__ __forceinline__ void gemm_body(
     // them (two copies would make the register allocator keep two accumulator sets).
     wait_stages<LPS, S - 2>(nkl - 2 - it);
     __syncthreads();
-    if (it + S < nkl) issue(kt0 + it + S, it % S);
-    read_frags(0, smem + ((it + 1) % S) * STAGE, kh * SPW);
-    mfmas((SPW - 1) & 1);
-    interleave();
+    if constexpr (BIG) {
+      // the next substep's reads first (the DMA's memory clobber would hold them back), then one DMA instruction of
+      // stage it + S after each MFMA of the last substep, so the MFMA pipe is not idle while the refill issues
+      read_frags(0, smem + ((it + 1) % S) * STAGE, kh * SPW);
+      const bool refill = it + S < nkl;
+      const int kk = (kt0 + it + S) * BK + dch * 8;
+      const int ka = kk < K ? kk : 0;
+      const uint32_t st = sbase + (uint32_t)((it % S) * STAGE * 2);
+      auto one = [&](int t) {  // t is a constant after unrolling
+        if (t < QA)
+          dma16(a_src[t < QA ? t : 0] + ka, __builtin_amdgcn_readfirstlane(st + (t * NW + wave) * 1024));
+        else
+          dma16(w_src[t >= QA && t - QA < QW ? t - QA : 0] + kk,
+                __builtin_amdgcn_readfirstlane(st + BM * 128 + ((t - QA) * NW + wave) * 1024));
+      };
+      constexpr int buf = (SPW - 1) & 1;
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++) {
+          mfma1(buf, i, j);
+          const int t = i * FM + j;
+          if (t < LPS) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (refill) one(t);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+#pragma unroll
+      for (int t = FN * FM; t < LPS; t++)
+        if (refill) one(t);
+    } else {
+      if (it + S < nkl) issue(kt0 + it + S, it % S);
+      read_frags(0, smem + ((it + 1) % S) * STAGE, kh * SPW);
+      mfmas((SPW - 1) & 1);
+      interleave();
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
   static_assert(SPW % 2 == 0, "the tail reads into buffer 0");
@@ -1017,7 +1054,10 @@ constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0, 4}, {64, 128, 4, 1, 0, 4}, {128, 64
                          {64, 64, 4, 2, 0, 8, 2},
                          // one wave row x 4 wave columns, 3 x 1 MFMA blocks per wave: 96-row tiles for M = 729
                          // (8 row tiles, the same 768 padded rows as 128 and a third more workgroups)
-                         {96, 128, 4, 1, 0, 4}};
+                         {96, 128, 4, 1, 0, 4},
+                         // large grids whose N is a multiple of 192 (1152, 3456): 192 x 192 over two k groups with a
+                         // 3-stage ring (two stages in flight), and 256 x 192 on 4 x 2 waves
+                         {192, 192, 3, 1, 0, 8, 2}, {256, 192, 2, 1, 0, 8}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -1180,7 +1220,8 @@ extern "C" long mx_gemm_ws_counters(int cfg, int splits, int M, int N) {
 // 256 CUs x per-tile time, with per-tile time ~ BM*BN*(k-steps)/efficiency. Returns cfg * 16 + splits.
 extern "C" int mx_gemm_pick(int M, int N, int Kw) {
   static const float eff[] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f, 1.0f, 1.0f, 1.0f,
-                              1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f, 1.4f, 1.1f, 0.9f, 0.9f, 0.7f, 0.9f};
+                              1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f, 1.4f, 1.1f, 0.9f, 0.9f, 0.7f, 0.9f,
+                              1.2f, 1.2f};
   static_assert(sizeof eff / sizeof eff[0] == kNCfg, "one efficiency per tile config");
   const int nk = Kw / BK;
   int best = 0, bsplit = 1;
@@ -1264,11 +1305,13 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
     case 16: e = launch<256, 128, 4, 2, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 17: e = launch<128, 256, 2, 4, 3>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
     case 18: e = L_(256, 256, 2); break;
+    case 25: e = launch<256, 192, 4, 2, 2>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols, ws, cnt); break;
 #define H_(BM, BN, S) launch_kh2<BM, BN, S>(st, splits, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
     case 19: e = H_(128, 128, 4); break;
     case 20: e = H_(64, 128, 4); break;
     case 21: e = H_(128, 64, 4); break;
     case 22: e = H_(64, 64, 4); break;
+    case 24: e = H_(192, 192, 3); break;
 #define W_(BM, BN, S, OCC) launch_ks<BM, BN, S, OCC>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
     case 8: e = W_(64, 64, 4, 2); break;
     case 9: e = W_(64, 128, 4, 1); break;
