@@ -1057,7 +1057,10 @@ constexpr Cfg kCfgs[] = {{128, 128, 4, 1, 0, 4}, {64, 128, 4, 1, 0, 4}, {128, 64
                          {96, 128, 4, 1, 0, 4},
                          // large grids whose N is a multiple of 192 (1152, 3456): 192 x 192 over two k groups with a
                          // 3-stage ring (two stages in flight), and 256 x 192 on 4 x 2 waves
-                         {192, 192, 3, 1, 0, 8, 2}, {256, 192, 2, 1, 0, 8}};
+                         {192, 192, 3, 1, 0, 8, 2}, {256, 192, 2, 1, 0, 8},
+                         // 730-row prompt-prefix GEMMs: 4 row tiles of 192 x 64 column tiles of 128 = 256 workgroups
+                         // for N = 8192; two k groups of 2 x 2 waves, 4-stage ring
+                         {192, 128, 4, 1, 0, 8, 2}, {128, 192, 4, 1, 0, 8, 2}};
 constexpr int kNCfg = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int BM, int BN, int WGM, int WGN, int S>
@@ -1221,7 +1224,7 @@ extern "C" long mx_gemm_ws_counters(int cfg, int splits, int M, int N) {
 extern "C" int mx_gemm_pick(int M, int N, int Kw) {
   static const float eff[] = {1.0f, 0.78f, 0.78f, 0.6f, 1.1f, 1.1f, 0.6f, 0.9f, 1.0f, 1.0f, 1.0f, 1.0f,
                               1.0f, 1.0f, 1.0f, 1.3f, 1.1f, 1.1f, 1.4f, 1.1f, 0.9f, 0.9f, 0.7f, 0.9f,
-                              1.2f, 1.2f};
+                              1.2f, 1.2f, 1.1f, 1.1f};
   static_assert(sizeof eff / sizeof eff[0] == kNCfg, "one efficiency per tile config");
   const int nk = Kw / BK;
   int best = 0, bsplit = 1;
@@ -1312,6 +1315,8 @@ extern "C" int mx_gemm_bf16(hipStream_t st, int cfg, int splits, const uint16_t*
     case 21: e = H_(128, 64, 4); break;
     case 22: e = H_(64, 64, 4); break;
     case 24: e = H_(192, 192, 3); break;
+    case 26: e = H_(192, 128, 4); break;
+    case 27: e = H_(128, 192, 4); break;
 #define W_(BM, BN, S, OCC) launch_ks<BM, BN, S, OCC>(st, A, lda, W, ldw, bias, R, ldr, r_rows, C, ldc, M, N, K, Kw, act, act_ncols)
     case 8: e = W_(64, 64, 4, 2); break;
     case 9: e = W_(64, 128, 4, 1); break;
@@ -1519,6 +1524,8 @@ extern "C" int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const u
     case 20: e = H_(64, 128, 4); break;
     case 21: e = H_(128, 64, 4); break;
     case 22: e = H_(64, 64, 4); break;
+    case 26: e = H_(192, 128, 4); break;
+    case 27: e = H_(128, 192, 4); break;
 #undef H_
     case 8: e = W_(64, 64, 4, 2); break;
     case 9: e = W_(64, 128, 4, 1); break;

@@ -98,6 +98,7 @@ class TextDecoder:
         self.last_idx = torch.zeros(self.nq, device=dev, dtype=torch.int64)
         self.prefix = None
         self.query_graph = None
+        self.prefill_graph = None  # (graph, hidden-state output, image rows, prompt length) of capture_prefill
         # ---- decode-step device state
         lib = _lib.load()
         if not 1 <= attn_splits <= 8:
@@ -186,7 +187,21 @@ class TextDecoder:
 
     def prefill(self, img_emb, prompt_ids):
         """[BOS] + image tokens (mask-free, md2fast.py:201-206), then the prompt (prefix + causal mask,
-        md2fast.py:208-212). Leaves the first generated token's argmax in `part` and returns the prompt's hidden states."""
+        md2fast.py:208-212). Leaves the first generated token's argmax in `part` and returns the prompt's hidden states.
+        With a graph from capture_prefill() for these shapes, the inputs are copied into its buffers and it is replayed
+        (the returned tensor is then the graph's output buffer, overwritten by the next replay)."""
+        pg = self.prefill_graph
+        if pg is not None and pg[2] == img_emb.shape[0] and pg[3] == prompt_ids.shape[0]:
+            self._check_prefix(img_emb.shape[0])
+            self.pf_img.copy_(img_emb)
+            self.pf_ids.copy_(prompt_ids)
+            pg[0].replay()
+            self.prefix = 1 + img_emb.shape[0]
+            self.pos_base = self.prefix + prompt_ids.shape[0]
+            return pg[1]
+        return self._prefill(img_emb, prompt_ids)
+
+    def _prefill(self, img_emb, prompt_ids):
         P = self.encode(img_emb)
         xp = self.wte[prompt_ids.to(self.dev)]
         xp = self._text_layers(xp, P, P)
@@ -194,12 +209,36 @@ class TextDecoder:
         self.lm_argmax(xp[-1], logits=True)
         return xp
 
+    def capture_prefill(self, n_img, n_prompt):
+        """HIP graph of prefill() for n_img image rows and n_prompt prompt ids (the reference records its encode step
+        the same way, md2fast.py:238-256): two eager warm-ups tune every GEMM shape outside capture, then the graph
+        reads the fixed device buffers pf_img / pf_ids, which prefill() fills before each replay."""
+        self._check_prefix(n_img)
+        self.pf_img = torch.zeros(n_img, self.D, device=self.dev, dtype=BF)
+        self.pf_ids = torch.zeros(n_prompt, device=self.dev, dtype=torch.int64)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self._prefill(self.pf_img, self.pf_ids)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = self._prefill(self.pf_img, self.pf_ids)
+        torch.cuda.synchronize()
+        self.prefill_graph = (g, out, n_img, n_prompt)
+        return g
+
+    def _check_prefix(self, n_img):
+        if 1 + n_img + self.L > self.ctx:
+            raise ValueError(f"prefix {1 + n_img} + L {self.L} exceeds the cache ({self.ctx})")
+
     def encode(self, img_emb):
         """Prefix prefill: [BOS] + image tokens, mask-free, K/V into every cache slot (md2fast.py:201-206).
         Returns the prefix length."""
+        self._check_prefix(img_emb.shape[0])
         x = torch.cat([self.wte[BOS:BOS + 1], img_emb.to(self.dev, BF)], dim=0)
-        if x.shape[0] + self.L > self.ctx:
-            raise ValueError(f"prefix {x.shape[0]} + L {self.L} exceeds the cache ({self.ctx})")
         self._text_layers(x, 0, None, bcast=True)
         self.prefix = x.shape[0]
         return self.prefix

@@ -317,6 +317,32 @@ def test_decoder_two_layers(dev, mk):
     assert dec.mk_error() == 0 and dec.mk_fallbacks == 0
 
 
+@pytest.mark.parametrize("w8a8", [False, True])
+def test_prefill_graph_equals_eager(dev, w8a8):
+    """capture_prefill records prefill() (prefix + 64-id prompt + LM head) as one HIP graph: replayed on new inputs it
+    gives the eager prefill's hidden states, logits, argmax parts and KV cache rows bit for bit (a replay on other
+    inputs in between overwrites every buffer), and generate() from it gives the eager tokens."""
+    w = S.text_weights(2, layers=2)
+    dec = mt.TextDecoder(w, ctx=1024, w8a8=w8a8)
+    img, img2 = S.activations(7, (729, 2048), "img").to(dev), S.activations(8, (729, 2048), "img").to(dev)
+    prompt, prompt2 = S.prompt_ids(9, 64), S.prompt_ids(10, 64)
+    n = 730 + 64
+    print(f"prefill graph vs eager, w8a8={w8a8}", flush=True)
+    xe = dec.prefill(img, prompt).clone()
+    ref = (dec.logits.clone(), dec.part.clone(), [k[0, :, :n].clone() for k in dec.kc], [v[0, :, :n].clone() for v in dec.vc])
+    toks_e = dec.generate(img, prompt, 12, use_graph=False).cpu().tolist()
+    dec.capture_prefill(729, 64)
+    dec.prefill(img2, prompt2)
+    xg = dec.prefill(img, prompt)
+    assert dec.prefix == 730 and dec.pos_base == n
+    assert torch.equal(xg, xe)
+    assert torch.equal(dec.logits, ref[0]) and torch.equal(dec.part, ref[1])
+    for i in range(len(dec.kc)):
+        assert torch.equal(dec.kc[i][0, :, :n], ref[2][i]) and torch.equal(dec.vc[i][0, :, :n], ref[3][i])
+    assert dec.generate(img, prompt, 12, use_graph=False).cpu().tolist() == toks_e
+    assert dec.mk_error() == 0 and dec.mk_fallbacks == 0
+
+
 def test_decode_one_launch_step_equals_layer_kernels(dev):
     """The one-launch step and the per-layer kernels on the same weights and inputs, 2 layers, 6 steps from the same
     prefill: the logits agree within a few bf16 roundings (their fp32 sums run in other orders: fc2 / proj row sums

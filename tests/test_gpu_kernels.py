@@ -49,10 +49,10 @@ def test_gemm_bias_vs_fp32(dev, M, K, N):
     assert (y.float().cpu() - ref).abs().max().item() < 0.02 * ref.abs().max().item() + 1e-2
 
 
-NCFG = 26  # tile configs the library exports
+NCFG = 28  # tile configs the library exports
 # 8-wave tiles, the 4-wave 256 x 256 tile and the 192 x 192 two-k-group tile: no partial-sum mode, no split-K
 NO_PSUM = {15, 16, 17, 18, 24, 25}
-KH2 = {19, 20, 21, 22}      # 2 x 2 tiles over two k groups of waves: partial-sum mode, no in-kernel split-K
+KH2 = {19, 20, 21, 22, 26, 27}  # 2 x 2 tiles over two k groups of waves: partial-sum mode, no in-kernel split-K
 
 
 @pytest.mark.parametrize("cfg", range(NCFG))
