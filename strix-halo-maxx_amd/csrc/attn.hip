@@ -388,10 +388,12 @@ extern "C" int mx_sdpa_check(const void* Q, long sq_t, const void* K, long sk_t,
 //  * many (batch, head, 128-query) tiles (wg4 >= 512): 4 query waves share each staged key block; with head dim 72
 //    two key waves split every 64-key block as well (vision batch 13: 64.4 -> 61.6, batch 256: 1261 -> 1188);
 //  * few tiles: key waves split each block so the grid still fills the GPU. 2 query waves x 4 key waves (8-wave
-//    workgroups) for the vision tower at batch 1 (11.1 -> 10.6 with a warm L2; 12.6 -> 12.4 on cold buffers), TRecViT
-//    (13.0 -> 12.7) and the yes/no query (10.3 -> 9.9); 4 x 4 (16 waves, 128 queries) for 32 heads of many queries
-//    (text prefix 15.2 -> 12.9); 1 x 4 for at most 64 queries (the 64-token prompt, 8.2: larger tiles leave most of
-//    their query waves empty).
+//    workgroups) for the vision tower at batch 1 (11.1 -> 10.6 with a warm L2; 12.6 -> 12.4 on cold buffers) and the
+//    yes/no query (10.3 -> 9.9); 2 x 8 over 256-key blocks (16 waves, each block's keys in 8 slices) for TRecViT's
+//    12 heads x 1280 tokens (2.062 -> 2.047 ms per streamed frame in one A/B; the same tiling made the batch-1 tower
+//    slower, 2.137 -> 2.171 ms); 4 x 4 (16 waves, 128 queries) for 32 heads of many queries (text prefix
+//    15.2 -> 12.9); 1 x 4 for at most 64 queries (the 64-token prompt, 8.2: larger tiles leave most of their query
+//    waves empty).
 // t[0..3] = query waves, key waves, keys per staged block, ring stages.
 extern "C" void mx_sdpa_tiling(int B, int H, int Tq, int D, int* t) {
   const long wg4 = (long)((Tq + 127) / 128) * H * B;
@@ -402,6 +404,8 @@ extern "C" void mx_sdpa_tiling(int B, int H, int Tq, int D, int* t) {
     q = 1;
   } else if (D == 64 && wg4 >= 160) {
     q = 4;
+  } else if (D == 64) {
+    k = 8, kb = 256;
   }
   t[0] = q, t[1] = k, t[2] = kb, t[3] = s;
 }
@@ -429,6 +433,7 @@ extern "C" int mx_sdpa(hipStream_t st, const uint16_t* Q, long sq_b, long sq_h, 
     else if (is(1, 4, 128, 2)) e = launch<64, 1, 4, 128, 2>(st, a);
     else if (is(4, 4, 128, 2)) e = launch<64, 4, 4, 128, 2>(st, a);
     else if (is(2, 4, 128, 2)) e = launch<64, 2, 4, 128, 2>(st, a);
+    else if (is(2, 8, 256, 2)) e = launch<64, 2, 8, 256, 2>(st, a);
   }
   return e == hipSuccess ? MX_OK : MX_ELAUNCH;
 }
