@@ -113,7 +113,7 @@ def test_sdpa_tiling_pick():
     assert ops.sdpa_tiling(13, 16, 729, 72) == (4, 2, 64, 4)      # batch 13 / 256
     assert ops.sdpa_tiling(1, 32, 64, 64) == (1, 4, 128, 2)       # 64-token prompt
     assert ops.sdpa_tiling(1, 32, 730, 64) == (4, 4, 128, 2)      # text prefix
-    assert ops.sdpa_tiling(1, 12, 1280, 64) == (2, 4, 128, 2)     # TRecViT
+    assert ops.sdpa_tiling(1, 12, 1280, 64) == (2, 8, 256, 2)     # TRecViT
     assert ops.sdpa_tiling(16, 12, 1280, 64) == (4, 1, 64, 3)     # TRecViT clip
     assert ops.sdpa_symbol(1, 16, 729, 72) == "attn_fwd_kernel<72, 2, 4, 128, 2>"
 
