@@ -185,9 +185,35 @@ class TextDecoder:
             x = b["fc2"](b["fc1"](h, gelu=True, pre=pre), res=r)
         return x
 
+    def _prefix_prompt_layers(self, x, P):
+        """The prefix and the prompt in one pass: x (n, D) holds the P prefix rows (positions 0 .. P - 1) then the
+        prompt rows (positions P .. n - 1). The Linears, norms and MLPs run once over all n rows (row-independent, so
+        every row's values are those of the two-pass order md2fast.py:201-212 uses); the rotary / KV write and the
+        attention run per part: prefix K/V into every cache slot (bcast) and prefix queries over the prefix keys,
+        mask-free; prompt K/V into slot 0 and prompt queries over keys 0 .. n - 1 with the causal mask from P on."""
+        n = x.shape[0]
+        H, hd = self.H, self.hd
+        for i, b in enumerate(self.blocks):
+            h = ops.layernorm(x, *b["ln"], eps=self.eps)
+            pre = b["qkv"].quant(h) if self.w8a8 else None
+            qkv = b["qkv"](h, pre=pre)
+            a = torch.empty(n, self.D, device=self.dev, dtype=BF)
+            for r0, r1, bc in ((0, P, 1), (P, n, 0)):
+                if r1 == r0:
+                    continue
+                q = torch.empty(1, H, r1 - r0, hd, device=self.dev, dtype=BF)
+                call("mx_rope_kv", stream(), qkv[r0:].data_ptr(), qkv.stride(0), self.cs.data_ptr(), q.data_ptr(),
+                     self.kc[i].data_ptr(), self.vc[i].data_ptr(), 1, r1 - r0, H, self.ctx, r0, self.nq, bc)
+                ops.sdpa(q, self.kc[i][:1, :, :r1], self.vc[i][:1, :, :r1], out=a[r0:r1].view(1, r1 - r0, self.D),
+                         qpos0=r0, causal_from=P if r0 else None)
+            r = b["proj"](a, res=x)
+            x = b["fc2"](b["fc1"](h, gelu=True, pre=pre), res=r)
+        return x
+
     def prefill(self, img_emb, prompt_ids):
         """[BOS] + image tokens (mask-free, md2fast.py:201-206), then the prompt (prefix + causal mask,
-        md2fast.py:208-212). Leaves the first generated token's argmax in `part` and returns the prompt's hidden states.
+        md2fast.py:208-212), as one pass over all rows (_prefix_prompt_layers). Leaves the first generated token's
+        argmax in `part` and returns the prompt's hidden states.
         With a graph from capture_prefill() for these shapes, the inputs are copied into its buffers and it is replayed
         (the returned tensor is then the graph's output buffer, overwritten by the next replay)."""
         pg = self.prefill_graph
@@ -202,10 +228,14 @@ class TextDecoder:
         return self._prefill(img_emb, prompt_ids)
 
     def _prefill(self, img_emb, prompt_ids):
-        P = self.encode(img_emb)
-        xp = self.wte[prompt_ids.to(self.dev)]
-        xp = self._text_layers(xp, P, P)
-        self.pos_base = P + xp.shape[0]
+        self._check_prefix(img_emb.shape[0])
+        P = 1 + img_emb.shape[0]
+        x = torch.cat([self.wte[BOS:BOS + 1], img_emb.to(self.dev, BF), self.wte[prompt_ids.to(self.dev)]], dim=0)
+        if x.shape[0] > self.ctx:
+            raise ValueError(f"prefill of {x.shape[0]} tokens exceeds the cache ({self.ctx})")
+        xp = self._prefix_prompt_layers(x, P)[P:]
+        self.prefix = P
+        self.pos_base = x.shape[0]
         self.lm_argmax(xp[-1], logits=True)
         return xp
 
