@@ -858,7 +858,7 @@ def large_batch_block_ops(vt, imgs):
             "fc2": (2 * M * F * D, 2 * (M * F + D * F + 2 * M * D), lambda: b["fc2"](f, res=x1, out=y))}
 
 
-PROBES = ("tower_b256", "trecvit", "scan", "decode_w8a8")
+PROBES = ("tower_b256", "trecvit", "scan", "decode_w8a8", "prefill")
 
 
 def _probe_classes(workload):
@@ -923,6 +923,19 @@ def _probe_classes(workload):
         algo = lin + 4 * L * (3 * D + D + F_ + D) + 2 * V * D + 2 * 2 * L * (dec.pos_base + 3) * D
         return ("moondream2 W8A8 one-launch decode step (mx_decode_step_mk_i8), 24 layers, from position "
                 f"{dec.pos_base + 2}", [("step", dec.decode_step, algo, None)])
+    if workload == "prefill":
+        import strix_halo_maxx_amd.md2text as mt
+        dec = mt.TextDecoder(S.text_weights(0), device=dev, ctx=1024)
+        img = S.activations(3, (729, 2048), "img").to(dev)
+        prompt = S.prompt_ids(4, 64)
+        for _ in range(2):
+            dec.prefill(img, prompt)
+        c = S.TXT
+        D, F_, L = c["dim"], c["ff"], c["layers"]
+        n, P = 729 + 1 + 64, 730
+        fl = 2 * L * (3 * D * D + D * D + 2 * D * F_) * n + 4 * L * D * (P * P + (n - P) * n)
+        return ("moondream2 text prefill, 24 layers, 730 prefix + 64 prompt rows in one pass, eager launches",
+                [("prefill", lambda: dec.prefill(img, prompt), None, fl)])
     raise ValueError(f"unknown probe {workload}; one of {PROBES}")
 
 

@@ -185,35 +185,14 @@ class TextDecoder:
             x = b["fc2"](b["fc1"](h, gelu=True, pre=pre), res=r)
         return x
 
-    def _prefix_prompt_layers(self, x, P):
-        """The prefix and the prompt in one pass: x (n, D) holds the P prefix rows (positions 0 .. P - 1) then the
-        prompt rows (positions P .. n - 1). The Linears, norms and MLPs run once over all n rows (row-independent, so
-        every row's values are those of the two-pass order md2fast.py:201-212 uses); the rotary / KV write and the
-        attention run per part: prefix K/V into every cache slot (bcast) and prefix queries over the prefix keys,
-        mask-free; prompt K/V into slot 0 and prompt queries over keys 0 .. n - 1 with the causal mask from P on."""
-        n = x.shape[0]
-        H, hd = self.H, self.hd
-        for i, b in enumerate(self.blocks):
-            h = ops.layernorm(x, *b["ln"], eps=self.eps)
-            pre = b["qkv"].quant(h) if self.w8a8 else None
-            qkv = b["qkv"](h, pre=pre)
-            a = torch.empty(n, self.D, device=self.dev, dtype=BF)
-            for r0, r1, bc in ((0, P, 1), (P, n, 0)):
-                if r1 == r0:
-                    continue
-                q = torch.empty(1, H, r1 - r0, hd, device=self.dev, dtype=BF)
-                call("mx_rope_kv", stream(), qkv[r0:].data_ptr(), qkv.stride(0), self.cs.data_ptr(), q.data_ptr(),
-                     self.kc[i].data_ptr(), self.vc[i].data_ptr(), 1, r1 - r0, H, self.ctx, r0, self.nq, bc)
-                ops.sdpa(q, self.kc[i][:1, :, :r1], self.vc[i][:1, :, :r1], out=a[r0:r1].view(1, r1 - r0, self.D),
-                         qpos0=r0, causal_from=P if r0 else None)
-            r = b["proj"](a, res=x)
-            x = b["fc2"](b["fc1"](h, gelu=True, pre=pre), res=r)
-        return x
-
     def prefill(self, img_emb, prompt_ids):
         """[BOS] + image tokens (mask-free, md2fast.py:201-206), then the prompt (prefix + causal mask,
-        md2fast.py:208-212), as one pass over all rows (_prefix_prompt_layers). Leaves the first generated token's
-        argmax in `part` and returns the prompt's hidden states.
+        md2fast.py:208-212), as one pass over all n rows: every layer is row-wise except the attention, and one
+        attention call with causal_from = P gives both parts their masks (key j is visible to query i iff j < P or
+        j <= i: prefix queries see the prefix only, mask-free; prompt queries the prefix and the prompt up to
+        themselves). All rows' K/V go into every cache slot (the prefix's must; the prompt rows in slots other than 0
+        are rewritten by query() before it reads them). Leaves the first generated token's argmax in `part` and returns
+        the prompt's hidden states.
         With a graph from capture_prefill() for these shapes, the inputs are copied into its buffers and it is replayed
         (the returned tensor is then the graph's output buffer, overwritten by the next replay)."""
         pg = self.prefill_graph
@@ -233,7 +212,7 @@ class TextDecoder:
         x = torch.cat([self.wte[BOS:BOS + 1], img_emb.to(self.dev, BF), self.wte[prompt_ids.to(self.dev)]], dim=0)
         if x.shape[0] > self.ctx:
             raise ValueError(f"prefill of {x.shape[0]} tokens exceeds the cache ({self.ctx})")
-        xp = self._prefix_prompt_layers(x, P)[P:]
+        xp = self._text_layers(x, 0, P, bcast=True)[P:]
         self.prefix = P
         self.pos_base = x.shape[0]
         self.lm_argmax(xp[-1], logits=True)
