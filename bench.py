@@ -740,6 +740,8 @@ def trecvit_bench(frames=64, clip=16):
         m.step(fr[t], qf, use_graph=True)
     torch.cuda.synchronize()
     ms_stream = (time.perf_counter() - t0) / frames * 1e3
+    if m.rln_error():  # a timed-out row-block wait of the fused residual-LayerNorm GEMM leaves undefined results
+        raise RuntimeError(f"fused residual-LayerNorm GEMM reported error {m.rln_error()}")
     m.graphs.clear()
     m.reset()
     m.clip_state(clip)

@@ -181,6 +181,10 @@ class TRecViT:
         # clip form) have enough tiles, and there the fp32 partials would only add traffic.
         self.fuse_norm = {"down", "mlp3"}
         self.splitk_max_rows = 8192
+        # residual Linears whose LayerNorm runs inside the GEMM's own launch (MxLin.res_ln: the tiles of a row block
+        # exchange row statistics) where the grid fits one tile per CU: the attention out-projection of one frame
+        # (20 x 12 tiles of 64 x 64) and ln_2 after it
+        self.fuse_rln = {"oproj"}
 
     def reset(self):
         """A new video: zero every block's conv history and RG-LRU state and mark the next frame first
@@ -236,6 +240,9 @@ class TRecViT:
         splitk_max_rows rows) the GEMM writes split-K fp32 partials and one row kernel adds them, the bias and the
         residual and applies the norm; otherwise the GEMM's residual epilogue, then the norm kernel."""
         M = a.shape[0]
+        if (name in self.fuse_rln and norm[0] == "ln" and hasattr(lin, "res_ln")
+                and ops.res_ln_fits(M, lin.N, a.device)):
+            return lin.res_ln(a, res, norm[1], eps=self.ln_eps)
         if name in self.fuse_norm and M <= self.splitk_max_rows and hasattr(lin, "partial"):
             P = lin.partial(a)
             kind, p = norm
@@ -318,8 +325,20 @@ class TRecViT:
         self.step(frame_u8, qfeat, use_graph)
         return self.tracks, self.logits, self.vis
 
+    def rln_ready(self):
+        """Create the fused residual-LayerNorm GEMMs' statistics words (they cannot be allocated during capture)."""
+        for name in self.fuse_rln:
+            if self.blocks and hasattr(self.blocks[0][name], "res_ln"):
+                ops.RlnWorkspace.get(self.dev, self.blocks[0][name].N)
+
+    def rln_error(self):
+        """Non-zero if a fused residual-LayerNorm launch timed out waiting for its row block (results undefined).
+        Synchronises."""
+        return ops.RlnWorkspace.device_error(self.dev)
+
     def capture(self):
         """One HIP graph per ring phase (kernel arguments differ only in which ring slots they read/write)."""
+        self.rln_ready()
         for phase in range(4):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
@@ -446,6 +465,7 @@ class CropTracker:
         phase = m.t % 4
         if use_graph:
             if (phase, n) not in self.graphs:
+                m.rln_ready()
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g):
                     out = self._frame(phase, n)

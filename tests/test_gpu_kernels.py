@@ -231,16 +231,17 @@ def test_residual_rmsnorm_matches_oracle(dev, splits):
     assert rel(acc, full) < 1e-5  # the partials cover the whole K range
 
 
-@pytest.mark.parametrize("M,K", [(729, 1152), (729, 4304), (100, 1152)])
-def test_gemm_res_ln_matches_unfused(dev, M, K):
+@pytest.mark.parametrize("M,K,N", [(729, 1152, 1152), (729, 4304, 1152), (100, 1152, 1152), (1280, 768, 768)])
+def test_gemm_res_ln_matches_unfused(dev, M, K, N):
     """mx_gemm_bf16_res_ln (residual Linear + LayerNorm in one launch, row statistics exchanged between the tiles of
     a row block): x' within one ulp of the pre-rounding sum plus one of x' of the CPU restatement (another summation
     order than the CPU's, as test_residual_layernorm_matches_unfused); y within one bf16 ulp (of the largest operand
     of its last step) of the row LayerNorm kernel applied to the same x' (statistics summed in another order), on at
     most 0.1 % of the elements, and as close to an fp32 LayerNorm as that
     kernel's output (its bf16 rounding, ~1.5e-3 rel-L2, within 5 %). Three calls
-    in a row with new inputs (each launch takes new epochs from the row blocks' generation counters), no timeout."""
-    N = 1152
+    in a row with new inputs (each launch takes new epochs from the row blocks' generation counters), no timeout.
+    Shapes: the batch-1 vision projection (and a 4304-deep K, and a 100-row grid) and TRecViT's attention
+    out-projection with ln_2 over one frame (1280 x 768: 20 x 12 tiles)."""
     g = gen(M + K)
     w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
     b = (torch.randn(N, generator=g) * 0.02).to(BF)
@@ -252,7 +253,7 @@ def test_gemm_res_ln_matches_unfused(dev, M, K):
     for call in range(3):
         x = torch.randn(M, K, generator=g).to(BF).to(dev)
         r = (torch.randn(M, N, generator=g) * 4).to(BF).to(dev)
-        print(f"res_ln M={M} K={K} call {call}", flush=True)
+        print(f"res_ln M={M} K={K} N={N} call {call}", flush=True)
         xo, yo = lin.res_ln(x, r, (gam, bet), eps=1e-6)
         torch.cuda.synchronize()
         assert ws.error() == 0
