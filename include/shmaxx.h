@@ -61,23 +61,34 @@ int mx_gemm_bf16_partial(hipStream_t st, int cfg, int splits, const uint16_t* A,
 int mx_gemm_reduce(hipStream_t st, const float* P, int nsplit, long p_split, long ldp, const float* bias,
                    const uint16_t* R, long ldr, int r_rows, uint16_t* C, long ldc, int M, int N, int act,
                    int act_ncols);
-/* Residual Linear and the LayerNorm that reads it, in one launch: X = bf16(bf16(A W^T + bias) + R) and
- * Y = LayerNorm(X; gamma, beta, eps), the roundings of mx_gemm_bf16_partial + mx_residual_layernorm. Replaces the
+/* Residual Linear and the LayerNorm that reads it, in one launch: X = bf16(bf16(A W^T + bias) + R) and Y =
+ * LayerNorm(X; gamma, beta, eps), the roundings of mx_gemm_bf16_partial + mx_residual_layernorm. Replaces the
  * block's lin_res(proj) + ln2 and lin_res(fc2) + the next block's ln1 (moondream/gpu/md2fast.py:153-157, the post-LN
- * at :158 for the last block). The 64 x 64 output tiles of a row block exchange their rows' sums and centred square
- * sums through stats (>= mx_gemm_res_ln_stats_words(M, N) 64-bit words) and wait for each other, so the whole grid
- * must be resident: N % 64 == 0, N <= 4096 and ((M + 63) / 64) * (N / 64) <= the device's CU count, else
- * MX_ESHAPE. sync (>= mx_gemm_res_ln_sync_words(M) 32-bit words) and stats are zeroed once by the caller and then
- * kept ready by the kernel; calls that share them must be ordered on one stream and have the same N (any M): where
- * a row block's words sit depends on N / 64, so a call of another N could meet old words carrying the epoch it
- * expects and accept stale statistics. Give each N its own stats / sync. sync[0] != 0 after a call: a wait
- * timed out and the results are undefined (zero both before the next call). The statistics combine per-tile sums in
- * fp32 in another order than mx_residual_layernorm's row sums (Y within a bf16 rounding of it; X identical for the
- * same k-loop). */
+ * at :158 for the last block), and TRecViT's `x2 = out_proj(a) + x1; ln_2(x2)` (tapnext/npu/step8.py:484-487). The
+ * 64 x 64 output tiles of a row block exchange their rows' sums and centred square sums through stats (>=
+ * mx_gemm_res_ln_stats_words(M, N) 64-bit words) and wait for each other, so the whole grid must be resident: N % 64
+ * == 0, N <= 4096 and ((M + 63) / 64) * (N / 64) <= the device's CU count, else MX_ESHAPE. sync (>=
+ * mx_gemm_res_ln_sync_words(M) 32-bit words) and stats are zeroed once by the caller and then kept ready by the
+ * kernel; calls that share them must be ordered on one stream and have the same N (any M): where a row block's words
+ * sit depends on N / 64, so a call of another N could meet old words carrying the epoch it expects and accept stale
+ * statistics. Give each N its own stats / sync. sync[0] != 0 after a call: a wait timed out and the results are
+ * undefined (zero both before the next call). The statistics combine per-tile sums in fp32 in another order than
+ * mx_residual_layernorm's row sums (Y within a bf16 rounding of it; X identical for the same k-loop). */
 int mx_gemm_bf16_res_ln(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* bias,
                         const uint16_t* R, long ldr, uint16_t* X, long ldx, const uint16_t* gamma,
                         const uint16_t* beta, uint16_t* Y, long ldy, int M, int N, int K, int Kw, float eps,
                         uint64_t* stats, long stats_words, uint32_t* sync, long sync_words);
+/* The same launch with the TRecViT RMSNorm in place of the LayerNorm: X as above, Y = bf16(bf16(X rstd) sc1) with
+ * rstd = bf16(1 / sqrt(bf16(bf16(sum bf16(X^2) / N) + eps))), sc1 = bf16(scale + 1), the roundings of
+ * mx_residual_rmsnorm. Replaces TRecViT's `x1 = linear_out(z) + x; channel_pre_norm(x1)` (tapnext/npu/step8.py:480-482;
+ * RMSNorm numerics tapnext/npu/pack8.py:222-229) where the grid fits (one frame: 20 x 12 tiles). The tiles exchange
+ * their rows' sums of bf16(X^2) (another fp32 summation order than the row kernel's, before the bf16 rounding of the
+ * mean square). Same shape rules, stats / sync words and error word as mx_gemm_bf16_res_ln; calls of either form
+ * with the same N may share them when ordered on one stream. */
+int mx_gemm_bf16_res_rms(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* bias,
+                         const uint16_t* R, long ldr, uint16_t* X, long ldx, const uint16_t* sc1, uint16_t* Y,
+                         long ldy, int M, int N, int K, int Kw, float eps, uint64_t* stats, long stats_words,
+                         uint32_t* sync, long sync_words);
 long mx_gemm_res_ln_stats_words(int M, int N);
 long mx_gemm_res_ln_sync_words(int M);
 

@@ -70,6 +70,7 @@ SIGNATURES = {
     "mx_gemm_bf16_noalloc": [P, I, I, P, L, P, L, P, P, L, I, P, L, I, I, I, I, I, I],
     "mx_gemm_noalloc_max_ws": [],
     "mx_gemm_bf16_res_ln": [P, P, L, P, L, P, P, L, P, L, P, P, P, L, I, I, I, I, F, P, L, P, L],
+    "mx_gemm_bf16_res_rms": [P, P, L, P, L, P, P, L, P, L, P, P, L, I, I, I, I, F, P, L, P, L],
     "mx_gemm_res_ln_stats_words": [I, I],
     "mx_gemm_res_ln_sync_words": [I],
 }

@@ -226,7 +226,7 @@ constexpr int kRlnMaxTiles = 64;             // column tiles per row (N <= 64 BN
 // KS = 2: 8 waves, the spatial WGM x WGN split twice over, each wave group taking half of every k-step's substeps
 // (same LDS bytes per k-step as KS = 1, twice the waves to pull them: a CU holding one workgroup reads its LDS at the
 // 8-wave rate); the second group's accumulators are added to the first's through LDS after the k loop.
-template <int BM, int BN, int WGM, int WGN, int S, bool I8, int KS = 1, bool RLN = false>
+template <int BM, int BN, int WGM, int WGN, int S, bool I8, int KS = 1, int RLN = 0>
 __device__ __forceinline__ void gemm_body(
     const uint16_t* __restrict__ A, long lda, const uint16_t* __restrict__ W, long ldw,
     const float* __restrict__ bias, const uint16_t* __restrict__ R, long ldr, int r_rows,
@@ -360,6 +360,8 @@ __device__ __forceinline__ void gemm_body(
   f32x4 swv[I8 ? FN : 1][4];
   float sav[I8 ? FM : 1];
   u32x2 rv[HOIST_R ? FN : 1][HOIST_R ? FM : 1][4];
+  // RLN: 0 plain epilogue, 1 residual + LayerNorm (gamma, beta), 2 residual + RMSNorm (gamma = sc1, no beta)
+  constexpr bool RMS = RLN == 2;
   u32x2 gmv[RLN ? FN : 1][4], btv[RLN ? FN : 1][4];
   if constexpr (RLN) {
 #pragma unroll
@@ -368,7 +370,7 @@ __device__ __forceinline__ void gemm_body(
       for (int g = 0; g < 4; g++) {
         const int c = n0 + wn * WTN + i * 32 + 8 * g + 4 * hk;  // < N: N is a multiple of BN in this mode
         gmv[i][g] = *reinterpret_cast<const u32x2*>(rl.gamma + c);
-        btv[i][g] = *reinterpret_cast<const u32x2*>(rl.beta + c);
+        btv[i][g] = RMS ? u32x2{0u, 0u} : *reinterpret_cast<const u32x2*>(rl.beta + c);
       }
   }
   if constexpr (EARLY) {
@@ -490,7 +492,8 @@ __device__ __forceinline__ void gemm_body(
     float* srstd = smean + BM;
     uint16_t* stx = reinterpret_cast<uint16_t*>(srstd + BM);  // staging tile of x', then of Y (BM x SP)
     static_assert((4 * QG * BM + 2 * BM) * 4 + BM * SP * 2 <= SMEM * 2, "the epilogue fits the ring");
-    // this tile's row sums, then centred square sums (two passes over registers, waves wn = 0, 1 combined in order)
+    // this tile's row sums, then centred square sums (two passes over registers, waves wn = 0, 1 combined in order);
+    // RMSNorm: the row sums of bf16(x'^2) only
     float tsum[FM], tm2[FM];
     __syncthreads();  // every wave is past its last ring read
 #pragma unroll
@@ -499,7 +502,7 @@ __device__ __forceinline__ void gemm_body(
 #pragma unroll
       for (int i = 0; i < FN; i++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) a += xv[i][j][e];
+        for (int e = 0; e < 16; e++) a += RMS ? rbf(xv[i][j][e] * xv[i][j][e]) : xv[i][j][e];
       a = halves_sum(a);
       if (hk == 0) red[wn * BM + wm * WTM + j * 32 + lr] = a;
     }
@@ -508,6 +511,7 @@ __device__ __forceinline__ void gemm_body(
     for (int j = 0; j < FM; j++) {
       const int r = wm * WTM + j * 32 + lr;
       tsum[j] = red[r] + red[BM + r];
+      if constexpr (RMS) continue;
       const float mt = tsum[j] * (1.0f / BN);
       float q = 0.f;
 #pragma unroll
@@ -533,7 +537,7 @@ __device__ __forceinline__ void gemm_body(
         }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < FM; j++) tm2[j] = red2[wm * WTM + j * 32 + lr] + red2[BM + wm * WTM + j * 32 + lr];
+    for (int j = 0; j < FM; j++) tm2[j] = RMS ? 0.f : red2[wm * WTM + j * 32 + lr] + red2[BM + wm * WTM + j * 32 + lr];
     // publish (one lane per row: the wn = 0, hk = 0 lanes)
     uint64_t* sbase = rl.stats + ((size_t)rb * tiles_n) * BM * 2;
     if (wn == 0 && hk == 0) {
@@ -588,6 +592,12 @@ __device__ __forceinline__ void gemm_body(
       float tot = 0.f;
 #pragma unroll
       for (int k2 = 0; k2 < QG; k2++) tot += red[k2 * BM + r];
+      if constexpr (RMS) {  // rstd = bf16(1 / sqrt(bf16(bf16(sum / N) + eps))), the rounding of rmsnorm_kernel
+        if (q == 0) {
+          smean[r] = 0.f;
+          srstd[r] = rbf(1.0f / sqrtf(rbf(rbf(tot / (float)N) + rl.eps)));
+        }
+      }
       const float mean = tot / (float)N;
       // M2 = sum over tiles of (M2_t + BN (mean_t - mean)^2): the centred square sum over the whole row
       float m2 = 0.f;
@@ -598,7 +608,7 @@ __device__ __forceinline__ void gemm_body(
       }
       red2[q * BM + r] = m2;
       __syncthreads();
-      if (q == 0) {
+      if (!RMS && q == 0) {
         float t2 = 0.f;
 #pragma unroll
         for (int k2 = 0; k2 < QG; k2++) t2 += red2[k2 * BM + r];
@@ -625,7 +635,8 @@ __device__ __forceinline__ void gemm_body(
           const float bb[4] = {lo_bf(btv[i][g].x), hi_bf(btv[i][g].x), lo_bf(btv[i][g].y), hi_bf(btv[i][g].y)};
           float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; e++) y[e] = (xv[i][j][4 * g + e] - mu) * rs2 * gg[e] + bb[e];
+          for (int e = 0; e < 4; e++)
+            y[e] = RMS ? rbf(xv[i][j][4 * g + e] * rs2) * gg[e] : (xv[i][j][4 * g + e] - mu) * rs2 * gg[e] + bb[e];
           const int c = wn * WTN + i * 32 + 8 * g + 4 * hk;
           *reinterpret_cast<u32x2*>(stx + r * SP + c) = u32x2{pack2(y[0], y[1]), pack2(y[2], y[3])};
         }
@@ -820,14 +831,15 @@ __global__ __launch_bounds__(512) void gemm_bf16_kh2_kernel(
                                        nullptr);
 }
 
-// The residual + LayerNorm form (RlnArgs): one k range per tile (no split-K), 4-wave 2 x 2 tiles
-template <int BM, int BN, int S>
+// The residual + LayerNorm (RLN 1) or RMSNorm (RLN 2) form (RlnArgs): one k range per tile (no split-K), 4-wave
+// 2 x 2 tiles
+template <int BM, int BN, int S, int RLN = 1>
 __global__ __launch_bounds__(256) void gemm_rln_kernel(const uint16_t* __restrict__ A, long lda,
                                                        const uint16_t* __restrict__ W, long ldw,
                                                        const float* __restrict__ bias, const uint16_t* __restrict__ R,
                                                        long ldr, int M, int N, int K, int Kw, int tiles_m, int tiles_n,
                                                        RlnArgs rl) {
-  gemm_body<BM, BN, 2, 2, S, false, 1, true>(A, lda, W, ldw, bias, R, ldr, 0, nullptr, 0, M, N, K, Kw, 0, 0, tiles_m,
+  gemm_body<BM, BN, 2, 2, S, false, 1, RLN>(A, lda, W, ldw, bias, R, ldr, 0, nullptr, 0, M, N, K, Kw, 0, 0, tiles_m,
                                              tiles_n, 1, Kw / BK, nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, rl);
 }
 
@@ -1603,12 +1615,13 @@ extern "C" int mx_gemm_i8(hipStream_t st, int cfg, const int8_t* A, long lda, co
 extern "C" long mx_gemm_res_ln_stats_words(int M, int N) { return (long)((M + 63) / 64) * (N / 64) * 64 * 2; }
 extern "C" long mx_gemm_res_ln_sync_words(int M) { return 1 + (long)((M + 63) / 64); }
 
-extern "C" int mx_gemm_bf16_res_ln(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw,
-                                   const float* bias, const uint16_t* R, long ldr, uint16_t* X, long ldx,
-                                   const uint16_t* gamma, const uint16_t* beta, uint16_t* Y, long ldy, int M, int N,
-                                   int K, int Kw, float eps, uint64_t* stats, long stats_words, uint32_t* sync,
-                                   long sync_words) {
-  if (!R || !X || !gamma || !beta || !Y || !stats || !sync) return MX_ENULL;
+namespace {
+template <int RLN>
+int launch_rln(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw, const float* bias,
+               const uint16_t* R, long ldr, uint16_t* X, long ldx, const uint16_t* gamma, const uint16_t* beta,
+               uint16_t* Y, long ldy, int M, int N, int K, int Kw, float eps, uint64_t* stats, long stats_words,
+               uint32_t* sync, long sync_words) {
+  if (!R || !X || !gamma || (RLN == 1 && !beta) || !Y || !stats || !sync) return MX_ENULL;
   int rc = mx_gemm_check(3, 1, A, lda, W, ldw, bias, R, ldr, X, ldx, M, N, K, Kw, 0, nullptr, 0, nullptr, 0);
   if (rc) return rc;
   if (N % 64 || N / 64 > kRlnMaxTiles) return MX_ESHAPE;
@@ -1621,7 +1634,29 @@ extern "C" int mx_gemm_bf16_res_ln(hipStream_t st, const uint16_t* A, long lda, 
     return MX_ELAUNCH;
   if ((long)tm * tn > cus) return MX_ESHAPE;  // every tile of a row block resident at once
   const RlnArgs rl{gamma, beta, X, ldx, Y, ldy, eps, stats, sync};
-  hipLaunchKernelGGL((gemm_rln_kernel<64, 64, 4>), dim3(tm * tn), dim3(256), 0, st, A, lda, W, ldw, bias, R, ldr, M,
-                     N, K, Kw, tm, tn, rl);
+  hipLaunchKernelGGL((gemm_rln_kernel<64, 64, 4, RLN>), dim3(tm * tn), dim3(256), 0, st, A, lda, W, ldw, bias, R, ldr,
+                     M, N, K, Kw, tm, tn, rl);
   return hipGetLastError() == hipSuccess ? MX_OK : MX_ELAUNCH;
+}
+}  // namespace
+
+extern "C" int mx_gemm_bf16_res_ln(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                                   const float* bias, const uint16_t* R, long ldr, uint16_t* X, long ldx,
+                                   const uint16_t* gamma, const uint16_t* beta, uint16_t* Y, long ldy, int M, int N,
+                                   int K, int Kw, float eps, uint64_t* stats, long stats_words, uint32_t* sync,
+                                   long sync_words) {
+  return launch_rln<1>(st, A, lda, W, ldw, bias, R, ldr, X, ldx, gamma, beta, Y, ldy, M, N, K, Kw, eps, stats,
+                       stats_words, sync, sync_words);
+}
+
+// The same launch with the TRecViT RMSNorm instead of the LayerNorm (the epilogue of mx_residual_rmsnorm): Y =
+// bf16(bf16(x' rstd) sc1), rstd = bf16(1 / sqrt(bf16(bf16(sum bf16(x'^2) / N) + eps))), sc1 = bf16(scale + 1). The
+// tiles exchange their rows' sums of bf16(x'^2); stats / sync are the same words as mx_gemm_bf16_res_ln's (calls of
+// either form with the same N may share them, ordered on one stream).
+extern "C" int mx_gemm_bf16_res_rms(hipStream_t st, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                                    const float* bias, const uint16_t* R, long ldr, uint16_t* X, long ldx,
+                                    const uint16_t* sc1, uint16_t* Y, long ldy, int M, int N, int K, int Kw, float eps,
+                                    uint64_t* stats, long stats_words, uint32_t* sync, long sync_words) {
+  return launch_rln<2>(st, A, lda, W, ldw, bias, R, ldr, X, ldx, sc1, nullptr, Y, ldy, M, N, K, Kw, eps, stats,
+                       stats_words, sync, sync_words);
 }

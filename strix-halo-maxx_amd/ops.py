@@ -227,6 +227,24 @@ class MxLin:
             ws.sync.numel()), "mx_gemm_bf16_res_ln")
         return X, Y
 
+    def res_rms(self, x, res, sc1, eps=1e-6, x_out=None, y_out=None):
+        """x' = bf16(bf16(x W^T + b) + res) and y = the TRecViT RMSNorm of x' (sc1 = bf16(scale + 1)) in one launch
+        (mx_gemm_bf16_res_rms). Only where res_ln_fits(M, N); returns (x', y)."""
+        x2 = _rows(x, self.K)
+        if x2.shape[1] != self.K:
+            raise ValueError(f"input width {x2.shape[1]} != {self.K}")
+        M, N = x2.shape[0], self.N
+        r2 = _rows(res, N)
+        X = x_out if x_out is not None else torch.empty(M, N, device=x2.device, dtype=BF)
+        Y = y_out if y_out is not None else torch.empty(M, N, device=x2.device, dtype=BF)
+        ws = RlnWorkspace.get(x2.device, N)
+        _lib.check(_lib.load().mx_gemm_bf16_res_rms(
+            stream(), x2.data_ptr(), x2.stride(0), self.w.data_ptr(), self.w.stride(0), ptr(self.b), r2.data_ptr(),
+            r2.stride(0), X.data_ptr(), X.stride(0), sc1.data_ptr(), Y.data_ptr(), Y.stride(0), M, N, self.K, self.Kw,
+            float(eps), ws.stats.data_ptr(), ws.stats.numel(), ws.sync.data_ptr(), ws.sync.numel()),
+            "mx_gemm_bf16_res_rms")
+        return X, Y
+
 
 _TUNED_P = {}  # (M, N, Kw) -> (cfg, splits) of the split-K partial GEMM
 
@@ -522,12 +540,12 @@ def layernorm(x, w, b, eps=1e-5, out=None):
 
 
 class RlnWorkspace:
-    """Row statistics and their generation counters for mx_gemm_bf16_res_ln, one per (device, N), allocated zeroed
-    once at their largest size (the launch allows at most one 64 x 64 tile per CU, so at most 256 tiles: 256 x 128
-    stats words; 1 + 2 x 256 sync words) and then owned by the kernel, which leaves them ready for the next call.
-    Keyed by N because where a row block's statistics sit depends on the tiles per row block (N / 64): calls of
-    another N on the same words could meet old words that carry the epoch they expect. Calls of one N may have any
-    M. Calls on one stream serialise; two streams must not share them."""
+    """Row statistics and their generation counters for mx_gemm_bf16_res_ln / _res_rms, one per (device, N), allocated
+    zeroed once at their largest size (the launch allows at most one 64 x 64 tile per CU, so at most 256 tiles: 256
+    x 128 stats words; 1 + 2 x 256 sync words) and then owned by the kernel, which leaves them ready for the next
+    call. Keyed by N because where a row block's statistics sit depends on the tiles per row block (N / 64): calls
+    of another N on the same words could meet old words that carry the epoch they expect. Calls of one N may have
+    any M. Calls on one stream serialise; two streams must not share them."""
     _by_key = {}
 
     def __init__(self, device):

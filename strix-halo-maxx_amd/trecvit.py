@@ -181,10 +181,10 @@ class TRecViT:
         # clip form) have enough tiles, and there the fp32 partials would only add traffic.
         self.fuse_norm = {"down", "mlp3"}
         self.splitk_max_rows = 8192
-        # residual Linears whose LayerNorm runs inside the GEMM's own launch (MxLin.res_ln: the tiles of a row block
-        # exchange row statistics) where the grid fits one tile per CU: the attention out-projection of one frame
-        # (20 x 12 tiles of 64 x 64) and ln_2 after it
-        self.fuse_rln = {"oproj"}
+        # residual Linears whose norm runs inside the GEMM's own launch (MxLin.res_ln / res_rms: the tiles of a row
+        # block exchange row statistics) where the grid fits one tile per CU (one frame: 20 x 12 tiles of 64 x 64):
+        # linear_out with channel_pre_norm (RMSNorm), the attention out-projection with ln_2 (LayerNorm)
+        self.fuse_rln = {"out", "oproj"}
 
     def reset(self):
         """A new video: zero every block's conv history and RG-LRU state and mark the next frame first
@@ -240,9 +240,11 @@ class TRecViT:
         splitk_max_rows rows) the GEMM writes split-K fp32 partials and one row kernel adds them, the bias and the
         residual and applies the norm; otherwise the GEMM's residual epilogue, then the norm kernel."""
         M = a.shape[0]
-        if (name in self.fuse_rln and norm[0] == "ln" and hasattr(lin, "res_ln")
-                and ops.res_ln_fits(M, lin.N, a.device)):
-            return lin.res_ln(a, res, norm[1], eps=self.ln_eps)
+        if name in self.fuse_rln and hasattr(lin, "res_ln") and ops.res_ln_fits(M, lin.N, a.device):
+            kind, p = norm
+            if kind == "rms":
+                return lin.res_rms(a, res, p, eps=self.rms_eps)
+            return lin.res_ln(a, res, p, eps=self.ln_eps)
         if name in self.fuse_norm and M <= self.splitk_max_rows and hasattr(lin, "partial"):
             P = lin.partial(a)
             kind, p = norm

@@ -305,6 +305,47 @@ def test_gemm_res_ln_interleaved_widths(dev):
         assert (yo.float().cpu() != y_row).float().mean().item() <= 1e-3, call
 
 
+@pytest.mark.parametrize("M", [1280, 100])
+def test_gemm_res_rms_matches_unfused(dev, M):
+    """mx_gemm_bf16_res_rms (residual Linear + the TRecViT RMSNorm in one launch) on TRecViT's linear_out shape
+    (M x 768, K = 768; a frame is 1280 rows, 20 x 12 tiles): x' within one ulp of the pre-rounding sum plus one of
+    the CPU restatement's x' (as the LayerNorm form); y against the oracle's RMSNorm chain (pack8.py:222-229) applied
+    to that x': at most one bf16 ulp anywhere, on at most 1 % of the elements (the tiles' fp32 sums of the rounded
+    squares run in another order than the oracle's). Each call alternates with the LayerNorm form on the same
+    statistics words (same N), which must give the same x' bit for bit (one kernel k loop); three of each, no
+    timeout."""
+    import oracle.trecvit as otr
+    N = K = 768
+    g = gen(501 + M)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(BF)
+    b = (torch.randn(N, generator=g) * 0.02).to(BF)
+    lin = ops.MxLin(w, b)
+    scale = (torch.randn(N, generator=g) * 0.3).to(BF)
+    sc1 = (scale.float() + 1).to(BF).to(dev)
+    gam = (1 + 0.1 * torch.randn(N, generator=g)).to(BF).to(dev)
+    bet = (0.1 * torch.randn(N, generator=g)).to(BF).to(dev)
+    assert ops.res_ln_fits(M, N, dev)
+    for call in range(3):
+        x = torch.randn(M, K, generator=g).to(BF).to(dev)
+        r = (torch.randn(M, N, generator=g) * 2).to(BF).to(dev)
+        print(f"res_rms M={M} call {call}", flush=True)
+        xo, yo = lin.res_rms(x, r, sc1, eps=1e-6)
+        xl, _ = lin.res_ln(x, r, (gam, bet), eps=1e-6)
+        torch.cuda.synchronize()
+        assert ops.RlnWorkspace.device_error(dev) == 0
+        assert torch.equal(xl, xo)
+        gsum = x.cpu().float() @ w.float().t() + lin.b.cpu().float()
+        exp = (gsum.to(BF).float() + r.cpu().float()).to(BF)
+        a, f = xo.float().cpu(), exp.float()
+        tol = 2.0 ** -7 * (gsum.abs() + torch.maximum(a.abs(), f.abs())) + 1e-30
+        assert int(((a - f).abs() > tol).sum()) == 0, call
+        ref = otr.rmsnorm(xo.cpu(), scale)
+        d = (yo.cpu().view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+        assert d.max().item() <= 1 and (d > 0).float().mean().item() <= 1e-2, (d.max().item(), (d > 0).float().mean())
+        y_row = ops.rmsnorm(xo, sc1, eps=1e-6)
+        assert (yo != y_row).float().mean().item() <= 1e-2
+
+
 def test_gemm_res_ln_refuses_a_grid_larger_than_the_gpu(dev):
     """Two crops (1458 rows: 23 x 18 tiles > 256 CUs) cannot all be resident: refused before launching."""
     lin = ops.MxLin(torch.zeros(1152, 1152, dtype=BF), torch.zeros(1152))
