@@ -99,6 +99,7 @@ class TextDecoder:
         self.prefix = None
         self.query_graph = None
         self.prefill_graph = None  # (graph, hidden-state output, image rows, prompt length) of capture_prefill
+        self.fuse_ln = True  # fc2's reduction with the next layer's LayerNorm in one kernel where it pays
         # ---- decode-step device state
         lib = _lib.load()
         if not 1 <= attn_splits <= 8:
@@ -172,8 +173,10 @@ class TextDecoder:
         n = x.shape[0] // B
         H, hd = self.H, self.hd
         Tk = pos0 + n
+        h = None
         for i, b in enumerate(self.blocks):
-            h = ops.layernorm(x, *b["ln"], eps=self.eps)
+            if h is None:
+                h = ops.layernorm(x, *b["ln"], eps=self.eps)
             # W8A8: the LN output is quantised once for qkv and fc1 (SHARE_QUANT, md2fast.py:52, 174)
             pre = b["qkv"].quant(h) if self.w8a8 else None
             qkv = b["qkv"](h, pre=pre)
@@ -182,8 +185,20 @@ class TextDecoder:
                  self.kc[i].data_ptr(), self.vc[i].data_ptr(), B, n, H, self.ctx, pos0, self.nq, int(bcast))
             a = ops.sdpa(q, self.kc[i][:B, :, :Tk], self.vc[i][:B, :, :Tk], qpos0=pos0, causal_from=causal_from)
             r = b["proj"](a.view(B * n, self.D), res=x)
-            x = b["fc2"](b["fc1"](h, gelu=True, pre=pre), res=r)
+            f = b["fc1"](h, gelu=True, pre=pre)
+            if i + 1 < len(self.blocks) and self._fuse_next_ln(b["fc2"], B * n):
+                # fc2 as split-K partials, reduced with its bias and the residual by the kernel that also applies the
+                # next layer's LayerNorm (one launch for the reduction and the norm)
+                x, h = ops.residual_layernorm(b["fc2"].partial(f), b["fc2"].b, r, self.blocks[i + 1]["ln"],
+                                              eps=self.eps)
+            else:
+                x, h = b["fc2"](f, res=r), None
         return x
+
+    def _fuse_next_ln(self, lin, M):
+        """fc2 + residual + the next layer's LayerNorm as partials + one row kernel: bf16 Linears over many rows (the
+        prefix / prefill passes), where the tile table holds the partial GEMM's pick."""
+        return self.fuse_ln and M >= 256 and hasattr(lin, "partial") and ops.has_partial_pick(M, lin)
 
     def prefill(self, img_emb, prompt_ids):
         """[BOS] + image tokens (mask-free, md2fast.py:201-206), then the prompt (prefix + causal mask,

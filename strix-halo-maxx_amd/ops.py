@@ -255,6 +255,13 @@ def _partial(lin, cfg, sp, x2, P, M):
                                             lin.Kw)
 
 
+def has_partial_pick(M, lin):
+    """Whether the split-K partial GEMM of (M, lin.N, lin.Kw) has a pick already (tuned in this process or in the
+    fixed table), so that a caller under graph capture does not fall back to the untuned default."""
+    key = (M, lin.N, lin.Kw)
+    return key in _TUNED_P or (MxLin.use_table and key in _FIXED_P)
+
+
 def _partial_cfg(lin, M, x2):
     """(cfg, splits) for the split-K partial GEMM: every config with a partial-sum mode x splits in 1..4 timed once on
     the real operands (outside graph capture), else 64x64 tiles with 2 splits."""
