@@ -192,6 +192,7 @@ int mx_resize_patchify_u8(hipStream_t st, const uint8_t* img, int Hs, int Ws, ui
 /* ============================================================================================ text decoder
  * Partial rotary (dims 0..31) of q and k from fused qkv rows at positions pos0.., q -> q_out [B][H][n][64], rotated k
  * and raw v -> caches [slot][H][ctx][64]; cs = (ctx_table, 16, 2) fp32 (cos, sin). bcast: B = 1 rows to every slot.
+ * qkv (ldq % 8 == 0), cs, q_out and the caches 16-byte aligned, else MX_ELAYOUT.
  * Replaces rope_cache / _rope_cache (moondream/gpu/fused.py:5-41; reference rotation fused.py:53-58). */
 int mx_rope_kv(hipStream_t st, const uint16_t* qkv, long ldq, const float* cs, uint16_t* q_out, uint16_t* kc,
                uint16_t* vc, int B, int n, int H, int ctx, int pos0, int nslots, int bcast);

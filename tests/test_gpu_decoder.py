@@ -41,23 +41,37 @@ def gen(s):
     return torch.Generator().manual_seed(s)
 
 
-def test_rope_kv_matches_oracle(dev):
+@pytest.mark.parametrize("B,nslots,bcast", [(1, 1, 0), (2, 3, 0), (1, 3, 1)])
+def test_rope_kv_matches_oracle(dev, B, nslots, bcast):
+    """mx_rope_kv bit for bit against the oracle's rotation (fused.py:53-58 restated): B sequences of n rows into
+    their own cache slots, or (bcast) one sequence into every slot; nothing outside rows pos0 .. pos0 + n - 1 of the
+    written slots changes."""
     H, n, ctx, pos0 = 32, 37, 1024, 730
-    qkv = torch.randn(n, 3 * H * 64, generator=gen(1)).to(BF)
+    qkv = torch.randn(B * n, 3 * H * 64, generator=gen(1 + B + bcast)).to(BF)
     fr = S.freqs_cis(32, 2048)
-    q_ref = ot.rope(qkv[:, :H * 64].view(1, n, H, 64).transpose(1, 2), fr[pos0:pos0 + n, :, 0], fr[pos0:pos0 + n, :, 1])
-    k_ref = ot.rope(qkv[:, H * 64:2 * H * 64].view(1, n, H, 64).transpose(1, 2), fr[pos0:pos0 + n, :, 0], fr[pos0:pos0 + n, :, 1])
-    v_ref = qkv[:, 2 * H * 64:].view(1, n, H, 64).transpose(1, 2)
+    c, s = fr[pos0:pos0 + n, :, 0], fr[pos0:pos0 + n, :, 1]
+    q_ref = ot.rope(qkv[:, :H * 64].view(B, n, H, 64).transpose(1, 2), c, s)
+    k_ref = ot.rope(qkv[:, H * 64:2 * H * 64].view(B, n, H, 64).transpose(1, 2), c, s)
+    v_ref = qkv[:, 2 * H * 64:].view(B, n, H, 64).transpose(1, 2)
     qd, frd = qkv.to(dev), fr.to(dev)
-    q = torch.empty(1, H, n, 64, device=dev, dtype=BF)
-    kc = torch.zeros(1, H, ctx, 64, device=dev, dtype=BF)
-    vc = torch.zeros(1, H, ctx, 64, device=dev, dtype=BF)
+    q = torch.empty(B, H, n, 64, device=dev, dtype=BF)
+    kc = torch.zeros(nslots, H, ctx, 64, device=dev, dtype=BF)
+    vc = torch.zeros(nslots, H, ctx, 64, device=dev, dtype=BF)
     _lib.call("mx_rope_kv", _lib.stream(), qd.data_ptr(), qd.stride(0), frd.data_ptr(), q.data_ptr(),
-              kc.data_ptr(), vc.data_ptr(), 1, n, H, ctx, pos0, 1, 0)
+              kc.data_ptr(), vc.data_ptr(), B, n, H, ctx, pos0, nslots, bcast)
     assert torch.equal(q.cpu(), q_ref)
-    assert torch.equal(kc[:, :, pos0:pos0 + n].cpu(), k_ref)
-    assert torch.equal(vc[:, :, pos0:pos0 + n].cpu(), v_ref)
-    assert torch.count_nonzero(kc[:, :, :pos0]) == 0
+    slots = range(nslots) if bcast else range(B)
+    for sl in slots:
+        src = 0 if bcast else sl
+        assert torch.equal(kc[sl, :, pos0:pos0 + n].cpu(), k_ref[src]), sl
+        assert torch.equal(vc[sl, :, pos0:pos0 + n].cpu(), v_ref[src]), sl
+    written = torch.zeros(nslots, dtype=torch.bool)
+    written[list(slots)] = True
+    for sl in range(nslots):
+        rest = torch.cat([kc[sl, :, :pos0], kc[sl, :, pos0 + n:], vc[sl, :, :pos0], vc[sl, :, pos0 + n:]], dim=1)
+        assert torch.count_nonzero(rest) == 0, sl
+        if not written[sl]:
+            assert torch.count_nonzero(kc[sl]) == 0 and torch.count_nonzero(vc[sl]) == 0, sl
 
 
 def test_ln_gemv2_and_dual_res(dev):
