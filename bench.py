@@ -108,7 +108,7 @@ def op_classes(vt, img):
         "attn": (attn_sym, 4 * B * H * T * T * hd, 8 * M * D, lambda i, b: ops.sdpa(*saved[i][2], out=a_out)),
     }
     if fused_proj:  # a, W, the residual in; x' and ln2(x') out
-        classes["proj"] = ("gemm_rln_kernel<64, 64, 4>", 2 * M * D * D, 2 * (M * D + D * D + 3 * M * D),
+        classes["proj"] = ("gemm_rln_kernel<64, 64, 4, 1>", 2 * M * D * D, 2 * (M * D + D * D + 3 * M * D),
                            lambda i, b: b["proj"].res_ln(saved[i][3], saved[i][0], b["ln2"], eps=vt.eps,
                                                          x_out=outs["x"], y_out=outs["h"]))
     else:
