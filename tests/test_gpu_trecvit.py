@@ -375,6 +375,7 @@ def test_twelve_blocks_streamed_graph_and_clip(dev):
         print(f"frame {t}: 12-block rel {errs[-1]:.2e}", flush=True)
         assert errs[-1] <= 2e-2, (t, errs[-1])
     h_stream = [h.clone() for h in m.h]
+    assert m.rln_error() == 0  # no row-block wait of the fused residual-norm GEMMs timed out
     m.reset()
     m.clip_state(NF)
     clip = m.forward_clip(frames.to(dev), qf.to(dev))
