@@ -236,7 +236,8 @@ class TRecViT:
         return ops.layernorm(x, *p, eps=self.ln_eps)
 
     def _linres_norm(self, name, lin, a, res, norm):
-        """x = lin(a) + res with torch's roundings and norm(x). For the Linears in fuse_norm (and at most
+        """x = lin(a) + res with torch's roundings and norm(x). The Linears in fuse_rln, where the grid fits one tile
+        per CU, run as one launch with the norm (res_ln / res_rms). For those in fuse_norm (and at most
         splitk_max_rows rows) the GEMM writes split-K fp32 partials and one row kernel adds them, the bias and the
         residual and applies the norm; otherwise the GEMM's residual epilogue, then the norm kernel."""
         M = a.shape[0]
