@@ -175,6 +175,22 @@ def test_other_entry_points_refuse_bad_shapes():
                                  3) == -2         # no gated GELU in W8A8
     assert lib.mx_gemm_i8_reduce(None, A16, 2, 64 * 2048, 2048, None, A16, None, None, 0, 0, A16, 2048, 64, 2048,
                                  0) == -6
+    # residual Linear + LayerNorm / RMSNorm in one launch (refused before the device query)
+    rl = lambda **kw: lib.mx_gemm_bf16_res_ln(*{**dict(
+        st=None, A=A16, lda=768, W=A16, ldw=768, bias=A16, R=A16, ldr=768, X=A16, ldx=768, g=A16, b=A16, Y=A16,
+        ldy=768, M=1280, N=768, K=768, Kw=768, eps=1e-6, stats=A16, sw=1 << 20, sync=A16, syw=1 << 10), **kw}.values())
+    assert rl(b=None) == -6 and rl(R=None) == -6 and rl(stats=None) == -6
+    assert rl(N=736, ldr=736, ldx=736, ldy=736) == -2                               # N % 64
+    assert rl(Y=A16 + 4) == -4 and rl(ldy=766) == -4                                # Y layout
+    assert rl(sw=10) == -2 and rl(syw=2) == -2                                      # statistics / sync words
+    rr = lambda **kw: lib.mx_gemm_bf16_res_rms(*{**dict(
+        st=None, A=A16, lda=768, W=A16, ldw=768, bias=A16, R=A16, ldr=768, X=A16, ldx=768, sc1=A16, Y=A16, ldy=768,
+        M=1280, N=768, K=768, Kw=768, eps=1e-6, stats=A16, sw=1 << 20, sync=A16, syw=1 << 10), **kw}.values())
+    assert rr(sc1=None) == -6 and rr(X=None) == -6 and rr(sync=None) == -6
+    assert rr(N=736, ldr=736, ldx=736, ldy=736) == -2
+    assert rr(sc1=A16 + 2) == -4 and rr(stats=A16 + 8) == -4
+    assert rr(sw=10) == -2
+    assert lib.mx_gemm_res_ln_stats_words(1280, 768) == 20 * 12 * 64 * 2 and lib.mx_gemm_res_ln_sync_words(1280) == 21
     # tracking heads
     assert lib.mx_track_head_blob_elems(768, 256, 512) == 768 * 256 + 6 * 256 + 256 * 256 + 256 * 512 + 512
     hd = lambda **kw: lib.mx_track_heads(*(lambda a: (a.update(kw), list(a.values()))[1])(dict(
