@@ -196,9 +196,10 @@ class TextDecoder:
         return x
 
     def _fuse_next_ln(self, lin, M):
-        """fc2 + residual + the next layer's LayerNorm as partials + one row kernel: bf16 Linears over many rows (the
-        prefix / prefill passes), where the tile table holds the partial GEMM's pick."""
-        return self.fuse_ln and M >= 256 and hasattr(lin, "partial") and ops.has_partial_pick(M, lin)
+        """fc2 + residual + the next layer's LayerNorm as partials + one row kernel: bf16 Linears whose row count has a
+        partial GEMM pick in the tile table (the prefix and prefill passes; the yes/no query's 32-row fc2 keeps its 8
+        raw splits, faster than 4 partial splits with the norm fused: the row kernel reads at most 4)."""
+        return self.fuse_ln and hasattr(lin, "partial") and ops.has_partial_pick(M, lin)
 
     def prefill(self, img_emb, prompt_ids):
         """[BOS] + image tokens (mask-free, md2fast.py:201-206), then the prompt (prefix + causal mask,
