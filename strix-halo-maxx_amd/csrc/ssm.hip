@@ -311,8 +311,13 @@ __global__ __launch_bounds__(256) void rglru_scan_kernel(const float* __restrict
 }
 
 // ---- chain scan: thread = (token, 4 consecutive channels), frames in order
-constexpr int CHF = 2;  // frames whose loads are issued before their arithmetic (2-4 measured best: occupancy)
+constexpr int CHF = 2;   // frames whose loads are issued before their arithmetic (2-4 measured best: occupancy)
+constexpr int ZB = 16;   // frames whose z stay in registers until one burst of stores after them
 
+// The loads of A and B and the stores of z are non-temporal (each byte is touched once), and the z of ZB frames are
+// stored together after their recurrence steps instead of one frame at a time between the next frames' loads: the
+// HBM then serves long runs of reads and of writes (16 frames, 1280 x 768: 38.3 -> 36.6 us per launch; with plain
+// stores the late burst is slower, 41.7 us).
 __global__ __launch_bounds__(256) void rglru_chain_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                           long fs_ab, float* __restrict__ h, int F, int T, int C,
                                                           const uint16_t* __restrict__ yg, long ld_y, long fs_y,
@@ -323,29 +328,33 @@ __global__ __launch_bounds__(256) void rglru_chain_kernel(const float* __restric
   const int t = (int)(i / c4n), c = (int)(i % c4n) * 4;
   const long o = (long)t * C + c;
   f32x4 hv = *reinterpret_cast<const f32x4*>(h + o);
-  for (int f0 = 0; f0 < F; f0 += CHF) {
-    const int nf = min(CHF, F - f0);
-    f32x4 av[CHF], bv[CHF];
-    u32x2 yv[CHF];
+  for (int f1 = 0; f1 < F; f1 += ZB) {
+    u32x2 zs[ZB];
 #pragma unroll
-    for (int k = 0; k < CHF; k++) {
-      if (k < nf) {
-        const long f = f0 + k;
-        av[k] = *reinterpret_cast<const f32x4*>(A + f * fs_ab + o);
-        bv[k] = *reinterpret_cast<const f32x4*>(B + f * fs_ab + o);
+    for (int f0 = 0; f0 < ZB; f0 += CHF) {
+      f32x4 av[CHF], bv[CHF];
+      u32x2 yv[CHF];
+#pragma unroll
+      for (int k = 0; k < CHF; k++) {  // frames past F reload the last one (never applied, never stored)
+        const long f = min(f1 + f0 + k, F - 1);
+        av[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(A + f * fs_ab + o));
+        bv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(B + f * fs_ab + o));
         yv[k] = *reinterpret_cast<const u32x2*>(yg + f * fs_y + (long)t * ld_y + c);
       }
-    }
 #pragma unroll
-    for (int k = 0; k < CHF; k++) {
-      if (k < nf) {
+      for (int k = 0; k < CHF; k++) {
+        if (f1 + f0 + k < F) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) hv[e] = __fadd_rn(__fmul_rn(av[k][e], hv[e]), bv[k][e]);
-        const u32x2 zo = {pack2(rbf(hv[0]) * lo_bf(yv[k].x), rbf(hv[1]) * hi_bf(yv[k].x)),
-                          pack2(rbf(hv[2]) * lo_bf(yv[k].y), rbf(hv[3]) * hi_bf(yv[k].y))};
-        *reinterpret_cast<u32x2*>(z + (long)(f0 + k) * fs_z + (long)t * ld_z + c) = zo;
+          for (int e = 0; e < 4; e++) hv[e] = __fadd_rn(__fmul_rn(av[k][e], hv[e]), bv[k][e]);
+        }
+        zs[f0 + k] = u32x2{pack2(rbf(hv[0]) * lo_bf(yv[k].x), rbf(hv[1]) * hi_bf(yv[k].x)),
+                           pack2(rbf(hv[2]) * lo_bf(yv[k].y), rbf(hv[3]) * hi_bf(yv[k].y))};
       }
     }
+#pragma unroll
+    for (int f = 0; f < ZB; f++)
+      if (f1 + f < F)
+        __builtin_nontemporal_store(zs[f], reinterpret_cast<u32x2*>(z + (long)(f1 + f) * fs_z + (long)t * ld_z + c));
   }
   *reinterpret_cast<f32x4*>(h + o) = hv;
 }
