@@ -1178,7 +1178,8 @@ def main():
         with torch.inference_mode():
             for B in (13, 256):
                 imgs = S.images_u8(2, B).to(dev)
-                sb = tower_time(vt, imgs, max(3, a.steps // 10), 2)
+                # ~0.3 s of timed replays each: 25 batches of 13, 5 of 256 at the default 50 steps
+                sb = tower_time(vt, imgs, max(5, a.steps // 2) if B == 13 else max(3, a.steps // 10), 2)
                 out.setdefault("extra", {})[f"tower_b{B}"] = {"ms_per_batch": round(sb * 1e3, 3),
                                                               "images_per_s": round(B / sb, 1),
                                                               "mfma_frac": round(B * tower_flops / sb / PEAK_BF16, 4)}
