@@ -646,25 +646,31 @@ __device__ __forceinline__ void gemm_body(
     return;
   }
 
-  // ---- KS = 2: the second k group's partial tiles join the first's, in a fixed order
+  // ---- KS = 2: the second k group's partial tiles join the first's, in a fixed order. The first group finishes
+  // every accumulator block, except in the partial-sum mode, where each group finishes every other block (sums
+  // and fp32 staging split over all 8 waves; the same bits, fp32 addition being commutative). Measured in context:
+  // TRecViT's 2-split partials 1.923-1.925 -> 1.909-1.912 ms per streamed frame, the tower unchanged; the same split
+  // of the bias / GELU epilogue made the batch-1 tower 0.8 % slower.
+  const bool split_epi = KS == 2 && (FN * FM) % 2 == 0 && PSUM && P != nullptr;
+  auto mine = [&](int i, int j) { return split_epi ? ((i * FM + j) & 1) == kh : owner; };
   if constexpr (KS == 2) {
     float* red = reinterpret_cast<float*>(smem);
     static_assert(NWS * FN * FM * 16 * 64 * 4 <= S * STAGE * 2, "the exchange fits the ring");
     __syncthreads();  // every wave is past its last ring read
-    if (!owner) {
 #pragma unroll
-      for (int i = 0; i < FN; i++)
+    for (int i = 0; i < FN; i++)
 #pragma unroll
-        for (int j = 0; j < FM; j++)
+      for (int j = 0; j < FM; j++)
+        if (!mine(i, j)) {
 #pragma unroll
           for (int e = 0; e < 16; e++) red[(((wsp * FN + i) * FM + j) * 16 + e) * 64 + lane] = acc[i][j][e];
-    }
+        }
     __syncthreads();
-    if (owner) {
 #pragma unroll
-      for (int i = 0; i < FN; i++)
+    for (int i = 0; i < FN; i++)
 #pragma unroll
-        for (int j = 0; j < FM; j++)
+      for (int j = 0; j < FM; j++)
+        if (mine(i, j)) {
 #pragma unroll
           for (int e = 0; e < 16; e++) {
             const float o = red[(((wsp * FN + i) * FM + j) * 16 + e) * 64 + lane];
@@ -673,7 +679,7 @@ __device__ __forceinline__ void gemm_body(
             else
               acc[i][j][e] += o;
           }
-    }
+        }
   }
 
   // ---- partial-sum mode (mx_gemm_bf16_partial): this split's raw fp32 sums to its slab of P, staged like the bf16
@@ -682,16 +688,16 @@ __device__ __forceinline__ void gemm_body(
     if (P) {
       float* stf = reinterpret_cast<float*>(smem);
       __syncthreads();
-      if (owner) {
 #pragma unroll
-        for (int i = 0; i < FN; i++)
+      for (int i = 0; i < FN; i++)
 #pragma unroll
-          for (int j = 0; j < FM; j++)
+        for (int j = 0; j < FM; j++)
+          if (mine(i, j)) {
 #pragma unroll
             for (int g = 0; g < 4; g++)
               *reinterpret_cast<f32x4*>(stf + (wm * WTM + j * 32 + lr) * SPF + wn * WTN + i * 32 + 8 * g + 4 * hk) =
                   f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-      }
+          }
       __syncthreads();
       store_staged<BM, BN, SPF, NT>(stf, P + split * p_split, ldp, m0, n0, M, N, tid);
       return;
