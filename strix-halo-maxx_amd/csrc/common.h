@@ -49,8 +49,31 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(c2, x * x, c1));
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
-// GELU, erf form (torch nn.GELU() default): 0.5 x (1 + erf(x / sqrt 2)).
-__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }
+// GELU, erf form (torch nn.GELU() default): 0.5 x (1 + erf(z)), z = x / sqrt 2, in torch's order, with
+// erf(z) = sign(z) (1 - erfc(|z|)) and erfc from the Chebyshev fit of Numerical Recipes (2nd ed., section 6.2, erfcc):
+// erfc(a) = t exp(-a^2 + P(t)), t = 1 / (1 + a / 2), P of degree 9, fractional error below 1.2e-7 for every a >= 0.
+// One hardware reciprocal and one exp2 like gelu_tanh, against the ~5x costlier library erff. For every bf16 input
+// the bf16 result equals that of the same formula with a correctly rounded erf (checked exhaustively in fp32 on the
+// CPU, 33,409 inputs in [-12, 12]; beyond, erf rounds to +-1 either way); the hardware rcp / exp2 can move a result
+// by one bf16 ulp.
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float z = x * 0.7071067811865476f;
+  const float a = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, a, 1.0f));
+  float p = 0.17087277f;
+  p = __builtin_fmaf(p, t, -0.82215223f);
+  p = __builtin_fmaf(p, t, 1.48851587f);
+  p = __builtin_fmaf(p, t, -1.13520398f);
+  p = __builtin_fmaf(p, t, 0.27886807f);
+  p = __builtin_fmaf(p, t, -0.18628806f);
+  p = __builtin_fmaf(p, t, 0.09678418f);
+  p = __builtin_fmaf(p, t, 0.37409196f);
+  p = __builtin_fmaf(p, t, 1.00002368f);
+  p = __builtin_fmaf(p, t, -1.26551223f);
+  const float erfc_a = t * __builtin_amdgcn_exp2f((p - a * a) * 1.4426950408889634f);
+  const float e = 1.0f - erfc_a;
+  return 0.5f * x * (1.0f + (z < 0.0f ? -e : e));
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
