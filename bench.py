@@ -449,7 +449,7 @@ def measured_traffic(label, sym):
 
 
 def _cpu_threads():
-    """Threads for the CPU baselines: the host's logical CPUs, at most 16 (the box's CPU share for one GPU)."""
+    """Threads for the CPU baselines: the host's logical CPUs, at most 16 (the CPU share of one GPU on an 8-GPU host)."""
     return min(os.cpu_count() or 1, 16)
 
 
