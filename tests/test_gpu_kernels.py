@@ -356,6 +356,36 @@ def test_gemm_res_ln_refuses_a_grid_larger_than_the_gpu(dev):
         lin.res_ln(x, x, ln)
 
 
+@pytest.mark.parametrize("cfg", [None, 0, 19])
+def test_gelu_epilogues_every_bf16_input(dev, cfg):
+    """The GELU epilogues (erf: a Chebyshev erfc fit; tanh: x / (1 + exp(-2u))) on every finite bf16 value in
+    [-12, 12]: an identity weight makes the linear output the input itself, so each value goes through the epilogue
+    once. Against torch's F.gelu in fp32 (tgemm.py:21-25 for tanh; nn.GELU for erf): for x >= -4, within two bf16
+    ulps and at most 0.5 % of the values differing at all (torch's own erf / tanh and the hardware exp2 / reciprocal
+    each round differently in the last fp32 bit); below, where torch's 1 + erf / 1 + tanh cancels and its result
+    carries fp32 noise of ~|x| 6e-8, within 2e-6 absolute (those outputs are below 1.3e-4)."""
+    allv = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(BF)
+    vals = allv[torch.isfinite(allv.float()) & (allv.float().abs() <= 12)]
+    K = 1024
+    M = (vals.numel() + K - 1) // K
+    x = torch.zeros(M * K, dtype=BF)
+    x[:vals.numel()] = vals
+    x = x.view(M, K)
+    lin = ops.MxLin(torch.eye(K, dtype=BF), torch.zeros(K, dtype=BF))
+    if cfg is not None:
+        lin.cfgs[M] = (cfg, 1)
+    print(f"gelu every bf16 cfg={cfg} values={vals.numel()}", flush=True)
+    xd = x.to(dev)
+    assert torch.equal(lin(xd).cpu(), x)  # the identity linear passes every value through unchanged
+    xf = x.float()
+    core = xf >= -4.0
+    for kw, ref in ((dict(act="erf"), F.gelu(xf)), (dict(gelu=True), F.gelu(xf, approximate="tanh"))):
+        y = lin(xd, **kw).cpu()
+        exp = ref.to(BF)
+        assert within_ulps(y[core], exp[core], n=2, frac=5e-3), kw
+        assert ((y[~core].float() - exp[~core].float()).abs() <= 2e-6).all(), kw
+
+
 @pytest.mark.parametrize("cfg", [None, 0, 7, 8, 12, 15, 16, 17])
 def test_gemm_epilogues_match_unfused(dev, cfg):
     """GELU applied to the bf16-rounded linear output, then + residual (md2fast.py:55-67; i8gemm.hip:378); the gated
